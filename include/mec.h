@@ -1,0 +1,128 @@
+/*
+ * mec.h — C ABI of the MI355X (gfx950) memory-efficient CLIP / LiT loss.
+ *
+ * This library replaces the four Triton kernels and the PyTorch glue of the
+ * reference's autograd Functions (b0nce/MemoryEfficientCLIP):
+ *   clip_sum_exp_kernel   clip_loss.py:9-64      -> mec_sumexp   (mode CLIP)
+ *   lit_sum_exp_kernel    lit_loss.py:9-62       -> mec_sumexp   (mode LIT)
+ *   forward epilogue      clip_loss.py:199-213,
+ *                         lit_loss.py:192-205    -> mec_finalize
+ *   clip_grad_kernel      clip_loss.py:67-156    -> mec_grad     (mode CLIP)
+ *   lit_grad_kernel       lit_loss.py:65-148     -> mec_grad     (mode LIT)
+ *   backward pro/epilogue clip_loss.py:234-256,
+ *                         lit_loss.py:226-247    -> mec_postpass
+ *   F.normalize(dim=1)    clip_loss.py:266-268,
+ *                         lit_loss.py:257-259    -> fused: mec_prepass + mec_postpass
+ *                                                   with normalize = 1
+ *   Function.forward      clip_loss.py:159-213   -> mec_forward  (prepass+sumexp+finalize)
+ *   Function.backward     clip_loss.py:215-256   -> mec_backward (grad+postpass)
+ *
+ * The reference has no FFI of its own: its boundary is the PyTorch
+ * autograd.Function (clip_loss.py:159, lit_loss.py:151).  These entry points
+ * are what that Function calls here, through ctypes.
+ *
+ * Conventions
+ *   - Every function returns MEC_OK (0) or a negative MEC_ERR_* code and never
+ *     throws.  mec_last_error() returns a thread-local description of the
+ *     last failure on the calling thread.
+ *   - Pointers are device pointers.  x and y are row-major [n, d] with row
+ *     strides ldx, ldy (in elements, >= d) and unit column stride.
+ *     x is the row side of S = x^ y^T: image for CLIP, text for LiT.
+ *   - dtype: MEC_DTYPE_F32 (float) or MEC_DTYPE_BF16 (uint16 bfloat16 bits).
+ *   - All work is enqueued on `stream` (a hipStream_t; NULL = default
+ *     stream).  No function synchronises the host and none allocates device
+ *     memory: the workspace and the gradient scratch are caller-owned.
+ *   - Argument validation is pure host code; invalid arguments are reported
+ *     before anything touches the GPU.
+ */
+#ifndef MEC_H_
+#define MEC_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MEC_OK 0
+#define MEC_ERR_INVALID (-1)     /* bad argument (null pointer, size, enum) */
+#define MEC_ERR_UNSUPPORTED (-2) /* valid but not supported by this build */
+#define MEC_ERR_HIP (-3)         /* a HIP runtime call failed */
+
+#define MEC_DTYPE_F32 0
+#define MEC_DTYPE_BF16 1
+
+#define MEC_MODE_CLIP 0 /* symmetric image<->text loss, gradients for x and y */
+#define MEC_MODE_LIT 1  /* text->image only (x = text), gradient for x only */
+
+/* Thread-local message for the last error on this thread ("" if none). */
+const char* mec_last_error(void);
+
+/* Library version string. */
+const char* mec_version(void);
+
+/* Number of floats of the per-call workspace: 8 vectors of length n
+ * (inverse norms rx, ry; raw diagonal x_i.y_i; off-diagonal row/column sums
+ * of E = exp((S-1)/T); 1/R; 1/C; diagonal gradient coefficient).  The same
+ * workspace must be passed to mec_forward and the matching mec_backward
+ * (it replaces ctx.save_for_backward of the sums, clip_loss.py:199). */
+int64_t mec_workspace_floats(int64_t n);
+
+/* Bytes of gradient scratch needed by mec_grad / mec_backward for (n, d,
+ * dtype).  It holds the gradient-matrix blocks of one block diagonal:
+ * about n * bs floats, with bs ~ 2d (so O(n*d)).  Returns < 0 on bad args. */
+int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype);
+
+/* rx, ry (1 if !normalize), diag; clears the sum accumulators. */
+int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
+                int dtype, int normalize, float* workspace, void* stream);
+
+/* Accumulates the off-diagonal sums sum_{j!=i} E_ij (and sum_{i!=j} E_ij for
+ * CLIP) into the workspace.  Requires mec_prepass first. */
+int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
+               int dtype, int mode, int normalize, float temperature, float* workspace,
+               void* stream);
+
+/* Loss (fp32 scalar at *loss, device pointer) and the backward's per-row
+ * vectors.  CLIP: mean over i of (CE_row_i + CE_col_i)/2; LiT: mean CE_row_i. */
+int mec_finalize(int64_t n, int mode, float temperature, float* workspace, float* loss,
+                 void* stream);
+
+/* prepass + sumexp + finalize. */
+int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
+                int dtype, int mode, int normalize, float temperature, float* workspace,
+                float* loss, void* stream);
+
+/* Off-diagonal gradient contractions into fp32 accumulators [n, d]
+ * (row stride d):  acc_x_i = sum_{j!=i} G'_ij y^_j,  acc_y_j = sum_{i!=j} G'_ij x^_i
+ * with G'_ij = E_ij (1/R_i + 1/C_j) (LiT: E_ij / R_i; acc_y is ignored).
+ * A NULL accumulator skips that side (e.g. a frozen tower); at least one is
+ * required.  scratch must hold mec_grad_scratch_bytes(n, d, dtype) bytes. */
+int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
+             int dtype, int mode, int normalize, float temperature, const float* workspace,
+             void* scratch, int64_t scratch_bytes, float* acc_x, float* acc_y, void* stream);
+
+/* Final gradients from the accumulators: scale a = grad_scale/(2n) (LiT:
+ * grad_scale/n), exact diagonal term, F.normalize backward when normalize,
+ * times *grad_output (device fp32 scalar, NULL = 1), cast to dtype.
+ * grad_scale is 1/T for the standard loss and sqrt(n/T) for the Stable
+ * variants (clip_loss.py:182, :299).  dx/dy are row-major [n, d] (row
+ * stride d) and may alias acc_x/acc_y when dtype is F32.  A side is skipped
+ * when both its accumulator and its output are NULL (LiT: always y). */
+int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
+                 int dtype, int mode, int normalize, float grad_scale, const float* workspace,
+                 const float* grad_output, const float* acc_x, const float* acc_y, void* dx,
+                 void* dy, void* stream);
+
+/* mec_grad + mec_postpass. */
+int mec_backward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
+                 int dtype, int mode, int normalize, float temperature, float grad_scale,
+                 const float* workspace, const float* grad_output, void* scratch,
+                 int64_t scratch_bytes, float* acc_x, float* acc_y, void* dx, void* dy,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEC_H_ */

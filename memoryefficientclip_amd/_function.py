@@ -1,0 +1,122 @@
+"""Host side of the contrastive-loss hot path: argument checks, buffer
+allocation and the calls into the HIP library (``include/mec.h``).
+
+This mirrors the glue of the reference's autograd Functions
+(``clip_loss.py:159-256``, ``lit_loss.py:151-247``): the same inputs, the same
+0-d fp32 loss, the same gradients.  Differences by design:
+
+* the loss epilogue, the gradient initialisation and ``grad_output`` scaling
+  run in HIP kernels (no PyTorch epilogue ops, no host sync on
+  ``grad_output != 1``, ``clip_loss.py:252``);
+* the optional L2 normalisation is fused (``normalize=True``) instead of
+  running ``F.normalize`` (``clip_loss.py:266-268``) as separate PyTorch ops;
+* any N >= 1 and D >= 1 is accepted, with exact masking of ragged tiles, and
+  inputs with a row stride are read in place (no ``.contiguous()`` copy).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def check_inputs(x: torch.Tensor, y: torch.Tensor) -> None:
+    """Argument checks; AssertionError where the reference asserts
+    (``clip_loss.py:166-167``), TypeError/ValueError for the rest."""
+    if not (isinstance(x, torch.Tensor) and isinstance(y, torch.Tensor)):
+        raise TypeError("features must be torch.Tensor")
+    if not (x.is_cuda and y.is_cuda):
+        raise AssertionError("MemoryEfficientCLIP: inputs must be GPU tensors (x.is_cuda and y.is_cuda)")
+    if x.shape != y.shape:
+        raise AssertionError(f"MemoryEfficientCLIP: shape mismatch {tuple(x.shape)} vs {tuple(y.shape)}")
+    if x.dim() != 2:
+        raise ValueError(f"features must be 2-D [batch, dim], got {x.dim()}-D")
+    if x.shape[0] < 1 or x.shape[1] < 1:
+        raise ValueError("features must have batch >= 1 and dim >= 1")
+    if x.dtype != y.dtype:
+        raise TypeError(f"dtype mismatch {x.dtype} vs {y.dtype}")
+    if x.dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {x.dtype}; supported: float32, bfloat16")
+    if x.device != y.device:
+        raise ValueError(f"inputs on different devices {x.device} vs {y.device}")
+
+
+def _rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """Tensor with unit column stride and its row stride (elements)."""
+    if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+        t = t.contiguous()
+    return t, t.stride(0)
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def forward(ctx, x: torch.Tensor, y: torch.Tensor, temperature: float, mode: int, normalize: bool,
+            stable: bool) -> torch.Tensor:
+    check_inputs(x, y)
+    temperature = float(temperature)
+    if not (temperature > 0.0 and math.isfinite(temperature)):
+        raise ValueError(f"temperature must be finite and > 0, got {temperature}")
+    x, ldx = _rows(x)
+    y, ldy = _rows(y)
+    n, d = x.shape
+    dev = x.device
+    dt = _DTYPES[x.dtype]
+    with torch.cuda.device(dev):
+        ws = torch.empty(_lib.load().mec_workspace_floats(n), dtype=torch.float32, device=dev)
+        loss = torch.empty((), dtype=torch.float32, device=dev)
+        _lib.call("mec_forward", x.data_ptr(), ldx, y.data_ptr(), ldy, n, d, dt, mode, int(normalize),
+                  temperature, ws.data_ptr(), loss.data_ptr(), _stream(dev))
+    ctx.save_for_backward(x, y, ws)
+    ctx.mec = (ldx, ldy, n, d, dt, mode, bool(normalize), temperature,
+               math.sqrt(n / temperature) if stable else 1.0 / temperature)
+    return loss
+
+
+def backward(ctx, grad_output: torch.Tensor, need_x: bool, need_y: bool):
+    """Returns (dx, dy); a side that is not needed comes back as None."""
+    x, y, ws = ctx.saved_tensors
+    ldx, ldy, n, d, dt, mode, normalize, temperature, grad_scale = ctx.mec
+    if mode == _lib.MODE_LIT:
+        need_y = False
+    if not (need_x or need_y):
+        return None, None
+    dev = x.device
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        go = grad_output.detach().to(device=dev, dtype=torch.float32).reshape(()).contiguous()
+        acc_x = torch.empty((n, d), dtype=torch.float32, device=dev) if need_x else None
+        acc_y = torch.empty((n, d), dtype=torch.float32, device=dev) if need_y else None
+        if dt == _lib.DTYPE_F32:
+            dx, dy = acc_x, acc_y  # the post-pass runs in place
+        else:
+            dx = torch.empty((n, d), dtype=x.dtype, device=dev) if need_x else None
+            dy = torch.empty((n, d), dtype=y.dtype, device=dev) if need_y else None
+        nbytes = lib.mec_grad_scratch_bytes(n, d, dt)
+        scratch = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+        def ptr(t):
+            return None if t is None else t.data_ptr()
+
+        _lib.call("mec_backward", x.data_ptr(), ldx, y.data_ptr(), ldy, n, d, dt, mode, int(normalize),
+                  temperature, grad_scale, ws.data_ptr(), go.data_ptr(), scratch.data_ptr(), nbytes,
+                  ptr(acc_x), ptr(acc_y), ptr(dx), ptr(dy), _stream(dev))
+    return dx, dy
+
+
+class ContrastiveLossFn(torch.autograd.Function):
+    """Fused loss used by the nn.Modules (normalisation optionally fused)."""
+
+    @staticmethod
+    def forward(ctx, x, y, temperature, mode, normalize, stable):
+        return forward(ctx, x, y, temperature, mode, normalize, stable)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        dx, dy = backward(ctx, grad_output, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        return dx, dy, None, None, None, None

@@ -1,0 +1,153 @@
+// O(N*D) and O(N) kernels around the MFMA hot loops: the normalisation /
+// diagonal pre-pass, the loss finalize, and the gradient post-pass.  These are
+// HBM-bound; one 64-lane wave owns one feature row.
+#pragma once
+#include "mec_common.h"
+
+namespace mec {
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
+};
+template <> struct Elem<uint16_t> {
+  static __device__ __forceinline__ float load(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+  static __device__ __forceinline__ void store(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+};
+
+// Per row i: rx = 1/max(||x_i||, 1e-12) (or 1), ry likewise, diag = x_i . y_i.
+// Also clears the off-diagonal sum accumulators used by the sum-exp kernel.
+// Follows F.normalize(dim=1) as applied at clip_loss.py:266-268 and the
+// einsum('bi,bi->b') diagonal at clip_loss.py:206.
+template <typename T, bool NORM>
+__global__ __launch_bounds__(256) void k_prepass(const T* __restrict__ X, int64_t ldx,
+                                                 const T* __restrict__ Y, int64_t ldy, int N, int D,
+                                                 float* __restrict__ ws) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= N) return;
+  const T* x = X + (int64_t)row * ldx;
+  const T* y = Y + (int64_t)row * ldy;
+  float sx = 0.f, sy = 0.f, sxy = 0.f;
+  for (int d = lane; d < D; d += 64) {
+    float a = Elem<T>::load(x, d), b = Elem<T>::load(y, d);
+    sx = fmaf(a, a, sx);
+    sy = fmaf(b, b, sy);
+    sxy = fmaf(a, b, sxy);
+  }
+  sx = wave_sum(sx);
+  sy = wave_sum(sy);
+  sxy = wave_sum(sxy);
+  if (lane == 0) {
+    const int64_t n = N;
+    float rx = 1.f, ry = 1.f;
+    if (NORM) {
+      rx = 1.f / fmaxf(sqrtf(sx), 1e-12f);
+      ry = 1.f / fmaxf(sqrtf(sy), 1e-12f);
+    }
+    ws[WS_RX * n + row] = rx;
+    ws[WS_RY * n + row] = ry;
+    ws[WS_DIAG * n + row] = sxy;
+    ws[WS_ROW_OFF * n + row] = 0.f;
+    ws[WS_COL_OFF * n + row] = 0.f;
+  }
+}
+
+// Loss epilogue (clip_loss.py:206-211, lit_loss.py:199-203) plus the per-row
+// quantities the backward needs.  In natural-log units with t_i = (s_ii-1)/T:
+//   R_i = row_off_i + e^{t_i},  l^r_i = ln R_i - t_i = softplus(ln row_off_i - t_i)
+// which is the same cross-entropy term as -ln(2^Sv_i / R_i) in the reference,
+// evaluated without cancellation.  CLIP averages (l^r + l^c)/2, LiT uses l^r.
+// kappa_i = -(row_off_i/R_i + col_off_i/C_i) is the exact diagonal entry of
+// the gradient matrix in units of a = grad_scale/(2N) (LiT: grad_scale/N).
+// Single workgroup, fp64 accumulation, deterministic.
+__device__ __forceinline__ double softplus_log_ratio(double off, double t) {
+  if (!(off > 0.0)) return 0.0;
+  double u = log(off) - t;
+  return u > 0.0 ? u + log1p(exp(-u)) : log1p(exp(u));
+}
+
+template <bool LIT>
+__global__ __launch_bounds__(1024) void k_finalize(int N, double inv_t, float* __restrict__ ws,
+                                                   float* __restrict__ loss) {
+  __shared__ double red[16];
+  const int64_t n = N;
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+    const double s = (double)ws[WS_DIAG * n + i] * (double)ws[WS_RX * n + i] * (double)ws[WS_RY * n + i];
+    const double t = (s - 1.0) * inv_t;
+    const double e = exp(t);
+    const double ro = ws[WS_ROW_OFF * n + i];
+    const double R = ro + e;
+    acc += softplus_log_ratio(ro, t);
+    ws[WS_INV_ROW * n + i] = (float)(1.0 / R);
+    double kap = -(ro / R);
+    if (!LIT) {
+      const double co = ws[WS_COL_OFF * n + i];
+      const double C = co + e;
+      acc += softplus_log_ratio(co, t);
+      ws[WS_INV_COL * n + i] = (float)(1.0 / C);
+      kap -= co / C;
+    }
+    ws[WS_KAPPA * n + i] = (float)kap;
+  }
+  acc = wave_sum_f64(acc);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) red[w] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double tot = 0.0;
+    for (int k = 0; k < (int)(blockDim.x >> 6); ++k) tot += red[k];
+    *loss = (float)(tot / (LIT ? (double)N : 2.0 * (double)N));
+  }
+}
+
+// Gradient post-pass for one side.  With acc the off-diagonal contraction
+// sum_{j != i} G'_ij * oth^_j (oth^ = normalised other side) and a the
+// scale grad_scale/(2N) (LiT: /N):
+//   d_own^_i = a * (acc_i + kappa_i * oth^_i)                       (diag term)
+//   d_own_i  = r_i (d_own^_i - own^_i <own^_i, d_own^_i>)            (F.normalize bwd)
+//            = r_i d_own^_i                                           (if ||own_i|| <= eps)
+//   out_i    = grad_output * d_own_i                                 (clip_loss.py:252-254)
+// out may alias acc (fp32 outputs): every element is read before it is written
+// by the same lane.
+template <typename T, bool NORM>
+__global__ __launch_bounds__(256) void k_postpass(const T* __restrict__ own, int64_t ld_own,
+                                                  const T* __restrict__ oth, int64_t ld_oth, int N, int D,
+                                                  const float* __restrict__ r_own, const float* __restrict__ r_oth,
+                                                  const float* __restrict__ kappa, float a,
+                                                  const float* __restrict__ grad_output,
+                                                  const float* acc, T* out) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= N) return;
+  const T* xo = own + (int64_t)row * ld_own;
+  const T* yo = oth + (int64_t)row * ld_oth;
+  const float* ac = acc + (int64_t)row * D;
+  T* o = out + (int64_t)row * D;
+  const float ro = r_own[row];
+  const float kq = kappa[row] * r_oth[row];
+  const float go = grad_output ? *grad_output : 1.f;
+  if (NORM) {
+    float dot = 0.f;
+    for (int d = lane; d < D; d += 64) {
+      float g = a * fmaf(kq, Elem<T>::load(yo, d), ac[d]);
+      dot = fmaf(Elem<T>::load(xo, d) * ro, g, dot);
+    }
+    dot = wave_sum(dot);
+    const bool clamped = ro >= 1e12f;
+    for (int d = lane; d < D; d += 64) {
+      float g = a * fmaf(kq, Elem<T>::load(yo, d), ac[d]);
+      float v = clamped ? ro * g : ro * (g - Elem<T>::load(xo, d) * ro * dot);
+      Elem<T>::store(o, d, go * v);
+    }
+  } else {
+    for (int d = lane; d < D; d += 64) {
+      float g = a * fmaf(kq, Elem<T>::load(yo, d), ac[d]);
+      Elem<T>::store(o, d, go * g);
+    }
+  }
+}
+
+}  // namespace mec

@@ -1,0 +1,105 @@
+"""The C-ABI library loads on a machine without a GPU, exports every function
+declared in include/mec.h, and rejects bad arguments in pure host code (no
+GPU work is launched by any call in this file)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from memoryefficientclip_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mec.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(mec_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    assert "mec_forward" in names and "mec_backward" in names and "mec_last_error" in names
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table and header disagree"
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+
+
+def test_sizes():
+    lib = _lib.load()
+    assert lib.mec_workspace_floats(1000) == 8000
+    assert lib.mec_workspace_floats(0) < 0
+    # scratch is O(n*d): one block diagonal of the N x N gradient matrix
+    for n, d in [(1024, 512), (32768, 1152), (65536, 768), (262144, 1152), (1000, 3)]:
+        b32 = lib.mec_grad_scratch_bytes(n, d, 0)
+        b16 = lib.mec_grad_scratch_bytes(n, d, 1)
+        assert b32 == 2 * b16 > 0
+        assert b32 <= 4 * (n + 128 * 64) * max(1024, 2 * d + 256), (n, d, b32)
+    assert lib.mec_grad_scratch_bytes(10, 10, 7) < 0
+
+
+VALID = dict(x=16, ldx=64, y=16, ldy=64, n=10, d=64, dtype=0, mode=0, normalize=1, temperature=0.07)
+
+
+@pytest.mark.parametrize("field,value,needle", [
+    ("n", 0, "n="), ("d", 0, "d="), ("ldx", 8, "row strides"), ("dtype", 5, "dtype"),
+    ("mode", 3, "mode"), ("temperature", -1.0, "temperature"), ("temperature", float("nan"), "temperature"),
+    ("x", None, "non-null"),
+])
+def test_sumexp_rejects_invalid_arguments(field, value, needle):
+    a = dict(VALID)
+    a[field] = value
+    lib = _lib.load()
+    rc = lib.mec_sumexp(a["x"], a["ldx"], a["y"], a["ldy"], a["n"], a["d"], a["dtype"], a["mode"], a["normalize"],
+                        a["temperature"], 16, None)
+    assert rc == _lib.MEC_ERR_INVALID
+    assert needle in _lib.last_error()
+
+
+def test_grad_rejects_small_scratch_and_missing_outputs():
+    lib = _lib.load()
+    need = lib.mec_grad_scratch_bytes(10, 64, 0)
+    rc = lib.mec_grad(16, 64, 16, 64, 10, 64, 0, 0, 1, 0.07, 16, 16, need - 1, 16, 16, None)
+    assert rc == _lib.MEC_ERR_INVALID and "scratch" in _lib.last_error()
+    rc = lib.mec_grad(16, 64, 16, 64, 10, 64, 0, 0, 1, 0.07, 16, 16, need, None, None, None)
+    assert rc == _lib.MEC_ERR_INVALID and "no gradient" in _lib.last_error()
+    rc = lib.mec_grad(16, 64, 16, 64, 10, 64, 0, 0, 1, 0.07, 16, 8, need, 16, 16, None)
+    assert rc == _lib.MEC_ERR_INVALID and "aligned" in _lib.last_error()
+
+
+def test_postpass_and_finalize_validation():
+    lib = _lib.load()
+    rc = lib.mec_postpass(16, 64, 16, 64, 10, 64, 0, 0, 1, 1.0, 16, None, 16, None, None, None, None)
+    assert rc == _lib.MEC_ERR_INVALID and "accumulator" in _lib.last_error()
+    rc = lib.mec_postpass(16, 64, 16, 64, 10, 64, 0, 0, 1, float("inf"), 16, None, 16, 16, 16, 16, None)
+    assert rc == _lib.MEC_ERR_INVALID and "grad_scale" in _lib.last_error()
+    assert lib.mec_finalize(10, 0, 0.07, None, None, None) == _lib.MEC_ERR_INVALID
+    assert lib.mec_finalize(0, 0, 0.07, 16, 16, None) == _lib.MEC_ERR_INVALID
+
+
+def test_error_string_is_thread_local():
+    import threading
+    lib = _lib.load()
+    lib.mec_finalize(10, 9, 0.07, 16, 16, None)
+    seen = {}
+
+    def other():
+        seen["msg"] = lib.mec_last_error().decode()
+
+    th = threading.Thread(target=other)
+    th.start()
+    th.join()
+    assert seen["msg"] == ""
+    assert "mode" in _lib.last_error()
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load(tmp_path / "nope.so")

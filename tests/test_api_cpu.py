@@ -1,0 +1,99 @@
+"""Host-side behaviour of the drop-in modules that needs no GPU: class names
+and signatures match the reference's, error behaviour on CPU tensors and bad
+shapes, no parameters/buffers, and no CPU fallback."""
+import inspect
+
+import pytest
+import torch
+
+import memoryefficientclip_amd as mec
+from memoryefficientclip_amd import clip_loss, lit_loss
+
+REFERENCE_NAMES = {
+    clip_loss: ["MemoryEfficientCLIPLossNormed", "MemoryEfficientCLIPLoss", "StableMemoryEfficientCLIPLossNormed",
+                "StableMemoryEfficientCLIPLoss"],
+    lit_loss: ["MemoryEfficientLiTLossNormed", "MemoryEfficientLiTLoss", "StableMemoryEfficientLiTLossNormed",
+               "StableMemoryEfficientLiTLoss"],
+}
+
+
+def test_reference_class_names_exist():
+    for mod, names in REFERENCE_NAMES.items():
+        for n in names:
+            assert hasattr(mod, n) and hasattr(mec, n)
+
+
+def test_signatures_match_reference():
+    # clip_loss.py:260, :265 ; lit_loss.py:251, :256 ; Function.forward clip_loss.py:161
+    for cls in [clip_loss.MemoryEfficientCLIPLoss, clip_loss.StableMemoryEfficientCLIPLoss]:
+        assert list(inspect.signature(cls.__init__).parameters) == ["self", "temperature", "normalized_inputs"]
+        assert list(inspect.signature(cls.forward).parameters) == ["self", "image_features", "text_features"]
+    for cls in [lit_loss.MemoryEfficientLiTLoss, lit_loss.StableMemoryEfficientLiTLoss]:
+        assert list(inspect.signature(cls.__init__).parameters) == ["self", "temperature", "normalized_inputs"]
+        assert list(inspect.signature(cls.forward).parameters) == ["self", "text_features", "image_features"]
+    for fn in [clip_loss.MemoryEfficientCLIPLossNormed, lit_loss.MemoryEfficientLiTLossNormed,
+               clip_loss.StableMemoryEfficientCLIPLossNormed, lit_loss.StableMemoryEfficientLiTLossNormed]:
+        sig = inspect.signature(fn.forward)
+        assert list(sig.parameters) == ["ctx", "x_normalized", "y_normalized", "temperature"]
+        assert sig.parameters["temperature"].default == 0.07
+        assert issubclass(fn, torch.autograd.Function)
+
+
+def test_defaults_and_empty_state_dict():
+    m = clip_loss.MemoryEfficientCLIPLoss()
+    assert m.temperature == 0.07 and m.normalized_inputs is False
+    assert m.state_dict() == {} and list(m.parameters()) == []
+
+
+@pytest.mark.parametrize("cls", [clip_loss.MemoryEfficientCLIPLoss, lit_loss.MemoryEfficientLiTLoss,
+                                 clip_loss.StableMemoryEfficientCLIPLoss, lit_loss.StableMemoryEfficientLiTLoss])
+def test_cpu_tensors_raise_like_reference(cls):
+    # reference: assert X.is_cuda and Y.is_cuda (clip_loss.py:166); no CPU fallback here either
+    a = torch.randn(8, 16)
+    with pytest.raises(AssertionError, match="GPU"):
+        cls(0.07)(a, a)
+    with pytest.raises(AssertionError, match="GPU"):
+        cls(0.07, normalized_inputs=True)(a, a)
+
+
+def test_normed_function_cpu_raises():
+    a = torch.randn(8, 16)
+    with pytest.raises(AssertionError):
+        clip_loss.MemoryEfficientCLIPLossNormed.apply(a, a, 0.07)
+    with pytest.raises(AssertionError):
+        lit_loss.MemoryEfficientLiTLossNormed.apply(a, a)
+
+
+def test_check_inputs_shape_and_dtype_rules():
+    from memoryefficientclip_amd._function import check_inputs
+
+    class FakeCuda(torch.Tensor):
+        @property
+        def is_cuda(self):
+            return True
+
+    def fake(shape, dtype=torch.float32):
+        return torch.zeros(shape, dtype=dtype).as_subclass(FakeCuda)
+
+    with pytest.raises(AssertionError, match="shape"):
+        check_inputs(fake((4, 8)), fake((4, 9)))
+    with pytest.raises(ValueError, match="2-D"):
+        check_inputs(fake((4,)), fake((4,)))
+    with pytest.raises(TypeError, match="unsupported dtype"):
+        check_inputs(fake((4, 8), torch.float64), fake((4, 8), torch.float64))
+    with pytest.raises(TypeError, match="dtype mismatch"):
+        check_inputs(fake((4, 8)), fake((4, 8), torch.bfloat16))
+    check_inputs(fake((4, 8), torch.bfloat16), fake((4, 8), torch.bfloat16))
+
+
+def test_product_path_does_not_import_oracle():
+    import ast
+    import pathlib
+    pkg = pathlib.Path(mec.__file__).parent
+    for f in pkg.rglob("*.py"):
+        tree = ast.parse(f.read_text())
+        for node in ast.walk(tree):
+            if isinstance(node, ast.Import):
+                assert not any(a.name.split(".")[0] == "oracle" for a in node.names), f
+            if isinstance(node, ast.ImportFrom):
+                assert (node.module or "").split(".")[0] != "oracle", f

@@ -1,0 +1,306 @@
+"""GPU parity: the HIP library (through its C ABI, via the drop-in modules and
+directly) against the fp64 CPU oracle on identical seeded inputs.
+
+Tolerances (from the task's correctness definition): fp32 loss rel 1e-4 and
+gradient max-rel (max|g - g_ref| / max|g_ref|) 1e-3; bf16 1e-2 for both.
+"""
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import TOL, correlated_pair, max_rel, randn_pair, rel_err
+from memoryefficientclip_amd import _lib
+from memoryefficientclip_amd.clip_loss import (
+    MemoryEfficientCLIPLoss,
+    MemoryEfficientCLIPLossNormed,
+    StableMemoryEfficientCLIPLoss,
+    StableMemoryEfficientCLIPLossNormed,
+)
+from memoryefficientclip_amd.lit_loss import (
+    MemoryEfficientLiTLoss,
+    MemoryEfficientLiTLossNormed,
+    StableMemoryEfficientLiTLoss,
+    StableMemoryEfficientLiTLossNormed,
+)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def run_module(module, a, b, grad_a=True, grad_b=True, grad_scale=None):
+    """Forward + backward on the GPU; returns (loss, da, db) on the CPU."""
+    ga = a.to(DEV).requires_grad_(grad_a)
+    gb = b.to(DEV).requires_grad_(grad_b)
+    loss = module(ga, gb)
+    if grad_scale is None:
+        loss.backward()
+    else:
+        (loss * grad_scale).backward()
+    torch.cuda.synchronize()
+    da = ga.grad.cpu() if grad_a else None
+    db = gb.grad.cpu() if grad_b else None
+    return loss.detach().cpu(), da, db
+
+
+def check(name, dtype, loss, ref_loss, grads):
+    tol = TOL[dtype]
+    le = rel_err(loss, ref_loss)
+    msg = f"{name}: loss {float(loss):.8f} ref {float(ref_loss):.8f} rel {le:.2e}"
+    errs = []
+    for gname, g, gref in grads:
+        e = max_rel(g, gref)
+        errs.append(e)
+        msg += f" | {gname} max-rel {e:.2e}"
+    say(msg)
+    if float(ref_loss) == 0.0:
+        assert abs(float(loss)) < 1e-6, msg
+    else:
+        assert le <= tol["loss"], msg
+    for e in errs:
+        assert e <= tol["grad"], msg
+
+
+# ---------------------------------------------------------------- golden fixtures
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz"))),
+                         ids=lambda p: os.path.basename(p)[:-4])
+def test_golden_fixture(path):
+    z = np.load(path)
+    name = os.path.basename(path)[:-4]
+    lit = name.startswith("lit")
+    t = float(z["temperature"])
+    normed, stable, bf16 = bool(z["normalized_inputs"]), bool(z["stable"]), bool(z["bf16"])
+    dtype = torch.bfloat16 if bf16 else torch.float32
+    a = torch.from_numpy(z["a"]).to(dtype)
+    b = torch.from_numpy(z["b"]).to(dtype)
+    say(f"golden {name} n={a.shape[0]} d={a.shape[1]} dtype={dtype}")
+    if lit:
+        mod = (StableMemoryEfficientLiTLoss if stable else MemoryEfficientLiTLoss)(t, normed)
+        loss, da, _ = run_module(mod, a, b, grad_b=False)
+        check(name, dtype, loss, z["loss"], [("d_text", da, torch.from_numpy(z["da"]))])
+    else:
+        mod = (StableMemoryEfficientCLIPLoss if stable else MemoryEfficientCLIPLoss)(t, normed)
+        loss, da, db = run_module(mod, a, b)
+        check(name, dtype, loss, z["loss"],
+              [("d_img", da, torch.from_numpy(z["da"])), ("d_txt", db, torch.from_numpy(z["db"]))])
+
+
+# ---------------------------------------------------------------- config 1 (full size)
+def test_config1_clip_fp32_parity():
+    a, b = randn_pair(1024, 512, seed=0)
+    say("config1 CLIP n=1024 d=512 fp32 unnormalised T=0.07")
+    loss, da, db = run_module(MemoryEfficientCLIPLoss(0.07, False), a, b)
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    check("config1", torch.float32, loss, rl, [("d_img", da, rda), ("d_txt", db, rdb)])
+    assert abs(float(loss) - (math.log(1024) + 1 / (2 * 512 * 0.07 ** 2))) < 0.1  # closed-form sanity
+
+
+# ---------------------------------------------------------------- scaled-down configs 2-5
+@pytest.mark.parametrize("n,d", [(2048, 1152), (1000, 1152)])
+def test_config2_shape_clip_fp32(n, d):
+    a, b = randn_pair(n, d, seed=2)
+    say(f"config2-shape CLIP n={n} d={d} fp32")
+    loss, da, db = run_module(MemoryEfficientCLIPLoss(0.07), a, b)
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    check(f"c2 n={n}", torch.float32, loss, rl, [("d_img", da, rda), ("d_txt", db, rdb)])
+
+
+@pytest.mark.parametrize("n,d", [(2048, 1152), (777, 1152)])
+def test_config3_shape_lit_fp32(n, d):
+    txt, img = randn_pair(n, d, seed=3)
+    say(f"config3-shape LiT n={n} d={d} fp32 (image frozen)")
+    loss, dt, _ = run_module(MemoryEfficientLiTLoss(0.07), txt, img, grad_b=False)
+    rl, rdt = oracle.lit_loss_and_grads(txt, img, 0.07)
+    check(f"c3 n={n}", torch.float32, loss, rl, [("d_text", dt, rdt)])
+
+
+@pytest.mark.parametrize("n,d,t", [(2048, 768, 0.07), (1536, 1152, 0.05)])
+def test_config4_5_shape_clip_bf16(n, d, t):
+    img, txt = correlated_pair(n, d, seed=4)
+    say(f"config4/5-shape CLIP n={n} d={d} bf16 normalized_inputs T={t}")
+    loss, da, db = run_module(MemoryEfficientCLIPLoss(t, normalized_inputs=True), img, txt)
+    rl, rda, rdb = oracle.clip_loss_and_grads(img.float(), txt.float(), t, normalized_inputs=True)
+    check(f"c4/5 n={n}", torch.bfloat16, loss, rl, [("d_img", da, rda), ("d_txt", db, rdb)])
+
+
+# ---------------------------------------------------------------- edge shapes
+@pytest.mark.parametrize("n,d", [(1, 1), (2, 3), (5, 17), (127, 64), (129, 100), (256, 4), (300, 768), (640, 20)])
+def test_edge_shapes_fp32(n, d):
+    a, b = randn_pair(n, d, seed=n + d)
+    say(f"edge CLIP n={n} d={d}")
+    loss, da, db = run_module(MemoryEfficientCLIPLoss(0.07), a, b)
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    check(f"edge n={n} d={d}", torch.float32, loss, rl, [("d_img", da, rda), ("d_txt", db, rdb)])
+
+
+@pytest.mark.parametrize("n,d", [(3, 8), (130, 24), (257, 200)])
+def test_edge_shapes_bf16(n, d):
+    a, b = randn_pair(n, d, seed=n * 3 + d, dtype=torch.bfloat16)
+    say(f"edge bf16 CLIP n={n} d={d}")
+    loss, da, db = run_module(MemoryEfficientCLIPLoss(0.1), a, b)
+    rl, rda, rdb = oracle.clip_loss_and_grads(a.float(), b.float(), 0.1)
+    check(f"edge bf16 n={n} d={d}", torch.bfloat16, loss, rl, [("d_img", da, rda), ("d_txt", db, rdb)])
+
+
+def test_row_strided_inputs():
+    """Inputs that are column slices of wider buffers are read in place."""
+    a, b = randn_pair(300, 96, seed=21)
+    wa = torch.zeros(300, 128)
+    wb = torch.zeros(300, 160)
+    wa[:, 5:101] = a
+    wb[:, 32:128] = b
+    ga = wa.to(DEV)[:, 5:101].requires_grad_(True)
+    gb = wb.to(DEV)[:, 32:128].requires_grad_(True)
+    say("row-strided inputs n=300 d=96 ld=128/160")
+    loss = MemoryEfficientCLIPLoss(0.07)(ga, gb)
+    loss.backward()
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    check("strided", torch.float32, loss.detach().cpu(), rl, [("d_img", ga.grad.cpu(), rda), ("d_txt", gb.grad.cpu(), rdb)])
+
+
+# ---------------------------------------------------------------- API behaviour
+def test_normed_functions_and_grad_output():
+    a, b = randn_pair(500, 64, seed=31)
+    an, bn = oracle.normalize(a).float(), oracle.normalize(b).float()
+    ga = an.to(DEV).requires_grad_(True)
+    gb = bn.to(DEV).requires_grad_(True)
+    say("MemoryEfficientCLIPLossNormed.apply with grad_output=-3")
+    loss = MemoryEfficientCLIPLossNormed.apply(ga, gb, 0.07)
+    (loss * -3.0).backward()
+    rl = oracle.clip_forward(an, bn, 0.07)
+    rda, rdb = oracle.clip_backward(an, bn, 0.07, grad_output=-3.0)
+    check("normed g=-3", torch.float32, loss.detach().cpu(), rl, [("dX", ga.grad.cpu(), rda), ("dY", gb.grad.cpu(), rdb)])
+    gt = an.to(DEV).requires_grad_(True)
+    loss = MemoryEfficientLiTLossNormed.apply(gt, bn.to(DEV), 0.05)
+    loss.backward()
+    rl = oracle.lit_forward(an, bn, 0.05)
+    check("lit normed", torch.float32, loss.detach().cpu(), rl, [("dX", gt.grad.cpu(), oracle.lit_backward(an, bn, 0.05))])
+
+
+def test_stable_variants():
+    a, b = randn_pair(384, 48, seed=41)
+    say("Stable CLIP / LiT (module and Normed)")
+    loss, da, db = run_module(StableMemoryEfficientCLIPLoss(0.07), a, b)
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07, stable=True)
+    check("stable clip", torch.float32, loss, rl, [("d_img", da, rda), ("d_txt", db, rdb)])
+    loss, dt, _ = run_module(StableMemoryEfficientLiTLoss(0.07), a, b, grad_b=False)
+    rl, rdt = oracle.lit_loss_and_grads(a, b, 0.07, stable=True)
+    check("stable lit", torch.float32, loss, rl, [("d_text", dt, rdt)])
+    an, bn = oracle.normalize(a).float(), oracle.normalize(b).float()
+    loss, dx, dy = run_module(lambda x, y: StableMemoryEfficientCLIPLossNormed.apply(x, y, 0.07), an, bn)
+    rdx, rdy = oracle.clip_backward(an, bn, 0.07, stable=True)
+    check("stable clip normed", torch.float32, loss, oracle.clip_forward(an, bn, 0.07), [("dX", dx, rdx), ("dY", dy, rdy)])
+    loss, dx, _ = run_module(lambda x, y: StableMemoryEfficientLiTLossNormed.apply(x, y, 0.07), an, bn, grad_b=False)
+    check("stable lit normed", torch.float32, loss, oracle.lit_forward(an, bn, 0.07),
+          [("dX", dx, oracle.lit_backward(an, bn, 0.07, stable=True))])
+
+
+def test_single_side_gradient():
+    a, b = randn_pair(260, 40, seed=51)
+    say("CLIP with frozen image tower")
+    loss, da, db = run_module(MemoryEfficientCLIPLoss(0.07), a, b, grad_a=False, grad_b=True)
+    rl, _, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    check("frozen image", torch.float32, loss, rl, [("d_txt", db, rdb)])
+    assert da is None
+
+
+def test_backward_is_deterministic_and_forward_reproducible():
+    a, b = randn_pair(1500, 256, seed=61)
+    say("determinism n=1500 d=256")
+    l1, a1, b1 = run_module(MemoryEfficientCLIPLoss(0.07), a, b)
+    l2, a2, b2 = run_module(MemoryEfficientCLIPLoss(0.07), a, b)
+    assert rel_err(l1, l2) < 1e-6
+    # the sums R, C come from relaxed atomics (order varies); the gradient
+    # contractions themselves use no atomics
+    assert max_rel(a1, a2) < 1e-6 and max_rel(b1, b2) < 1e-6
+
+
+def test_known_answers_gpu():
+    say("known answers: identical rows -> ln N, zero gradient")
+    n = 300
+    v = torch.nn.functional.normalize(torch.randn(1, 32, generator=torch.Generator().manual_seed(3)), dim=1)
+    v = v.repeat(n, 1)
+    loss, da, db = run_module(MemoryEfficientCLIPLoss(0.07, normalized_inputs=True), v, v)
+    assert abs(float(loss) - math.log(n)) < 1e-4 * math.log(n)
+    assert da.abs().max() < 1e-6 and db.abs().max() < 1e-6
+    eye = torch.eye(200, 256)
+    loss, _, _ = run_module(MemoryEfficientCLIPLoss(0.07, normalized_inputs=True), eye, eye)
+    assert rel_err(loss, math.log1p(199 * math.exp(-1 / 0.07))) < 1e-4
+
+
+# ---------------------------------------------------------------- per-entry-point checks through the C ABI
+def _ptr(t):
+    return t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+@pytest.mark.parametrize("mode", [_lib.MODE_CLIP, _lib.MODE_LIT])
+@pytest.mark.parametrize("normalize", [0, 1])
+def test_abi_stages(mode, normalize):
+    n, d, t = 700, 72, 0.07
+    a, b = randn_pair(n, d, seed=71 + mode + 2 * normalize)
+    if not normalize:
+        a, b = oracle.normalize(a).float(), oracle.normalize(b).float()
+    x, y = a.to(DEV), b.to(DEV)
+    lib = _lib.load()
+    ws = torch.empty(lib.mec_workspace_floats(n), device=DEV)
+    loss = torch.empty((), device=DEV)
+    say(f"ABI stages mode={mode} normalize={normalize}")
+    _lib.call("mec_prepass", _ptr(x), d, _ptr(y), d, n, d, 0, normalize, _ptr(ws), _stream())
+    _lib.call("mec_sumexp", _ptr(x), d, _ptr(y), d, n, d, 0, mode, normalize, t, _ptr(ws), _stream())
+    w = ws.view(8, n).cpu().double()
+    xh, yh = oracle.normalize(a), oracle.normalize(b)
+    s, e, r, c = oracle.similarity_sums(xh, yh, t)
+    ed = torch.diagonal(e)
+    if normalize:
+        assert torch.allclose(w[0], 1 / a.double().norm(dim=1), rtol=1e-6)
+        assert torch.allclose(w[1], 1 / b.double().norm(dim=1), rtol=1e-6)
+    assert torch.allclose(w[2], (a.double() * b.double()).sum(1), rtol=1e-5, atol=1e-5)
+    assert max_rel(w[3], r - ed) < 1e-5
+    if mode == _lib.MODE_CLIP:
+        assert max_rel(w[4], c - ed) < 1e-5
+    _lib.call("mec_finalize", n, mode, t, _ptr(ws), _ptr(loss), _stream())
+    w = ws.view(8, n).cpu().double()
+    ref = oracle.clip_forward(xh, yh, t) if mode == _lib.MODE_CLIP else oracle.lit_forward(xh, yh, t)
+    assert rel_err(loss.item(), ref) < 1e-5
+    assert max_rel(w[5], 1 / r) < 1e-5
+    if mode == _lib.MODE_CLIP:
+        assert max_rel(w[6], 1 / c) < 1e-5
+        assert max_rel(w[7], -((r - ed) / r + (c - ed) / c)) < 1e-5
+    else:
+        assert max_rel(w[7], -((r - ed) / r)) < 1e-5
+    # contractions (off-diagonal, unscaled): acc_x_i = sum_{j != i} G'_ij y^_j
+    acc_x = torch.empty(n, d, device=DEV)
+    acc_y = torch.empty(n, d, device=DEV) if mode == _lib.MODE_CLIP else None
+    nbytes = lib.mec_grad_scratch_bytes(n, d, 0)
+    scratch = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    _lib.call("mec_grad", _ptr(x), d, _ptr(y), d, n, d, 0, mode, normalize, t, _ptr(ws), _ptr(scratch), nbytes,
+              _ptr(acc_x), None if acc_y is None else _ptr(acc_y), _stream())
+    off = 1.0 - torch.eye(n, dtype=torch.float64)
+    gp = e * (1 / r)[:, None] * off
+    if mode == _lib.MODE_CLIP:
+        gp = gp + e * (1 / c)[None, :] * off
+        assert max_rel(acc_y.cpu(), gp.T @ xh) < 1e-5
+    assert max_rel(acc_x.cpu(), gp @ yh) < 1e-5
+
+
+def test_abi_rejects_bad_arguments_on_gpu_box():
+    lib = _lib.load()
+    x = torch.zeros(4, 4, device=DEV)
+    ws = torch.empty(lib.mec_workspace_floats(4), device=DEV)
+    assert lib.mec_forward(_ptr(x), 4, _ptr(x), 4, 4, 4, 0, 0, 0, 0.0, _ptr(ws), _ptr(ws), None) == _lib.MEC_ERR_INVALID
+    assert "temperature" in _lib.last_error()
+    assert lib.mec_grad(_ptr(x), 4, _ptr(x), 4, 4, 4, 0, 0, 0, 0.07, _ptr(ws), _ptr(ws), 1, _ptr(ws), _ptr(ws),
+                        None) == _lib.MEC_ERR_INVALID
+    assert "scratch" in _lib.last_error()
