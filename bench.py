@@ -1,0 +1,297 @@
+#!/usr/bin/env python3
+"""Throughput of the fused CLIP / LiT contrastive loss (forward + backward) on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--no-cpu]
+
+A step is one ``loss = module(a, b); loss.backward()`` through the drop-in
+``nn.Module`` on synthetic inputs already resident in HBM.  The default
+workload is the headline configuration (CLIP, N=32768, D=1152, fp32,
+normalized_inputs=False, T=0.07); ``--config`` selects another row of the
+benchmark table for exploration.  Rank 0 prints ONE JSON line:
+
+* ``value``: whole-job TFLOP/s, algorithmic flop 8 N^2 D (CLIP) / 6 N^2 D
+  (LiT) per step (the backward counts the similarity recompute) over the
+  wall-clock of K timed steps;
+* ``roofline``: the dominant kernel's algorithmic flop per launch over its
+  average launch time, measured with HIP events on the stream the library
+  launches on (torch's current stream), against the dense MFMA peak of the
+  input dtype;
+* ``cpu_baseline``: the dense PyTorch loss (fp32) on the host cores, on a
+  bounded sample of the same workload (smaller N, same D and generator),
+  scaled to TFLOP/s with the same flop convention.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "CLIP fwd+bwd ms & TFLOP/s (% MFMA peak) at N=32768 D=1152, 1 MI355X"
+# MI355X published dense MFMA peaks (256 CUs at 2.4 GHz), TFLOP/s.
+PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6}
+
+# config -> (mode, n, d, dtype, normalized_inputs, temperature, generator, cpu sample n)
+CONFIGS = {
+    1: ("clip", 1024, 512, "f32", False, 0.07, "randn", 1024),
+    2: ("clip", 32768, 1152, "f32", False, 0.07, "randn", 8192),
+    3: ("lit", 32768, 1152, "f32", False, 0.07, "randn", 8192),
+    4: ("clip", 65536, 768, "bf16", True, 0.07, "correlated", 8192),
+    5: ("clip", 262144, 1152, "bf16", True, 0.05, "correlated", 8192),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_inputs(n, d, gen, seed=0):
+    """Seeded host generator (bitwise reproducible), fp32 math."""
+    import torch
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(seed)
+    if gen == "randn":
+        a = torch.randn(n, d, generator=g)
+        b = torch.randn(n, d, generator=g)
+    else:
+        a = F.normalize(torch.randn(n, d, generator=g), dim=1)
+        b = F.normalize(a + 0.5 * torch.randn(n, d, generator=g), dim=1)
+    return a, b
+
+
+def algo_flop(mode, n, d):
+    return (8.0 if mode == "clip" else 6.0) * n * n * d
+
+
+def time_stage(fn, reps, stream):
+    """Average launch time (ms) of fn() over reps, HIP events on `stream`."""
+    import torch
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for s, e in ev:
+        s.record(stream)
+        fn()
+        e.record(stream)
+    torch.cuda.synchronize()
+    return statistics.mean(s.elapsed_time(e) for s, e in ev)
+
+
+def kernel_leg(x, y, mode, dt, normalize, temperature, reps):
+    """Times each C-ABI stage of the path on its own (same inputs, same stream).
+
+    Returns {stage: (avg ms per call, launches per call, algorithmic flop per call)}."""
+    import torch
+    from memoryefficientclip_amd import _lib
+    lib = _lib.load()
+    n, d = x.shape
+    m = _lib.MODE_CLIP if mode == "clip" else _lib.MODE_LIT
+    dtc = _lib.DTYPE_F32 if dt == "f32" else _lib.DTYPE_BF16
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    ws = torch.empty(lib.mec_workspace_floats(n), device=x.device)
+    loss = torch.empty((), device=x.device)
+    nbytes = lib.mec_grad_scratch_bytes(n, d, dtc)
+    scratch = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    acc_x = torch.empty(n, d, device=x.device)
+    acc_y = torch.empty(n, d, device=x.device) if m == _lib.MODE_CLIP else None
+    pa = acc_y.data_ptr() if acc_y is not None else None
+    X, Y = x.data_ptr(), y.data_ptr()
+    norm = int(normalize)
+
+    def prepass():
+        _lib.call("mec_prepass", X, d, Y, d, n, d, dtc, norm, ws.data_ptr(), sp)
+
+    def sumexp():
+        _lib.call("mec_sumexp", X, d, Y, d, n, d, dtc, m, norm, temperature, ws.data_ptr(), sp)
+
+    def finalize():
+        _lib.call("mec_finalize", n, m, temperature, ws.data_ptr(), loss.data_ptr(), sp)
+
+    def grad():
+        _lib.call("mec_grad", X, d, Y, d, n, d, dtc, m, norm, temperature, ws.data_ptr(), scratch.data_ptr(),
+                  nbytes, acc_x.data_ptr(), pa, sp)
+
+    def postpass():
+        # fp32 accumulators converted in a separate output so repeated calls stay valid
+        _lib.call("mec_postpass", X, d, Y, d, n, d, dtc, m, norm, 1.0 / temperature, ws.data_ptr(), None,
+                  acc_x.data_ptr(), pa, out_x.data_ptr(), None if acc_y is None else out_y.data_ptr(), sp)
+
+    out_x = torch.empty(n, d, dtype=x.dtype, device=x.device)
+    out_y = torch.empty(n, d, dtype=x.dtype, device=x.device) if acc_y is not None else None
+    prepass()
+    sumexp()
+    finalize()
+    grad()
+    torch.cuda.synchronize()
+    sides = 2 if m == _lib.MODE_CLIP else 1
+    res = {}
+    res["prepass"] = (time_stage(prepass, reps, stream), 1, 0.0)
+    prepass()
+    res["sumexp"] = (time_stage(sumexp, reps, stream), 1, 2.0 * n * n * d)
+    prepass()
+    sumexp()
+    res["finalize"] = (time_stage(finalize, reps, stream), 1, 0.0)
+    res["grad"] = (time_stage(grad, reps, stream), 0, 2.0 * n * n * d * (1 + sides))
+    res["postpass"] = (time_stage(postpass, reps, stream), sides, 0.0)
+    return res
+
+
+def cpu_baseline(mode, d, dt, normalized, temperature, gen, n_cpu, budget_s=20.0):
+    """Dense PyTorch loss on the host cores on an (n_cpu, d) sample of the workload."""
+    import torch
+    from oracle.cpu_baseline import dense_step
+    a, b = make_inputs(n_cpu, d, gen, seed=0)
+    if dt == "bf16":
+        a, b = a.bfloat16().float(), b.bfloat16().float()
+    dense_step(a, b, temperature, mode == "lit", normalized)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s * 0.5 and len(times) < 10):
+        t0 = time.perf_counter()
+        dense_step(a, b, temperature, mode == "lit", normalized)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s:
+            break
+    med = statistics.median(times)
+    return {
+        "value": round(algo_flop(mode, n_cpu, d) / med / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"dense fp32 PyTorch {mode.upper()} fwd+bwd (F.normalize, logits, cross_entropy, autograd) "
+                   f"at N={n_cpu}, D={d}, same generator; median of {len(times)} runs = {med * 1e3:.1f} ms; "
+                   f"flop {('8' if mode == 'clip' else '6')}*N^2*D"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--kernel-reps", type=int, default=0, help="launches per stage in the kernel leg (default: steps)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs the whole N x N loss on one GPU (no collectives); "
+              f"--gpus {args.gpus} / WORLD_SIZE={world} is not supported, run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
+        sys.exit(1)
+    from memoryefficientclip_amd import MemoryEfficientCLIPLoss, MemoryEfficientLiTLoss, _lib
+    _lib.load()  # fail loudly if the HIP library is missing
+
+    mode, n, d, dt, normalized, temperature, gen, n_cpu = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    tdtype = torch.float32 if dt == "f32" else torch.bfloat16
+    log(f"bench: config {args.config} {mode} n={n} d={d} {dt} normalized_inputs={normalized} T={temperature}")
+    a_h, b_h = make_inputs(n, d, gen, seed=0)
+    a = a_h.to(dev, tdtype).requires_grad_(True)
+    b = b_h.to(dev, tdtype).requires_grad_(mode == "clip")
+    del a_h, b_h
+    module = (MemoryEfficientCLIPLoss if mode == "clip" else MemoryEfficientLiTLoss)(temperature, normalized)
+
+    def step(evs=None):
+        if evs is not None:
+            evs[0].record()
+        loss = module(a, b)
+        if evs is not None:
+            evs[1].record()
+        loss.backward()
+        if evs is not None:
+            evs[2].record()
+        a.grad = None
+        b.grad = None
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log("bench: warm-up done")
+
+    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    loss = step()
+    torch.cuda.synchronize()
+    peak_extra = torch.cuda.max_memory_allocated(dev) - base
+    loss_val = float(loss)
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        step(evs[k])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    fwd_ms = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+    bwd_ms = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
+    ms = wall * 1e3 / args.steps
+    flop = algo_flop(mode, n, d)
+    tflops = flop / (ms * 1e-3) / 1e12
+    log(f"bench: {args.steps} steps, {ms:.3f} ms/step (fwd {fwd_ms:.3f}, bwd {bwd_ms:.3f}), {tflops:.2f} TFLOP/s, "
+        f"loss {loss_val:.6f}")
+
+    # kernel leg: per-stage launch times on the library's stream
+    x = a.detach()
+    y = b.detach()
+    reps = args.kernel_reps or args.steps
+    stages = kernel_leg(x, y, mode, dt, not normalized, temperature, reps)
+    for k, (t, nl, fl) in stages.items():
+        log(f"bench: stage {k:9s} {t:9.3f} ms" + (f"  {fl / (t * 1e-3) / 1e12:8.2f} TFLOP/s" if fl else ""))
+    # dominant single-launch kernel: the forward similarity kernel (one launch, 2 N^2 D flop)
+    t_k = stages["sumexp"][0]
+    f_k = stages["sumexp"][2]
+    peak = PEAK_TFLOPS[dt]
+    achieved = f_k / (t_k * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "kernel": "k_sumexp", "achieved": round(achieved, 3), "peak": peak,
+                "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+                "launch_ms": round(t_k, 4), "flop_per_launch": f_k}
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"bench: CPU baseline at n={n_cpu} ...")
+        cpu = cpu_baseline(mode, d, dt, normalized, temperature, gen, n_cpu)
+        log(f"bench: CPU baseline {cpu['value']} TFLOP/s on {cpu['cores']} threads")
+
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dt,
+        "data": "synthetic",
+        "config": {"workload": f"{mode}_loss_fwd_bwd", "n": n, "d": d, "temperature": temperature,
+                   "normalized_inputs": normalized, "input_dtype": dt, "parallelism": "none (1 GPU)"},
+        "fwd_ms": round(fwd_ms, 4),
+        "bwd_ms": round(bwd_ms, 4),
+        "frac_of_peak": round(tflops / peak, 4),
+        "peak_extra_hbm_bytes": int(peak_extra),
+        "loss": loss_val,
+        "stages_ms": {k: round(v[0], 4) for k, v in stages.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -258,3 +258,18 @@ def test_golden_fixtures(path):
             loss, da = oracle.lit_loss_and_grads(a, b, t, normed, stable)
         assert abs(loss.item() - float(z["loss"])) <= 1e-11 * max(1.0, abs(float(z["loss"]))), f
         assert torch.allclose(da, torch.from_numpy(z["da"]), rtol=1e-9, atol=1e-15), f
+
+
+def test_cpu_baseline_matches_oracle():
+    """The dense fp32 CPU baseline timed by bench.py computes the same loss."""
+    from oracle.cpu_baseline import dense_step
+    a, b = _inputs(96, 40, seed=77, dtype=torch.float32)
+    loss, da, db = dense_step(a, b, 0.07, lit=False, normalized_inputs=False)
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    assert abs(loss.item() - rl.item()) < 1e-5 * rl.item()
+    assert torch.allclose(da.double(), rda, rtol=1e-3, atol=1e-6 * rda.abs().max().item())
+    assert torch.allclose(db.double(), rdb, rtol=1e-3, atol=1e-6 * rdb.abs().max().item())
+    loss, dt, none = dense_step(a, b, 0.05, lit=True, normalized_inputs=False)
+    rl, rdt = oracle.lit_loss_and_grads(a, b, 0.05)
+    assert none is None and abs(loss.item() - rl.item()) < 1e-5 * rl.item()
+    assert torch.allclose(dt.double(), rdt, rtol=1e-3, atol=1e-6 * rdt.abs().max().item())
