@@ -82,10 +82,25 @@ def time_stage(fn, reps, stream):
     return statistics.mean(s.elapsed_time(e) for s, e in ev)
 
 
+def grad_step_flop(n, d, bs, nb, sides):
+    """Algorithmic flop of each backward pipeline step t = 0..nb: step t
+    recomputes the similarity blocks of diagonal t (2 d per pair) and
+    contracts diagonal t-1 (2 d per pair and side)."""
+    rows = [min(bs, n - i * bs) for i in range(nb)]
+    pairs = [sum(rows[i] * rows[(i + s) % nb] for i in range(nb)) for s in range(nb)]
+    out = []
+    for t in range(nb + 1):
+        f = 2.0 * d * pairs[t] if t < nb else 0.0
+        if t >= 1:
+            f += sides * 2.0 * d * pairs[t - 1]
+        out.append(f)
+    return out
+
+
 def kernel_leg(x, y, mode, dt, normalize, temperature, reps):
     """Times each C-ABI stage of the path on its own (same inputs, same stream).
 
-    Returns {stage: (avg ms per call, launches per call, algorithmic flop per call)}."""
+    Returns {stage: (avg ms per launch, launches per step, algorithmic flop per launch)}."""
     import torch
     from memoryefficientclip_amd import _lib
     lib = _lib.load()
@@ -100,9 +115,13 @@ def kernel_leg(x, y, mode, dt, normalize, temperature, reps):
     scratch = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
     acc_x = torch.empty(n, d, device=x.device)
     acc_y = torch.empty(n, d, device=x.device) if m == _lib.MODE_CLIP else None
+    out_x = torch.empty(n, d, dtype=x.dtype, device=x.device)
+    out_y = torch.empty(n, d, dtype=x.dtype, device=x.device) if acc_y is not None else None
     pa = acc_y.data_ptr() if acc_y is not None else None
     X, Y = x.data_ptr(), y.data_ptr()
     norm = int(normalize)
+    bs, nb = _lib.grad_blocking(n, d, dtc)
+    sides = 2 if m == _lib.MODE_CLIP else 1
 
     def prepass():
         _lib.call("mec_prepass", X, d, Y, d, n, d, dtc, norm, ws.data_ptr(), sp)
@@ -113,23 +132,19 @@ def kernel_leg(x, y, mode, dt, normalize, temperature, reps):
     def finalize():
         _lib.call("mec_finalize", n, m, temperature, ws.data_ptr(), loss.data_ptr(), sp)
 
-    def grad():
-        _lib.call("mec_grad", X, d, Y, d, n, d, dtc, m, norm, temperature, ws.data_ptr(), scratch.data_ptr(),
-                  nbytes, acc_x.data_ptr(), pa, sp)
+    def grad_step(t):
+        _lib.call("mec_grad_step", X, d, Y, d, n, d, dtc, m, norm, temperature, ws.data_ptr(), t,
+                  scratch.data_ptr(), nbytes, acc_x.data_ptr(), pa, sp)
 
     def postpass():
-        # fp32 accumulators converted in a separate output so repeated calls stay valid
+        # the fp32 accumulators are converted into separate outputs so repeated calls stay valid
         _lib.call("mec_postpass", X, d, Y, d, n, d, dtc, m, norm, 1.0 / temperature, ws.data_ptr(), None,
-                  acc_x.data_ptr(), pa, out_x.data_ptr(), None if acc_y is None else out_y.data_ptr(), sp)
+                  acc_x.data_ptr(), pa, out_x.data_ptr(), None if out_y is None else out_y.data_ptr(), sp)
 
-    out_x = torch.empty(n, d, dtype=x.dtype, device=x.device)
-    out_y = torch.empty(n, d, dtype=x.dtype, device=x.device) if acc_y is not None else None
     prepass()
     sumexp()
     finalize()
-    grad()
     torch.cuda.synchronize()
-    sides = 2 if m == _lib.MODE_CLIP else 1
     res = {}
     res["prepass"] = (time_stage(prepass, reps, stream), 1, 0.0)
     prepass()
@@ -137,9 +152,32 @@ def kernel_leg(x, y, mode, dt, normalize, temperature, reps):
     prepass()
     sumexp()
     res["finalize"] = (time_stage(finalize, reps, stream), 1, 0.0)
-    res["grad"] = (time_stage(grad, reps, stream), 0, 2.0 * n * n * d * (1 + sides))
+    # every launch of the backward pipeline, in order, reps times
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nb + 1)]
+          for _ in range(reps)]
+    for r in range(reps):
+        for t in range(nb + 1):
+            ev[r][t][0].record(stream)
+            grad_step(t)
+            ev[r][t][1].record(stream)
+    torch.cuda.synchronize()
+    per_step = [statistics.mean(ev[r][t][0].elapsed_time(ev[r][t][1]) for r in range(reps)) for t in range(nb + 1)]
+    flops = grad_step_flop(n, d, bs, nb, sides)
+    res["grad_step"] = (statistics.mean(per_step), nb + 1, sum(flops) / (nb + 1))
     res["postpass"] = (time_stage(postpass, reps, stream), sides, 0.0)
-    return res
+    return res, {"block_rows": bs, "num_blocks": nb, "step_ms": [round(v, 4) for v in per_step]}
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` at `workload` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/traffic_<workload>.md,
+    machine-readable copy in profiles/traffic.json), or None if not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)[workload][kernel]["bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(mode, d, dt, normalized, temperature, gen, n_cpu, budget_s=20.0):
@@ -178,6 +216,8 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-reps", type=int, default=0, help="launches per stage in the kernel leg (default: steps)")
+    ap.add_argument("--probe", choices=["copy"], default=None,
+                    help="copy: only run 5 plain device copies of 1 GiB (calibrates the rocprofv3 byte counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -190,6 +230,15 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
         sys.exit(1)
+    if args.probe == "copy":
+        src = torch.ones(1 << 28, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"probe": "copy", "bytes_read_per_copy": src.numel() * 4,
+                          "bytes_written_per_copy": dst.numel() * 4}), flush=True)
+        return
     from memoryefficientclip_amd import MemoryEfficientCLIPLoss, MemoryEfficientLiTLoss, _lib
     _lib.load()  # fail loudly if the HIP library is missing
 
@@ -227,7 +276,7 @@ def main():
     loss = step()
     torch.cuda.synchronize()
     peak_extra = torch.cuda.max_memory_allocated(dev) - base
-    loss_val = float(loss)
+    loss_val = float(loss.detach())
 
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     torch.cuda.synchronize()
@@ -248,17 +297,22 @@ def main():
     x = a.detach()
     y = b.detach()
     reps = args.kernel_reps or args.steps
-    stages = kernel_leg(x, y, mode, dt, not normalized, temperature, reps)
+    stages, blocking = kernel_leg(x, y, mode, dt, not normalized, temperature, reps)
     for k, (t, nl, fl) in stages.items():
-        log(f"bench: stage {k:9s} {t:9.3f} ms" + (f"  {fl / (t * 1e-3) / 1e12:8.2f} TFLOP/s" if fl else ""))
-    # dominant single-launch kernel: the forward similarity kernel (one launch, 2 N^2 D flop)
-    t_k = stages["sumexp"][0]
-    f_k = stages["sumexp"][2]
+        log(f"bench: stage {k:9s} {t:9.3f} ms x {nl:3d}" + (f"  {fl / (t * 1e-3) / 1e12:8.2f} TFLOP/s" if fl else ""))
+    log(f"bench: backward blocking {blocking}")
+    # dominant kernel: k_grad_step (nb + 1 launches per step, about 3/4 of the step's flop)
+    t_k, nl_k, f_k = stages["grad_step"]
     peak = PEAK_TFLOPS[dt]
     achieved = f_k / (t_k * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": "k_sumexp", "achieved": round(achieved, 3), "peak": peak,
-                "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
-                "launch_ms": round(t_k, 4), "flop_per_launch": f_k}
+    roofline = {"bound": "mfma", "kernel": "k_grad_step", "achieved": round(achieved, 3), "peak": peak,
+                "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
+                "traffic": measured_traffic(f"{mode}_n{n}_d{d}_{dt}", "k_grad_step"),
+                "launch_ms": round(t_k, 4), "flop_per_launch": f_k, "launches_per_step": nl_k}
+    t_f, _, f_f = stages["sumexp"]
+    roofline_fwd = {"kernel": "k_sumexp", "achieved": round(f_f / (t_f * 1e-3) / 1e12, 3),
+                    "frac": round(f_f / (t_f * 1e-3) / 1e12 / peak, 4), "launch_ms": round(t_f, 4),
+                    "flop_per_launch": f_f}
 
     cpu = None
     if not args.no_cpu:
@@ -288,6 +342,8 @@ def main():
         "loss": loss_val,
         "stages_ms": {k: round(v[0], 4) for k, v in stages.items()},
         "roofline": roofline,
+        "roofline_forward": roofline_fwd,
+        "backward_blocking": blocking,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

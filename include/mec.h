@@ -68,10 +68,20 @@ const char* mec_version(void);
  * (it replaces ctx.save_for_backward of the sums, clip_loss.py:199). */
 int64_t mec_workspace_floats(int64_t n);
 
-/* Bytes of gradient scratch needed by mec_grad / mec_backward for (n, d,
- * dtype).  It holds the gradient-matrix blocks of one block diagonal:
- * about n * bs floats, with bs ~ 2d (so O(n*d)).  Returns < 0 on bad args. */
+/* Bytes of gradient scratch needed by mec_grad / mec_grad_step /
+ * mec_backward for (n, d, dtype), all in the input dtype: two buffers holding
+ * one block diagonal of the off-diagonal gradient matrix each (nb blocks of
+ * bs x bs, bs ~ 2d), the same blocks transposed, and transposed normalised
+ * copies of x and y ([d][n rounded up to 128]); O(n*d) in total.
+ * Returns < 0 on bad args. */
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype);
+
+/* Block decomposition of the backward for (n, d, dtype): the n x n gradient
+ * matrix is cut into num_blocks^2 blocks of block_rows rows (the last block
+ * may be short); mec_grad runs num_blocks + 1 pipeline steps.  No counterpart
+ * in the reference (its backward grid is fixed at 64 x 64 tiles,
+ * clip_loss.py:239-249); exposed so callers can size and drive the steps. */
+int mec_grad_blocking(int64_t n, int64_t d, int dtype, int64_t* block_rows, int64_t* num_blocks);
 
 /* rx, ry (1 if !normalize), diag; clears the sum accumulators. */
 int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
@@ -96,11 +106,25 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
 /* Off-diagonal gradient contractions into fp32 accumulators [n, d]
  * (row stride d):  acc_x_i = sum_{j!=i} G'_ij y^_j,  acc_y_j = sum_{i!=j} G'_ij x^_i
  * with G'_ij = E_ij (1/R_i + 1/C_j) (LiT: E_ij / R_i; acc_y is ignored).
- * A NULL accumulator skips that side (e.g. a frozen tower); at least one is
- * required.  scratch must hold mec_grad_scratch_bytes(n, d, dtype) bytes. */
+ * Replaces clip_grad_kernel (clip_loss.py:67-156) and lit_grad_kernel
+ * (lit_loss.py:65-148).  A NULL accumulator skips that side (e.g. a frozen
+ * tower); at least one is required.  scratch must hold
+ * mec_grad_scratch_bytes(n, d, dtype) bytes, 16-byte aligned.
+ * Equivalent to mec_grad_step for step = 0 .. num_blocks in order. */
 int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
              int dtype, int mode, int normalize, float temperature, const float* workspace,
              void* scratch, int64_t scratch_bytes, float* acc_x, float* acc_y, void* stream);
+
+/* One pipeline step of mec_grad (one kernel launch): step t in
+ * [0, num_blocks] recomputes the similarity blocks of block diagonal t and
+ * stores their gradient-matrix blocks in scratch buffer t % 2, and contracts
+ * diagonal t - 1 from the other buffer into the accumulators (step 1
+ * overwrites them, later steps add).  Steps must run in order on one
+ * stream with the same scratch. */
+int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
+                  int dtype, int mode, int normalize, float temperature, const float* workspace,
+                  int64_t step, void* scratch, int64_t scratch_bytes, float* acc_x, float* acc_y,
+                  void* stream);
 
 /* Final gradients from the accumulators: scale a = grad_scale/(2n) (LiT:
  * grad_scale/n), exact diagonal term, F.normalize backward when normalize,

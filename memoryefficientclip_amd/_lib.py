@@ -34,12 +34,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mec_version": (ctypes.c_char_p, []),
     "mec_workspace_floats": (_i64, [_i64]),
     "mec_grad_scratch_bytes": (_i64, [_i64, _i64, _int]),
+    "mec_grad_blocking": (_int, [_i64, _i64, _int, _vp, _vp]),
     "mec_prepass": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp]),
     "mec_sumexp": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _int, _f32, _vp, _vp]),
     "mec_finalize": (_int, [_i64, _int, _f32, _vp, _vp, _vp]),
     "mec_forward": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _int, _f32, _vp, _vp, _vp]),
     "mec_grad": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _int, _f32, _vp, _vp, _i64, _vp, _vp,
                         _vp]),
+    "mec_grad_step": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _int, _f32, _vp, _i64, _vp, _i64,
+                             _vp, _vp, _vp]),
     "mec_postpass": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _int, _f32, _vp, _vp, _vp, _vp, _vp,
                             _vp, _vp]),
     "mec_backward": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _int, _f32, _f32, _vp, _vp, _vp, _i64,
@@ -79,6 +82,13 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         if path is None:
             _lib = lib
         return lib
+
+
+def grad_blocking(n: int, d: int, dtype: int) -> tuple[int, int]:
+    """(block_rows, num_blocks) of the backward's block decomposition."""
+    bs, nb = ctypes.c_int64(), ctypes.c_int64()
+    call("mec_grad_blocking", n, d, dtype, ctypes.byref(bs), ctypes.byref(nb))
+    return bs.value, nb.value
 
 
 def last_error() -> str:

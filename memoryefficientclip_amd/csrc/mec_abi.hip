@@ -70,8 +70,12 @@ bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, i
   return aligned16(x) && aligned16(y) && d % per == 0 && ldx % per == 0 && ldy % per == 0;
 }
 
-// Block decomposition of the N x N gradient matrix for the backward: blocks
-// of tb 128-row tiles with tb ~ 2d/128 (>= 8), balanced over nb blocks.
+// Block decomposition of the N x N gradient matrix for the backward: nb
+// blocks of tb 128-row tiles.  The target is tb ~ 2d/128 (>= 8), which keeps
+// the scratch at O(n d) and the contraction depth (bs = 128 tb) about twice
+// the similarity depth d.  An exact divisor of the tile count within a factor
+// of two of the target is preferred (no short last block, whose contractions
+// would have a short K); otherwise the tiles are balanced over the blocks.
 void grad_blocks(int64_t n, int64_t d, int* bs, int* nb) {
   const int64_t tiles = (n + 127) / 128;
   int64_t target = (2 * d + 127) / 128;
@@ -80,19 +84,52 @@ void grad_blocks(int64_t n, int64_t d, int* bs, int* nb) {
     long v = std::strtol(env, nullptr, 10);
     if (v >= 1 && v <= 4096) target = v;
   }
-  if (target > tiles) target = tiles;
-  const int64_t nbv = (tiles + target - 1) / target;
-  const int64_t tb = (tiles + nbv - 1) / nbv;
+  int64_t tb;
+  if (target >= tiles) {
+    tb = tiles;
+  } else {
+    int64_t best = -1;
+    for (int64_t c = (target + 1) / 2; c <= 2 * target && c <= tiles; ++c) {
+      if (tiles % c) continue;
+      const int64_t dc = c > target ? c - target : target - c;
+      const int64_t db = best > target ? best - target : target - best;
+      if (best < 0 || dc < db || (dc == db && c > best)) best = c;
+    }
+    if (best > 0) {
+      tb = best;
+    } else {
+      const int64_t nbv = (tiles + target - 1) / target;
+      tb = (tiles + nbv - 1) / nbv;
+    }
+  }
   *bs = (int)(tb * 128);
-  *nb = (int)nbv;
+  *nb = (int)((tiles + tb - 1) / tb);
 }
 
-int64_t scratch_bytes_for(int64_t n, int64_t d, int dtype) {
+// Scratch layout of the backward (element type = input dtype):
+//   [G0 | G1 | GT0 | GT1 | XT | YT]
+// G0/G1 (and their transposes GT0/GT1) double-buffer one block diagonal of
+// G' (nb blocks of bs x bs); XT/YT are the normalised inputs transposed,
+// [d][ldt] with ldt = n rounded up to 128.
+struct ScratchLayout {
   int bs, nb;
-  grad_blocks(n, d, &bs, &nb);
+  int64_t ldt, gbuf, tbuf, total;  // bytes except ldt (elements)
+};
+
+ScratchLayout scratch_layout(int64_t n, int64_t d, int dtype) {
+  ScratchLayout L;
+  grad_blocks(n, d, &L.bs, &L.nb);
   const int64_t elem = dtype == MEC_DTYPE_F32 ? 4 : 2;
-  return (int64_t)nb * bs * bs * elem;
+  L.ldt = (n + 127) / 128 * 128;
+  L.gbuf = (int64_t)L.nb * L.bs * L.bs * elem;
+  L.tbuf = d * L.ldt * elem;
+  L.total = 4 * L.gbuf + 2 * L.tbuf;
+  return L;
 }
+
+int64_t scratch_bytes_for(int64_t n, int64_t d, int dtype) { return scratch_layout(n, d, dtype).total; }
+
+int round8(int v) { return (v + 7) & ~7; }
 
 #define DISPATCH_BOOL(cond, NAME, ...) \
   do {                                 \
@@ -202,9 +239,21 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
   return rc;
 }
 
-int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
-             int mode, int normalize, float temperature, const float* workspace, void* scratch,
-             int64_t scratch_bytes, float* acc_x, float* acc_y, void* stream) {
+int mec_grad_blocking(int64_t n, int64_t d, int dtype, int64_t* block_rows, int64_t* num_blocks) {
+  g_err.clear();
+  if (n < 1 || n > kMaxN || d < 1 || d > kMaxD) return fail(MEC_ERR_INVALID, "n or d out of range");
+  if (dtype != MEC_DTYPE_F32 && dtype != MEC_DTYPE_BF16) return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
+  if (!block_rows || !num_blocks) return fail(MEC_ERR_INVALID, "block_rows and num_blocks must be non-null");
+  int bs, nb;
+  grad_blocks(n, d, &bs, &nb);
+  *block_rows = bs;
+  *num_blocks = nb;
+  return MEC_OK;
+}
+
+int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
+                  int mode, int normalize, float temperature, const float* workspace, int64_t step, void* scratch,
+                  int64_t scratch_bytes, float* acc_x, float* acc_y, void* stream) {
   g_err.clear();
   int rc = check_common(x, ldx, y, ldy, n, d, dtype);
   if (!rc) rc = check_mode(mode);
@@ -219,45 +268,86 @@ int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, 
     return fail(MEC_ERR_INVALID, "scratch holds %lld bytes, %lld needed", (long long)scratch_bytes,
                 (long long)need);
   if (!aligned16(scratch)) return fail(MEC_ERR_INVALID, "scratch must be 16-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
+  const ScratchLayout L = scratch_layout(n, d, dtype);
+  const int bs = L.bs, nb = L.nb;
+  if (step < 0 || step > nb)
+    return fail(MEC_ERR_INVALID, "step %lld out of range [0, %d]", (long long)step, nb);
   const int N = (int)n, D = (int)d;
   const float c = (float)(1.4426950408889634 / (double)temperature);
+  BlockGrid bg{bs, nb, bs / 128};
+  const int tdn = (D + 127) / 128;
+  StepPlan sp{};
+  sp.diag_g = step < nb ? (int)step : -1;
+  sp.diag_c = step > 0 ? (int)step - 1 : -1;
+  sp.accumulate = step > 1;
+  sp.g_n = sp.diag_g >= 0 ? nb * bg.tpb * bg.tpb : 0;
+  sp.cx_n = (sp.diag_c >= 0 && acc_x) ? nb * bg.tpb * tdn : 0;
+  sp.cy_n = (sp.diag_c >= 0 && acc_y) ? nb * bg.tpb * tdn : 0;
+  sp.g_pad = round8(sp.g_n);
+  sp.cx_pad = round8(sp.cx_n);
+  sp.cy_pad = round8(sp.cy_n);
+  const int64_t grid = (int64_t)sp.g_pad + sp.cx_pad + sp.cy_pad;
+  if (grid > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "backward grid too large");
+  char* base = (char*)scratch;
+  GradBufs gb;
+  gb.g[0] = base;
+  gb.g[1] = base + L.gbuf;
+  gb.gt[0] = base + 2 * L.gbuf;
+  gb.gt[1] = base + 3 * L.gbuf;
+  gb.xt = base + 4 * L.gbuf;
+  gb.yt = base + 4 * L.gbuf + L.tbuf;
+  gb.ldt = L.ldt;
+  hipStream_t s = (hipStream_t)stream;
+  if (step == 0) {
+    // transposed normalised operands of the contractions: YT for the x side, XT for the y side
+    const int64_t n64 = n;
+    dim3 tgrid((unsigned)(L.ldt / 64), (unsigned)((d + 63) / 64));
+    if (dtype == MEC_DTYPE_F32) {
+      DISPATCH_BOOL(normalize, NORM, {
+        if (acc_x)
+          k_transpose<float, NORM><<<tgrid, 256, 0, s>>>((const float*)y, ldy, N, D, workspace + WS_RY * n64,
+                                                         (float*)gb.yt, L.ldt);
+        if (acc_y)
+          k_transpose<float, NORM><<<tgrid, 256, 0, s>>>((const float*)x, ldx, N, D, workspace + WS_RX * n64,
+                                                         (float*)gb.xt, L.ldt);
+      });
+    } else {
+      DISPATCH_BOOL(normalize, NORM, {
+        if (acc_x)
+          k_transpose<uint16_t, NORM><<<tgrid, 256, 0, s>>>((const uint16_t*)y, ldy, N, D,
+                                                            workspace + WS_RY * n64, (uint16_t*)gb.yt, L.ldt);
+        if (acc_y)
+          k_transpose<uint16_t, NORM><<<tgrid, 256, 0, s>>>((const uint16_t*)x, ldx, N, D,
+                                                            workspace + WS_RX * n64, (uint16_t*)gb.xt, L.ldt);
+      });
+    }
+    rc = check_launch("transpose");
+    if (rc) return rc;
+  }
+  const bool vec = vec_ok(x, ldx, y, ldy, d, dtype);
+  if (dtype == MEC_DTYPE_F32) {
+    DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
+        k_grad_step<float, LIT, NORM, VEC><<<(unsigned)grid, 256, 0, s>>>(
+            (const float*)x, ldx, (const float*)y, ldy, N, D, c, workspace, gb, bg, sp, acc_x, acc_y))));
+  } else {
+    DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
+        k_grad_step<uint16_t, LIT, NORM, VEC><<<(unsigned)grid, 256, 0, s>>>(
+            (const uint16_t*)x, ldx, (const uint16_t*)y, ldy, N, D, c, workspace, gb, bg, sp, acc_x, acc_y))));
+  }
+  return check_launch("grad_step");
+}
+
+int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
+             int mode, int normalize, float temperature, const float* workspace, void* scratch,
+             int64_t scratch_bytes, float* acc_x, float* acc_y, void* stream) {
+  g_err.clear();
+  int rc = check_common(x, ldx, y, ldy, n, d, dtype);
+  if (rc) return rc;
   int bs, nb;
   grad_blocks(n, d, &bs, &nb);
-  BlockGrid bg{bs, nb, bs / 128, 0};
-  const int tdn = (D + 127) / 128;
-  const int tiles_side = nb * bg.tpb * tdn;
-  const int tiles_x = acc_x ? tiles_side : 0;
-  const unsigned grid_g = (unsigned)(nb * bg.tpb * bg.tpb);
-  const unsigned grid_c = (unsigned)(tiles_x + (acc_y ? tiles_side : 0));
-  const bool vec = vec_ok(x, ldx, y, ldy, d, dtype);
-  for (int shift = 0; shift < nb; ++shift) {
-    bg.shift = shift;
-    const bool accum = shift > 0;
-    if (dtype == MEC_DTYPE_F32) {
-      const float* X = (const float*)x;
-      const float* Y = (const float*)y;
-      float* G = (float*)scratch;
-      DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-          k_grad_g<float, LIT, NORM, VEC><<<grid_g, 256, 0, s>>>(X, ldx, Y, ldy, N, D, c, workspace, G, bg))));
-      rc = check_launch("grad_g");
-      if (rc) return rc;
-      DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, DISPATCH_BOOL(accum, ACC,
-          k_grad_contract<float, NORM, VEC, ACC><<<grid_c, 256, 0, s>>>(X, ldx, Y, ldy, N, D, workspace, G, bg,
-                                                                     tiles_x, acc_x, acc_y))));
-    } else {
-      const uint16_t* X = (const uint16_t*)x;
-      const uint16_t* Y = (const uint16_t*)y;
-      uint16_t* G = (uint16_t*)scratch;
-      DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-          k_grad_g<uint16_t, LIT, NORM, VEC><<<grid_g, 256, 0, s>>>(X, ldx, Y, ldy, N, D, c, workspace, G, bg))));
-      rc = check_launch("grad_g");
-      if (rc) return rc;
-      DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, DISPATCH_BOOL(accum, ACC,
-          k_grad_contract<uint16_t, NORM, VEC, ACC><<<grid_c, 256, 0, s>>>(X, ldx, Y, ldy, N, D, workspace, G, bg,
-                                                                      tiles_x, acc_x, acc_y))));
-    }
-    rc = check_launch("grad_contract");
+  for (int t = 0; t <= nb; ++t) {
+    rc = mec_grad_step(x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, t, scratch,
+                       scratch_bytes, acc_x, acc_y, stream);
     if (rc) return rc;
   }
   return MEC_OK;

@@ -54,14 +54,16 @@ __device__ __forceinline__ int acc_row(int r, int lane) {
   return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
 }
 
-// Map a linear workgroup id to a logical tile id so that the workgroups that
-// run concurrently on one XCD (ids congruent mod 8) get consecutive logical
-// ids, then order logical ids in groups of `group_m` tile rows so that
-// neighbouring workgroups share operand rows in that XCD's L2.
-__device__ __forceinline__ void tile_swizzle(int bid, int nbid, int tiles_m, int tiles_n,
-                                             int group_m, int& tm, int& tn) {
-  int pid = bid;
-  if ((nbid & 7) == 0) pid = (bid & 7) * (nbid >> 3) + (bid >> 3);
+// Workgroup ids are dispatched round-robin over the 8 XCDs (id % 8).  Remap a
+// launch-local id in [0, nbid) (nbid a multiple of 8) so that each XCD gets a
+// contiguous range of logical ids; identity when nbid is not a multiple of 8.
+__device__ __forceinline__ int xcd_remap(int bid, int nbid) {
+  return (nbid & 7) == 0 ? (bid & 7) * (nbid >> 3) + (bid >> 3) : bid;
+}
+
+// Order logical ids pid in [0, tiles_m * tiles_n) in groups of `group_m` tile
+// rows, so that neighbouring workgroups share operand rows in one XCD's L2.
+__device__ __forceinline__ void group_tile(int pid, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
   int per_group = group_m * tiles_n;
   int gid = pid / per_group;
   int first_m = gid * group_m;
@@ -70,6 +72,12 @@ __device__ __forceinline__ void tile_swizzle(int bid, int nbid, int tiles_m, int
   int in_group = pid - gid * per_group;
   tm = first_m + in_group % gsize;
   tn = in_group / gsize;
+}
+
+// Both steps for a launch of exactly tiles_m * tiles_n workgroups.
+__device__ __forceinline__ void tile_swizzle(int bid, int nbid, int tiles_m, int tiles_n,
+                                             int group_m, int& tm, int& tn) {
+  group_tile(xcd_remap(bid, nbid), tiles_m, tiles_n, group_m, tm, tn);
 }
 
 // Wave-wide sum over the 32 lanes of each half-wave (lanes l and l^32 are not mixed).

@@ -3,13 +3,11 @@
 // v_mfma_f32_32x32x16_bf16 (fp32 accumulate).  K is staged through LDS in
 // chunks of 32 with double buffering.
 //
-// Both operand modes end up in LDS as [row][k] (k contiguous, 80-byte rows):
-//   KMAJOR : element (row, k) at base[row * ld + k]; copied as 16-byte vectors.
-//   MNMAJOR: element (k, col) at base[k * ld + col]; every thread reads a pair
-//            of columns from 8 consecutive k rows (coalesced 4-byte loads) and
-//            writes the two transposed 8-element k runs as 16-byte LDS stores.
-// Within a chunk the logical k fed to MFMA step s (0..1) by lane half h,
-// element e (0..7) is h*16 + s*8 + e for both operands.
+// Both operands are K-major in global memory (element (row, k) at
+// base[row * ld + k]) and in LDS ([row][k], 80-byte padded rows): 16-byte
+// global loads, conflict-free 16-byte LDS reads.  Within a chunk the logical k
+// fed to MFMA step s (0..1) by lane half h, element e (0..7) is h*16 + s*8 + e
+// for both operands.
 #pragma once
 #include "mec_common.h"
 
@@ -19,90 +17,47 @@ namespace g16 {
 constexpr int BM = 128;
 constexpr int BK = 32;
 constexpr int NT = 256;
-constexpr int LD = BK + 8;            // 40 bf16 = 80-byte rows
-constexpr int TILE = BM * LD;         // 5120 bf16 = 10 KiB per operand per stage
+constexpr int LD = BK + 8;               // 40 bf16 = 80-byte rows
+constexpr int TILE = BM * LD;            // 5120 bf16 = 10 KiB per operand per stage
 constexpr int LDS_ELEMS = 2 * 2 * TILE;  // 40 KiB
 
-enum { KMAJOR = 0, MNMAJOR = 1 };
-
 struct Operand {
-  const uint16_t* base;
+  const uint16_t* base;  // element (row, k) at base[row * ld + k]
   int64_t ld;
-  int extent;           // KMAJOR: valid rows; MNMAJOR: valid columns
-  int kmax;             // valid k range [0, kmax)
-  const float* kscale;  // MNMAJOR: optional per-k-row scale (nullptr = 1)
+  int extent;            // valid rows
+  int kmax;              // valid k range [0, kmax)
 };
 
 struct Regs {
   i16x8 v[2];
 };
 
-__device__ __forceinline__ uint16_t scale_bf16(uint16_t b, float s) { return f32_to_bf16(bf16_to_f32(b) * s); }
-
-template <int MODE, bool VEC>
+// VEC requires 16-byte aligned rows and, when kmax % 8 != 0, finite padding up
+// to the next multiple of 8 behind kmax.
+template <bool VEC>
 __device__ __forceinline__ void load_chunk(const Operand& op, int k0, Regs& r) {
   const int t = threadIdx.x;
-  if (MODE == KMAJOR) {
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      const int row = (t >> 2) + 64 * v;
-      const int kk = k0 + (t & 3) * 8;
-      const uint16_t* p = op.base + (int64_t)row * op.ld + kk;
-      if (VEC) {
-        if (row < op.extent && kk < op.kmax) r.v[v] = *(const i16x8*)p;
-        else r.v[v] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      } else {
+  for (int v = 0; v < 2; ++v) {
+    const int row = (t >> 2) + 64 * v;
+    const int kk = k0 + (t & 3) * 8;
+    const uint16_t* p = op.base + (int64_t)row * op.ld + kk;
+    if (VEC) {
+      if (row < op.extent && kk < op.kmax) r.v[v] = *(const i16x8*)p;
+      else r.v[v] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) r.v[v][e] = (row < op.extent && kk + e < op.kmax) ? (short)p[e] : (short)0;
-      }
-    }
-  } else {
-    const int p2 = (t & 63) * 2;        // column pair within the 128-wide tile
-    const int kb = k0 + (t >> 6) * 8;   // first of 8 k rows
-    uint32_t w[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int kk = kb + e;
-      const uint16_t* p = op.base + (int64_t)kk * op.ld + p2;
-      uint32_t u = 0;
-      if (kk < op.kmax) {
-        if (VEC) {
-          if (p2 < op.extent) u = *(const uint32_t*)p;
-        } else {
-          uint32_t lo = p2 < op.extent ? p[0] : 0u;
-          uint32_t hi = p2 + 1 < op.extent ? p[1] : 0u;
-          u = lo | (hi << 16);
-        }
-        if (op.kscale != nullptr) {
-          const float sc = op.kscale[kk];
-          u = (uint32_t)scale_bf16((uint16_t)(u & 0xFFFFu), sc) |
-              ((uint32_t)scale_bf16((uint16_t)(u >> 16), sc) << 16);
-        }
-      }
-      w[e] = u;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      r.v[0][e] = (short)(w[e] & 0xFFFFu);
-      r.v[1][e] = (short)(w[e] >> 16);
+      for (int e = 0; e < 8; ++e) r.v[v][e] = (row < op.extent && kk + e < op.kmax) ? (short)p[e] : (short)0;
     }
   }
 }
 
-template <int MODE>
 __device__ __forceinline__ void store_chunk(uint16_t* lds, const Regs& r) {
   const int t = threadIdx.x;
-  if (MODE == KMAJOR) {
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      const int row = (t >> 2) + 64 * v;
-      *(i16x8*)(lds + row * LD + (t & 3) * 8) = r.v[v];
-    }
-  } else {
-    const int p2 = (t & 63) * 2;
-    const int kc = (t >> 6) * 8;
-    *(i16x8*)(lds + p2 * LD + kc) = r.v[0];
-    *(i16x8*)(lds + (p2 + 1) * LD + kc) = r.v[1];
+  for (int v = 0; v < 2; ++v) {
+    const int row = (t >> 2) + 64 * v;
+    *(i16x8*)(lds + row * LD + (t & 3) * 8) = r.v[v];
   }
 }
 
@@ -128,7 +83,8 @@ __device__ __forceinline__ void compute_chunk(const uint16_t* la, const uint16_t
       for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16_32x32x16(a[i][s], b[j][s], acc[i][j]);
 }
 
-template <int AMODE, int BMODE, bool VEC>
+// acc[i][j] (this wave's 64x64 sub-tile) = sum_k A(m, k) * B(n, k) over k in [0, K).
+template <bool VECA, bool VECB>
 __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int K, uint16_t* lds,
                                          f32x16 (&acc)[2][2]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -142,24 +98,24 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
   const int nk = (K + BK - 1) / BK;
   if (nk <= 0) return;
   Regs ra, rb;
-  load_chunk<AMODE, VEC>(A, 0, ra);
-  load_chunk<BMODE, VEC>(B, 0, rb);
-  store_chunk<AMODE>(lds, ra);
-  store_chunk<BMODE>(lds + TILE, rb);
+  load_chunk<VECA>(A, 0, ra);
+  load_chunk<VECB>(B, 0, rb);
+  store_chunk(lds, ra);
+  store_chunk(lds + TILE, rb);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      load_chunk<AMODE, VEC>(A, (kt + 1) * BK, ra);
-      load_chunk<BMODE, VEC>(B, (kt + 1) * BK, rb);
+      load_chunk<VECA>(A, (kt + 1) * BK, ra);
+      load_chunk<VECB>(B, (kt + 1) * BK, rb);
     }
     const uint16_t* la = lds + cur * 2 * TILE;
     compute_chunk(la, la + TILE, wm, wn, lane, acc);
     if (more) {
       uint16_t* ln = lds + (cur ^ 1) * 2 * TILE;
-      store_chunk<AMODE>(ln, ra);
-      store_chunk<BMODE>(ln + TILE, rb);
+      store_chunk(ln, ra);
+      store_chunk(ln + TILE, rb);
     }
     __syncthreads();
   }

@@ -1,134 +1,111 @@
 // fp32 MFMA tile core for gfx950: 128x128 output tile per 256-thread workgroup,
 // 4 waves in a 2x2 arrangement, each wave owning a 64x64 sub-tile computed as
-// 2x2 blocks of v_mfma_f32_32x32x2_f32.  K is staged through LDS in chunks of
-// 16 with double buffering (one barrier per chunk).
+// 2x2 blocks of v_mfma_f32_32x32x2_f32.
 //
-// Operand staging modes:
-//   KMAJOR : element (row, k) at base[row * ld + k]   (k contiguous, e.g. X, Y, G)
-//   MNMAJOR: element (k, col) at base[k * ld + col]   (col contiguous, e.g. Y as the
-//            right operand of G.Y, or G read transposed)
+// Both operands are K-major in global memory: element (row, k) at
+// base[row * ld + k] (X, Y, their transposes and the gradient-matrix blocks
+// are all stored that way).  K is staged through LDS in chunks of BK as
+// [row][k] with a padded row pitch, so every global load is a 16-byte vector
+// and every MFMA operand read a conflict-free ds_read_b128.  The next chunk is
+// prefetched into registers while the current one is multiplied (STAGES = 2:
+// double-buffered LDS, one barrier per chunk; STAGES = 1: one LDS buffer, two
+// barriers per chunk, half the LDS).
 //
-// Within a 16-wide chunk the logical k index fed to MFMA step s (0..7) by lane
-// half h = lane/32 is h*8 + s.  Both operands use the same assignment, so the
-// contraction is exact; for KMAJOR tiles it makes each lane's 8 values
-// contiguous (two ds_read_b128).
+// Within a chunk the logical k fed to MFMA step s (0..BK/2-1) by lane half
+// h = lane/32 is h*BK/2 + s for both operands, so the contraction is exact and
+// each lane's k-values are contiguous in LDS.
 #pragma once
 #include "mec_common.h"
+
+#ifndef MEC_F32_BK
+#define MEC_F32_BK 16
+#endif
+#ifndef MEC_F32_STAGES
+#define MEC_F32_STAGES 1
+#endif
 
 namespace mec {
 namespace g32 {
 
 constexpr int BM = 128;
-constexpr int BK = 16;
+constexpr int BK = MEC_F32_BK;          // k depth of one LDS chunk
+constexpr int STAGES = MEC_F32_STAGES;  // LDS buffers
 constexpr int NT = 256;
-constexpr int KM_LD = BK + 4;           // 80-byte rows: conflict-free b128 reads
-constexpr int MN_LD = BM + 4;           // 528-byte rows
-constexpr int KM_TILE = BM * KM_LD;     // 2560 floats
-constexpr int MN_TILE = BK * MN_LD;     // 2112 floats
-constexpr int TILE = KM_TILE;           // slot size per operand per stage
-constexpr int LDS_FLOATS = 2 * 2 * TILE;  // 2 stages x 2 operands = 40 KiB
-
-enum { KMAJOR = 0, MNMAJOR = 1 };
+constexpr int LD = BK + 4;              // padded LDS row pitch (floats)
+constexpr int TILE = BM * LD;           // floats per operand per stage
+constexpr int LDS_FLOATS = STAGES * 2 * TILE;
+constexpr int KQ = BK / 4;              // 16-byte k quads per row
+constexpr int NV = BM * KQ / NT;        // vectors per thread per operand per chunk
+static_assert(BK % 16 == 0 && NV >= 1, "BK must be a multiple of 16");
 
 struct Operand {
-  const float* base;    // see modes above
-  int64_t ld;           // row stride in elements
-  int extent;           // KMAJOR: valid rows from base; MNMAJOR: valid columns from base
-  int kmax;             // valid k range [0, kmax)
-  const float* kscale;  // MNMAJOR: optional scale per k row (nullptr = 1)
+  const float* base;  // element (row, k) at base[row * ld + k]
+  int64_t ld;         // row stride in elements
+  int extent;         // valid rows from base
+  int kmax;           // valid k range [0, kmax)
 };
 
-// Global -> registers for one 16-deep chunk starting at k0.  Each thread moves
-// two float4.  VEC requires 16-byte aligned rows and extents (k for KMAJOR,
-// columns for MNMAJOR) that are multiples of 4.
-template <int MODE, bool VEC>
-__device__ __forceinline__ void load_chunk(const Operand& op, int k0, f32x4 (&r)[2]) {
+// Global -> registers for the chunk starting at k0: KQ consecutive threads
+// cover one row.  VEC requires 16-byte aligned rows and, when kmax % 4 != 0,
+// finite padding up to the next multiple of 4 behind kmax (it is multiplied
+// by zeros of the other operand).
+template <bool VEC>
+__device__ __forceinline__ void load_chunk(const Operand& op, int k0, f32x4 (&r)[NV]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int v = 0; v < 2; ++v) {
-    if (MODE == KMAJOR) {
-      const int row = (t >> 2) + 64 * v;
-      const int kk = k0 + (t & 3) * 4;
-      const float* p = op.base + (int64_t)row * op.ld + kk;
-      if (VEC) {
-        if (row < op.extent && kk < op.kmax) r[v] = *(const f32x4*)p;
-        else r[v] = f32x4{0.f, 0.f, 0.f, 0.f};
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) r[v][e] = (row < op.extent && kk + e < op.kmax) ? p[e] : 0.f;
-      }
+  for (int v = 0; v < NV; ++v) {
+    const int row = t / KQ + v * (NT / KQ);
+    const int kk = k0 + (t % KQ) * 4;
+    const float* p = op.base + (int64_t)row * op.ld + kk;
+    if (VEC) {
+      if (row < op.extent && kk < op.kmax) r[v] = *(const f32x4*)p;
+      else r[v] = f32x4{0.f, 0.f, 0.f, 0.f};
     } else {
-      const int kr = (t >> 5) + 8 * v;
-      const int col = (t & 31) * 4;
-      const int kk = k0 + kr;
-      const float* p = op.base + (int64_t)kk * op.ld + col;
-      const bool krow = kk < op.kmax;
-      if (VEC) {
-        if (krow && col < op.extent) r[v] = *(const f32x4*)p;
-        else r[v] = f32x4{0.f, 0.f, 0.f, 0.f};
-      } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[v][e] = (krow && col + e < op.extent) ? p[e] : 0.f;
-      }
-      if (op.kscale != nullptr && krow) {
-        const float sc = op.kscale[kk];
-        r[v] *= sc;
-      }
+      for (int e = 0; e < 4; ++e) r[v][e] = (row < op.extent && kk + e < op.kmax) ? p[e] : 0.f;
     }
   }
 }
 
-template <int MODE>
-__device__ __forceinline__ void store_chunk(float* lds, const f32x4 (&r)[2]) {
+__device__ __forceinline__ void store_chunk(float* lds, const f32x4 (&r)[NV]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int v = 0; v < 2; ++v) {
-    if (MODE == KMAJOR) {
-      const int row = (t >> 2) + 64 * v;
-      *(f32x4*)(lds + row * KM_LD + (t & 3) * 4) = r[v];
-    } else {
-      const int kr = (t >> 5) + 8 * v;
-      *(f32x4*)(lds + kr * MN_LD + (t & 31) * 4) = r[v];
-    }
+  for (int v = 0; v < NV; ++v) {
+    const int row = t / KQ + v * (NT / KQ);
+    *(f32x4*)(lds + row * LD + (t % KQ) * 4) = r[v];
   }
 }
 
-// Read this lane's 8 k-values for MFMA block `blk` (32 rows/cols starting at
-// `off` within the 128-wide tile).
-template <int MODE>
-__device__ __forceinline__ void read_operand(const float* lds, int off, int lane, float (&o)[8]) {
+// MFMA steps [s0, s0 + 8) of the chunk in LDS: this lane's k-values of its
+// two A rows and two B rows (8 each), then 32 MFMAs.
+__device__ __forceinline__ void compute_part(const float* la, const float* lb, int wm, int wn, int lane, int s0,
+                                             f32x16 (&acc)[2][2]) {
   const int q = lane & 31, h = lane >> 5;
-  if (MODE == KMAJOR) {
-    const float* p = lds + (off + q) * KM_LD + h * 8;
-    f32x4 u = *(const f32x4*)p;
-    f32x4 w = *(const f32x4*)(p + 4);
-    o[0] = u[0]; o[1] = u[1]; o[2] = u[2]; o[3] = u[3];
-    o[4] = w[0]; o[5] = w[1]; o[6] = w[2]; o[7] = w[3];
-  } else {
+  f32x4 a[2][2], b[2][2];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) o[s] = lds[(h * 8 + s) * MN_LD + off + q];
+  for (int i = 0; i < 2; ++i) {
+    const float* p = la + (wm * 64 + i * 32 + q) * LD + h * (BK / 2) + s0;
+    a[i][0] = *(const f32x4*)p;
+    a[i][1] = *(const f32x4*)(p + 4);
   }
-}
-
-template <int AMODE, int BMODE>
-__device__ __forceinline__ void compute_chunk(const float* la, const float* lb, int wm, int wn,
-                                              int lane, f32x16 (&acc)[2][2]) {
-  float a[2][8], b[2][8];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) read_operand<AMODE>(la, wm * 64 + i * 32, lane, a[i]);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) read_operand<BMODE>(lb, wn * 64 + j * 32, lane, b[j]);
+  for (int j = 0; j < 2; ++j) {
+    const float* p = lb + (wn * 64 + j * 32 + q) * LD + h * (BK / 2) + s0;
+    b[j][0] = *(const f32x4*)p;
+    b[j][1] = *(const f32x4*)(p + 4);
+  }
 #pragma unroll
   for (int s = 0; s < 8; ++s)
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = mfma_f32_32x32x2(a[i][s], b[j][s], acc[i][j]);
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = mfma_f32_32x32x2(a[i][s >> 2][s & 3], b[j][s >> 2][s & 3], acc[i][j]);
 }
 
-// acc[i][j] (this wave's 64x64 sub-tile) = sum_k A(m, k) * B(k, n) over k in [0, K).
+// acc[i][j] (this wave's 64x64 sub-tile) = sum_k A(m, k) * B(n, k) over k in [0, K).
 // lds must hold LDS_FLOATS floats.  Ends with a barrier, so lds may be reused.
-template <int AMODE, int BMODE, bool VEC>
+template <bool VECA, bool VECB>
 __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int K, float* lds,
                                          f32x16 (&acc)[2][2]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -141,27 +118,37 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   const int nk = (K + BK - 1) / BK;
   if (nk <= 0) return;
-  f32x4 ra[2], rb[2];
-  load_chunk<AMODE, VEC>(A, 0, ra);
-  load_chunk<BMODE, VEC>(B, 0, rb);
-  store_chunk<AMODE>(lds, ra);
-  store_chunk<BMODE>(lds + TILE, rb);
+  f32x4 ra[NV], rb[NV];
+  load_chunk<VECA>(A, 0, ra);
+  load_chunk<VECB>(B, 0, rb);
+  store_chunk(lds, ra);
+  store_chunk(lds + TILE, rb);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
+    const int cur = STAGES == 2 ? (kt & 1) : 0;
     const bool more = kt + 1 < nk;
     if (more) {
-      load_chunk<AMODE, VEC>(A, (kt + 1) * BK, ra);
-      load_chunk<BMODE, VEC>(B, (kt + 1) * BK, rb);
+      load_chunk<VECA>(A, (kt + 1) * BK, ra);
+      load_chunk<VECB>(B, (kt + 1) * BK, rb);
     }
     const float* la = lds + cur * 2 * TILE;
-    compute_chunk<AMODE, BMODE>(la, la + TILE, wm, wn, lane, acc);
-    if (more) {
-      float* ln = lds + (cur ^ 1) * 2 * TILE;
-      store_chunk<AMODE>(ln, ra);
-      store_chunk<BMODE>(ln + TILE, rb);
+#pragma unroll
+    for (int s0 = 0; s0 < BK / 2; s0 += 8) compute_part(la, la + TILE, wm, wn, lane, s0, acc);
+    if (STAGES == 2) {
+      if (more) {
+        float* ln = lds + (cur ^ 1) * 2 * TILE;
+        store_chunk(ln, ra);
+        store_chunk(ln + TILE, rb);
+      }
+      __syncthreads();
+    } else {
+      __syncthreads();
+      if (more) {
+        store_chunk(lds, ra);
+        store_chunk(lds + TILE, rb);
+        __syncthreads();
+      }
     }
-    __syncthreads();
   }
 }
 

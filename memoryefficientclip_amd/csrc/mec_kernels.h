@@ -4,40 +4,51 @@
 //                       row (and column) partial sums, one atomic per row/column
 //                       per tile.  Replaces clip_sum_exp_kernel (clip_loss.py:9-64)
 //                       and lit_sum_exp_kernel (lit_loss.py:9-62).
-//   k_grad_g        backward step 1: recompute S for the block pairs of one
-//                       block diagonal and write the gradient-matrix blocks
+//   k_grad_step     backward, one launch per pipeline step t = 0..nb over
+//                       the block diagonals of the N x N gradient matrix:
+//                       recompute S for diagonal t and write the blocks
 //                       G'_ij = E_ij (1/R_i + 1/C_j) (LiT: E_ij / R_i), i != j,
-//                       to a bounded scratch (clip_loss.py:96-124, lit_loss.py:94-120).
-//   k_grad_contract backward step 2: dX_I += G'_IJ Y^_J and dY_J += G'_IJ^T X^_I
-//                       as plain MFMA contractions (clip_loss.py:127-156,
-//                       lit_loss.py:123-148) without atomics.
+//                       to one of two bounded scratch buffers
+//                       (clip_loss.py:96-124, lit_loss.py:94-120), while
+//                       contracting diagonal t-1 from the other buffer:
+//                       dX_I += G'_IJ Y^_J and dY_J += G'_IJ^T X^_I as plain MFMA
+//                       contractions without atomics (clip_loss.py:127-156,
+//                       lit_loss.py:123-148).
 #pragma once
 #include "mec_gemm_f32.h"
 #include "mec_gemm_bf16.h"
 
 namespace mec {
 
-// Element-type traits: which MFMA core runs the tile, and how G is stored.
+// Element-type traits: which MFMA core runs the tile, and how G' is stored.
 template <typename T> struct Core;
 template <> struct Core<float> {
   using Op = g32::Operand;
-  static constexpr int KM = g32::KMAJOR, MN = g32::MNMAJOR;
   static constexpr int LDS_BYTES = g32::LDS_FLOATS * 4;
-  template <int AM, int BM_, bool VEC>
+  template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[2][2]) {
-    g32::mainloop<AM, BM_, VEC>(a, b, K, (float*)lds, acc);
+    g32::mainloop<VECA, VECB>(a, b, K, (float*)lds, acc);
   }
   static __device__ __forceinline__ float pack(float v) { return v; }
+  // 4 consecutive values as one vector store
+  static __device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+    *(f32x4*)p = f32x4{a, b, c, d};
+  }
 };
 template <> struct Core<uint16_t> {
   using Op = g16::Operand;
-  static constexpr int KM = g16::KMAJOR, MN = g16::MNMAJOR;
   static constexpr int LDS_BYTES = g16::LDS_ELEMS * 2;
-  template <int AM, int BM_, bool VEC>
+  template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[2][2]) {
-    g16::mainloop<AM, BM_, VEC>(a, b, K, (uint16_t*)lds, acc);
+    g16::mainloop<VECA, VECB>(a, b, K, (uint16_t*)lds, acc);
   }
   static __device__ __forceinline__ uint16_t pack(float v) { return f32_to_bf16(v); }
+  static __device__ __forceinline__ void store4(uint16_t* p, float a, float b, float c, float d) {
+    uint2 u;
+    u.x = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+    u.y = (uint32_t)f32_to_bf16(c) | ((uint32_t)f32_to_bf16(d) << 16);
+    *(uint2*)p = u;
+  }
 };
 
 // ---------------------------------------------------------------- forward
@@ -54,10 +65,10 @@ __global__ __launch_bounds__(256, 2) void k_sumexp(const T* __restrict__ X, int6
   const int m0 = tm * 128, n0 = tn * 128;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1;
 
-  typename C::Op A{X + (int64_t)m0 * ldx, ldx, N - m0, D, nullptr};
-  typename C::Op B{Y + (int64_t)n0 * ldy, ldy, N - n0, D, nullptr};
+  typename C::Op A{X + (int64_t)m0 * ldx, ldx, N - m0, D};
+  typename C::Op B{Y + (int64_t)n0 * ldy, ldy, N - n0, D};
   f32x16 acc[2][2];
-  C::template run<C::KM, C::KM, VEC>(A, B, D, lds, acc);
+  C::template run<VEC, VEC>(A, B, D, lds, acc);
 
   if (t < 128) {
     s_rx[t] = (NORM && m0 + t < N) ? ws[WS_RX * n64 + m0 + t] : 1.f;
@@ -123,38 +134,62 @@ __global__ __launch_bounds__(256, 2) void k_sumexp(const T* __restrict__ X, int6
 
 // ---------------------------------------------------------------- backward
 // Block decomposition of the N x N gradient matrix: nb blocks of bs rows
-// (bs a multiple of 128; the last block may be short).  Diagonal `shift`
-// pairs block I with block J = (I + shift) mod nb, so one launch touches every
-// block row and every block column exactly once.
+// (bs a multiple of 128; the last block may be short).  Diagonal s pairs block
+// I with block J = (I + s) mod nb, so one diagonal touches every block row and
+// every block column exactly once.
 struct BlockGrid {
-  int bs;      // block size (rows), multiple of 128
-  int nb;      // number of blocks
-  int tpb;     // 128-tiles per block side = bs / 128
-  int shift;   // diagonal index
+  int bs;   // block size (rows), multiple of 128
+  int nb;   // number of blocks (= number of diagonals)
+  int tpb;  // 128-tiles per block side = bs / 128
 };
 
+// Scratch of the backward (all in the input dtype T, row-major):
+//   G[2]   two buffers of nb blocks of bs x bs: block I of buffer s&1 holds
+//          G'(I, (I+s) mod nb) of diagonal s;
+//   GT[2]  the same blocks transposed (CLIP only);
+//   XT, YT the normalised inputs transposed, [D][ldt] with ldt = N rounded
+//          up to 128 and zero columns [N, ldt): element (d, i) = rx_i x_i[d].
+// Every contraction operand is then K-major (k contiguous).
+struct GradBufs {
+  void* g[2];
+  void* gt[2];
+  const void* xt;
+  const void* yt;
+  int64_t ldt;
+};
+
+// One pipeline step of the backward (launch t = 0 .. nb):
+//   workgroups [0, cx_pad)               x side of the contraction of diagonal t-1
+//   [cx_pad, cx_pad + cy_pad)            y side (CLIP)
+//   [cx_pad + cy_pad, ... + g_pad)       G' tiles of diagonal t
+// The long contraction tiles (K = bs) come first so the short G' tiles
+// (K = d) fill the tail of the launch.  Each sub-range starts at a multiple
+// of 8, so `id % 8` is still the XCD a workgroup runs on.
+struct StepPlan {
+  int diag_g;        // diagonal whose G' this launch writes (-1: none)
+  int diag_c;        // diagonal this launch contracts (-1: none)
+  int accumulate;    // contraction adds to the accumulators (else overwrites)
+  int g_n, g_pad;    // G' tiles (nb * tpb * tpb or 0), padded to a multiple of 8
+  int cx_n, cx_pad;  // x-side contraction tiles (nb * tpb * ceil(D/128) or 0), padded
+  int cy_n, cy_pad;  // y-side contraction tiles, padded
+};
+
+// Recompute the similarity tile (i0, j0) and store G'_ij = E_ij (1/R_i + 1/C_j)
+// (LiT: E_ij / R_i) for i != j, 0 on the diagonal and outside [0, N), into
+// the G' block at Gb (row pitch bs) and, for CLIP, transposed at GTb.
+// Follows clip_loss.py:96-124 / lit_loss.py:94-120.
 template <typename T, bool LIT, bool NORM, bool VEC>
-__global__ __launch_bounds__(256, 2) void k_grad_g(const T* __restrict__ X, int64_t ldx,
-                                                   const T* __restrict__ Y, int64_t ldy, int N,
-                                                   int D, float c, const float* __restrict__ ws,
-                                                   T* __restrict__ G, BlockGrid bg) {
+__device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y,
+                                            int64_t ldy, int N, int D, float c, const float* __restrict__ ws,
+                                            T* __restrict__ Gb, T* __restrict__ GTb, int bs, int i0, int j0,
+                                            char* lds, float* s_rx, float* s_ry, float* s_ir, float* s_ic) {
   using C = Core<T>;
-  __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
-  __shared__ float s_rx[128], s_ry[128], s_ir[128], s_ic[128];
   const int64_t n64 = N;
-  int tmg, tn;
-  tile_swizzle(blockIdx.x, gridDim.x, bg.nb * bg.tpb, bg.tpb, 8, tmg, tn);
-  const int I = tmg / bg.tpb, tm = tmg - I * bg.tpb;
-  const int J = (I + bg.shift) % bg.nb;
-  const int i0 = I * bg.bs + tm * 128, j0 = J * bg.bs + tn * 128;
-  if (i0 >= N || j0 >= N) return;  // never read by the contraction kernel
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1;
-
-  typename C::Op A{X + (int64_t)i0 * ldx, ldx, N - i0, D, nullptr};
-  typename C::Op B{Y + (int64_t)j0 * ldy, ldy, N - j0, D, nullptr};
+  typename C::Op A{X + (int64_t)i0 * ldx, ldx, N - i0, D};
+  typename C::Op B{Y + (int64_t)j0 * ldy, ldy, N - j0, D};
   f32x16 acc[2][2];
-  C::template run<C::KM, C::KM, VEC>(A, B, D, lds, acc);
-
+  C::template run<VEC, VEC>(A, B, D, lds, acc);
   if (t < 128) {
     const bool ok = i0 + t < N;
     s_rx[t] = (NORM && ok) ? ws[WS_RX * n64 + i0 + t] : 1.f;
@@ -166,8 +201,6 @@ __global__ __launch_bounds__(256, 2) void k_grad_g(const T* __restrict__ X, int6
     s_ic[u] = (!LIT && ok) ? ws[WS_INV_COL * n64 + j0 + u] : 0.f;
   }
   __syncthreads();
-
-  T* Gb = G + (int64_t)I * bg.bs * bg.bs + (int64_t)(tm * 128) * bg.bs + tn * 128;
 #pragma unroll
   for (int bm = 0; bm < 2; ++bm) {
 #pragma unroll
@@ -175,6 +208,7 @@ __global__ __launch_bounds__(256, 2) void k_grad_g(const T* __restrict__ X, int6
       const int nl = wn * 64 + bn * 32 + (lane & 31);
       const int j = j0 + nl;
       const float ryj = s_ry[nl], icj = s_ic[nl];
+      float gv[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int ml = wm * 64 + bm * 32 + acc_row(r, lane);
@@ -182,52 +216,43 @@ __global__ __launch_bounds__(256, 2) void k_grad_g(const T* __restrict__ X, int6
         float s = acc[bm][bn][r];
         if (NORM) s *= s_rx[ml] * ryj;
         const float e = fast_exp2(fmaf(s, c, -c));
-        float gv = LIT ? e * s_ir[ml] : e * (s_ir[ml] + icj);
-        gv = (i < N && j < N && i != j) ? gv : 0.f;
-        Gb[(int64_t)ml * bg.bs + nl] = C::pack(gv);
+        float g = LIT ? e * s_ir[ml] : e * (s_ir[ml] + icj);
+        gv[r] = (i < N && j < N && i != j) ? g : 0.f;
+        Gb[(int64_t)ml * bs + nl] = C::pack(gv[r]);
+      }
+      if (!LIT) {
+        // registers 4g..4g+3 hold 4 consecutive rows: one vector store per group
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ml = wm * 64 + bm * 32 + acc_row(4 * g, lane);
+          C::store4(GTb + (int64_t)nl * bs + ml, gv[4 * g], gv[4 * g + 1], gv[4 * g + 2], gv[4 * g + 3]);
+        }
       }
     }
   }
 }
 
-// One launch per diagonal.  Workgroups [0, tiles_x) produce dX tiles, the rest
-// (CLIP only) dY tiles; each output tile is owned by exactly one workgroup, so
-// accumulation across diagonals is a plain read-modify-write.
-template <typename T, bool NORM, bool VEC, bool ACCUM>
-__global__ __launch_bounds__(256, 2) void k_grad_contract(
-    const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D,
-    const float* __restrict__ ws, const T* __restrict__ G, BlockGrid bg, int tiles_x,
-    float* __restrict__ acc_x, float* __restrict__ acc_y) {
+// One 128 x 128 output tile of a contraction: rows r0.. of block P, feature
+// columns d0..:
+//   x side: acc_x[i, d] (+)= sum_{j in Q} G'(P,Q)[i, j]  * YT[d, j]   (Q = P + s)
+//   y side: acc_y[j, d] (+)= sum_{i in Q} G'T(Q,P)[j, i] * XT[d, i]   (Q = P - s)
+// Each output tile has one owner per launch, so accumulation across launches
+// is a plain read-modify-write (replaces the atomics of clip_loss.py:148-156).
+template <typename T>
+__device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __restrict__ Gblk,
+                                                   const T* __restrict__ OT, int64_t ldt, const BlockGrid& bg,
+                                                   int P, int Q, int tm, int td, bool accumulate,
+                                                   float* __restrict__ out, char* lds) {
   using C = Core<T>;
-  __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
-  const int64_t n64 = N;
-  const int tdn = (D + 127) / 128;
-  const bool is_x = (int)blockIdx.x < tiles_x;
-  const int bid = is_x ? blockIdx.x : blockIdx.x - tiles_x;
-  const int nbid = is_x ? tiles_x : gridDim.x - tiles_x;
-  int tmg, td;
-  tile_swizzle(bid, nbid, bg.nb * bg.tpb, tdn, 8, tmg, td);
-  const int P = tmg / bg.tpb, tm = tmg - P * bg.tpb;  // P: block owning the output rows
   const int r0 = P * bg.bs + tm * 128;
   if (r0 >= N) return;
   const int d0 = td * 128;
-  // partner block along the contraction index
-  const int Q = is_x ? (P + bg.shift) % bg.nb : (P - bg.shift + bg.nb) % bg.nb;
   const int q0 = Q * bg.bs;
   const int qn = min(bg.bs, N - q0);
+  typename C::Op A{Gblk + (int64_t)(tm * 128) * bg.bs, bg.bs, 128, qn};
+  typename C::Op B{OT + (int64_t)d0 * ldt + q0, ldt, D - d0, qn};
   f32x16 acc[2][2];
-  if (is_x) {
-    // dX[i, d] += sum_j G'[i, j] * ry_j * Y[j, d],  G' block (P, Q) row-major
-    typename C::Op A{G + (int64_t)P * bg.bs * bg.bs + (int64_t)(tm * 128) * bg.bs, bg.bs, 128, qn, nullptr};
-    typename C::Op B{Y + (int64_t)q0 * ldy + d0, ldy, D - d0, qn, NORM ? ws + WS_RY * n64 + q0 : nullptr};
-    C::template run<C::KM, C::MN, VEC>(A, B, qn, lds, acc);
-  } else {
-    // dY[j, d] += sum_i G'[i, j] * rx_i * X[i, d],  G' block (Q, P) read transposed
-    typename C::Op A{G + (int64_t)Q * bg.bs * bg.bs + tm * 128, bg.bs, 128, qn, nullptr};
-    typename C::Op B{X + (int64_t)q0 * ldx + d0, ldx, D - d0, qn, NORM ? ws + WS_RX * n64 + q0 : nullptr};
-    C::template run<C::MN, C::MN, VEC>(A, B, qn, lds, acc);
-  }
-  float* out = is_x ? acc_x : acc_y;
+  C::template run<true, true>(A, B, qn, lds, acc);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
 #pragma unroll
   for (int bm = 0; bm < 2; ++bm) {
@@ -239,11 +264,59 @@ __global__ __launch_bounds__(256, 2) void k_grad_contract(
         const int row = r0 + wm * 64 + bm * 32 + acc_row(r, lane);
         if (row < N && d < D) {
           float* p = out + (int64_t)row * D + d;
-          *p = ACCUM ? *p + acc[bm][bn][r] : acc[bm][bn][r];
+          *p = accumulate ? *p + acc[bm][bn][r] : acc[bm][bn][r];
         }
       }
     }
   }
+}
+
+template <typename T, bool LIT, bool NORM, bool VEC>
+__global__ __launch_bounds__(256, 2) void k_grad_step(const T* __restrict__ X, int64_t ldx,
+                                                      const T* __restrict__ Y, int64_t ldy, int N, int D,
+                                                      float c, const float* __restrict__ ws, GradBufs gb,
+                                                      BlockGrid bg, StepPlan sp, float* __restrict__ acc_x,
+                                                      float* __restrict__ acc_y) {
+  using C = Core<T>;
+  __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
+  __shared__ float s_rx[128], s_ry[128], s_ir[128], s_ic[128];
+  const int tdn = (D + 127) / 128;
+  const int64_t blk = (int64_t)bg.bs * bg.bs;  // elements per G' block
+  int sub = blockIdx.x;
+  if (sub < sp.cx_pad + sp.cy_pad) {
+    const bool is_x = sub < sp.cx_pad;
+    if (!is_x) sub -= sp.cx_pad;
+    const int pid = xcd_remap(sub, is_x ? sp.cx_pad : sp.cy_pad);
+    if (pid >= (is_x ? sp.cx_n : sp.cy_n)) return;
+    int tmg, td;
+    group_tile(pid, bg.nb * bg.tpb, tdn, 8, tmg, td);
+    const int P = tmg / bg.tpb, tm = tmg - P * bg.tpb;  // P: block owning the output rows
+    const int buf = sp.diag_c & 1;
+    if (is_x) {
+      const int Q = (P + sp.diag_c) % bg.nb;
+      grad_contract_tile<T>(N, D, (const T*)gb.g[buf] + P * blk, (const T*)gb.yt, gb.ldt, bg, P, Q, tm, td,
+                            sp.accumulate != 0, acc_x, lds);
+    } else {
+      const int Q = (P - sp.diag_c + bg.nb) % bg.nb;
+      grad_contract_tile<T>(N, D, (const T*)gb.gt[buf] + Q * blk, (const T*)gb.xt, gb.ldt, bg, P, Q, tm, td,
+                            sp.accumulate != 0, acc_y, lds);
+    }
+    return;
+  }
+  sub -= sp.cx_pad + sp.cy_pad;
+  const int pid = xcd_remap(sub, sp.g_pad);
+  if (pid >= sp.g_n) return;
+  int tmg, tn;
+  group_tile(pid, bg.nb * bg.tpb, bg.tpb, 8, tmg, tn);
+  const int I = tmg / bg.tpb, tm = tmg - I * bg.tpb;
+  const int J = (I + sp.diag_g) % bg.nb;
+  const int i0 = I * bg.bs + tm * 128, j0 = J * bg.bs + tn * 128;
+  if (i0 >= N || j0 >= N) return;  // never read by the contraction
+  const int buf = sp.diag_g & 1;
+  T* Gb = (T*)gb.g[buf] + I * blk + (int64_t)(tm * 128) * bg.bs + tn * 128;
+  T* GTb = LIT ? nullptr : (T*)gb.gt[buf] + I * blk + (int64_t)(tn * 128) * bg.bs + tm * 128;
+  grad_g_tile<T, LIT, NORM, VEC>(X, ldx, Y, ldy, N, D, c, ws, Gb, GTb, bg.bs, i0, j0, lds, s_rx, s_ry, s_ir,
+                                 s_ic);
 }
 
 }  // namespace mec

@@ -150,4 +150,31 @@ __global__ __launch_bounds__(256) void k_postpass(const T* __restrict__ own, int
   }
 }
 
+// Transposed, normalised copy of one feature matrix for the backward's
+// contractions: XT[d, i] = scale_i * X[i, d] (scale = 1/max(||x_i||, 1e-12)
+// when NORM) for i < N and 0 for N <= i < ldt, rounded to T once.  64 x 64
+// tiles through LDS; both the loads and the stores are coalesced.
+template <typename T, bool NORM>
+__global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ X, int64_t ldx, int N, int D,
+                                                   const float* __restrict__ scale, T* __restrict__ XT,
+                                                   int64_t ldt) {
+  __shared__ float tile[64][65];
+  const int i0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int i = i0 + r, d = d0 + tx;
+    float v = 0.f;
+    if (i < N && d < D) {
+      v = Elem<T>::load(X, (int64_t)i * ldx + d);
+      if (NORM) v *= scale[i];
+    }
+    tile[r][tx] = v;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int d = d0 + r, i = i0 + tx;
+    if (d < D && i < ldt) Elem<T>::store(XT, (int64_t)d * ldt + i, tile[tx][r]);
+  }
+}
+
 }  // namespace mec

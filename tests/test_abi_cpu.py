@@ -36,13 +36,28 @@ def test_sizes():
     lib = _lib.load()
     assert lib.mec_workspace_floats(1000) == 8000
     assert lib.mec_workspace_floats(0) < 0
-    # scratch is O(n*d): one block diagonal of the N x N gradient matrix
-    for n, d in [(1024, 512), (32768, 1152), (65536, 768), (262144, 1152), (1000, 3)]:
+    # scratch is O(n*d): two block diagonals of the N x N gradient matrix, in
+    # both layouts, plus transposed copies of the two inputs
+    for n, d in [(1024, 512), (32768, 1152), (65536, 768), (262144, 1152), (1000, 3), (777, 1152)]:
         b32 = lib.mec_grad_scratch_bytes(n, d, 0)
         b16 = lib.mec_grad_scratch_bytes(n, d, 1)
         assert b32 == 2 * b16 > 0
-        assert b32 <= 4 * (n + 128 * 64) * max(1024, 2 * d + 256), (n, d, b32)
+        bs, nb = _lib.grad_blocking(n, d, 0)
+        assert bs % 128 == 0 and nb * bs >= n > (nb - 1) * bs
+        ldt = (n + 127) // 128 * 128
+        assert b32 == (4 * nb * bs * bs + 2 * d * ldt) * 4
+        bs_max = 2 * max(1024, 2 * d + 128)
+        assert bs <= bs_max and b32 <= 4 * (4 * (n + bs_max) * bs_max + 2 * d * (n + 128)), (n, d, b32)
     assert lib.mec_grad_scratch_bytes(10, 10, 7) < 0
+
+
+def test_blocking_prefers_exact_divisors():
+    # the headline and bf16 shapes split into equal blocks (no short last block)
+    for n, d in [(32768, 1152), (65536, 768), (262144, 1152), (1024, 512)]:
+        bs, nb = _lib.grad_blocking(n, d, 0)
+        assert nb * bs == n, (n, d, bs, nb)
+    assert _lib.grad_blocking(32768, 1152, 0) == (2048, 16)
+    assert _lib.grad_blocking(1000, 64, 0) == (1024, 1)
 
 
 VALID = dict(x=16, ldx=64, y=16, ldy=64, n=10, d=64, dtype=0, mode=0, normalize=1, temperature=0.07)
@@ -72,6 +87,17 @@ def test_grad_rejects_small_scratch_and_missing_outputs():
     assert rc == _lib.MEC_ERR_INVALID and "no gradient" in _lib.last_error()
     rc = lib.mec_grad(16, 64, 16, 64, 10, 64, 0, 0, 1, 0.07, 16, 8, need, 16, 16, None)
     assert rc == _lib.MEC_ERR_INVALID and "aligned" in _lib.last_error()
+
+
+def test_grad_step_validation():
+    lib = _lib.load()
+    need = lib.mec_grad_scratch_bytes(10, 64, 0)
+    rc = lib.mec_grad_step(16, 64, 16, 64, 10, 64, 0, 0, 1, 0.07, 16, 2, 16, need, 16, 16, None)
+    assert rc == _lib.MEC_ERR_INVALID and "step" in _lib.last_error()
+    rc = lib.mec_grad_step(16, 64, 16, 64, 10, 64, 0, 0, 1, 0.07, 16, -1, 16, need, 16, 16, None)
+    assert rc == _lib.MEC_ERR_INVALID and "step" in _lib.last_error()
+    with pytest.raises(_lib.MecError, match="out of range"):
+        _lib.grad_blocking(0, 64, 0)
 
 
 def test_postpass_and_finalize_validation():
