@@ -8,7 +8,7 @@
 #include <cstring>
 #include <string>
 
-#include "../../include/mec.h"
+#include "mec.h"
 #include "mec_kernels.h"
 #include "mec_rowops.h"
 

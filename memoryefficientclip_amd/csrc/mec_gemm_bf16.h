@@ -1,25 +1,38 @@
 // bf16 MFMA tile core for gfx950: 128x128 output tile per 256-thread
 // workgroup, 4 waves in 2x2, each wave a 64x64 sub-tile of 2x2 blocks of
-// v_mfma_f32_32x32x16_bf16 (fp32 accumulate).  K is staged through LDS in
-// chunks of 32 with double buffering.
+// v_mfma_f32_32x32x16_bf16 (fp32 accumulate).
 //
 // Both operands are K-major in global memory (element (row, k) at
-// base[row * ld + k]) and in LDS ([row][k], 80-byte padded rows): 16-byte
-// global loads, conflict-free 16-byte LDS reads.  Within a chunk the logical k
-// fed to MFMA step s (0..1) by lane half h, element e (0..7) is h*16 + s*8 + e
-// for both operands.
+// base[row * ld + k]) and in LDS ([row][k], rows padded by 16 bytes): 16-byte
+// global loads, conflict-free 16-byte LDS reads.  K is staged in chunks of BK
+// with the next chunk prefetched into registers during the MFMAs (STAGES = 2:
+// double-buffered LDS, one barrier per chunk; STAGES = 1: two barriers, half
+// the LDS).  Within a chunk the logical k fed to MFMA step s (0..BK/16-1) by
+// lane half h, element e (0..7) is h*BK/2 + s*8 + e for both operands.
 #pragma once
 #include "mec_common.h"
+
+#ifndef MEC_BF16_BK
+#define MEC_BF16_BK 64
+#endif
+#ifndef MEC_BF16_STAGES
+#define MEC_BF16_STAGES 1
+#endif
 
 namespace mec {
 namespace g16 {
 
 constexpr int BM = 128;
-constexpr int BK = 32;
+constexpr int BK = MEC_BF16_BK;
+constexpr int STAGES = MEC_BF16_STAGES;
 constexpr int NT = 256;
-constexpr int LD = BK + 8;               // 40 bf16 = 80-byte rows
-constexpr int TILE = BM * LD;            // 5120 bf16 = 10 KiB per operand per stage
-constexpr int LDS_ELEMS = 2 * 2 * TILE;  // 40 KiB
+constexpr int LD = BK + 8;                     // padded row pitch (elements)
+constexpr int TILE = BM * LD;                  // elements per operand per stage
+constexpr int LDS_ELEMS = STAGES * 2 * TILE;
+constexpr int KV = BK / 8;                     // 16-byte vectors per row
+constexpr int NV = BM * KV / NT;               // vectors per thread per operand per chunk
+constexpr int NS = BK / 16;                    // MFMA k-steps per chunk
+static_assert(BK % 32 == 0 && NV >= 1, "BK must be a multiple of 32");
 
 struct Operand {
   const uint16_t* base;  // element (row, k) at base[row * ld + k]
@@ -28,53 +41,58 @@ struct Operand {
   int kmax;              // valid k range [0, kmax)
 };
 
-struct Regs {
-  i16x8 v[2];
-};
+// Vector v of thread t carries row slot_row(t, v), k vector slot_kv(t): KV
+// consecutive lanes read one row's BK*2 contiguous bytes (the global loads
+// coalesce by consecutive lanes).
+__device__ __forceinline__ int slot_row(int t, int v) { return t / KV + v * (NT / KV); }
+__device__ __forceinline__ int slot_kv(int t) { return t % KV; }
 
 // VEC requires 16-byte aligned rows and, when kmax % 8 != 0, finite padding up
 // to the next multiple of 8 behind kmax.
 template <bool VEC>
-__device__ __forceinline__ void load_chunk(const Operand& op, int k0, Regs& r) {
+__device__ __forceinline__ void load_chunk(const Operand& op, int k0, i16x8 (&r)[NV]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int v = 0; v < 2; ++v) {
-    const int row = (t >> 2) + 64 * v;
-    const int kk = k0 + (t & 3) * 8;
+  for (int v = 0; v < NV; ++v) {
+    const int row = slot_row(t, v);
+    const int kk = k0 + slot_kv(t) * 8;
     const uint16_t* p = op.base + (int64_t)row * op.ld + kk;
     if (VEC) {
-      if (row < op.extent && kk < op.kmax) r.v[v] = *(const i16x8*)p;
-      else r.v[v] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (row < op.extent && kk < op.kmax) r[v] = *(const i16x8*)p;
+      else r[v] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) r.v[v][e] = (row < op.extent && kk + e < op.kmax) ? (short)p[e] : (short)0;
+      for (int e = 0; e < 8; ++e) r[v][e] = (row < op.extent && kk + e < op.kmax) ? (short)p[e] : (short)0;
     }
   }
 }
 
-__device__ __forceinline__ void store_chunk(uint16_t* lds, const Regs& r) {
+__device__ __forceinline__ void store_chunk(uint16_t* lds, const i16x8 (&r)[NV]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int v = 0; v < 2; ++v) {
-    const int row = (t >> 2) + 64 * v;
-    *(i16x8*)(lds + row * LD + (t & 3) * 8) = r.v[v];
+  for (int v = 0; v < NV; ++v) {
+    *(i16x8*)(lds + slot_row(t, v) * LD + slot_kv(t) * 8) = r[v];
   }
 }
 
-__device__ __forceinline__ void read_operand(const uint16_t* lds, int off, int lane, i16x8 (&o)[2]) {
+// MFMA steps [s0, s0 + 2) of the chunk: this lane's 16 k-values of its two A
+// rows and two B rows, then 8 MFMAs.
+__device__ __forceinline__ void compute_part(const uint16_t* la, const uint16_t* lb, int wm, int wn, int lane,
+                                             int s0, f32x16 (&acc)[2][2]) {
   const int q = lane & 31, h = lane >> 5;
-  const uint16_t* p = lds + (off + q) * LD + h * 16;
-  o[0] = *(const i16x8*)p;
-  o[1] = *(const i16x8*)(p + 8);
-}
-
-__device__ __forceinline__ void compute_chunk(const uint16_t* la, const uint16_t* lb, int wm, int wn, int lane,
-                                              f32x16 (&acc)[2][2]) {
   i16x8 a[2][2], b[2][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) read_operand(la, wm * 64 + i * 32, lane, a[i]);
+  for (int i = 0; i < 2; ++i) {
+    const uint16_t* p = la + (wm * 64 + i * 32 + q) * LD + h * (BK / 2) + s0 * 8;
+    a[i][0] = *(const i16x8*)p;
+    a[i][1] = *(const i16x8*)(p + 8);
+  }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) read_operand(lb, wn * 64 + j * 32, lane, b[j]);
+  for (int j = 0; j < 2; ++j) {
+    const uint16_t* p = lb + (wn * 64 + j * 32 + q) * LD + h * (BK / 2) + s0 * 8;
+    b[j][0] = *(const i16x8*)p;
+    b[j][1] = *(const i16x8*)(p + 8);
+  }
 #pragma unroll
   for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -97,27 +115,37 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   const int nk = (K + BK - 1) / BK;
   if (nk <= 0) return;
-  Regs ra, rb;
+  i16x8 ra[NV], rb[NV];
   load_chunk<VECA>(A, 0, ra);
   load_chunk<VECB>(B, 0, rb);
   store_chunk(lds, ra);
   store_chunk(lds + TILE, rb);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
+    const int cur = STAGES == 2 ? (kt & 1) : 0;
     const bool more = kt + 1 < nk;
     if (more) {
       load_chunk<VECA>(A, (kt + 1) * BK, ra);
       load_chunk<VECB>(B, (kt + 1) * BK, rb);
     }
     const uint16_t* la = lds + cur * 2 * TILE;
-    compute_chunk(la, la + TILE, wm, wn, lane, acc);
-    if (more) {
-      uint16_t* ln = lds + (cur ^ 1) * 2 * TILE;
-      store_chunk(ln, ra);
-      store_chunk(ln + TILE, rb);
+#pragma unroll
+    for (int s0 = 0; s0 < NS; s0 += 2) compute_part(la, la + TILE, wm, wn, lane, s0, acc);
+    if (STAGES == 2) {
+      if (more) {
+        uint16_t* ln = lds + (cur ^ 1) * 2 * TILE;
+        store_chunk(ln, ra);
+        store_chunk(ln + TILE, rb);
+      }
+      __syncthreads();
+    } else {
+      __syncthreads();
+      if (more) {
+        store_chunk(lds, ra);
+        store_chunk(lds + TILE, rb);
+        __syncthreads();
+      }
     }
-    __syncthreads();
   }
 }
 

@@ -52,6 +52,37 @@ template <> struct Core<uint16_t> {
 };
 
 // ---------------------------------------------------------------- forward
+// E = exp2(S c - c) of this wave's 64x64 accumulators (S scaled by rx_i ry_j
+// when NORM); rowv[bm * 16 + r] and colv[bn] collect this lane's partial row
+// and column sums.  MASK zeroes the diagonal and entries outside [0, N).
+template <bool NORM, bool MASK>
+__device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[2][2], float c, int m0, int n0, int N,
+                                                const float* s_rx, const float* s_ry, float (&rowv)[32],
+                                                float (&colv)[2]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) rowv[k] = 0.f;
+#pragma unroll
+  for (int bm = 0; bm < 2; ++bm) {
+#pragma unroll
+    for (int bn = 0; bn < 2; ++bn) {
+      const int nl = wn * 64 + bn * 32 + (lane & 31);
+      const int j = n0 + nl;
+      const float cy = NORM ? c * s_ry[nl] : c;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ml = wm * 64 + bm * 32 + acc_row(r, lane);
+        const int i = m0 + ml;
+        const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
+        float e = fast_exp2(fmaf(sc, cy, -c));
+        if (MASK) e = (i < N && j < N && i != j) ? e : 0.f;
+        rowv[bm * 16 + r] += e;
+        colv[bn] += e;
+      }
+    }
+  }
+}
+
 template <typename T, bool LIT, bool NORM, bool VEC>
 __global__ __launch_bounds__(256, 2) void k_sumexp(const T* __restrict__ X, int64_t ldx,
                                                    const T* __restrict__ Y, int64_t ldy, int N,
@@ -82,28 +113,11 @@ __global__ __launch_bounds__(256, 2) void k_sumexp(const T* __restrict__ X, int6
 
   float rowv[32];
   float colv[2] = {0.f, 0.f};
-#pragma unroll
-  for (int k = 0; k < 32; ++k) rowv[k] = 0.f;
-#pragma unroll
-  for (int bm = 0; bm < 2; ++bm) {
-#pragma unroll
-    for (int bn = 0; bn < 2; ++bn) {
-      const int nl = wn * 64 + bn * 32 + (lane & 31);
-      const int j = n0 + nl;
-      const float ryj = s_ry[nl];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ml = wm * 64 + bm * 32 + acc_row(r, lane);
-        const int i = m0 + ml;
-        float s = acc[bm][bn][r];
-        if (NORM) s *= s_rx[ml] * ryj;
-        float e = fast_exp2(fmaf(s, c, -c));
-        e = (i < N && j < N && i != j) ? e : 0.f;
-        rowv[bm * 16 + r] += e;
-        colv[bn] += e;
-      }
-    }
-  }
+  // interior tiles (no diagonal entry, no row or column beyond N) need no mask
+  if (m0 != n0 && m0 + 128 <= N && n0 + 128 <= N)
+    sumexp_epilogue<NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
+  else
+    sumexp_epilogue<NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
   const float rs = transpose_reduce32(rowv, lane);
   {
     const int q = lane & 31;
@@ -174,6 +188,46 @@ struct StepPlan {
   int cy_n, cy_pad;  // y-side contraction tiles, padded
 };
 
+// G'_ij of this wave's 64x64 accumulators into Gb (and GTb for CLIP).  MASK
+// zeroes the diagonal and entries outside [0, N).
+template <typename T, bool LIT, bool NORM, bool MASK>
+__device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[2][2], float c, int i0, int j0, int N,
+                                             T* __restrict__ Gb, T* __restrict__ GTb, int bs, const float* s_rx,
+                                             const float* s_ry, const float* s_ir, const float* s_ic) {
+  using C = Core<T>;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+#pragma unroll
+  for (int bm = 0; bm < 2; ++bm) {
+#pragma unroll
+    for (int bn = 0; bn < 2; ++bn) {
+      const int nl = wn * 64 + bn * 32 + (lane & 31);
+      const int j = j0 + nl;
+      const float cy = NORM ? c * s_ry[nl] : c;
+      const float icj = s_ic[nl];
+      float gv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ml = wm * 64 + bm * 32 + acc_row(r, lane);
+        const int i = i0 + ml;
+        const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
+        const float e = fast_exp2(fmaf(sc, cy, -c));
+        float g = LIT ? e * s_ir[ml] : e * (s_ir[ml] + icj);
+        if (MASK) g = (i < N && j < N && i != j) ? g : 0.f;
+        gv[r] = g;
+        Gb[(int64_t)ml * bs + nl] = C::pack(g);
+      }
+      if (!LIT) {
+        // registers 4g..4g+3 hold 4 consecutive rows: one vector store per group
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ml = wm * 64 + bm * 32 + acc_row(4 * g, lane);
+          C::store4(GTb + (int64_t)nl * bs + ml, gv[4 * g], gv[4 * g + 1], gv[4 * g + 2], gv[4 * g + 3]);
+        }
+      }
+    }
+  }
+}
+
 // Recompute the similarity tile (i0, j0) and store G'_ij = E_ij (1/R_i + 1/C_j)
 // (LiT: E_ij / R_i) for i != j, 0 on the diagonal and outside [0, N), into
 // the G' block at Gb (row pitch bs) and, for CLIP, transposed at GTb.
@@ -185,7 +239,7 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
                                             char* lds, float* s_rx, float* s_ry, float* s_ir, float* s_ic) {
   using C = Core<T>;
   const int64_t n64 = N;
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1;
+  const int t = threadIdx.x;
   typename C::Op A{X + (int64_t)i0 * ldx, ldx, N - i0, D};
   typename C::Op B{Y + (int64_t)j0 * ldy, ldy, N - j0, D};
   f32x16 acc[2][2];
@@ -201,35 +255,10 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
     s_ic[u] = (!LIT && ok) ? ws[WS_INV_COL * n64 + j0 + u] : 0.f;
   }
   __syncthreads();
-#pragma unroll
-  for (int bm = 0; bm < 2; ++bm) {
-#pragma unroll
-    for (int bn = 0; bn < 2; ++bn) {
-      const int nl = wn * 64 + bn * 32 + (lane & 31);
-      const int j = j0 + nl;
-      const float ryj = s_ry[nl], icj = s_ic[nl];
-      float gv[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ml = wm * 64 + bm * 32 + acc_row(r, lane);
-        const int i = i0 + ml;
-        float s = acc[bm][bn][r];
-        if (NORM) s *= s_rx[ml] * ryj;
-        const float e = fast_exp2(fmaf(s, c, -c));
-        float g = LIT ? e * s_ir[ml] : e * (s_ir[ml] + icj);
-        gv[r] = (i < N && j < N && i != j) ? g : 0.f;
-        Gb[(int64_t)ml * bs + nl] = C::pack(gv[r]);
-      }
-      if (!LIT) {
-        // registers 4g..4g+3 hold 4 consecutive rows: one vector store per group
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int ml = wm * 64 + bm * 32 + acc_row(4 * g, lane);
-          C::store4(GTb + (int64_t)nl * bs + ml, gv[4 * g], gv[4 * g + 1], gv[4 * g + 2], gv[4 * g + 3]);
-        }
-      }
-    }
-  }
+  if (i0 != j0 && i0 + 128 <= N && j0 + 128 <= N)
+    grad_g_store<T, LIT, NORM, false>(acc, c, i0, j0, N, Gb, GTb, bs, s_rx, s_ry, s_ir, s_ic);
+  else
+    grad_g_store<T, LIT, NORM, true>(acc, c, i0, j0, N, Gb, GTb, bs, s_rx, s_ry, s_ir, s_ic);
 }
 
 // One 128 x 128 output tile of a contraction: rows r0.. of block P, feature
@@ -272,7 +301,7 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
 }
 
 template <typename T, bool LIT, bool NORM, bool VEC>
-__global__ __launch_bounds__(256, 2) void k_grad_step(const T* __restrict__ X, int64_t ldx,
+__global__ __launch_bounds__(256, 3) void k_grad_step(const T* __restrict__ X, int64_t ldx,
                                                       const T* __restrict__ Y, int64_t ldy, int N, int D,
                                                       float c, const float* __restrict__ ws, GradBufs gb,
                                                       BlockGrid bg, StepPlan sp, float* __restrict__ acc_x,
