@@ -21,8 +21,15 @@
 namespace mec {
 
 // Element-type traits: which MFMA core runs the tile, and how G' is stored.
-template <typename T> struct Core;
-template <> struct Core<float> {
+// BKB is the K chunk depth of the bf16 core (the fp32 core has one depth).
+#ifndef MEC_BF16_BK_FWD
+#define MEC_BF16_BK_FWD 64
+#endif
+#ifndef MEC_BF16_BK_BWD
+#define MEC_BF16_BK_BWD 64
+#endif
+template <typename T, int BKB> struct Core;
+template <int BKB> struct Core<float, BKB> {
   using Op = g32::Operand;
   static constexpr int LDS_BYTES = g32::LDS_FLOATS * 4;
   template <bool VECA, bool VECB>
@@ -35,12 +42,12 @@ template <> struct Core<float> {
     *(f32x4*)p = f32x4{a, b, c, d};
   }
 };
-template <> struct Core<uint16_t> {
+template <int BKB> struct Core<uint16_t, BKB> {
   using Op = g16::Operand;
-  static constexpr int LDS_BYTES = g16::LDS_ELEMS * 2;
+  static constexpr int LDS_BYTES = g16::Cfg<BKB>::LDS_ELEMS * 2;
   template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[2][2]) {
-    g16::mainloop<VECA, VECB>(a, b, K, (uint16_t*)lds, acc);
+    g16::mainloop<BKB, VECA, VECB>(a, b, K, (uint16_t*)lds, acc);
   }
   static __device__ __forceinline__ uint16_t pack(float v) { return f32_to_bf16(v); }
   static __device__ __forceinline__ void store4(uint16_t* p, float a, float b, float c, float d) {
@@ -50,6 +57,8 @@ template <> struct Core<uint16_t> {
     *(uint2*)p = u;
   }
 };
+template <typename T> using CoreFwd = Core<T, MEC_BF16_BK_FWD>;
+template <typename T> using CoreBwd = Core<T, MEC_BF16_BK_BWD>;
 
 // ---------------------------------------------------------------- forward
 // E = exp2(S c - c) of this wave's 64x64 accumulators (S scaled by rx_i ry_j
@@ -87,7 +96,7 @@ template <typename T, bool LIT, bool NORM, bool VEC>
 __global__ __launch_bounds__(256, 2) void k_sumexp(const T* __restrict__ X, int64_t ldx,
                                                    const T* __restrict__ Y, int64_t ldy, int N,
                                                    int D, float c, float* __restrict__ ws, int tiles) {
-  using C = Core<T>;
+  using C = CoreFwd<T>;
   __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
   __shared__ float s_rx[128], s_ry[128], s_row[128], s_col[128];
   const int64_t n64 = N;
@@ -194,7 +203,7 @@ template <typename T, bool LIT, bool NORM, bool MASK>
 __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[2][2], float c, int i0, int j0, int N,
                                              T* __restrict__ Gb, T* __restrict__ GTb, int bs, const float* s_rx,
                                              const float* s_ry, const float* s_ir, const float* s_ic) {
-  using C = Core<T>;
+  using C = CoreBwd<T>;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
 #pragma unroll
   for (int bm = 0; bm < 2; ++bm) {
@@ -237,7 +246,7 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
                                             int64_t ldy, int N, int D, float c, const float* __restrict__ ws,
                                             T* __restrict__ Gb, T* __restrict__ GTb, int bs, int i0, int j0,
                                             char* lds, float* s_rx, float* s_ry, float* s_ir, float* s_ic) {
-  using C = Core<T>;
+  using C = CoreBwd<T>;
   const int64_t n64 = N;
   const int t = threadIdx.x;
   typename C::Op A{X + (int64_t)i0 * ldx, ldx, N - i0, D};
@@ -265,14 +274,16 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
 // columns d0..:
 //   x side: acc_x[i, d] (+)= sum_{j in Q} G'(P,Q)[i, j]  * YT[d, j]   (Q = P + s)
 //   y side: acc_y[j, d] (+)= sum_{i in Q} G'T(Q,P)[j, i] * XT[d, i]   (Q = P - s)
-// Each output tile has one owner per launch, so accumulation across launches
-// is a plain read-modify-write (replaces the atomics of clip_loss.py:148-156).
+// Each output tile has one owner per launch: accumulation across launches
+// adds each element once per launch, in launch order (the reference instead
+// lets every (row-tile, column-tile) program add into dX/dY with contending
+// atomics, clip_loss.py:148-156).
 template <typename T>
 __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __restrict__ Gblk,
                                                    const T* __restrict__ OT, int64_t ldt, const BlockGrid& bg,
                                                    int P, int Q, int tm, int td, bool accumulate,
                                                    float* __restrict__ out, char* lds) {
-  using C = Core<T>;
+  using C = CoreBwd<T>;
   const int r0 = P * bg.bs + tm * 128;
   if (r0 >= N) return;
   const int d0 = td * 128;
@@ -293,7 +304,13 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
         const int row = r0 + wm * 64 + bm * 32 + acc_row(r, lane);
         if (row < N && d < D) {
           float* p = out + (int64_t)row * D + d;
-          *p = accumulate ? *p + acc[bm][bn][r] : acc[bm][bn][r];
+          // a fire-and-forget add in L2 instead of a load-add-store round trip;
+          // the tile has one owner per launch, so the summation order (launch
+          // order) and the result are deterministic
+          if (accumulate)
+            __hip_atomic_fetch_add(p, acc[bm][bn][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          else
+            *p = acc[bm][bn][r];
         }
       }
     }
@@ -306,7 +323,7 @@ __global__ __launch_bounds__(256, 3) void k_grad_step(const T* __restrict__ X, i
                                                       float c, const float* __restrict__ ws, GradBufs gb,
                                                       BlockGrid bg, StepPlan sp, float* __restrict__ acc_x,
                                                       float* __restrict__ acc_y) {
-  using C = Core<T>;
+  using C = CoreBwd<T>;
   __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
   __shared__ float s_rx[128], s_ry[128], s_ir[128], s_ic[128];
   const int tdn = (D + 127) / 128;
