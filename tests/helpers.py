@@ -40,3 +40,53 @@ TOL = {
     torch.float32: dict(loss=1e-4, grad=1e-3),
     torch.bfloat16: dict(loss=1e-2, grad=1e-2),
 }
+
+
+def ref_fp64(a, b, t, lit, normalized, chunk):
+    """Loss and input gradients of the dense definition, fp64 on the GPU.
+
+    a: rows of S (image for CLIP, text for LiT); b: columns."""
+    x = a.double()
+    y = b.double()
+    xh = x if normalized else F.normalize(x, dim=1)
+    yh = y if normalized else F.normalize(y, dim=1)
+    n = x.shape[0]
+    r = torch.zeros(n, dtype=torch.float64, device=x.device)
+    c = torch.zeros(n, dtype=torch.float64, device=x.device)
+    for i0 in range(0, n, chunk):
+        e = torch.exp((xh[i0:i0 + chunk] @ yh.T - 1.0) / t)
+        r[i0:i0 + chunk] = e.sum(dim=1)
+        if not lit:
+            c += e.sum(dim=0)
+        del e
+    tdiag = ((xh * yh).sum(dim=1) - 1.0) / t
+    loss = (torch.log(r) - tdiag).mean()
+    if not lit:
+        loss = 0.5 * (loss + (torch.log(c) - tdiag).mean())
+    # G = (E/R_i + E/C_j)/(2 N t) - I/(N t)   (LiT: E/R_i/(N t) - I/(N t))
+    dxh = torch.zeros_like(xh)
+    dyh = None if lit else torch.zeros_like(yh)
+    s = 1.0 / (n * t) if lit else 1.0 / (2 * n * t)
+    for i0 in range(0, n, chunk):
+        e = torch.exp((xh[i0:i0 + chunk] @ yh.T - 1.0) / t)
+        g = e / r[i0:i0 + chunk, None]
+        if not lit:
+            g += e / c[None, :]
+        del e
+        g *= s
+        dxh[i0:i0 + chunk] = g @ yh
+        if not lit:
+            dyh += g.T @ xh[i0:i0 + chunk]
+        del g
+    dxh -= yh / (n * t)
+    if not lit:
+        dyh -= xh / (n * t)
+
+    def norm_bwd(v, dvh):
+        if normalized:
+            return dvh
+        nrm = v.norm(dim=1, keepdim=True).clamp_min(1e-12)
+        vh = v / nrm
+        return (dvh - vh * (vh * dvh).sum(dim=1, keepdim=True)) / nrm
+
+    return loss, norm_bwd(x, dxh), (None if lit else norm_bwd(y, dyh))

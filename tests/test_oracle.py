@@ -273,3 +273,23 @@ def test_cpu_baseline_matches_oracle():
     rl, rdt = oracle.lit_loss_and_grads(a, b, 0.05)
     assert none is None and abs(loss.item() - rl.item()) < 1e-5 * rl.item()
     assert torch.allclose(dt.double(), rdt, rtol=1e-3, atol=1e-6 * rdt.abs().max().item())
+
+
+@pytest.mark.parametrize("lit", [False, True])
+@pytest.mark.parametrize("normalized", [False, True])
+def test_fullsize_reference_matches_oracle(lit, normalized):
+    """The chunked fp64 reference used at full size on the GPU (tests/helpers.py
+    ref_fp64) agrees with the oracle, chunk boundaries included."""
+    from helpers import ref_fp64
+    x, y = _inputs(150, 24, seed=31 + lit + 2 * normalized)
+    if normalized:
+        x, y = F.normalize(x, dim=1), F.normalize(y, dim=1)
+    loss, dx, dy = ref_fp64(x, y, 0.05, lit, normalized, chunk=64)
+    if lit:
+        rl, rdx = oracle.lit_loss_and_grads(x, y, 0.05, normalized_inputs=normalized)
+        assert dy is None
+    else:
+        rl, rdx, rdy = oracle.clip_loss_and_grads(x, y, 0.05, normalized_inputs=normalized)
+        assert torch.allclose(dy, rdy, rtol=1e-10, atol=1e-14)
+    assert abs(loss.item() - rl.item()) < 1e-12 * abs(rl.item())
+    assert torch.allclose(dx, rdx, rtol=1e-10, atol=1e-14)
