@@ -37,6 +37,9 @@ int check_launch(const char* what) {
 
 constexpr int64_t kMaxN = int64_t(1) << 30;
 constexpr int64_t kMaxD = int64_t(1) << 20;
+// bf16 contractions address a 128-row panel of the transposed inputs
+// ([d][ldt], ldt ~ n) with 32-bit buffer offsets
+constexpr int64_t kMaxNBf16 = int64_t(1) << 22;
 
 int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                  int dtype) {
@@ -48,6 +51,8 @@ int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   if (dtype != MEC_DTYPE_F32 && dtype != MEC_DTYPE_BF16)
     return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
   if (x == nullptr || y == nullptr) return fail(MEC_ERR_INVALID, "x and y must be non-null");
+  if (dtype == MEC_DTYPE_BF16 && n > kMaxNBf16)
+    return fail(MEC_ERR_UNSUPPORTED, "bf16 supports n <= 2^22 (n=%lld)", (long long)n);
   return MEC_OK;
 }
 
@@ -71,15 +76,18 @@ bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, i
 }
 
 // Block decomposition of the N x N gradient matrix for the backward: nb
-// blocks of tb 128-row tiles.  The target is tb ~ 2d/128 (>= 8), which keeps
-// the scratch at O(n d) and the contraction depth (bs = 128 tb) about twice
-// the similarity depth d.  An exact divisor of the tile count within a factor
-// of two of the target is preferred (no short last block, whose contractions
-// would have a short K); otherwise the tiles are balanced over the blocks.
-void grad_blocks(int64_t n, int64_t d, int* bs, int* nb) {
-  const int64_t tiles = (n + 127) / 128;
-  int64_t target = (2 * d + 127) / 128;
-  if (target < 8) target = 8;
+// blocks of tb quanta of q rows (q = block_quantum: 128 for fp32, 256 for
+// bf16, so every tile kind divides a block).  The target is tb ~ 2d/q (and
+// at least 1024 rows), which keeps the scratch at O(n d) and the contraction
+// depth (bs = q tb) about twice the similarity depth d.  An exact divisor of
+// the quantum count within a factor of two of the target is preferred (no
+// short last block, whose contractions would have a short K); otherwise the
+// quanta are balanced over the blocks.
+void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
+  const int64_t q = block_quantum(dtype);
+  const int64_t tiles = (n + q - 1) / q;
+  int64_t target = (2 * d + q - 1) / q;
+  if (target < 1024 / q) target = 1024 / q;
   if (const char* env = std::getenv("MEC_GRAD_BLOCK_TILES")) {
     long v = std::strtol(env, nullptr, 10);
     if (v >= 1 && v <= 4096) target = v;
@@ -102,28 +110,30 @@ void grad_blocks(int64_t n, int64_t d, int* bs, int* nb) {
       tb = (tiles + nbv - 1) / nbv;
     }
   }
-  *bs = (int)(tb * 128);
+  *bs = (int)(tb * q);
   *nb = (int)((tiles + tb - 1) / tb);
 }
 
 // Scratch layout of the backward (element type = input dtype):
-//   [G0 | G1 | GT0 | GT1 | XT | YT]
+//   fp32: [G0 | G1 | GT0 | GT1 | XT | YT]     bf16: [GT0 | GT1 | XT | YT]
 // G0/G1 (and their transposes GT0/GT1) double-buffer one block diagonal of
-// G' (nb blocks of bs x bs); XT/YT are the normalised inputs transposed,
-// [d][ldt] with ldt = n rounded up to 128.
+// G' (nb blocks of bs x bs; bf16 keeps only the transposed copy); XT/YT are
+// the normalised inputs transposed, [d][ldt] with ldt = n rounded up to 128.
 struct ScratchLayout {
   int bs, nb;
+  int ncopies;                     // gradient-matrix buffers: 4 (G, GT double-buffered) or 2 (GT)
   int64_t ldt, gbuf, tbuf, total;  // bytes except ldt (elements)
 };
 
 ScratchLayout scratch_layout(int64_t n, int64_t d, int dtype) {
   ScratchLayout L;
-  grad_blocks(n, d, &L.bs, &L.nb);
+  grad_blocks(n, d, dtype, &L.bs, &L.nb);
   const int64_t elem = dtype == MEC_DTYPE_F32 ? 4 : 2;
   L.ldt = (n + 127) / 128 * 128;
   L.gbuf = (int64_t)L.nb * L.bs * L.bs * elem;
   L.tbuf = d * L.ldt * elem;
-  L.total = 4 * L.gbuf + 2 * L.tbuf;
+  L.ncopies = dtype == MEC_DTYPE_F32 ? 4 : 2;
+  L.total = L.ncopies * L.gbuf + 2 * L.tbuf;
   return L;
 }
 
@@ -193,18 +203,21 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   hipStream_t s = (hipStream_t)stream;
   const int N = (int)n, D = (int)d;
   const float c = (float)(1.4426950408889634 / (double)temperature);
-  const int tiles = (int)((n + 127) / 128);
-  dim3 grid((unsigned)((int64_t)tiles * tiles));
   const bool vec = vec_ok(x, ldx, y, ldy, d, dtype);
+  const TileDims td = fwd_tile_dims(dtype, vec);
+  const int tiles_m = (int)((n + td.bm - 1) / td.bm), tiles_n = (int)((n + td.bn - 1) / td.bn);
+  const int64_t nwg = (int64_t)tiles_m * tiles_n;
+  if (nwg > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "forward grid too large");
+  dim3 grid((unsigned)nwg);
   const bool lit = mode == MEC_MODE_LIT;
   if (dtype == MEC_DTYPE_F32) {
     DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
         k_sumexp<float, LIT, NORM, VEC><<<grid, 256, 0, s>>>((const float*)x, ldx, (const float*)y, ldy, N, D,
-                                                          c, workspace, tiles))));
+                                                          D, c, workspace, tiles_m, tiles_n))));
   } else {
     DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
         k_sumexp<uint16_t, LIT, NORM, VEC><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (const uint16_t*)y, ldy,
-                                                           N, D, c, workspace, tiles))));
+                                                           N, D, D, c, workspace, tiles_m, tiles_n))));
   }
   return check_launch("sumexp");
 }
@@ -245,7 +258,7 @@ int mec_grad_blocking(int64_t n, int64_t d, int dtype, int64_t* block_rows, int6
   if (dtype != MEC_DTYPE_F32 && dtype != MEC_DTYPE_BF16) return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
   if (!block_rows || !num_blocks) return fail(MEC_ERR_INVALID, "block_rows and num_blocks must be non-null");
   int bs, nb;
-  grad_blocks(n, d, &bs, &nb);
+  grad_blocks(n, d, dtype, &bs, &nb);
   *block_rows = bs;
   *num_blocks = nb;
   return MEC_OK;
@@ -274,15 +287,16 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
     return fail(MEC_ERR_INVALID, "step %lld out of range [0, %d]", (long long)step, nb);
   const int N = (int)n, D = (int)d;
   const float c = (float)(1.4426950408889634 / (double)temperature);
-  BlockGrid bg{bs, nb, bs / 128};
-  const int tdn = (D + 127) / 128;
+  const bool vec = vec_ok(x, ldx, y, ldy, d, dtype);
+  const TileDims tf = fwd_tile_dims(dtype, vec), tc = con_tile_dims(dtype);
+  BlockGrid bg{bs, nb, bs / tf.bm, bs / tf.bn, bs / tc.bm, (D + tc.bn - 1) / tc.bn};
   StepPlan sp{};
   sp.diag_g = step < nb ? (int)step : -1;
   sp.diag_c = step > 0 ? (int)step - 1 : -1;
   sp.accumulate = step > 1;
-  sp.g_n = sp.diag_g >= 0 ? nb * bg.tpb * bg.tpb : 0;
-  sp.cx_n = (sp.diag_c >= 0 && acc_x) ? nb * bg.tpb * tdn : 0;
-  sp.cy_n = (sp.diag_c >= 0 && acc_y) ? nb * bg.tpb * tdn : 0;
+  sp.g_n = sp.diag_g >= 0 ? nb * bg.gtm * bg.gtn : 0;
+  sp.cx_n = (sp.diag_c >= 0 && acc_x) ? nb * bg.ctm * bg.ctd : 0;
+  sp.cy_n = (sp.diag_c >= 0 && acc_y) ? nb * bg.ctm * bg.ctd : 0;
   sp.g_pad = round8(sp.g_n);
   sp.cx_pad = round8(sp.cx_n);
   sp.cy_pad = round8(sp.cy_n);
@@ -290,12 +304,18 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
   if (grid > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "backward grid too large");
   char* base = (char*)scratch;
   GradBufs gb;
-  gb.g[0] = base;
-  gb.g[1] = base + L.gbuf;
-  gb.gt[0] = base + 2 * L.gbuf;
-  gb.gt[1] = base + 3 * L.gbuf;
-  gb.xt = base + 4 * L.gbuf;
-  gb.yt = base + 4 * L.gbuf + L.tbuf;
+  if (L.ncopies == 4) {
+    gb.g[0] = base;
+    gb.g[1] = base + L.gbuf;
+    gb.gt[0] = base + 2 * L.gbuf;
+    gb.gt[1] = base + 3 * L.gbuf;
+  } else {
+    gb.g[0] = gb.g[1] = nullptr;
+    gb.gt[0] = base;
+    gb.gt[1] = base + L.gbuf;
+  }
+  gb.xt = base + L.ncopies * L.gbuf;
+  gb.yt = base + L.ncopies * L.gbuf + L.tbuf;
   gb.ldt = L.ldt;
   hipStream_t s = (hipStream_t)stream;
   if (step == 0) {
@@ -324,15 +344,14 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
     rc = check_launch("transpose");
     if (rc) return rc;
   }
-  const bool vec = vec_ok(x, ldx, y, ldy, d, dtype);
   if (dtype == MEC_DTYPE_F32) {
     DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
         k_grad_step<float, LIT, NORM, VEC><<<(unsigned)grid, 256, 0, s>>>(
-            (const float*)x, ldx, (const float*)y, ldy, N, D, c, workspace, gb, bg, sp, acc_x, acc_y))));
+            (const float*)x, ldx, (const float*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y))));
   } else {
     DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
         k_grad_step<uint16_t, LIT, NORM, VEC><<<(unsigned)grid, 256, 0, s>>>(
-            (const uint16_t*)x, ldx, (const uint16_t*)y, ldy, N, D, c, workspace, gb, bg, sp, acc_x, acc_y))));
+            (const uint16_t*)x, ldx, (const uint16_t*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y))));
   }
   return check_launch("grad_step");
 }
@@ -344,7 +363,7 @@ int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, 
   int rc = check_common(x, ldx, y, ldy, n, d, dtype);
   if (rc) return rc;
   int bs, nb;
-  grad_blocks(n, d, &bs, &nb);
+  grad_blocks(n, d, dtype, &bs, &nb);
   for (int t = 0; t <= nb; ++t) {
     rc = mec_grad_step(x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, t, scratch,
                        scratch_bytes, acc_x, acc_y, stream);

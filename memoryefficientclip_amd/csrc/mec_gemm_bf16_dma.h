@@ -1,0 +1,281 @@
+// bf16 MFMA tile core for gfx950 with direct global->LDS loads.
+//
+// Geometry: a BM x BN output tile per 256-thread workgroup, 4 waves in 2x2,
+// each wave a (BM/2) x (BN/2) sub-tile of v_mfma_f32_32x32x16_bf16 blocks
+// (fp32 accumulate).  Two workgroups share a CU (72 KB of LDS each), so one
+// workgroup's epilogue (exp, reductions, stores) runs while the other's MFMAs
+// do: the forward and gradient-matrix tiles are 128 x 256, the contractions
+// 256 x 128.
+//
+// Operands are K-major (element (row, k) at base[row * ld + k]).  K is staged
+// in chunks of BK = 32 through a ring of S = 3 LDS stages ([row][32] bf16, 64
+// bytes per row).  Each chunk arrives by buffer_load_dwordx4 ... lds: every
+// lane of a wave moves 16 bytes and the wave writes one contiguous 1 KB block
+// (16 rows) of the stage; which 16-byte k-vector of a row a lane fetches is
+// XOR-swizzled (vector v of row r sits in slot v ^ ((r >> 2) & 3)) so that the
+// MFMA operand reads (ds_read_b128, lanes 0..15 on rows 0..15 at one k-vector)
+// hit 16 distinct 16-byte bank groups.  The loads of chunk kt+S-1 are spread
+// over the MFMAs of chunk kt; one barrier per chunk.
+//
+// Masking costs nothing in the loop: each operand's buffer descriptor covers
+// exactly its valid rows and k range, so rows beyond `rows` read as zero, and
+// lanes whose k-vector lies at or beyond kmax in the tail chunk get an
+// out-of-range offset (also zero).  Requirements (checked by the host):
+// 16-byte aligned base, ld % 8 == 0, kmax % 8 == 0, (rows - 1) * ld + kmax
+// < 2^31 elements / 2 (byte offsets are 32-bit).
+//
+// Within a chunk the logical k fed to MFMA step s (0, 1) by lane half
+// h = lane / 32 is the 16-byte vector h * 2 + s for both operands, so the
+// contraction over the chunk is exact.
+//
+// Transposed A (TA = true): A is stored k-row-major (element (m, k) at
+// base[k * ld + m], m contiguous), e.g. a transposed gradient-matrix block.
+// Its stage region is [32 k-rows][BM m] (2 k-rows per 1 KB load block, the
+// 16-byte slot of m-vector v in k-row r at v ^ 4 (r & 3)), and each MFMA
+// fragment (8 consecutive k at one m) is assembled from two
+// ds_read_b64_tr_b16: within each group of 16 lanes, source lane j points at
+// 4 consecutive m of k-row k0 + j / 4, and result lane i receives k-rows
+// k0 .. k0 + 3 of column m0 + i.  With the swizzle, the 32 lanes of a pass
+// (4 k-rows x 32 m x 2 bytes) cover all 64 banks once.
+#pragma once
+#include "mec_common.h"
+
+namespace mec {
+namespace g16d {
+
+constexpr int BK = 32;            // k per chunk
+constexpr int S = 3;              // LDS stages
+constexpr int NT = 256;           // threads (4 waves, 2 x 2)
+constexpr int ROWB = BK * 2;      // bytes per staged row
+constexpr int RPB = 16;           // rows per 1 KB load block
+constexpr int NS = BK / 16;       // MFMA k-steps per chunk
+constexpr uint32_t OOB = 0x80000000u;  // buffer offset that reads as zero
+
+template <int BM_, int BN_, bool TA_ = false>
+struct Geo {
+  static constexpr int BM = BM_, BN = BN_;
+  static constexpr bool TA = TA_;                      // A stored k-row-major
+  static_assert(!TA || BM == 256, "transposed A: 512-byte k-rows (BM = 256)");
+  static constexpr int TM = BM / 2, TN = BN / 2;       // wave sub-tile
+  static constexpr int FM = TM / 32, FN = TN / 32;     // 32x32 MFMA blocks per wave
+  static constexpr int ROWS = BM + BN;
+  static constexpr int STAGE = ROWS * ROWB;
+  static constexpr int LDS_BYTES = S * STAGE;
+  static constexpr int IPW = ROWS / RPB / 4;           // load instructions per wave per chunk
+  static constexpr int NMF = FM * FN;                  // MFMAs per k-step
+  static constexpr int LPS = (IPW + NS - 1) / NS;      // loads interleaved per k-step
+  static_assert(ROWS % (RPB * 4) == 0 && BM % RPB == 0, "load split");
+};
+
+struct Operand {
+  const uint16_t* base;  // element (row, k) at base[row * ld + k] (transposed A: base[k * ld + row])
+  int64_t ld;
+  int rows;              // valid rows from base (rows beyond read as 0; transposed A: all BM rows readable)
+  int kmax;              // valid k range [0, kmax), a multiple of 8
+};
+
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& op) {
+  const int64_t elems = op.rows > 0 ? (int64_t)(op.rows - 1) * op.ld + op.kmax : 0;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)op.base, 0, (int)(elems * 2), 0x00020000);
+}
+// transposed A: k-rows [0, kmax) of BM elements
+template <int BM>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_t(const Operand& op) {
+  const int64_t elems = op.kmax > 0 ? (int64_t)(op.kmax - 1) * op.ld + BM : 0;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)op.base, 0, (int)(elems * 2), 0x00020000);
+}
+
+// This wave's IPW loads of every chunk: per-lane byte offset at k = 0, the
+// lane's k-vector start, and the 1 KB LDS block each load fills.
+template <class G>
+struct LoadPlan {
+  __amdgpu_buffer_rsrc_t ra, rb;
+  uint32_t voff[G::IPW];
+  int kv;          // k of this lane's 16-byte vector within a chunk (K-major operands)
+  int kr;          // k-row of this lane within a 1 KB block (transposed A: 0 or 1)
+  int kmax_a, kmax_b;
+  int64_t lda;     // transposed A: bytes per k-row
+  __device__ __forceinline__ void init(const Operand& A, const Operand& B) {
+    ra = G::TA ? make_rsrc_t<G::BM>(A) : make_rsrc(A);
+    rb = make_rsrc(B);
+    kmax_a = A.kmax;
+    kmax_b = B.kmax;
+    lda = A.ld * 2;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rib = lane >> 2, phys = lane & 3;
+    // rows of one load block are b*16 .. b*16+15, so swz(r) = (rib >> 2) & 3
+    kv = (phys ^ swz(rib)) * 8;
+    kr = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < G::IPW; ++i) {
+      const int b = w * G::IPW + i;
+      const bool isa = b * RPB < G::BM;
+      if (G::TA && isa) {
+        // block b holds k-rows 2b, 2b+1 (within the chunk); lane l fills slot l % 32 of k-row 2b + l / 32
+        const int krow = 2 * b + kr;
+        const int slot = (lane & 31) ^ (4 * (krow & 3));
+        voff[i] = (uint32_t)((int64_t)krow * A.ld + slot * 8) * 2;
+      } else {
+        const int r = b * RPB + rib;
+        voff[i] = (uint32_t)(((isa ? (int64_t)r * A.ld : (int64_t)(r - G::BM) * B.ld) + kv) * 2);
+      }
+    }
+  }
+  // load i of the chunk starting at k0 into `stage`
+  __device__ __forceinline__ void issue(int i, int k0, char* stage) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int b = w * G::IPW + i;
+    const bool isa = b * RPB < G::BM;
+    uint32_t off, soff;
+    if (G::TA && isa) {
+      off = (k0 + 2 * b + kr < kmax_a) ? voff[i] : OOB;
+      soff = (uint32_t)(k0 * lda);
+    } else {
+      off = (k0 + kv < (isa ? kmax_a : kmax_b)) ? voff[i] : OOB;
+      soff = (uint32_t)k0 * 2;
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(isa ? ra : rb,
+                                             (__attribute__((address_space(3))) void*)(stage + b * 1024), 16, off,
+                                             soff, 0, 0);
+  }
+};
+
+template <class G>
+struct Frags {
+  i16x8 a[G::FM], b[G::FN];
+};
+
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+// 4 k-rows of one column per lane (see the transposed-A note above)
+__device__ __forceinline__ i16x4_t read_tr4(const char* p) {
+  return __builtin_bit_cast(
+      i16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)p));
+}
+
+template <class G>
+__device__ __forceinline__ void read_frags(const char* stage, int s, Frags<G>& f) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int q = lane & 31, h = lane >> 5;
+  const int off = (((h * NS + s) ^ swz(q)) << 4);
+  if (G::TA) {
+    // fragment of 32 m x 16 k: lane group g = lane / 16 covers m0 + 16 (g & 1) .. + 15 and
+    // logical k-vector (g >> 1) * 2 + s; source lane j reads k-row kb + j / 4, m-quad j % 4
+    const int g = lane >> 4, j = lane & 15;
+    const int kb = ((g >> 1) * NS + s) * 8;
+#pragma unroll
+    for (int i = 0; i < G::FM; ++i) {
+      const int m = wm * G::TM + i * 32 + 16 * (g & 1) + 4 * (j & 3);
+      i16x4_t lo, hi;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int krow = kb + 4 * half + (j >> 2);
+        const int slot = (m >> 3) ^ (4 * (krow & 3));
+        const i16x4_t v = read_tr4(stage + krow * (G::BM * 2) + slot * 16 + (m & 7) * 2);
+        if (half == 0) lo = v;
+        else hi = v;
+      }
+      f.a[i] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < G::FM; ++i) f.a[i] = *(const i16x8*)(stage + (wm * G::TM + i * 32 + q) * ROWB + off);
+  }
+#pragma unroll
+  for (int j = 0; j < G::FN; ++j) f.b[j] = *(const i16x8*)(stage + (G::BM + wn * G::TN + j * 32 + q) * ROWB + off);
+}
+
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// vmcnt <= N and lgkmcnt == 0, then a workgroup barrier.  __syncthreads()
+// would also wait for every outstanding LDS DMA (its release fence counts them
+// as LDS stores), which would serialise the prefetch ring; the explicit vmcnt
+// covers the chunk that must have landed, lgkmcnt(0) the operand reads of the
+// stage that is refilled after the barrier.
+template <int N>
+__device__ __forceinline__ void wait_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// MFMAs of one k-step with loads [L0, L1) interleaved, in program order.
+template <class G, int L0, int L1>
+__device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const LoadPlan<G>& lp,
+                                          bool do_load, int k0, char* stage) {
+  constexpr int NL = L1 - L0;
+  static_assert(NL <= G::NMF, "at most one load per MFMA");
+  // one load after every EVERY-th MFMA: floor(NMF / EVERY) >= NL slots
+  constexpr int EVERY = NL > 0 ? G::NMF / (NL > 0 ? NL : 1) : G::NMF + 1;
+#pragma unroll
+  for (int m = 0; m < G::NMF; ++m) {
+    const int i = m / G::FN, j = m % G::FN;
+    acc[i][j] = mfma_bf16_32x32x16(f.a[i], f.b[j], acc[i][j]);
+    if (NL > 0 && (m % EVERY) == EVERY - 1 && L0 + m / EVERY < L1) {
+      sched_fence();
+      if (do_load) lp.issue(L0 + m / EVERY, k0, stage);
+      sched_fence();
+    }
+  }
+}
+
+// acc[i][j] (this wave's sub-tile) = sum_k A(m, k) * B(n, k) over k in [0, K),
+// K > 0 (chunks past kmax read as zero).  Uses LDS_BYTES of `lds`; ends with
+// every wave past its last LDS read of the ring (callers may reuse it after a
+// barrier).
+template <class G>
+__device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int K, char* lds,
+                                         f32x16 (&acc)[G::FM][G::FN]) {
+#pragma unroll
+  for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < G::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  const int nk = (K + BK - 1) / BK;
+  LoadPlan<G> lp;
+  lp.init(A, B);
+  // prologue: chunks 0 .. S-2 in flight
+#pragma unroll
+  for (int c = 0; c + 1 < S; ++c)
+    if (c < nk) {
+#pragma unroll
+      for (int i = 0; i < G::IPW; ++i) lp.issue(i, c * BK, lds + c * G::STAGE);
+    }
+  Frags<G> f0, f1;
+  int cur = 0;      // stage of chunk kt
+  int fre = S - 1;  // stage of chunk kt-1 = stage of chunk kt+S-1
+  for (int kt = 0; kt < nk; ++kt) {
+    // chunk kt landed: min(S-2, nk-1-kt) newer chunks may still be in flight
+    if (kt + S - 2 < nk) wait_barrier<G::IPW*(S - 2)>();
+    else wait_barrier<0>();
+    char* cs = lds + cur * G::STAGE;
+    char* fs = lds + fre * G::STAGE;
+    const bool ld = kt + S - 1 < nk;
+    const int k0 = (kt + S - 1) * BK;
+    read_frags<G>(cs, 0, f0);
+    sched_fence();
+    // the previous chunk's last k-step (its operands are already in registers)
+    if (kt > 0) {
+      mfma_step<G, 0, G::LPS>(f1, acc, lp, ld, k0, fs);
+    } else if (ld) {
+#pragma unroll
+      for (int i = 0; i < G::LPS; ++i) lp.issue(i, k0, fs);
+    }
+    sched_fence();
+    read_frags<G>(cs, 1, f1);
+    sched_fence();
+    mfma_step<G, G::LPS, G::IPW>(f0, acc, lp, ld, k0, fs);
+    sched_fence();
+    cur = cur + 1 == S ? 0 : cur + 1;
+    fre = fre + 1 == S ? 0 : fre + 1;
+  }
+  mfma_step<G, 0, 0>(f1, acc, lp, false, 0, lds);
+}
+
+}  // namespace g16d
+}  // namespace mec

@@ -1,5 +1,6 @@
 // MFMA tile kernels of the contrastive-loss hot path (fp32 and bf16 inputs;
-// the element type selects the MFMA core, the epilogues are shared):
+// the element type and layout select the MFMA core and tile shape, the
+// epilogues are shared):
 //   k_sumexp        forward: tiled S = X Y^T, E = exp2(S c - c), off-diagonal
 //                       row (and column) partial sums, one atomic per row/column
 //                       per tile.  Replaces clip_sum_exp_kernel (clip_loss.py:9-64)
@@ -12,43 +13,42 @@
 //                       (clip_loss.py:96-124, lit_loss.py:94-120), while
 //                       contracting diagonal t-1 from the other buffer:
 //                       dX_I += G'_IJ Y^_J and dY_J += G'_IJ^T X^_I as plain MFMA
-//                       contractions without atomics (clip_loss.py:127-156,
-//                       lit_loss.py:123-148).
+//                       contractions without contending atomics
+//                       (clip_loss.py:127-156, lit_loss.py:123-148).
 #pragma once
 #include "mec_gemm_f32.h"
 #include "mec_gemm_bf16.h"
+#include "mec_gemm_bf16_dma.h"
+#include "mec_tiles.h"
 
 namespace mec {
 
-// Element-type traits: which MFMA core runs the tile, and how G' is stored.
-// BKB is the K chunk depth of the bf16 core (the fp32 core has one depth).
+// ------------------------------------------------------------ tile configs
+// Every config: BM x BN output tile per 256-thread workgroup, 4 waves in 2 x 2,
+// each wave a TM x TN sub-tile of FM x FN 32x32 MFMA blocks whose
+// accumulator register r of lane l holds element (acc_row(r, l), l % 32).
 #ifndef MEC_BF16_BK_FWD
 #define MEC_BF16_BK_FWD 64
 #endif
-#ifndef MEC_BF16_BK_BWD
-#define MEC_BF16_BK_BWD 64
-#endif
-template <typename T, int BKB> struct Core;
-template <int BKB> struct Core<float, BKB> {
+
+// fp32, 128 x 128, operands staged through registers
+struct TileF32 {
+  using Elem = float;
   using Op = g32::Operand;
+  static constexpr bool TA = false;
+  static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2;
   static constexpr int LDS_BYTES = g32::LDS_FLOATS * 4;
   template <bool VECA, bool VECB>
-  static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[2][2]) {
+  static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
     g32::mainloop<VECA, VECB>(a, b, K, (float*)lds, acc);
   }
   static __device__ __forceinline__ float pack(float v) { return v; }
-  // 4 consecutive values as one vector store
   static __device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
     *(f32x4*)p = f32x4{a, b, c, d};
   }
 };
-template <int BKB> struct Core<uint16_t, BKB> {
-  using Op = g16::Operand;
-  static constexpr int LDS_BYTES = g16::Cfg<BKB>::LDS_ELEMS * 2;
-  template <bool VECA, bool VECB>
-  static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[2][2]) {
-    g16::mainloop<BKB, VECA, VECB>(a, b, K, (uint16_t*)lds, acc);
-  }
+
+struct PackBf16 {
   static __device__ __forceinline__ uint16_t pack(float v) { return f32_to_bf16(v); }
   static __device__ __forceinline__ void store4(uint16_t* p, float a, float b, float c, float d) {
     uint2 u;
@@ -57,119 +57,180 @@ template <int BKB> struct Core<uint16_t, BKB> {
     *(uint2*)p = u;
   }
 };
-template <typename T> using CoreFwd = Core<T, MEC_BF16_BK_FWD>;
-template <typename T> using CoreBwd = Core<T, MEC_BF16_BK_BWD>;
+
+// bf16, 128 x 128, operands staged through registers (any alignment / D)
+struct TileB16V : PackBf16 {
+  using Elem = uint16_t;
+  using Op = g16::Operand;
+  static constexpr bool TA = false;
+  static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2;
+  static constexpr int LDS_BYTES = g16::Cfg<MEC_BF16_BK_FWD>::LDS_ELEMS * 2;
+  template <bool VECA, bool VECB>
+  static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
+    g16::mainloop<MEC_BF16_BK_FWD, VECA, VECB>(a, b, K, (uint16_t*)lds, acc);
+  }
+};
+
+// bf16, BM_ x BN_, direct global->LDS loads (16-byte aligned rows, ld and kmax
+// multiples of 8); TA_: A stored k-row-major (a transposed gradient-matrix block)
+template <int BM_, int BN_, bool TA_ = false>
+struct TileB16D : PackBf16 {
+  using Elem = uint16_t;
+  using Op = g16d::Operand;
+  using G = g16d::Geo<BM_, BN_, TA_>;
+  static constexpr bool TA = TA_;
+  static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
+  static constexpr int LDS_BYTES = G::LDS_BYTES;
+  template <bool VECA, bool VECB>
+  static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
+    g16d::mainloop<G>(a, b, K, (char*)lds, acc);
+  }
+};
+
+// forward sums and gradient-matrix tiles; contractions (see mec_tiles.h)
+template <typename T, bool VEC> struct FwdTileSel;
+template <bool VEC> struct FwdTileSel<float, VEC> { using type = TileF32; };
+template <> struct FwdTileSel<uint16_t, true> { using type = TileB16D<128, 256>; };
+template <> struct FwdTileSel<uint16_t, false> { using type = TileB16V; };
+template <typename T, bool VEC> using FwdTile = typename FwdTileSel<T, VEC>::type;
+// Contractions.  fp32 stores the gradient-matrix blocks in both layouts (G'
+// for the x side, G'^T for the y side); bf16 stores only G'^T, which the y
+// side reads K-major and the x side reads transposed through LDS.
+template <typename T> struct ConTileSel;
+template <> struct ConTileSel<float> { using x = TileF32; using y = TileF32; };
+template <> struct ConTileSel<uint16_t> { using x = TileB16D<256, 128, true>; using y = TileB16D<256, 128>; };
+template <typename T> using ConTileX = typename ConTileSel<T>::x;
+template <typename T> using ConTileY = typename ConTileSel<T>::y;
+// bf16 keeps one layout of the gradient-matrix blocks (G'^T)
+template <typename T> struct GtOnly { static constexpr bool value = false; };
+template <> struct GtOnly<uint16_t> { static constexpr bool value = true; };
+
+// workgroups per CU the launch bounds promise (the bf16 direct-load configs
+// use 72 KB of LDS: two workgroups, one's epilogue overlapping the other's MFMAs)
+template <typename T> struct Occ;
+template <> struct Occ<float> { static constexpr int fwd = 2, bwd = 3; };
+template <> struct Occ<uint16_t> { static constexpr int fwd = 2, bwd = 2; };
+
+template <int A, int B> struct CMax { static constexpr int value = A > B ? A : B; };
 
 // ---------------------------------------------------------------- forward
-// E = exp2(S c - c) of this wave's 64x64 accumulators (S scaled by rx_i ry_j
+// E = exp2(S c - c) of this wave's TM x TN accumulators (S scaled by rx_i ry_j
 // when NORM); rowv[bm * 16 + r] and colv[bn] collect this lane's partial row
 // and column sums.  MASK zeroes the diagonal and entries outside [0, N).
-template <bool NORM, bool MASK>
-__device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[2][2], float c, int m0, int n0, int N,
-                                                const float* s_rx, const float* s_ry, float (&rowv)[32],
-                                                float (&colv)[2]) {
+template <class TL, bool NORM, bool MASK>
+__device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::FN], float c, int m0, int n0, int N,
+                                                const float* s_rx, const float* s_ry, float (&rowv)[TL::FM * 16],
+                                                float (&colv)[TL::FN]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
 #pragma unroll
-  for (int k = 0; k < 32; ++k) rowv[k] = 0.f;
+  for (int k = 0; k < TL::FM * 16; ++k) rowv[k] = 0.f;
 #pragma unroll
-  for (int bm = 0; bm < 2; ++bm) {
+  for (int bn = 0; bn < TL::FN; ++bn) {
+    const int nl = wn * TL::TN + bn * 32 + (lane & 31);
+    const int j = n0 + nl;
+    const float cy = NORM ? c * s_ry[nl] : c;
+    float cs = 0.f;
 #pragma unroll
-    for (int bn = 0; bn < 2; ++bn) {
-      const int nl = wn * 64 + bn * 32 + (lane & 31);
-      const int j = n0 + nl;
-      const float cy = NORM ? c * s_ry[nl] : c;
+    for (int bm = 0; bm < TL::FM; ++bm) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int ml = wm * 64 + bm * 32 + acc_row(r, lane);
+        const int ml = wm * TL::TM + bm * 32 + acc_row(r, lane);
         const int i = m0 + ml;
         const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
         float e = fast_exp2(fmaf(sc, cy, -c));
         if (MASK) e = (i < N && j < N && i != j) ? e : 0.f;
         rowv[bm * 16 + r] += e;
-        colv[bn] += e;
+        cs += e;
       }
     }
+    colv[bn] = cs;
   }
 }
 
 template <typename T, bool LIT, bool NORM, bool VEC>
-__global__ __launch_bounds__(256, 2) void k_sumexp(const T* __restrict__ X, int64_t ldx,
-                                                   const T* __restrict__ Y, int64_t ldy, int N,
-                                                   int D, float c, float* __restrict__ ws, int tiles) {
-  using C = CoreFwd<T>;
-  __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
-  __shared__ float s_rx[128], s_ry[128], s_row[128], s_col[128];
+__global__ __launch_bounds__(256, Occ<T>::fwd) void k_sumexp(const T* __restrict__ X, int64_t ldx,
+                                                            const T* __restrict__ Y, int64_t ldy, int N, int D,
+                                                            int kmax, float c, float* __restrict__ ws, int tiles_m,
+                                                            int tiles_n) {
+  using TL = FwdTile<T, VEC>;
+  static_assert(TL::FM == 2, "row reduction assumes 64-row wave sub-tiles");
+  __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
+  __shared__ float s_rx[TL::BM], s_ry[TL::BN], s_row[TL::BM], s_col[TL::BN];
   const int64_t n64 = N;
   int tm, tn;
-  tile_swizzle(blockIdx.x, gridDim.x, tiles, tiles, 8, tm, tn);
-  const int m0 = tm * 128, n0 = tn * 128;
+  tile_swizzle(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
+  const int m0 = tm * TL::BM, n0 = tn * TL::BN;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1;
 
-  typename C::Op A{X + (int64_t)m0 * ldx, ldx, N - m0, D};
-  typename C::Op B{Y + (int64_t)n0 * ldy, ldy, N - n0, D};
-  f32x16 acc[2][2];
-  C::template run<VEC, VEC>(A, B, D, lds, acc);
+  typename TL::Op A{X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax};
+  typename TL::Op B{Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax};
+  f32x16 acc[TL::FM][TL::FN];
+  TL::template run<VEC, VEC>(A, B, D, lds, acc);
 
-  if (t < 128) {
-    s_rx[t] = (NORM && m0 + t < N) ? ws[WS_RX * n64 + m0 + t] : 1.f;
-    s_row[t] = 0.f;
-  } else {
-    const int u = t - 128;
+  for (int u = t; u < TL::BM; u += 256) {
+    s_rx[u] = (NORM && m0 + u < N) ? ws[WS_RX * n64 + m0 + u] : 1.f;
+    s_row[u] = 0.f;
+  }
+  for (int u = t; u < TL::BN; u += 256) {
     s_ry[u] = (NORM && n0 + u < N) ? ws[WS_RY * n64 + n0 + u] : 1.f;
     s_col[u] = 0.f;
   }
   __syncthreads();
 
-  float rowv[32];
-  float colv[2] = {0.f, 0.f};
+  float rowv[TL::FM * 16];
+  float colv[TL::FN];
   // interior tiles (no diagonal entry, no row or column beyond N) need no mask
-  if (m0 != n0 && m0 + 128 <= N && n0 + 128 <= N)
-    sumexp_epilogue<NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
+  const bool diag = m0 < n0 + TL::BN && n0 < m0 + TL::BM;
+  if (!diag && m0 + TL::BM <= N && n0 + TL::BN <= N)
+    sumexp_epilogue<TL, NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
   else
-    sumexp_epilogue<NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
+    sumexp_epilogue<TL, NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
   const float rs = transpose_reduce32(rowv, lane);
   {
     const int q = lane & 31;
-    const int ml = wm * 64 + (q >> 4) * 32 + acc_row(q & 15, lane);
+    const int ml = wm * TL::TM + (q >> 4) * 32 + acc_row(q & 15, lane);
     __hip_atomic_fetch_add(&s_row[ml], rs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   if (!LIT) {
 #pragma unroll
-    for (int bn = 0; bn < 2; ++bn) {
+    for (int bn = 0; bn < TL::FN; ++bn) {
       colv[bn] += __shfl_xor(colv[bn], 32, 64);
       if (lane < 32)
-        __hip_atomic_fetch_add(&s_col[wn * 64 + bn * 32 + lane], colv[bn], __ATOMIC_RELAXED,
+        __hip_atomic_fetch_add(&s_col[wn * TL::TN + bn * 32 + lane], colv[bn], __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
   __syncthreads();
-  if (t < 128) {
-    if (m0 + t < N)
-      __hip_atomic_fetch_add(&ws[WS_ROW_OFF * n64 + m0 + t], s_row[t], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-  } else if (!LIT) {
-    const int u = t - 128;
-    if (n0 + u < N)
-      __hip_atomic_fetch_add(&ws[WS_COL_OFF * n64 + n0 + u], s_col[u], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+  for (int u = t; u < TL::BM; u += 256)
+    if (m0 + u < N)
+      __hip_atomic_fetch_add(&ws[WS_ROW_OFF * n64 + m0 + u], s_row[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (!LIT) {
+    for (int u = t; u < TL::BN; u += 256)
+      if (n0 + u < N)
+        __hip_atomic_fetch_add(&ws[WS_COL_OFF * n64 + n0 + u], s_col[u], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 // ---------------------------------------------------------------- backward
 // Block decomposition of the N x N gradient matrix: nb blocks of bs rows
-// (bs a multiple of 128; the last block may be short).  Diagonal s pairs block
-// I with block J = (I + s) mod nb, so one diagonal touches every block row and
-// every block column exactly once.
+// (bs a multiple of block_quantum; the last block may be short).  Diagonal s
+// pairs block I with block J = (I + s) mod nb, so one diagonal touches every
+// block row and every block column exactly once.
 struct BlockGrid {
-  int bs;   // block size (rows), multiple of 128
-  int nb;   // number of blocks (= number of diagonals)
-  int tpb;  // 128-tiles per block side = bs / 128
+  int bs;    // block size (rows)
+  int nb;    // number of blocks (= number of diagonals)
+  int gtm;   // gradient-matrix tiles per block, row direction (bs / BM)
+  int gtn;   // gradient-matrix tiles per block, column direction (bs / BN)
+  int ctm;   // contraction tiles per block, row direction (bs / BM of the contraction)
+  int ctd;   // contraction tiles over the features (ceil(D / BN of the contraction))
 };
 
 // Scratch of the backward (all in the input dtype T, row-major):
 //   G[2]   two buffers of nb blocks of bs x bs: block I of buffer s&1 holds
-//          G'(I, (I+s) mod nb) of diagonal s;
-//   GT[2]  the same blocks transposed (CLIP only);
+//          G'(I, (I+s) mod nb) of diagonal s (fp32 only);
+//   GT[2]  the same blocks transposed (fp32: CLIP only; bf16: always, the
+//          only copy);
 //   XT, YT the normalised inputs transposed, [D][ldt] with ldt = N rounded
 //          up to 128 and zero columns [N, ldt): element (d, i) = rx_i x_i[d].
 // Every contraction operand is then K-major (k contiguous).
@@ -192,48 +253,98 @@ struct StepPlan {
   int diag_g;        // diagonal whose G' this launch writes (-1: none)
   int diag_c;        // diagonal this launch contracts (-1: none)
   int accumulate;    // contraction adds to the accumulators (else overwrites)
-  int g_n, g_pad;    // G' tiles (nb * tpb * tpb or 0), padded to a multiple of 8
-  int cx_n, cx_pad;  // x-side contraction tiles (nb * tpb * ceil(D/128) or 0), padded
+  int g_n, g_pad;    // G' tiles (nb * gtm * gtn or 0), padded to a multiple of 8
+  int cx_n, cx_pad;  // x-side contraction tiles (nb * ctm * ctd or 0), padded
   int cy_n, cy_pad;  // y-side contraction tiles, padded
 };
 
-// G'_ij of this wave's 64x64 accumulators into Gb (and GTb for CLIP).  MASK
-// zeroes the diagonal and entries outside [0, N).
-template <typename T, bool LIT, bool NORM, bool MASK>
-__device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[2][2], float c, int i0, int j0, int N,
-                                             T* __restrict__ Gb, T* __restrict__ GTb, int bs, const float* s_rx,
-                                             const float* s_ry, const float* s_ir, const float* s_ic) {
-  using C = CoreBwd<T>;
+// G'_ij of this wave's TM x TN accumulators into Gb (and GTb for CLIP), both
+// with row pitch bs.  MASK zeroes the diagonal and entries outside [0, N).
+template <class TL, bool LIT, bool NORM, bool MASK>
+__device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0, int N,
+                                             typename TL::Elem* __restrict__ Gb, typename TL::Elem* __restrict__ GTb,
+                                             int bs, const float* s_rx, const float* s_ry, const float* s_ir,
+                                             const float* s_ic) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
 #pragma unroll
-  for (int bm = 0; bm < 2; ++bm) {
+  for (int bm = 0; bm < TL::FM; ++bm) {
 #pragma unroll
-    for (int bn = 0; bn < 2; ++bn) {
-      const int nl = wn * 64 + bn * 32 + (lane & 31);
+    for (int bn = 0; bn < TL::FN; ++bn) {
+      const int nl = wn * TL::TN + bn * 32 + (lane & 31);
       const int j = j0 + nl;
       const float cy = NORM ? c * s_ry[nl] : c;
       const float icj = s_ic[nl];
       float gv[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int ml = wm * 64 + bm * 32 + acc_row(r, lane);
+        const int ml = wm * TL::TM + bm * 32 + acc_row(r, lane);
         const int i = i0 + ml;
         const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
         const float e = fast_exp2(fmaf(sc, cy, -c));
         float g = LIT ? e * s_ir[ml] : e * (s_ir[ml] + icj);
         if (MASK) g = (i < N && j < N && i != j) ? g : 0.f;
         gv[r] = g;
-        Gb[(int64_t)ml * bs + nl] = C::pack(g);
+        Gb[(int64_t)ml * bs + nl] = TL::pack(g);
       }
       if (!LIT) {
         // registers 4g..4g+3 hold 4 consecutive rows: one vector store per group
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int ml = wm * 64 + bm * 32 + acc_row(4 * g, lane);
-          C::store4(GTb + (int64_t)nl * bs + ml, gv[4 * g], gv[4 * g + 1], gv[4 * g + 2], gv[4 * g + 3]);
+          const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g, lane);
+          TL::store4(GTb + (int64_t)nl * bs + ml, gv[4 * g], gv[4 * g + 1], gv[4 * g + 2], gv[4 * g + 3]);
         }
       }
     }
+  }
+}
+
+// bf16: G'_ij of this wave's TM x TN accumulators, staged through LDS as
+// [j][i] (row pitch GT_PITCH bytes; 4 consecutive i per 8-byte write), then
+// written to GTb (row pitch bs) as whole 256-byte tile rows, 16 bytes per
+// lane.  MASK zeroes the diagonal and entries outside [0, N).  Every row of
+// the tile is written (zeros for j >= N), so the contractions may read a
+// tile's rows and columns past N as zeros.  lds must hold BN * GT_PITCH bytes
+// and be free (no wave still reading it).
+constexpr int GT_PITCH = 272;
+template <class TL, bool LIT, bool NORM, bool MASK>
+__device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0, int N,
+                                                  uint16_t* __restrict__ GTb, int bs, const float* s_rx,
+                                                  const float* s_ry, const float* s_ir, const float* s_ic,
+                                                  char* lds) {
+  static_assert(TL::BM * 2 + 16 <= GT_PITCH && GT_PITCH % 16 == 0, "tile row fits the pitch");
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+#pragma unroll
+  for (int bm = 0; bm < TL::FM; ++bm) {
+#pragma unroll
+    for (int bn = 0; bn < TL::FN; ++bn) {
+      const int nl = wn * TL::TN + bn * 32 + (lane & 31);
+      const int j = j0 + nl;
+      const float cy = NORM ? c * s_ry[nl] : c;
+      const float icj = s_ic[nl];
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        float gv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g4 + e;
+          const int ml = wm * TL::TM + bm * 32 + acc_row(r, lane);
+          const int i = i0 + ml;
+          const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
+          const float ex = fast_exp2(fmaf(sc, cy, -c));
+          float g = LIT ? ex * s_ir[ml] : ex * (s_ir[ml] + icj);
+          if (MASK) g = (i < N && j < N && i != j) ? g : 0.f;
+          gv[e] = g;
+        }
+        const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g4, lane);
+        PackBf16::store4((uint16_t*)(lds + nl * GT_PITCH + ml * 2), gv[0], gv[1], gv[2], gv[3]);
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int VPR = TL::BM * 2 / 16;  // 16-byte vectors per tile row
+  for (int v = threadIdx.x; v < TL::BN * VPR; v += 256) {
+    const int row = v / VPR, cv = v - row * VPR;
+    *(i16x8*)(GTb + (int64_t)row * bs + cv * 8) = *(const i16x8*)(lds + row * GT_PITCH + cv * 16);
   }
 }
 
@@ -241,67 +352,77 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[2][2], float c,
 // (LiT: E_ij / R_i) for i != j, 0 on the diagonal and outside [0, N), into
 // the G' block at Gb (row pitch bs) and, for CLIP, transposed at GTb.
 // Follows clip_loss.py:96-124 / lit_loss.py:94-120.
-template <typename T, bool LIT, bool NORM, bool VEC>
+template <class TL, typename T, bool LIT, bool NORM, bool VEC>
 __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y,
-                                            int64_t ldy, int N, int D, float c, const float* __restrict__ ws,
+                                            int64_t ldy, int N, int D, int kmax, float c, const float* __restrict__ ws,
                                             T* __restrict__ Gb, T* __restrict__ GTb, int bs, int i0, int j0,
                                             char* lds, float* s_rx, float* s_ry, float* s_ir, float* s_ic) {
-  using C = CoreBwd<T>;
   const int64_t n64 = N;
   const int t = threadIdx.x;
-  typename C::Op A{X + (int64_t)i0 * ldx, ldx, N - i0, D};
-  typename C::Op B{Y + (int64_t)j0 * ldy, ldy, N - j0, D};
-  f32x16 acc[2][2];
-  C::template run<VEC, VEC>(A, B, D, lds, acc);
-  if (t < 128) {
-    const bool ok = i0 + t < N;
-    s_rx[t] = (NORM && ok) ? ws[WS_RX * n64 + i0 + t] : 1.f;
-    s_ir[t] = ok ? ws[WS_INV_ROW * n64 + i0 + t] : 0.f;
-  } else {
-    const int u = t - 128;
+  typename TL::Op A{X + (int64_t)i0 * ldx, ldx, min(N - i0, TL::BM), kmax};
+  typename TL::Op B{Y + (int64_t)j0 * ldy, ldy, min(N - j0, TL::BN), kmax};
+  f32x16 acc[TL::FM][TL::FN];
+  TL::template run<VEC, VEC>(A, B, D, lds, acc);
+  for (int u = t; u < TL::BM; u += 256) {
+    const bool ok = i0 + u < N;
+    s_rx[u] = (NORM && ok) ? ws[WS_RX * n64 + i0 + u] : 1.f;
+    s_ir[u] = ok ? ws[WS_INV_ROW * n64 + i0 + u] : 0.f;
+  }
+  for (int u = t; u < TL::BN; u += 256) {
     const bool ok = j0 + u < N;
     s_ry[u] = (NORM && ok) ? ws[WS_RY * n64 + j0 + u] : 1.f;
     s_ic[u] = (!LIT && ok) ? ws[WS_INV_COL * n64 + j0 + u] : 0.f;
   }
   __syncthreads();
-  if (i0 != j0 && i0 + 128 <= N && j0 + 128 <= N)
-    grad_g_store<T, LIT, NORM, false>(acc, c, i0, j0, N, Gb, GTb, bs, s_rx, s_ry, s_ir, s_ic);
-  else
-    grad_g_store<T, LIT, NORM, true>(acc, c, i0, j0, N, Gb, GTb, bs, s_rx, s_ry, s_ir, s_ic);
+  const bool diag = i0 < j0 + TL::BN && j0 < i0 + TL::BM;
+  if constexpr (GtOnly<T>::value) {
+    if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
+      grad_gt_store_lds<TL, LIT, NORM, false>(acc, c, i0, j0, N, (uint16_t*)GTb, bs, s_rx, s_ry, s_ir, s_ic, lds);
+    else
+      grad_gt_store_lds<TL, LIT, NORM, true>(acc, c, i0, j0, N, (uint16_t*)GTb, bs, s_rx, s_ry, s_ir, s_ic, lds);
+  } else {
+    if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
+      grad_g_store<TL, LIT, NORM, false>(acc, c, i0, j0, N, Gb, GTb, bs, s_rx, s_ry, s_ir, s_ic);
+    else
+      grad_g_store<TL, LIT, NORM, true>(acc, c, i0, j0, N, Gb, GTb, bs, s_rx, s_ry, s_ir, s_ic);
+  }
 }
 
-// One 128 x 128 output tile of a contraction: rows r0.. of block P, feature
+// One BM x BN output tile of a contraction: rows r0.. of block P, feature
 // columns d0..:
 //   x side: acc_x[i, d] (+)= sum_{j in Q} G'(P,Q)[i, j]  * YT[d, j]   (Q = P + s)
+//           (bf16: G'(P,Q)[i, j] read from the transposed block G'T(P,Q)[j, i])
 //   y side: acc_y[j, d] (+)= sum_{i in Q} G'T(Q,P)[j, i] * XT[d, i]   (Q = P - s)
 // Each output tile has one owner per launch: accumulation across launches
 // adds each element once per launch, in launch order (the reference instead
 // lets every (row-tile, column-tile) program add into dX/dY with contending
 // atomics, clip_loss.py:148-156).
-template <typename T>
+template <class TC, typename T>
 __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __restrict__ Gblk,
                                                    const T* __restrict__ OT, int64_t ldt, const BlockGrid& bg,
                                                    int P, int Q, int tm, int td, bool accumulate,
                                                    float* __restrict__ out, char* lds) {
-  using C = CoreBwd<T>;
-  const int r0 = P * bg.bs + tm * 128;
+  const int r0 = P * bg.bs + tm * TC::BM;
   if (r0 >= N) return;
-  const int d0 = td * 128;
+  const int d0 = td * TC::BN;
   const int q0 = Q * bg.bs;
   const int qn = min(bg.bs, N - q0);
-  typename C::Op A{Gblk + (int64_t)(tm * 128) * bg.bs, bg.bs, 128, qn};
-  typename C::Op B{OT + (int64_t)d0 * ldt + q0, ldt, D - d0, qn};
-  f32x16 acc[2][2];
-  C::template run<true, true>(A, B, qn, lds, acc);
+  // entries of G' and XT/YT at k in [qn, round8(qn)) are stored zeros
+  const int kq = (qn + 7) & ~7;
+  // A: rows tm*BM.. of the block (K-major), or columns tm*BM.. of a transposed block
+  typename TC::Op A{Gblk + (TC::TA ? (int64_t)(tm * TC::BM) : (int64_t)(tm * TC::BM) * bg.bs), bg.bs, TC::BM, kq};
+  typename TC::Op B{OT + (int64_t)d0 * ldt + q0, ldt, min(D - d0, TC::BN), kq};
+  f32x16 acc[TC::FM][TC::FN];
+  TC::template run<true, true>(A, B, kq, lds, acc);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
 #pragma unroll
-  for (int bm = 0; bm < 2; ++bm) {
+  for (int bm = 0; bm < TC::FM; ++bm) {
 #pragma unroll
-    for (int bn = 0; bn < 2; ++bn) {
-      const int d = d0 + wn * 64 + bn * 32 + (lane & 31);
+    for (int bn = 0; bn < TC::FN; ++bn) {
+      const int d = d0 + wn * TC::TN + bn * 32 + (lane & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = r0 + wm * 64 + bm * 32 + acc_row(r, lane);
+        const int row = r0 + wm * TC::TM + bm * 32 + acc_row(r, lane);
         if (row < N && d < D) {
           float* p = out + (int64_t)row * D + d;
           // a fire-and-forget add in L2 instead of a load-add-store round trip;
@@ -318,15 +439,19 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
 }
 
 template <typename T, bool LIT, bool NORM, bool VEC>
-__global__ __launch_bounds__(256, 3) void k_grad_step(const T* __restrict__ X, int64_t ldx,
-                                                      const T* __restrict__ Y, int64_t ldy, int N, int D,
-                                                      float c, const float* __restrict__ ws, GradBufs gb,
-                                                      BlockGrid bg, StepPlan sp, float* __restrict__ acc_x,
-                                                      float* __restrict__ acc_y) {
-  using C = CoreBwd<T>;
-  __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
-  __shared__ float s_rx[128], s_ry[128], s_ir[128], s_ic[128];
-  const int tdn = (D + 127) / 128;
+__global__ __launch_bounds__(256, Occ<T>::bwd) void k_grad_step(const T* __restrict__ X, int64_t ldx,
+                                                               const T* __restrict__ Y, int64_t ldy, int N, int D,
+                                                               int kmax, float c, const float* __restrict__ ws,
+                                                               GradBufs gb, BlockGrid bg, StepPlan sp,
+                                                               float* __restrict__ acc_x, float* __restrict__ acc_y) {
+  using TF = FwdTile<T, VEC>;
+  using TCX = ConTileX<T>;
+  using TCY = ConTileY<T>;
+  static_assert(TCX::BM == TCY::BM && TCX::BN == TCY::BN, "one contraction tile shape");
+  constexpr int GT_LDS = GtOnly<T>::value ? TF::BN * GT_PITCH : 0;
+  __shared__ __attribute__((aligned(1024)))
+  char lds[CMax<CMax<TF::LDS_BYTES, GT_LDS>::value, CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value>::value];
+  __shared__ float s_rx[TF::BM], s_ry[TF::BN], s_ir[TF::BM], s_ic[TF::BN];
   const int64_t blk = (int64_t)bg.bs * bg.bs;  // elements per G' block
   int sub = blockIdx.x;
   if (sub < sp.cx_pad + sp.cy_pad) {
@@ -335,17 +460,18 @@ __global__ __launch_bounds__(256, 3) void k_grad_step(const T* __restrict__ X, i
     const int pid = xcd_remap(sub, is_x ? sp.cx_pad : sp.cy_pad);
     if (pid >= (is_x ? sp.cx_n : sp.cy_n)) return;
     int tmg, td;
-    group_tile(pid, bg.nb * bg.tpb, tdn, 8, tmg, td);
-    const int P = tmg / bg.tpb, tm = tmg - P * bg.tpb;  // P: block owning the output rows
+    group_tile(pid, bg.nb * bg.ctm, bg.ctd, 8, tmg, td);
+    const int P = tmg / bg.ctm, tm = tmg - P * bg.ctm;  // P: block owning the output rows
     const int buf = sp.diag_c & 1;
     if (is_x) {
       const int Q = (P + sp.diag_c) % bg.nb;
-      grad_contract_tile<T>(N, D, (const T*)gb.g[buf] + P * blk, (const T*)gb.yt, gb.ldt, bg, P, Q, tm, td,
-                            sp.accumulate != 0, acc_x, lds);
+      const T* gx = (const T*)(GtOnly<T>::value ? gb.gt[buf] : gb.g[buf]) + P * blk;
+      grad_contract_tile<TCX, T>(N, D, gx, (const T*)gb.yt, gb.ldt, bg, P, Q, tm, td, sp.accumulate != 0, acc_x,
+                                 lds);
     } else {
       const int Q = (P - sp.diag_c + bg.nb) % bg.nb;
-      grad_contract_tile<T>(N, D, (const T*)gb.gt[buf] + Q * blk, (const T*)gb.xt, gb.ldt, bg, P, Q, tm, td,
-                            sp.accumulate != 0, acc_y, lds);
+      grad_contract_tile<TCY, T>(N, D, (const T*)gb.gt[buf] + Q * blk, (const T*)gb.xt, gb.ldt, bg, P, Q, tm, td,
+                                 sp.accumulate != 0, acc_y, lds);
     }
     return;
   }
@@ -353,16 +479,17 @@ __global__ __launch_bounds__(256, 3) void k_grad_step(const T* __restrict__ X, i
   const int pid = xcd_remap(sub, sp.g_pad);
   if (pid >= sp.g_n) return;
   int tmg, tn;
-  group_tile(pid, bg.nb * bg.tpb, bg.tpb, 8, tmg, tn);
-  const int I = tmg / bg.tpb, tm = tmg - I * bg.tpb;
+  group_tile(pid, bg.nb * bg.gtm, bg.gtn, 8, tmg, tn);
+  const int I = tmg / bg.gtm, tm = tmg - I * bg.gtm;
   const int J = (I + sp.diag_g) % bg.nb;
-  const int i0 = I * bg.bs + tm * 128, j0 = J * bg.bs + tn * 128;
+  const int i0 = I * bg.bs + tm * TF::BM, j0 = J * bg.bs + tn * TF::BN;
   if (i0 >= N || j0 >= N) return;  // never read by the contraction
   const int buf = sp.diag_g & 1;
-  T* Gb = (T*)gb.g[buf] + I * blk + (int64_t)(tm * 128) * bg.bs + tn * 128;
-  T* GTb = LIT ? nullptr : (T*)gb.gt[buf] + I * blk + (int64_t)(tn * 128) * bg.bs + tm * 128;
-  grad_g_tile<T, LIT, NORM, VEC>(X, ldx, Y, ldy, N, D, c, ws, Gb, GTb, bg.bs, i0, j0, lds, s_rx, s_ry, s_ir,
-                                 s_ic);
+  T* Gb = GtOnly<T>::value ? nullptr : (T*)gb.g[buf] + I * blk + (int64_t)(tm * TF::BM) * bg.bs + tn * TF::BN;
+  T* GTb = (LIT && !GtOnly<T>::value) ? nullptr
+                                      : (T*)gb.gt[buf] + I * blk + (int64_t)(tn * TF::BN) * bg.bs + tm * TF::BM;
+  grad_g_tile<TF, T, LIT, NORM, VEC>(X, ldx, Y, ldy, N, D, kmax, c, ws, Gb, GTb, bg.bs, i0, j0, lds, s_rx, s_ry,
+                                     s_ir, s_ic);
 }
 
 }  // namespace mec

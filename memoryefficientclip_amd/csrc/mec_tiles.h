@@ -1,0 +1,39 @@
+// Tile geometry of the MFMA kernels, shared by host and device code.
+//
+//   fp32                      128 x 128 tiles everywhere (mec_gemm_f32.h)
+//   bf16, 16-byte vectors     forward sums and gradient-matrix tiles 128 x 256
+//                             (x rows x y rows), contractions 256 x 128
+//                             (output rows x feature columns), direct
+//                             global->LDS loads (mec_gemm_bf16_dma.h)
+//   bf16, other layouts       forward sums and gradient-matrix tiles 128 x 128
+//                             staged through registers (mec_gemm_bf16.h);
+//                             the contractions read internal buffers, which
+//                             are always 16-byte vectors, so they keep 256 x 128
+//
+// The backward's block decomposition uses blocks of a multiple of
+// block_quantum(dtype) rows, so that every tile kind divides a block.
+#pragma once
+#include <stdint.h>
+
+namespace mec {
+
+struct TileDims {
+  int bm, bn;
+};
+
+constexpr int kDtypeF32 = 0;
+constexpr int kDtypeBF16 = 1;
+
+// forward sums and gradient-matrix tiles (x rows x y rows)
+inline TileDims fwd_tile_dims(int dtype, bool vec) {
+  if (dtype == kDtypeF32) return {128, 128};
+  return vec ? TileDims{128, 256} : TileDims{128, 128};
+}
+// contraction tiles (output rows x feature columns)
+inline TileDims con_tile_dims(int dtype) {
+  if (dtype == kDtypeF32) return {128, 128};
+  return {256, 128};
+}
+inline int block_quantum(int dtype) { return dtype == kDtypeF32 ? 128 : 256; }
+
+}  // namespace mec

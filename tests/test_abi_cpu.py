@@ -36,28 +36,33 @@ def test_sizes():
     lib = _lib.load()
     assert lib.mec_workspace_floats(1000) == 8000
     assert lib.mec_workspace_floats(0) < 0
-    # scratch is O(n*d): two block diagonals of the N x N gradient matrix, in
-    # both layouts, plus transposed copies of the two inputs
+    # scratch is O(n*d): two block diagonals of the N x N gradient matrix (fp32:
+    # in both layouts; bf16: transposed only), plus transposed copies of the two
+    # inputs; blocks are a multiple of 128 rows (fp32) or 256 rows (bf16: its
+    # tiles are 128 x 256 and 256 x 128)
     for n, d in [(1024, 512), (32768, 1152), (65536, 768), (262144, 1152), (1000, 3), (777, 1152)]:
-        b32 = lib.mec_grad_scratch_bytes(n, d, 0)
-        b16 = lib.mec_grad_scratch_bytes(n, d, 1)
-        assert b32 == 2 * b16 > 0
-        bs, nb = _lib.grad_blocking(n, d, 0)
-        assert bs % 128 == 0 and nb * bs >= n > (nb - 1) * bs
-        ldt = (n + 127) // 128 * 128
-        assert b32 == (4 * nb * bs * bs + 2 * d * ldt) * 4
-        bs_max = 2 * max(1024, 2 * d + 128)
-        assert bs <= bs_max and b32 <= 4 * (4 * (n + bs_max) * bs_max + 2 * d * (n + 128)), (n, d, b32)
+        for dt, elem, q, copies in [(0, 4, 128, 4), (1, 2, 256, 2)]:
+            b = lib.mec_grad_scratch_bytes(n, d, dt)
+            bs, nb = _lib.grad_blocking(n, d, dt)
+            assert bs % q == 0 and nb * bs >= n > (nb - 1) * bs, (n, d, dt, bs, nb)
+            ldt = (n + 127) // 128 * 128
+            assert b == (copies * nb * bs * bs + 2 * d * ldt) * elem, (n, d, dt)
+            bs_max = 2 * max(1024, 2 * d + q)
+            assert bs <= bs_max and b <= elem * (4 * (n + bs_max) * bs_max + 2 * d * (n + 128)), (n, d, dt, b)
     assert lib.mec_grad_scratch_bytes(10, 10, 7) < 0
 
 
 def test_blocking_prefers_exact_divisors():
     # the headline and bf16 shapes split into equal blocks (no short last block)
     for n, d in [(32768, 1152), (65536, 768), (262144, 1152), (1024, 512)]:
-        bs, nb = _lib.grad_blocking(n, d, 0)
-        assert nb * bs == n, (n, d, bs, nb)
+        for dt in (0, 1):
+            bs, nb = _lib.grad_blocking(n, d, dt)
+            assert nb * bs == n, (n, d, dt, bs, nb)
     assert _lib.grad_blocking(32768, 1152, 0) == (2048, 16)
+    assert _lib.grad_blocking(65536, 768, 1) == (2048, 32)
+    assert _lib.grad_blocking(262144, 1152, 1) == (2048, 128)
     assert _lib.grad_blocking(1000, 64, 0) == (1024, 1)
+    assert _lib.grad_blocking(1000, 64, 1) == (1024, 1)
 
 
 VALID = dict(x=16, ldx=64, y=16, ldy=64, n=10, d=64, dtype=0, mode=0, normalize=1, temperature=0.07)
