@@ -460,7 +460,15 @@ __global__ __launch_bounds__(256, Occ<T>::bwd) void k_grad_step(const T* __restr
     const int pid = xcd_remap(sub, is_x ? sp.cx_pad : sp.cy_pad);
     if (pid >= (is_x ? sp.cx_n : sp.cy_n)) return;
     int tmg, td;
-    group_tile(pid, bg.nb * bg.ctm, bg.ctd, 8, tmg, td);
+    if constexpr (GtOnly<T>::value) {
+      // bf16: feature tiles fastest, so the tiles sharing one gradient-matrix
+      // panel run side by side on one XCD and the panel is fetched from HBM
+      // about once (its contractions are bound by that traffic)
+      tmg = pid / bg.ctd;
+      td = pid - tmg * bg.ctd;
+    } else {
+      group_tile(pid, bg.nb * bg.ctm, bg.ctd, 8, tmg, td);
+    }
     const int P = tmg / bg.ctm, tm = tmg - P * bg.ctm;  // P: block owning the output rows
     const int buf = sp.diag_c & 1;
     if (is_x) {
