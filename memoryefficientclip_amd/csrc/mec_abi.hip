@@ -304,8 +304,17 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
   sp.g_pad = round8(sp.g_n);
   sp.cx_pad = round8(sp.cx_n);
   sp.cy_pad = round8(sp.cy_n);
-  const int64_t grid = (int64_t)sp.g_pad + sp.cx_pad + sp.cy_pad;
-  if (grid > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "backward grid too large");
+  // bf16: the contractions of diagonal t-1 run in k_grad_contract, before the
+  // G' tiles of diagonal t (different scratch buffers, so either order works)
+  const bool split = separate_contractions(dtype);
+  StepPlan sp_g = sp, sp_c = sp;
+  if (split) {
+    sp_g.cx_n = sp_g.cy_n = sp_g.cx_pad = sp_g.cy_pad = 0;
+    sp_c.g_n = sp_c.g_pad = 0;
+  }
+  const int64_t grid = split ? (int64_t)sp.g_pad : (int64_t)sp.g_pad + sp.cx_pad + sp.cy_pad;
+  const int64_t grid_c = split ? (int64_t)sp.cx_pad + sp.cy_pad : 0;
+  if (grid > 0x7fffffff || grid_c > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "backward grid too large");
   char* base = (char*)scratch;
   GradBufs gb;
   if (L.ncopies == 4) {
@@ -353,9 +362,18 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
         k_grad_step<float, LIT, NORM, VEC><<<(unsigned)grid, 256, 0, s>>>(
             (const float*)x, ldx, (const float*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y))));
   } else {
-    DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-        k_grad_step<uint16_t, LIT, NORM, VEC><<<(unsigned)grid, 256, 0, s>>>(
-            (const uint16_t*)x, ldx, (const uint16_t*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y))));
+    if (grid_c > 0) {
+      k_grad_contract<uint16_t><<<(unsigned)grid_c, ConTileX<uint16_t>::NT, 0, s>>>(N, D, gb, bg, sp_c, acc_x,
+                                                                                    acc_y);
+      rc = check_launch("grad_contract");
+      if (rc) return rc;
+    }
+    if (grid > 0) {
+      DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
+          k_grad_step<uint16_t, LIT, NORM, VEC><<<(unsigned)grid, 256, 0, s>>>(
+              (const uint16_t*)x, ldx, (const uint16_t*)y, ldy, N, D, D, c, workspace, gb, bg, sp_g, acc_x,
+              acc_y))));
+    }
   }
   return check_launch("grad_step");
 }

@@ -28,14 +28,16 @@ enum WsSlot {
   WS_INV_ROW = 5, WS_INV_COL = 6, WS_KAPPA = 7, WS_NSLOTS = 8
 };
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
-// round-to-nearest-even fp32 -> bf16 (inputs here are finite)
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  uint32_t r = 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)((u + r) >> 16);
+// fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32 on gfx950)
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+// two values in one dword, a in the low half
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)a, (__bf16)b});
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

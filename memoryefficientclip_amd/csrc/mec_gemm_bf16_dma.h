@@ -1,11 +1,13 @@
 // bf16 MFMA tile core for gfx950 with direct global->LDS loads.
 //
-// Geometry: a BM x BN output tile per 256-thread workgroup, 4 waves in 2x2,
-// each wave a (BM/2) x (BN/2) sub-tile of v_mfma_f32_32x32x16_bf16 blocks
-// (fp32 accumulate).  Two workgroups share a CU (72 KB of LDS each), so one
+// Geometry: a BM x BN output tile per workgroup of WM x WN waves, each wave a
+// (BM/WM) x (BN/WN) sub-tile of v_mfma_f32_32x32x16_bf16 blocks (fp32
+// accumulate).  The forward and gradient-matrix tiles are 128 x 256 with
+// 2 x 2 waves: two workgroups share a CU (72 KB of LDS each), so one
 // workgroup's epilogue (exp, reductions, stores) runs while the other's MFMAs
-// do: the forward and gradient-matrix tiles are 128 x 256, the contractions
-// 256 x 128.
+// do.  The contractions, whose epilogue is a few atomics, are 256 x 256 with
+// 4 x 2 waves, one workgroup per CU: fewer operand bytes per MFMA through the
+// global->LDS path (≈64 B/clk per CU), which bounds these kernels.
 //
 // Operands are K-major (element (row, k) at base[row * ld + k]).  K is staged
 // in chunks of BK = 32 through a ring of S = 3 LDS stages ([row][32] bf16, 64
@@ -45,26 +47,27 @@ namespace g16d {
 
 constexpr int BK = 32;            // k per chunk
 constexpr int S = 3;              // LDS stages
-constexpr int NT = 256;           // threads (4 waves, 2 x 2)
 constexpr int ROWB = BK * 2;      // bytes per staged row
 constexpr int RPB = 16;           // rows per 1 KB load block
 constexpr int NS = BK / 16;       // MFMA k-steps per chunk
 constexpr uint32_t OOB = 0x80000000u;  // buffer offset that reads as zero
 
-template <int BM_, int BN_, bool TA_ = false>
+template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_;
   static constexpr bool TA = TA_;                      // A stored k-row-major
   static_assert(!TA || BM == 256, "transposed A: 512-byte k-rows (BM = 256)");
-  static constexpr int TM = BM / 2, TN = BN / 2;       // wave sub-tile
+  static constexpr int WM = WM_, WN = WN_, NW = WM * WN, NT = 64 * NW;
+  static constexpr int TM = BM / WM, TN = BN / WN;     // wave sub-tile
   static constexpr int FM = TM / 32, FN = TN / 32;     // 32x32 MFMA blocks per wave
   static constexpr int ROWS = BM + BN;
   static constexpr int STAGE = ROWS * ROWB;
   static constexpr int LDS_BYTES = S * STAGE;
-  static constexpr int IPW = ROWS / RPB / 4;           // load instructions per wave per chunk
+  static constexpr int IPW = ROWS / RPB / NW;          // load instructions per wave per chunk
   static constexpr int NMF = FM * FN;                  // MFMAs per k-step
   static constexpr int LPS = (IPW + NS - 1) / NS;      // loads interleaved per k-step
-  static_assert(ROWS % (RPB * 4) == 0 && BM % RPB == 0, "load split");
+  static_assert(ROWS % (RPB * NW) == 0 && BM % RPB == 0, "load split");
+  static_assert(TM % 32 == 0 && TN % 32 == 0, "wave sub-tile of 32x32 blocks");
 };
 
 struct Operand {
@@ -159,7 +162,7 @@ __device__ __forceinline__ i16x4_t read_tr4(const char* p) {
 template <class G>
 __device__ __forceinline__ void read_frags(const char* stage, int s, Frags<G>& f) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / G::WN, wn = w % G::WN;
   const int q = lane & 31, h = lane >> 5;
   const int off = (((h * NS + s) ^ swz(q)) << 4);
   if (G::TA) {

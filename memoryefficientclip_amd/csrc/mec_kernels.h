@@ -16,6 +16,8 @@
 //                       contractions without contending atomics
 //                       (clip_loss.py:127-156, lit_loss.py:123-148).
 #pragma once
+#include <type_traits>
+
 #include "mec_gemm_f32.h"
 #include "mec_gemm_bf16.h"
 #include "mec_gemm_bf16_dma.h"
@@ -24,8 +26,8 @@
 namespace mec {
 
 // ------------------------------------------------------------ tile configs
-// Every config: BM x BN output tile per 256-thread workgroup, 4 waves in 2 x 2,
-// each wave a TM x TN sub-tile of FM x FN 32x32 MFMA blocks whose
+// Every config: BM x BN output tile per workgroup of WM x WN waves (NT
+// threads), each wave a TM x TN sub-tile of FM x FN 32x32 MFMA blocks whose
 // accumulator register r of lane l holds element (acc_row(r, l), l % 32).
 #ifndef MEC_BF16_BK_FWD
 #define MEC_BF16_BK_FWD 64
@@ -36,7 +38,7 @@ struct TileF32 {
   using Elem = float;
   using Op = g32::Operand;
   static constexpr bool TA = false;
-  static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2;
+  static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2, WM = 2, WN = 2, NT = 256;
   static constexpr int LDS_BYTES = g32::LDS_FLOATS * 4;
   template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
@@ -51,10 +53,7 @@ struct TileF32 {
 struct PackBf16 {
   static __device__ __forceinline__ uint16_t pack(float v) { return f32_to_bf16(v); }
   static __device__ __forceinline__ void store4(uint16_t* p, float a, float b, float c, float d) {
-    uint2 u;
-    u.x = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
-    u.y = (uint32_t)f32_to_bf16(c) | ((uint32_t)f32_to_bf16(d) << 16);
-    *(uint2*)p = u;
+    *(uint2*)p = uint2{pack2_bf16(a, b), pack2_bf16(c, d)};
   }
 };
 
@@ -63,7 +62,7 @@ struct TileB16V : PackBf16 {
   using Elem = uint16_t;
   using Op = g16::Operand;
   static constexpr bool TA = false;
-  static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2;
+  static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2, WM = 2, WN = 2, NT = 256;
   static constexpr int LDS_BYTES = g16::Cfg<MEC_BF16_BK_FWD>::LDS_ELEMS * 2;
   template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
@@ -73,13 +72,14 @@ struct TileB16V : PackBf16 {
 
 // bf16, BM_ x BN_, direct global->LDS loads (16-byte aligned rows, ld and kmax
 // multiples of 8); TA_: A stored k-row-major (a transposed gradient-matrix block)
-template <int BM_, int BN_, bool TA_ = false>
+template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2>
 struct TileB16D : PackBf16 {
   using Elem = uint16_t;
   using Op = g16d::Operand;
-  using G = g16d::Geo<BM_, BN_, TA_>;
+  using G = g16d::Geo<BM_, BN_, TA_, WM_, WN_>;
   static constexpr bool TA = TA_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
+  static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
   static constexpr int LDS_BYTES = G::LDS_BYTES;
   template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
@@ -94,11 +94,16 @@ template <> struct FwdTileSel<uint16_t, true> { using type = TileB16D<128, 256>;
 template <> struct FwdTileSel<uint16_t, false> { using type = TileB16V; };
 template <typename T, bool VEC> using FwdTile = typename FwdTileSel<T, VEC>::type;
 // Contractions.  fp32 stores the gradient-matrix blocks in both layouts (G'
-// for the x side, G'^T for the y side); bf16 stores only G'^T, which the y
-// side reads K-major and the x side reads transposed through LDS.
+// for the x side, G'^T for the y side) and runs them inside k_grad_step; bf16
+// stores only G'^T, which the y side reads K-major and the x side reads
+// transposed through LDS, in a kernel of its own (k_grad_contract) with
+// 256 x 256 tiles of 8 waves.
 template <typename T> struct ConTileSel;
 template <> struct ConTileSel<float> { using x = TileF32; using y = TileF32; };
-template <> struct ConTileSel<uint16_t> { using x = TileB16D<256, 128, true>; using y = TileB16D<256, 128>; };
+template <> struct ConTileSel<uint16_t> {
+  using x = TileB16D<256, 256, true, 4, 2>;
+  using y = TileB16D<256, 256, false, 4, 2>;
+};
 template <typename T> using ConTileX = typename ConTileSel<T>::x;
 template <typename T> using ConTileY = typename ConTileSel<T>::y;
 // bf16 keeps one layout of the gradient-matrix blocks (G'^T)
@@ -154,6 +159,7 @@ __global__ __launch_bounds__(256, Occ<T>::fwd) void k_sumexp(const T* __restrict
                                                             int tiles_n) {
   using TL = FwdTile<T, VEC>;
   static_assert(TL::FM == 2, "row reduction assumes 64-row wave sub-tiles");
+  static_assert(TL::WM == 2 && TL::WN == 2 && TL::NT == 256, "epilogues assume 2 x 2 waves");
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
   __shared__ float s_rx[TL::BM], s_ry[TL::BN], s_row[TL::BM], s_col[TL::BN];
   const int64_t n64 = N;
@@ -305,6 +311,9 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN]
 // the tile is written (zeros for j >= N), so the contractions may read a
 // tile's rows and columns past N as zeros.  lds must hold BN * GT_PITCH bytes
 // and be free (no wave still reading it).
+// The 8-byte chunk c of row j sits at chunk c ^ ((j >> 4) & 1): the 32 lanes
+// of a half-wave write one chunk of 32 consecutive rows, which then fall on
+// 32 distinct bank pairs (rows j and j + 16 would share them at this pitch).
 constexpr int GT_PITCH = 272;
 template <class TL, bool LIT, bool NORM, bool MASK>
 __device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0, int N,
@@ -336,7 +345,8 @@ __device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL
           gv[e] = g;
         }
         const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g4, lane);
-        PackBf16::store4((uint16_t*)(lds + nl * GT_PITCH + ml * 2), gv[0], gv[1], gv[2], gv[3]);
+        const int chunk = (ml >> 2) ^ ((nl >> 4) & 1);
+        PackBf16::store4((uint16_t*)(lds + nl * GT_PITCH + chunk * 8), gv[0], gv[1], gv[2], gv[3]);
       }
     }
   }
@@ -344,7 +354,9 @@ __device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL
   constexpr int VPR = TL::BM * 2 / 16;  // 16-byte vectors per tile row
   for (int v = threadIdx.x; v < TL::BN * VPR; v += 256) {
     const int row = v / VPR, cv = v - row * VPR;
-    *(i16x8*)(GTb + (int64_t)row * bs + cv * 8) = *(const i16x8*)(lds + row * GT_PITCH + cv * 16);
+    uint4 u = *(const uint4*)(lds + row * GT_PITCH + cv * 16);
+    if ((row >> 4) & 1) u = uint4{u.z, u.w, u.x, u.y};  // undo the chunk swizzle
+    *(uint4*)(GTb + (int64_t)row * bs + cv * 8) = u;
   }
 }
 
@@ -414,7 +426,7 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
   typename TC::Op B{OT + (int64_t)d0 * ldt + q0, ldt, min(D - d0, TC::BN), kq};
   f32x16 acc[TC::FM][TC::FN];
   TC::template run<true, true>(A, B, kq, lds, acc);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TC::WN, wn = w % TC::WN;
 #pragma unroll
   for (int bm = 0; bm < TC::FM; ++bm) {
 #pragma unroll
@@ -438,6 +450,53 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
   }
 }
 
+// Contraction workgroup `sub` (in [0, cx_pad + cy_pad)) of one pipeline step.
+template <class TCX, class TCY, typename T>
+__device__ __forceinline__ void grad_contract_dispatch(int sub, int N, int D, const GradBufs& gb, const BlockGrid& bg,
+                                                       const StepPlan& sp, float* __restrict__ acc_x,
+                                                       float* __restrict__ acc_y, char* lds) {
+  const int64_t blk = (int64_t)bg.bs * bg.bs;  // elements per G' block
+  const bool is_x = sub < sp.cx_pad;
+  if (!is_x) sub -= sp.cx_pad;
+  const int pid = xcd_remap(sub, is_x ? sp.cx_pad : sp.cy_pad);
+  if (pid >= (is_x ? sp.cx_n : sp.cy_n)) return;
+  int tmg, td;
+  if constexpr (GtOnly<T>::value) {
+    // bf16: feature tiles fastest, so the tiles sharing one gradient-matrix
+    // panel run side by side on one XCD and the panel is fetched from HBM
+    // about once (its contractions are bound by that traffic)
+    tmg = pid / bg.ctd;
+    td = pid - tmg * bg.ctd;
+  } else {
+    group_tile(pid, bg.nb * bg.ctm, bg.ctd, 8, tmg, td);
+  }
+  const int P = tmg / bg.ctm, tm = tmg - P * bg.ctm;  // P: block owning the output rows
+  const int buf = sp.diag_c & 1;
+  if (is_x) {
+    const int Q = (P + sp.diag_c) % bg.nb;
+    const T* gx = (const T*)(GtOnly<T>::value ? gb.gt[buf] : gb.g[buf]) + P * blk;
+    grad_contract_tile<TCX, T>(N, D, gx, (const T*)gb.yt, gb.ldt, bg, P, Q, tm, td, sp.accumulate != 0, acc_x, lds);
+  } else {
+    const int Q = (P - sp.diag_c + bg.nb) % bg.nb;
+    grad_contract_tile<TCY, T>(N, D, (const T*)gb.gt[buf] + Q * blk, (const T*)gb.xt, gb.ldt, bg, P, Q, tm, td,
+                               sp.accumulate != 0, acc_y, lds);
+  }
+}
+
+// bf16 contractions of one pipeline step (the x side of diagonal diag_c, then the y side).
+template <typename T>
+__global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int D, GradBufs gb, BlockGrid bg,
+                                                                     StepPlan sp, float* __restrict__ acc_x,
+                                                                     float* __restrict__ acc_y) {
+  using TCX = ConTileX<T>;
+  using TCY = ConTileY<T>;
+  static_assert(TCX::BM == TCY::BM && TCX::BN == TCY::BN && TCX::NT == TCY::NT, "one contraction tile shape");
+  __shared__ __attribute__((aligned(1024))) char lds[CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value];
+  grad_contract_dispatch<TCX, TCY, T>(blockIdx.x, N, D, gb, bg, sp, acc_x, acc_y, lds);
+}
+
+// One pipeline step: G' tiles of diagonal diag_g and, for fp32, the
+// contractions of diagonal diag_c (bf16 runs those in k_grad_contract).
 template <typename T, bool LIT, bool NORM, bool VEC>
 __global__ __launch_bounds__(256, Occ<T>::bwd) void k_grad_step(const T* __restrict__ X, int64_t ldx,
                                                                const T* __restrict__ Y, int64_t ldy, int N, int D,
@@ -445,9 +504,11 @@ __global__ __launch_bounds__(256, Occ<T>::bwd) void k_grad_step(const T* __restr
                                                                GradBufs gb, BlockGrid bg, StepPlan sp,
                                                                float* __restrict__ acc_x, float* __restrict__ acc_y) {
   using TF = FwdTile<T, VEC>;
-  using TCX = ConTileX<T>;
-  using TCY = ConTileY<T>;
-  static_assert(TCX::BM == TCY::BM && TCX::BN == TCY::BN, "one contraction tile shape");
+  static_assert(TF::WM == 2 && TF::WN == 2, "epilogues assume 2 x 2 waves");
+  constexpr bool FUSED = !GtOnly<T>::value;  // contractions in this kernel
+  using TCX = typename std::conditional<FUSED, ConTileX<T>, TF>::type;
+  using TCY = typename std::conditional<FUSED, ConTileY<T>, TF>::type;
+  static_assert(TF::NT == 256 && TCX::NT == 256 && TCY::NT == 256, "256-thread tiles");
   constexpr int GT_LDS = GtOnly<T>::value ? TF::BN * GT_PITCH : 0;
   __shared__ __attribute__((aligned(1024)))
   char lds[CMax<CMax<TF::LDS_BYTES, GT_LDS>::value, CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value>::value];
@@ -455,32 +516,7 @@ __global__ __launch_bounds__(256, Occ<T>::bwd) void k_grad_step(const T* __restr
   const int64_t blk = (int64_t)bg.bs * bg.bs;  // elements per G' block
   int sub = blockIdx.x;
   if (sub < sp.cx_pad + sp.cy_pad) {
-    const bool is_x = sub < sp.cx_pad;
-    if (!is_x) sub -= sp.cx_pad;
-    const int pid = xcd_remap(sub, is_x ? sp.cx_pad : sp.cy_pad);
-    if (pid >= (is_x ? sp.cx_n : sp.cy_n)) return;
-    int tmg, td;
-    if constexpr (GtOnly<T>::value) {
-      // bf16: feature tiles fastest, so the tiles sharing one gradient-matrix
-      // panel run side by side on one XCD and the panel is fetched from HBM
-      // about once (its contractions are bound by that traffic)
-      tmg = pid / bg.ctd;
-      td = pid - tmg * bg.ctd;
-    } else {
-      group_tile(pid, bg.nb * bg.ctm, bg.ctd, 8, tmg, td);
-    }
-    const int P = tmg / bg.ctm, tm = tmg - P * bg.ctm;  // P: block owning the output rows
-    const int buf = sp.diag_c & 1;
-    if (is_x) {
-      const int Q = (P + sp.diag_c) % bg.nb;
-      const T* gx = (const T*)(GtOnly<T>::value ? gb.gt[buf] : gb.g[buf]) + P * blk;
-      grad_contract_tile<TCX, T>(N, D, gx, (const T*)gb.yt, gb.ldt, bg, P, Q, tm, td, sp.accumulate != 0, acc_x,
-                                 lds);
-    } else {
-      const int Q = (P - sp.diag_c + bg.nb) % bg.nb;
-      grad_contract_tile<TCY, T>(N, D, (const T*)gb.gt[buf] + Q * blk, (const T*)gb.xt, gb.ldt, bg, P, Q, tm, td,
-                                 sp.accumulate != 0, acc_y, lds);
-    }
+    if constexpr (FUSED) grad_contract_dispatch<TCX, TCY, T>(sub, N, D, gb, bg, sp, acc_x, acc_y, lds);
     return;
   }
   sub -= sp.cx_pad + sp.cy_pad;

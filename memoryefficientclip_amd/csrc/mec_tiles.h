@@ -2,13 +2,14 @@
 //
 //   fp32                      128 x 128 tiles everywhere (mec_gemm_f32.h)
 //   bf16, 16-byte vectors     forward sums and gradient-matrix tiles 128 x 256
-//                             (x rows x y rows), contractions 256 x 128
-//                             (output rows x feature columns), direct
-//                             global->LDS loads (mec_gemm_bf16_dma.h)
+//                             (x rows x y rows), direct global->LDS loads
+//                             (mec_gemm_bf16_dma.h); contractions 256 x 256
+//                             (output rows x feature columns, 8 waves) in a
+//                             kernel of their own
 //   bf16, other layouts       forward sums and gradient-matrix tiles 128 x 128
 //                             staged through registers (mec_gemm_bf16.h);
 //                             the contractions read internal buffers, which
-//                             are always 16-byte vectors, so they keep 256 x 128
+//                             are always 16-byte vectors, so they keep 256 x 256
 //
 // The backward's block decomposition uses blocks of a multiple of
 // block_quantum(dtype) rows, so that every tile kind divides a block.
@@ -32,8 +33,10 @@ inline TileDims fwd_tile_dims(int dtype, bool vec) {
 // contraction tiles (output rows x feature columns)
 inline TileDims con_tile_dims(int dtype) {
   if (dtype == kDtypeF32) return {128, 128};
-  return {256, 128};
+  return {256, 256};
 }
+// contractions run in their own kernel (k_grad_contract) rather than inside k_grad_step
+inline bool separate_contractions(int dtype) { return dtype != kDtypeF32; }
 inline int block_quantum(int dtype) { return dtype == kDtypeF32 ? 128 : 256; }
 
 }  // namespace mec
