@@ -78,19 +78,20 @@ bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, i
 // Block decomposition of the N x N gradient matrix for the backward: nb
 // blocks of tb quanta of q rows (q = block_quantum: 128 for fp32, 256 for
 // bf16, so every tile kind divides a block).  The target is bs ~ 2d rows for
-// fp32 and ~4d for bf16 (at least 1024 rows), which keeps the scratch at
+// fp32 and ~8d for bf16 (at least 1024 rows), which keeps the scratch at
 // O(n d).  Longer blocks mean fewer pipeline launches and fewer fp32
 // accumulator updates through HBM (one per launch); bf16, whose MFMAs are 16x
-// faster, is bound by that traffic (measured at n = 65536, d = 768: 28.9 ms
-// with 2048-row blocks, 26.1 ms with 4096, 25.5 ms with 8192), fp32 is not
-// (57.9 vs 58.1 ms at the headline shape).  An exact divisor of
+// faster, is bound by that traffic (backward at n = 65536, d = 768: 24.5 ms
+// with 4096-row blocks, 22.7 ms with 8192; at n = 262144, d = 1152: 561 vs
+// 553 ms), fp32 is not (57.9 vs 58.1 ms at the headline shape with 2048- and
+// 4096-row blocks).  An exact divisor of
 // the quantum count within a factor of two of the target is preferred (no
 // short last block, whose contractions would have a short K); otherwise the
 // quanta are balanced over the blocks.
 void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
   const int64_t q = block_quantum(dtype);
   const int64_t tiles = (n + q - 1) / q;
-  int64_t target = ((dtype == MEC_DTYPE_F32 ? 2 : 4) * d + q - 1) / q;
+  int64_t target = ((dtype == MEC_DTYPE_F32 ? 2 : 8) * d + q - 1) / q;
   if (target < 1024 / q) target = 1024 / q;
   if (const char* env = std::getenv("MEC_GRAD_BLOCK_TILES")) {
     long v = std::strtol(env, nullptr, 10);
