@@ -19,7 +19,8 @@
  *
  * The reference has no FFI of its own: its boundary is the PyTorch
  * autograd.Function (clip_loss.py:159, lit_loss.py:151).  These entry points
- * are what that Function calls here, through ctypes.
+ * are what that Function calls here, through ctypes
+ * (memoryefficientclip_amd/_lib.py).
  *
  * Conventions
  *   - Every function returns MEC_OK (0) or a negative MEC_ERR_* code and never
@@ -29,6 +30,10 @@
  *     strides ldx, ldy (in elements, >= d) and unit column stride.
  *     x is the row side of S = x^ y^T: image for CLIP, text for LiT.
  *   - dtype: MEC_DTYPE_F32 (float) or MEC_DTYPE_BF16 (uint16 bfloat16 bits).
+ *     Sizes: 1 <= d <= 2^20; 1 <= n <= 2^30 for fp32 and n <= 2^22 for bf16
+ *     (MEC_ERR_UNSUPPORTED beyond).  bf16 rows that are 16-byte aligned (x, y
+ *     16-byte aligned, d, ldx, ldy multiples of 8) use the direct-to-LDS
+ *     tiles; other layouts are supported at lower speed.
  *   - All work is enqueued on `stream` (a hipStream_t; NULL = default
  *     stream).  No function synchronises the host and none allocates device
  *     memory: the workspace and the gradient scratch are caller-owned.
