@@ -68,9 +68,11 @@ const char* mec_version(void);
 
 /* Number of floats of the per-call workspace: 8 vectors of length n
  * (inverse norms rx, ry; raw diagonal x_i.y_i; off-diagonal row/column sums
- * of E = exp((S-1)/T); 1/R; 1/C; diagonal gradient coefficient).  The same
- * workspace must be passed to mec_forward and the matching mec_backward
- * (it replaces ctx.save_for_backward of the sums, clip_loss.py:199). */
+ * of E = exp((S-1)/T); 1/R; 1/C; diagonal gradient coefficient), then
+ * ceil(n/1024) doubles of loss partials (mec_finalize).  The workspace must
+ * be 8-byte aligned.  The same workspace must be passed to mec_forward and
+ * the matching mec_backward (it replaces ctx.save_for_backward of the sums,
+ * clip_loss.py:199). */
 int64_t mec_workspace_floats(int64_t n);
 
 /* Bytes of gradient scratch needed by mec_grad / mec_grad_step /

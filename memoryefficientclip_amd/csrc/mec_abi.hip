@@ -167,7 +167,7 @@ const char* mec_version(void) { return "memoryefficientclip_amd 0.1.0 gfx950"; }
 
 int64_t mec_workspace_floats(int64_t n) {
   if (n < 1 || n > kMaxN) return -1;
-  return (int64_t)WS_NSLOTS * n;
+  return (int64_t)WS_NSLOTS * n + 2 * ((n + FIN_ROWS - 1) / FIN_ROWS);
 }
 
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype) {
@@ -234,12 +234,19 @@ int mec_finalize(int64_t n, int mode, float temperature, float* workspace, float
   if (!rc) rc = check_temperature(temperature);
   if (rc) return rc;
   if (!workspace || !loss) return fail(MEC_ERR_INVALID, "workspace and loss must be non-null");
+  if (reinterpret_cast<uintptr_t>(workspace) & 7u) return fail(MEC_ERR_INVALID, "workspace must be 8-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   const double inv_t = 1.0 / (double)temperature;
-  if (mode == MEC_MODE_LIT)
-    k_finalize<true><<<1, 1024, 0, s>>>((int)n, inv_t, workspace, loss);
-  else
-    k_finalize<false><<<1, 1024, 0, s>>>((int)n, inv_t, workspace, loss);
+  const int nparts = (int)((n + FIN_ROWS - 1) / FIN_ROWS);
+  // partials after the 8 slots (8 n floats: 8-byte aligned when the workspace is)
+  double* partial = (double*)(workspace + (int64_t)WS_NSLOTS * n);
+  if (mode == MEC_MODE_LIT) {
+    k_finalize_rows<true><<<nparts, FIN_ROWS, 0, s>>>((int)n, inv_t, workspace, partial);
+    k_finalize_sum<true><<<1, 1024, 0, s>>>((int)n, nparts, partial, loss);
+  } else {
+    k_finalize_rows<false><<<nparts, FIN_ROWS, 0, s>>>((int)n, inv_t, workspace, partial);
+    k_finalize_sum<false><<<1, 1024, 0, s>>>((int)n, nparts, partial, loss);
+  }
   return check_launch("finalize");
 }
 

@@ -22,11 +22,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// Workspace layout: 8 float vectors of length n (see include/mec.h).
+// Workspace layout: 8 float vectors of length n, then ceil(n / FIN_ROWS)
+// doubles of per-workgroup loss partials (see include/mec.h).
 enum WsSlot {
   WS_RX = 0, WS_RY = 1, WS_DIAG = 2, WS_ROW_OFF = 3, WS_COL_OFF = 4,
   WS_INV_ROW = 5, WS_INV_COL = 6, WS_KAPPA = 7, WS_NSLOTS = 8
 };
+constexpr int FIN_ROWS = 1024;  // rows per workgroup of the loss finalize
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 

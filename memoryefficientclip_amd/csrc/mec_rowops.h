@@ -61,20 +61,24 @@ __global__ __launch_bounds__(256) void k_prepass(const T* __restrict__ X, int64_
 // evaluated without cancellation.  CLIP averages (l^r + l^c)/2, LiT uses l^r.
 // kappa_i = -(row_off_i/R_i + col_off_i/C_i) is the exact diagonal entry of
 // the gradient matrix in units of a = grad_scale/(2N) (LiT: grad_scale/N).
-// Single workgroup, fp64 accumulation, deterministic.
+// Two passes (rows, then the sum of per-workgroup partials), fp64
+// accumulation in a fixed order: deterministic.
 __device__ __forceinline__ double softplus_log_ratio(double off, double t) {
   if (!(off > 0.0)) return 0.0;
   double u = log(off) - t;
   return u > 0.0 ? u + log1p(exp(-u)) : log1p(exp(u));
 }
 
+// Pass 1: one thread per row (rows beyond N contribute nothing); each
+// workgroup writes the fp64 sum of its rows' loss terms to partial[blockIdx.x].
 template <bool LIT>
-__global__ __launch_bounds__(1024) void k_finalize(int N, double inv_t, float* __restrict__ ws,
-                                                   float* __restrict__ loss) {
-  __shared__ double red[16];
+__global__ __launch_bounds__(FIN_ROWS) void k_finalize_rows(int N, double inv_t, float* __restrict__ ws,
+                                                            double* __restrict__ partial) {
+  __shared__ double red[FIN_ROWS / 64];
   const int64_t n = N;
+  const int i = blockIdx.x * FIN_ROWS + threadIdx.x;
   double acc = 0.0;
-  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+  if (i < N) {
     const double s = (double)ws[WS_DIAG * n + i] * (double)ws[WS_RX * n + i] * (double)ws[WS_RY * n + i];
     const double t = (s - 1.0) * inv_t;
     const double e = exp(t);
@@ -92,6 +96,24 @@ __global__ __launch_bounds__(1024) void k_finalize(int N, double inv_t, float* _
     }
     ws[WS_KAPPA * n + i] = (float)kap;
   }
+  acc = wave_sum_f64(acc);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) red[w] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double tot = 0.0;
+    for (int k = 0; k < FIN_ROWS / 64; ++k) tot += red[k];
+    partial[blockIdx.x] = tot;
+  }
+}
+
+// Pass 2 (one workgroup): loss = sum of the partials in a fixed order / (N or 2N).
+template <bool LIT>
+__global__ __launch_bounds__(1024) void k_finalize_sum(int N, int nparts, const double* __restrict__ partial,
+                                                       float* __restrict__ loss) {
+  __shared__ double red[16];
+  double acc = 0.0;
+  for (int k = threadIdx.x; k < nparts; k += blockDim.x) acc += partial[k];
   acc = wave_sum_f64(acc);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (lane == 0) red[w] = acc;

@@ -34,7 +34,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_sizes():
     lib = _lib.load()
-    assert lib.mec_workspace_floats(1000) == 8000
+    assert lib.mec_workspace_floats(1000) == 8000 + 2      # 8 vectors + one fp64 loss partial
+    assert lib.mec_workspace_floats(1025) == 8 * 1025 + 4
     assert lib.mec_workspace_floats(0) < 0
     # scratch is O(n*d): two block diagonals of the N x N gradient matrix (fp32:
     # in both layouts; bf16: transposed only), plus transposed copies of the two
