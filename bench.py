@@ -36,7 +36,8 @@ if ROOT not in sys.path:
 
 METRIC = "CLIP fwd+bwd ms & TFLOP/s (% MFMA peak) at N=32768 D=1152, 1 MI355X"
 # MI355X published dense MFMA peaks (256 CUs at 2.4 GHz), TFLOP/s.
-PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6}
+PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6, "f16": 2516.6}
+TORCH_DTYPE = {"f32": "float32", "bf16": "bfloat16", "f16": "float16"}
 
 # config -> (mode, n, d, dtype, normalized_inputs, temperature, generator, cpu sample n)
 CONFIGS = {
@@ -106,7 +107,7 @@ def kernel_leg(x, y, mode, dt, normalize, temperature, reps):
     lib = _lib.load()
     n, d = x.shape
     m = _lib.MODE_CLIP if mode == "clip" else _lib.MODE_LIT
-    dtc = _lib.DTYPE_F32 if dt == "f32" else _lib.DTYPE_BF16
+    dtc = {"f32": _lib.DTYPE_F32, "bf16": _lib.DTYPE_BF16, "f16": _lib.DTYPE_F16}[dt]
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     ws = torch.empty(lib.mec_workspace_floats(n), device=x.device)
@@ -185,8 +186,9 @@ def cpu_baseline(mode, d, dt, normalized, temperature, gen, n_cpu, budget_s=20.0
     import torch
     from oracle.cpu_baseline import dense_step
     a, b = make_inputs(n_cpu, d, gen, seed=0)
-    if dt == "bf16":
-        a, b = a.bfloat16().float(), b.bfloat16().float()
+    if dt != "f32":
+        tdt = getattr(torch, TORCH_DTYPE[dt])
+        a, b = a.to(tdt).float(), b.to(tdt).float()
     dense_step(a, b, temperature, mode == "lit", normalized)  # warm-up
     times = []
     t_start = time.perf_counter()
@@ -214,6 +216,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--dtype", choices=sorted(PEAK_TFLOPS), default=None,
+                    help="input dtype instead of the config's own (e.g. --config 4 --dtype f16)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-reps", type=int, default=0, help="launches per stage in the kernel leg (default: steps)")
     ap.add_argument("--probe", choices=["copy"], default=None,
@@ -243,9 +247,10 @@ def main():
     _lib.load()  # fail loudly if the HIP library is missing
 
     mode, n, d, dt, normalized, temperature, gen, n_cpu = CONFIGS[args.config]
+    dt = args.dtype or dt
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    tdtype = torch.float32 if dt == "f32" else torch.bfloat16
+    tdtype = getattr(torch, TORCH_DTYPE[dt])
     log(f"bench: config {args.config} {mode} n={n} d={d} {dt} normalized_inputs={normalized} T={temperature}")
     a_h, b_h = make_inputs(n, d, gen, seed=0)
     a = a_h.to(dev, tdtype).requires_grad_(True)

@@ -29,11 +29,13 @@
  *   - Pointers are device pointers.  x and y are row-major [n, d] with row
  *     strides ldx, ldy (in elements, >= d) and unit column stride.
  *     x is the row side of S = x^ y^T: image for CLIP, text for LiT.
- *   - dtype: MEC_DTYPE_F32 (float) or MEC_DTYPE_BF16 (uint16 bfloat16 bits).
- *     Sizes: 1 <= d <= 2^20; 1 <= n <= 2^30 for fp32 and n <= 2^22 for bf16
- *     (MEC_ERR_UNSUPPORTED beyond).  bf16 rows that are 16-byte aligned (x, y
- *     16-byte aligned, d, ldx, ldy multiples of 8) use the direct-to-LDS
- *     tiles; other layouts are supported at lower speed.
+ *   - dtype: MEC_DTYPE_F32 (float), MEC_DTYPE_BF16 (uint16 bfloat16 bits) or
+ *     MEC_DTYPE_F16 (uint16 IEEE binary16 bits).  All arithmetic accumulates
+ *     in fp32 (sums and loss in fp64).  Sizes: 1 <= d <= 2^20; 1 <= n <= 2^30
+ *     for fp32 and n <= 2^22 for the 16-bit types (MEC_ERR_UNSUPPORTED
+ *     beyond).  16-bit rows that are 16-byte aligned (x, y 16-byte aligned, d,
+ *     ldx, ldy multiples of 8) use the direct-to-LDS tiles; other layouts are
+ *     supported at lower speed.
  *   - All work is enqueued on `stream` (a hipStream_t; NULL = default
  *     stream).  No function synchronises the host and none allocates device
  *     memory: the workspace and the gradient scratch are caller-owned.
@@ -56,6 +58,7 @@ extern "C" {
 
 #define MEC_DTYPE_F32 0
 #define MEC_DTYPE_BF16 1
+#define MEC_DTYPE_F16 2
 
 #define MEC_MODE_CLIP 0 /* symmetric image<->text loss, gradients for x and y */
 #define MEC_MODE_LIT 1  /* text->image only (x = text), gradient for x only */
@@ -78,9 +81,9 @@ int64_t mec_workspace_floats(int64_t n);
 /* Bytes of gradient scratch needed by mec_grad / mec_grad_step /
  * mec_backward for (n, d, dtype), all in the input dtype: two buffers holding
  * one block diagonal of the off-diagonal gradient matrix each (nb blocks of
- * bs x bs, bs ~ 2d), the same blocks transposed, and transposed normalised
- * copies of x and y ([d][n rounded up to 128]); O(n*d) in total.
- * Returns < 0 on bad args. */
+ * bs x bs, bs ~ 2d for fp32 and ~8d for the 16-bit types), for fp32 the same
+ * blocks transposed as well, and transposed normalised copies of x and y
+ * ([d][n rounded up to 128]); O(n*d) in total.  Returns < 0 on bad args. */
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype);
 
 /* Block decomposition of the backward for (n, d, dtype): the n x n gradient

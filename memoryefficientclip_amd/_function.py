@@ -21,7 +21,7 @@ import torch
 
 from . import _lib
 
-_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
 
 
 def check_inputs(x: torch.Tensor, y: torch.Tensor) -> None:
@@ -40,7 +40,7 @@ def check_inputs(x: torch.Tensor, y: torch.Tensor) -> None:
     if x.dtype != y.dtype:
         raise TypeError(f"dtype mismatch {x.dtype} vs {y.dtype}")
     if x.dtype not in _DTYPES:
-        raise TypeError(f"unsupported dtype {x.dtype}; supported: float32, bfloat16")
+        raise TypeError(f"unsupported dtype {x.dtype}; supported: float32, bfloat16, float16")
     if x.device != y.device:
         raise ValueError(f"inputs on different devices {x.device} vs {y.device}")
 

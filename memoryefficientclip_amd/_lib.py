@@ -20,6 +20,7 @@ MEC_ERR_HIP = -3
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2
 MODE_CLIP = 0
 MODE_LIT = 1
 

@@ -37,9 +37,13 @@ int check_launch(const char* what) {
 
 constexpr int64_t kMaxN = int64_t(1) << 30;
 constexpr int64_t kMaxD = int64_t(1) << 20;
-// bf16 contractions address a 128-row panel of the transposed inputs
+// the 16-bit contractions address a 256-row panel of the transposed inputs
 // ([d][ldt], ldt ~ n) with 32-bit buffer offsets
-constexpr int64_t kMaxNBf16 = int64_t(1) << 22;
+constexpr int64_t kMaxN16 = int64_t(1) << 22;
+
+bool known_dtype(int dtype) {
+  return dtype == MEC_DTYPE_F32 || dtype == MEC_DTYPE_BF16 || dtype == MEC_DTYPE_F16;
+}
 
 int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                  int dtype) {
@@ -48,11 +52,10 @@ int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   if (ldx < d || ldy < d)
     return fail(MEC_ERR_INVALID, "row strides ldx=%lld ldy=%lld must be >= d=%lld", (long long)ldx,
                 (long long)ldy, (long long)d);
-  if (dtype != MEC_DTYPE_F32 && dtype != MEC_DTYPE_BF16)
-    return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
+  if (!known_dtype(dtype)) return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
   if (x == nullptr || y == nullptr) return fail(MEC_ERR_INVALID, "x and y must be non-null");
-  if (dtype == MEC_DTYPE_BF16 && n > kMaxNBf16)
-    return fail(MEC_ERR_UNSUPPORTED, "bf16 supports n <= 2^22 (n=%lld)", (long long)n);
+  if (dtype != MEC_DTYPE_F32 && n > kMaxN16)
+    return fail(MEC_ERR_UNSUPPORTED, "bf16 and fp16 support n <= 2^22 (n=%lld)", (long long)n);
   return MEC_OK;
 }
 
@@ -77,10 +80,10 @@ bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, i
 
 // Block decomposition of the N x N gradient matrix for the backward: nb
 // blocks of tb quanta of q rows (q = block_quantum: 128 for fp32, 256 for
-// bf16, so every tile kind divides a block).  The target is bs ~ 2d rows for
-// fp32 and ~8d for bf16 (at least 1024 rows), which keeps the scratch at
-// O(n d).  Longer blocks mean fewer pipeline launches and fewer fp32
-// accumulator updates through HBM (one per launch); bf16, whose MFMAs are 16x
+// the 16-bit types, so every tile kind divides a block).  The target is
+// bs ~ 2d rows for fp32 and ~8d for bf16 / fp16 (at least 1024 rows), which
+// keeps the scratch at O(n d).  Longer blocks mean fewer pipeline launches and
+// fewer fp32 accumulator updates through HBM (one per launch); bf16, whose MFMAs are 16x
 // faster, is bound by that traffic (backward at n = 65536, d = 768: 24.5 ms
 // with 4096-row blocks, 22.7 ms with 8192; at n = 262144, d = 1152: 561 vs
 // 553 ms), fp32 is not (57.9 vs 58.1 ms at the headline shape with 2048- and
@@ -120,9 +123,9 @@ void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
 }
 
 // Scratch layout of the backward (element type = input dtype):
-//   fp32: [G0 | G1 | GT0 | GT1 | XT | YT]     bf16: [GT0 | GT1 | XT | YT]
+//   fp32: [G0 | G1 | GT0 | GT1 | XT | YT]     bf16, fp16: [GT0 | GT1 | XT | YT]
 // G0/G1 (and their transposes GT0/GT1) double-buffer one block diagonal of
-// G' (nb blocks of bs x bs; bf16 keeps only the transposed copy); XT/YT are
+// G' (nb blocks of bs x bs; the 16-bit types keep only the transposed copy); XT/YT are
 // the normalised inputs transposed, [d][ldt] with ldt = n rounded up to 128.
 struct ScratchLayout {
   int bs, nb;
@@ -145,6 +148,21 @@ ScratchLayout scratch_layout(int64_t n, int64_t d, int dtype) {
 int64_t scratch_bytes_for(int64_t n, int64_t d, int dtype) { return scratch_layout(n, d, dtype).total; }
 
 int round8(int v) { return (v + 7) & ~7; }
+
+// T = element type of dtype: float, bf16 bits (uint16_t) or fp16 (_Float16)
+#define DISPATCH_DTYPE(dtype, T, ...)   \
+  do {                                  \
+    if ((dtype) == MEC_DTYPE_F32) {     \
+      using T = float;                  \
+      __VA_ARGS__;                      \
+    } else if ((dtype) == MEC_DTYPE_BF16) { \
+      using T = uint16_t;               \
+      __VA_ARGS__;                      \
+    } else {                            \
+      using T = _Float16;               \
+      __VA_ARGS__;                      \
+    }                                   \
+  } while (0)
 
 #define DISPATCH_BOOL(cond, NAME, ...) \
   do {                                 \
@@ -172,7 +190,7 @@ int64_t mec_workspace_floats(int64_t n) {
 
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype) {
   if (n < 1 || n > kMaxN || d < 1 || d > kMaxD) return -1;
-  if (dtype != MEC_DTYPE_F32 && dtype != MEC_DTYPE_BF16) return -1;
+  if (!known_dtype(dtype)) return -1;
   return scratch_bytes_for(n, d, dtype);
 }
 
@@ -185,15 +203,8 @@ int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
   hipStream_t s = (hipStream_t)stream;
   const int N = (int)n, D = (int)d;
   dim3 grid((unsigned)((n + 3) / 4));
-  if (dtype == MEC_DTYPE_F32) {
-    DISPATCH_BOOL(normalize, NORM,
-                  k_prepass<float, NORM><<<grid, 256, 0, s>>>((const float*)x, ldx, (const float*)y, ldy, N, D,
-                                                              workspace));
-  } else {
-    DISPATCH_BOOL(normalize, NORM,
-                  k_prepass<uint16_t, NORM><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (const uint16_t*)y,
-                                                                 ldy, N, D, workspace));
-  }
+  DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM,
+      k_prepass<T, NORM><<<grid, 256, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, workspace)));
   return check_launch("prepass");
 }
 
@@ -215,15 +226,9 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   if (nwg > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "forward grid too large");
   dim3 grid((unsigned)nwg);
   const bool lit = mode == MEC_MODE_LIT;
-  if (dtype == MEC_DTYPE_F32) {
-    DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-        k_sumexp<float, LIT, NORM, VEC><<<grid, 256, 0, s>>>((const float*)x, ldx, (const float*)y, ldy, N, D,
-                                                          D, c, workspace, tiles_m, tiles_n))));
-  } else {
-    DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-        k_sumexp<uint16_t, LIT, NORM, VEC><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (const uint16_t*)y, ldy,
-                                                           N, D, D, c, workspace, tiles_m, tiles_n))));
-  }
+  DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
+      k_sumexp<T, LIT, NORM, VEC><<<grid, FwdTile<T, VEC>::NT, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, D,
+                                                                      c, workspace, tiles_m, tiles_n)))));
   return check_launch("sumexp");
 }
 
@@ -267,7 +272,7 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
 int mec_grad_blocking(int64_t n, int64_t d, int dtype, int64_t* block_rows, int64_t* num_blocks) {
   g_err.clear();
   if (n < 1 || n > kMaxN || d < 1 || d > kMaxD) return fail(MEC_ERR_INVALID, "n or d out of range");
-  if (dtype != MEC_DTYPE_F32 && dtype != MEC_DTYPE_BF16) return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
+  if (!known_dtype(dtype)) return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
   if (!block_rows || !num_blocks) return fail(MEC_ERR_INVALID, "block_rows and num_blocks must be non-null");
   int bs, nb;
   grad_blocks(n, d, dtype, &bs, &nb);
@@ -343,46 +348,32 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
     // transposed normalised operands of the contractions: YT for the x side, XT for the y side
     const int64_t n64 = n;
     dim3 tgrid((unsigned)(L.ldt / 64), (unsigned)((d + 63) / 64));
-    if (dtype == MEC_DTYPE_F32) {
-      DISPATCH_BOOL(normalize, NORM, {
-        if (acc_x)
-          k_transpose<float, NORM><<<tgrid, 256, 0, s>>>((const float*)y, ldy, N, D, workspace + WS_RY * n64,
-                                                         (float*)gb.yt, L.ldt);
-        if (acc_y)
-          k_transpose<float, NORM><<<tgrid, 256, 0, s>>>((const float*)x, ldx, N, D, workspace + WS_RX * n64,
-                                                         (float*)gb.xt, L.ldt);
-      });
-    } else {
-      DISPATCH_BOOL(normalize, NORM, {
-        if (acc_x)
-          k_transpose<uint16_t, NORM><<<tgrid, 256, 0, s>>>((const uint16_t*)y, ldy, N, D,
-                                                            workspace + WS_RY * n64, (uint16_t*)gb.yt, L.ldt);
-        if (acc_y)
-          k_transpose<uint16_t, NORM><<<tgrid, 256, 0, s>>>((const uint16_t*)x, ldx, N, D,
-                                                            workspace + WS_RX * n64, (uint16_t*)gb.xt, L.ldt);
-      });
-    }
+    DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, {
+      if (acc_x)
+        k_transpose<T, NORM><<<tgrid, 256, 0, s>>>((const T*)y, ldy, N, D, workspace + WS_RY * n64, (T*)gb.yt,
+                                                   L.ldt);
+      if (acc_y)
+        k_transpose<T, NORM><<<tgrid, 256, 0, s>>>((const T*)x, ldx, N, D, workspace + WS_RX * n64, (T*)gb.xt,
+                                                   L.ldt);
+    }));
     rc = check_launch("transpose");
     if (rc) return rc;
   }
-  if (dtype == MEC_DTYPE_F32) {
-    DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-        k_grad_step<float, LIT, NORM, VEC><<<(unsigned)grid, 256, 0, s>>>(
-            (const float*)x, ldx, (const float*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y))));
-  } else {
+  DISPATCH_DTYPE(dtype, T, {
     if (grid_c > 0) {
-      k_grad_contract<uint16_t><<<(unsigned)grid_c, ConTileX<uint16_t>::NT, 0, s>>>(N, D, gb, bg, sp_c, acc_x,
-                                                                                    acc_y);
-      rc = check_launch("grad_contract");
-      if (rc) return rc;
+      if constexpr (Is16<T>::value) {
+        k_grad_contract<T><<<(unsigned)grid_c, ConTileX<T>::NT, 0, s>>>(N, D, gb, bg, sp_c, acc_x, acc_y);
+        rc = check_launch("grad_contract");
+      }
     }
-    if (grid > 0) {
+    if (!rc && grid > 0) {
       DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-          k_grad_step<uint16_t, LIT, NORM, VEC><<<(unsigned)grid, 256, 0, s>>>(
-              (const uint16_t*)x, ldx, (const uint16_t*)y, ldy, N, D, D, c, workspace, gb, bg, sp_g, acc_x,
+          k_grad_step<T, LIT, NORM, VEC><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
+              (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, split ? sp_g : sp, acc_x,
               acc_y))));
     }
-  }
+  });
+  if (rc) return rc;
   return check_launch("grad_step");
 }
 
@@ -424,25 +415,14 @@ int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   const float* kap = workspace + WS_KAPPA * n64;
   const float a = (float)((double)grad_scale / (lit ? (double)n : 2.0 * (double)n));
   dim3 grid((unsigned)((n + 3) / 4));
-  if (dtype == MEC_DTYPE_F32) {
-    DISPATCH_BOOL(normalize, NORM, {
-      if (acc_x)
-        k_postpass<float, NORM><<<grid, 256, 0, s>>>((const float*)x, ldx, (const float*)y, ldy, N, D, rx, ry,
-                                                     kap, a, grad_output, acc_x, (float*)dx);
-      if (acc_y)
-        k_postpass<float, NORM><<<grid, 256, 0, s>>>((const float*)y, ldy, (const float*)x, ldx, N, D, ry, rx,
-                                                     kap, a, grad_output, acc_y, (float*)dy);
-    });
-  } else {
-    DISPATCH_BOOL(normalize, NORM, {
-      if (acc_x)
-        k_postpass<uint16_t, NORM><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (const uint16_t*)y, ldy, N, D,
-                                                        rx, ry, kap, a, grad_output, acc_x, (uint16_t*)dx);
-      if (acc_y)
-        k_postpass<uint16_t, NORM><<<grid, 256, 0, s>>>((const uint16_t*)y, ldy, (const uint16_t*)x, ldx, N,
-                                                        D, ry, rx, kap, a, grad_output, acc_y, (uint16_t*)dy);
-    });
-  }
+  DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, {
+    if (acc_x)
+      k_postpass<T, NORM><<<grid, 256, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, rx, ry, kap, a,
+                                               grad_output, acc_x, (T*)dx);
+    if (acc_y)
+      k_postpass<T, NORM><<<grid, 256, 0, s>>>((const T*)y, ldy, (const T*)x, ldx, N, D, ry, rx, kap, a,
+                                               grad_output, acc_y, (T*)dy);
+  }));
   return check_launch("postpass");
 }
 

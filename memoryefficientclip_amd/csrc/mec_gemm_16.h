@@ -1,6 +1,7 @@
-// bf16 MFMA tile core for gfx950: 128x128 output tile per 256-thread
-// workgroup, 4 waves in 2x2, each wave a 64x64 sub-tile of 2x2 blocks of
-// v_mfma_f32_32x32x16_bf16 (fp32 accumulate).
+// 16-bit (bf16 or fp16) MFMA tile core for gfx950, operands staged through
+// registers: 128x128 output tile per 256-thread workgroup, 4 waves in 2x2,
+// each wave a 64x64 sub-tile of 2x2 blocks of v_mfma_f32_32x32x16_{bf16,f16}
+// (fp32 accumulate; F16 selects the format, the data movement is the same).
 //
 // Both operands are K-major in global memory (element (row, k) at
 // base[row * ld + k]) and in LDS ([row][k], rows padded by 16 bytes): 16-byte
@@ -79,7 +80,7 @@ __device__ __forceinline__ void store_chunk(uint16_t* lds, const i16x8 (&r)[Cfg<
 
 // MFMA steps [s0, s0 + 2) of the chunk: this lane's 16 k-values of its two A
 // rows and two B rows, then 8 MFMAs.
-template <int BK>
+template <int BK, bool F16>
 __device__ __forceinline__ void compute_part(const uint16_t* la, const uint16_t* lb, int wm, int wn, int lane,
                                              int s0, f32x16 (&acc)[2][2]) {
   using G = Cfg<BK>;
@@ -102,11 +103,11 @@ __device__ __forceinline__ void compute_part(const uint16_t* la, const uint16_t*
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16_32x32x16(a[i][s], b[j][s], acc[i][j]);
+      for (int j = 0; j < 2; ++j) acc[i][j] = mfma16_32x32x16<F16>(a[i][s], b[j][s], acc[i][j]);
 }
 
 // acc[i][j] (this wave's 64x64 sub-tile) = sum_k A(m, k) * B(n, k) over k in [0, K).
-template <int BK, bool VECA, bool VECB>
+template <int BK, bool VECA, bool VECB, bool F16>
 __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int K, uint16_t* lds,
                                          f32x16 (&acc)[2][2]) {
   using G = Cfg<BK>;
@@ -135,7 +136,7 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
     }
     const uint16_t* la = lds + cur * 2 * G::TILE;
 #pragma unroll
-    for (int s0 = 0; s0 < G::NS; s0 += 2) compute_part<BK>(la, la + G::TILE, wm, wn, lane, s0, acc);
+    for (int s0 = 0; s0 < G::NS; s0 += 2) compute_part<BK, F16>(la, la + G::TILE, wm, wn, lane, s0, acc);
     if (STAGES == 2) {
       if (more) {
         uint16_t* ln = lds + (cur ^ 1) * 2 * G::TILE;

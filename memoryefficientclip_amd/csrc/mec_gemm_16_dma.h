@@ -1,12 +1,14 @@
-// bf16 MFMA tile core for gfx950 with direct global->LDS loads.
+// 16-bit (bf16 or fp16) MFMA tile core for gfx950 with direct global->LDS
+// loads.
 //
 // Geometry: a BM x BN output tile per workgroup of WM x WN waves, each wave a
-// (BM/WM) x (BN/WN) sub-tile of v_mfma_f32_32x32x16_bf16 blocks (fp32
-// accumulate).  The forward and gradient-matrix tiles are 128 x 256 with
-// 2 x 2 waves: two workgroups share a CU (72 KB of LDS each), so one
-// workgroup's epilogue (exp, reductions, stores) runs while the other's MFMAs
-// do.  The contractions, whose epilogue is a few atomics, are 256 x 256 with
-// 4 x 2 waves, one workgroup per CU: fewer operand bytes per MFMA through the
+// (BM/WM) x (BN/WN) sub-tile of v_mfma_f32_32x32x16_{bf16,f16} blocks (fp32
+// accumulate; Geo::F16 selects the format, the data movement is the same).
+// The forward and gradient-matrix tiles are 128 x 256 with 2 x 2 waves: two
+// workgroups share a CU (72 KB of LDS each), so one workgroup's epilogue
+// (exp, reductions, stores) runs while the other's MFMAs do.  The
+// contractions, whose epilogue is a few atomics, are 256 x 256 with 4 x 2
+// waves, one workgroup per CU: fewer operand bytes per MFMA through the
 // global->LDS path (≈64 B/clk per CU), which bounds these kernels.
 //
 // Operands are K-major (element (row, k) at base[row * ld + k]).  K is staged
@@ -52,9 +54,10 @@ constexpr int RPB = 16;           // rows per 1 KB load block
 constexpr int NS = BK / 16;       // MFMA k-steps per chunk
 constexpr uint32_t OOB = 0x80000000u;  // buffer offset that reads as zero
 
-template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2>
+template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, bool F16_ = false>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_;
+  static constexpr bool F16 = F16_;                    // fp16 MFMAs (else bf16)
   static constexpr bool TA = TA_;                      // A stored k-row-major
   static_assert(!TA || BM == 256, "transposed A: 512-byte k-rows (BM = 256)");
   static constexpr int WM = WM_, WN = WN_, NW = WM * WN, NT = 64 * NW;
@@ -217,7 +220,7 @@ __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM
 #pragma unroll
   for (int m = 0; m < G::NMF; ++m) {
     const int i = m / G::FN, j = m % G::FN;
-    acc[i][j] = mfma_bf16_32x32x16(f.a[i], f.b[j], acc[i][j]);
+    acc[i][j] = mfma16_32x32x16<G::F16>(f.a[i], f.b[j], acc[i][j]);
     if (NL > 0 && (m % EVERY) == EVERY - 1 && L0 + m / EVERY < L1) {
       sched_fence();
       if (do_load) lp.issue(L0 + m / EVERY, k0, stage);

@@ -19,8 +19,8 @@
 #include <type_traits>
 
 #include "mec_gemm_f32.h"
-#include "mec_gemm_bf16.h"
-#include "mec_gemm_bf16_dma.h"
+#include "mec_gemm_16.h"
+#include "mec_gemm_16_dma.h"
 #include "mec_tiles.h"
 
 namespace mec {
@@ -50,15 +50,21 @@ struct TileF32 {
   }
 };
 
-struct PackBf16 {
-  static __device__ __forceinline__ uint16_t pack(float v) { return f32_to_bf16(v); }
+// fp32 -> 16-bit packing of the gradient-matrix tiles
+template <bool F16>
+struct Pack16 {
+  static __device__ __forceinline__ uint16_t pack(float v) { return F16 ? f32_to_f16(v) : f32_to_bf16(v); }
   static __device__ __forceinline__ void store4(uint16_t* p, float a, float b, float c, float d) {
-    *(uint2*)p = uint2{pack2_bf16(a, b), pack2_bf16(c, d)};
+    if constexpr (F16)
+      *(uint2*)p = uint2{pack2_f16(a, b), pack2_f16(c, d)};
+    else
+      *(uint2*)p = uint2{pack2_bf16(a, b), pack2_bf16(c, d)};
   }
 };
 
-// bf16, 128 x 128, operands staged through registers (any alignment / D)
-struct TileB16V : PackBf16 {
+// bf16 / fp16, 128 x 128, operands staged through registers (any alignment / D)
+template <bool F16>
+struct Tile16V : Pack16<F16> {
   using Elem = uint16_t;
   using Op = g16::Operand;
   static constexpr bool TA = false;
@@ -66,17 +72,18 @@ struct TileB16V : PackBf16 {
   static constexpr int LDS_BYTES = g16::Cfg<MEC_BF16_BK_FWD>::LDS_ELEMS * 2;
   template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
-    g16::mainloop<MEC_BF16_BK_FWD, VECA, VECB>(a, b, K, (uint16_t*)lds, acc);
+    g16::mainloop<MEC_BF16_BK_FWD, VECA, VECB, F16>(a, b, K, (uint16_t*)lds, acc);
   }
 };
 
-// bf16, BM_ x BN_, direct global->LDS loads (16-byte aligned rows, ld and kmax
-// multiples of 8); TA_: A stored k-row-major (a transposed gradient-matrix block)
-template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2>
-struct TileB16D : PackBf16 {
+// bf16 / fp16, BM_ x BN_, direct global->LDS loads (16-byte aligned rows, ld
+// and kmax multiples of 8); TA_: A stored k-row-major (a transposed
+// gradient-matrix block)
+template <int BM_, int BN_, bool TA_, int WM_, int WN_, bool F16>
+struct Tile16D : Pack16<F16> {
   using Elem = uint16_t;
   using Op = g16d::Operand;
-  using G = g16d::Geo<BM_, BN_, TA_, WM_, WN_>;
+  using G = g16d::Geo<BM_, BN_, TA_, WM_, WN_, F16>;
   static constexpr bool TA = TA_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
@@ -87,34 +94,51 @@ struct TileB16D : PackBf16 {
   }
 };
 
+// Input element types: float, bf16 bits (uint16_t), fp16 (_Float16).  The
+// 16-bit types share every tile and kernel; F16 selects the MFMA and packing.
+template <typename T> struct Is16 { static constexpr bool value = false, f16 = false; };
+template <> struct Is16<uint16_t> { static constexpr bool value = true, f16 = false; };
+template <> struct Is16<_Float16> { static constexpr bool value = true, f16 = true; };
+
 // forward sums and gradient-matrix tiles; contractions (see mec_tiles.h)
-template <typename T, bool VEC> struct FwdTileSel;
-template <bool VEC> struct FwdTileSel<float, VEC> { using type = TileF32; };
-template <> struct FwdTileSel<uint16_t, true> { using type = TileB16D<128, 256>; };
-template <> struct FwdTileSel<uint16_t, false> { using type = TileB16V; };
+template <typename T, bool VEC, bool IS16 = Is16<T>::value> struct FwdTileSel;
+template <typename T, bool VEC> struct FwdTileSel<T, VEC, false> { using type = TileF32; };
+template <typename T> struct FwdTileSel<T, true, true> { using type = Tile16D<128, 256, false, 2, 2, Is16<T>::f16>; };
+template <typename T> struct FwdTileSel<T, false, true> { using type = Tile16V<Is16<T>::f16>; };
 template <typename T, bool VEC> using FwdTile = typename FwdTileSel<T, VEC>::type;
 // Contractions.  fp32 stores the gradient-matrix blocks in both layouts (G'
-// for the x side, G'^T for the y side) and runs them inside k_grad_step; bf16
-// stores only G'^T, which the y side reads K-major and the x side reads
-// transposed through LDS, in a kernel of its own (k_grad_contract) with
-// 256 x 256 tiles of 8 waves.
-template <typename T> struct ConTileSel;
-template <> struct ConTileSel<float> { using x = TileF32; using y = TileF32; };
-template <> struct ConTileSel<uint16_t> {
-  using x = TileB16D<256, 256, true, 4, 2>;
-  using y = TileB16D<256, 256, false, 4, 2>;
+// for the x side, G'^T for the y side) and runs them inside k_grad_step; the
+// 16-bit types store only G'^T, which the y side reads K-major and the x side
+// reads transposed through LDS, in a kernel of their own (k_grad_contract)
+// with 256 x 256 tiles of 8 waves.
+template <typename T, bool IS16 = Is16<T>::value> struct ConTileSel;
+template <typename T> struct ConTileSel<T, false> { using x = TileF32; using y = TileF32; };
+template <typename T> struct ConTileSel<T, true> {
+  using x = Tile16D<256, 256, true, 4, 2, Is16<T>::f16>;
+  using y = Tile16D<256, 256, false, 4, 2, Is16<T>::f16>;
 };
 template <typename T> using ConTileX = typename ConTileSel<T>::x;
 template <typename T> using ConTileY = typename ConTileSel<T>::y;
-// bf16 keeps one layout of the gradient-matrix blocks (G'^T)
-template <typename T> struct GtOnly { static constexpr bool value = false; };
-template <> struct GtOnly<uint16_t> { static constexpr bool value = true; };
+// the 16-bit types keep one layout of the gradient-matrix blocks (G'^T)
+template <typename T> struct GtOnly { static constexpr bool value = Is16<T>::value; };
+// Scale of the stored gradient-matrix entries.  0 < G'_ij <= 2 (E_ij <= 1,
+// E_ij / R_i <= 1, E_ij / C_j <= 1) and typical entries are ~1/N, which are
+// fp16 subnormals from N ~ 2^14 on: fp16 stores 2^14 G' (at most 2^15, below
+// the fp16 maximum 65504) and the contractions scale back by 2^-14 (exact).
+template <typename T> struct GScale { static constexpr float value = 1.f; };
+template <> struct GScale<_Float16> { static constexpr float value = 16384.f; };
 
-// workgroups per CU the launch bounds promise (the bf16 direct-load configs
+// workgroups per CU the launch bounds promise (the 16-bit direct-load configs
 // use 72 KB of LDS: two workgroups, one's epilogue overlapping the other's MFMAs)
-template <typename T> struct Occ;
-template <> struct Occ<float> { static constexpr int fwd = 2, bwd = 3; };
-template <> struct Occ<uint16_t> { static constexpr int fwd = 2, bwd = 2; };
+template <typename T> struct Occ {
+  static constexpr int fwd = 2, bwd = Is16<T>::value ? 2 : 3;
+};
+
+// Operand of a tile core from a typed pointer (the 16-bit cores address bits)
+template <class TL, typename T>
+__device__ __forceinline__ typename TL::Op tile_op(const T* p, int64_t ld, int rows, int kmax) {
+  return typename TL::Op{reinterpret_cast<const typename TL::Elem*>(p), ld, rows, kmax};
+}
 
 template <int A, int B> struct CMax { static constexpr int value = A > B ? A : B; };
 
@@ -126,7 +150,7 @@ template <class TL, bool NORM, bool MASK>
 __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::FN], float c, int m0, int n0, int N,
                                                 const float* s_rx, const float* s_ry, float (&rowv)[TL::FM * 16],
                                                 float (&colv)[TL::FN]) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
 #pragma unroll
   for (int k = 0; k < TL::FM * 16; ++k) rowv[k] = 0.f;
 #pragma unroll
@@ -153,31 +177,30 @@ __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::
 }
 
 template <typename T, bool LIT, bool NORM, bool VEC>
-__global__ __launch_bounds__(256, Occ<T>::fwd) void k_sumexp(const T* __restrict__ X, int64_t ldx,
+__global__ __launch_bounds__((FwdTile<T, VEC>::NT), Occ<T>::fwd) void k_sumexp(const T* __restrict__ X, int64_t ldx,
                                                             const T* __restrict__ Y, int64_t ldy, int N, int D,
                                                             int kmax, float c, float* __restrict__ ws, int tiles_m,
                                                             int tiles_n) {
   using TL = FwdTile<T, VEC>;
   static_assert(TL::FM == 2, "row reduction assumes 64-row wave sub-tiles");
-  static_assert(TL::WM == 2 && TL::WN == 2 && TL::NT == 256, "epilogues assume 2 x 2 waves");
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
   __shared__ float s_rx[TL::BM], s_ry[TL::BN], s_row[TL::BM], s_col[TL::BN];
   const int64_t n64 = N;
   int tm, tn;
   tile_swizzle(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
   const int m0 = tm * TL::BM, n0 = tn * TL::BN;
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / TL::WN, wn = w % TL::WN;
 
-  typename TL::Op A{X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax};
-  typename TL::Op B{Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax};
+  const auto A = tile_op<TL>(X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax);
+  const auto B = tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax);
   f32x16 acc[TL::FM][TL::FN];
   TL::template run<VEC, VEC>(A, B, D, lds, acc);
 
-  for (int u = t; u < TL::BM; u += 256) {
+  for (int u = t; u < TL::BM; u += TL::NT) {
     s_rx[u] = (NORM && m0 + u < N) ? ws[WS_RX * n64 + m0 + u] : 1.f;
     s_row[u] = 0.f;
   }
-  for (int u = t; u < TL::BN; u += 256) {
+  for (int u = t; u < TL::BN; u += TL::NT) {
     s_ry[u] = (NORM && n0 + u < N) ? ws[WS_RY * n64 + n0 + u] : 1.f;
     s_col[u] = 0.f;
   }
@@ -207,11 +230,11 @@ __global__ __launch_bounds__(256, Occ<T>::fwd) void k_sumexp(const T* __restrict
     }
   }
   __syncthreads();
-  for (int u = t; u < TL::BM; u += 256)
+  for (int u = t; u < TL::BM; u += TL::NT)
     if (m0 + u < N)
       __hip_atomic_fetch_add(&ws[WS_ROW_OFF * n64 + m0 + u], s_row[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (!LIT) {
-    for (int u = t; u < TL::BN; u += 256)
+    for (int u = t; u < TL::BN; u += TL::NT)
       if (n0 + u < N)
         __hip_atomic_fetch_add(&ws[WS_COL_OFF * n64 + n0 + u], s_col[u], __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
@@ -271,7 +294,7 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN]
                                              typename TL::Elem* __restrict__ Gb, typename TL::Elem* __restrict__ GTb,
                                              int bs, const float* s_rx, const float* s_ry, const float* s_ir,
                                              const float* s_ic) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
 #pragma unroll
   for (int bm = 0; bm < TL::FM; ++bm) {
 #pragma unroll
@@ -305,23 +328,24 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN]
 }
 
 // bf16: G'_ij of this wave's TM x TN accumulators, staged through LDS as
-// [j][i] (row pitch GT_PITCH bytes; 4 consecutive i per 8-byte write), then
+// [j][i] (row pitch gt_pitch(BM) = 2 BM + 16 bytes; 4 consecutive i per 8-byte write), then
 // written to GTb (row pitch bs) as whole 256-byte tile rows, 16 bytes per
 // lane.  MASK zeroes the diagonal and entries outside [0, N).  Every row of
 // the tile is written (zeros for j >= N), so the contractions may read a
-// tile's rows and columns past N as zeros.  lds must hold BN * GT_PITCH bytes
+// tile's rows and columns past N as zeros.  lds must hold BN * gt_pitch(BM) bytes
 // and be free (no wave still reading it).
 // The 8-byte chunk c of row j sits at chunk c ^ ((j >> 4) & 1): the 32 lanes
 // of a half-wave write one chunk of 32 consecutive rows, which then fall on
 // 32 distinct bank pairs (rows j and j + 16 would share them at this pitch).
-constexpr int GT_PITCH = 272;
+constexpr int gt_pitch(int bm) { return 2 * bm + 16; }
 template <class TL, bool LIT, bool NORM, bool MASK>
 __device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0, int N,
                                                   uint16_t* __restrict__ GTb, int bs, const float* s_rx,
                                                   const float* s_ry, const float* s_ir, const float* s_ic,
                                                   char* lds) {
-  static_assert(TL::BM * 2 + 16 <= GT_PITCH && GT_PITCH % 16 == 0, "tile row fits the pitch");
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+  constexpr int PITCH = gt_pitch(TL::BM);
+  static_assert(PITCH % 256 == 16, "rows j and j + 16 share banks only as the swizzle assumes");
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
 #pragma unroll
   for (int bm = 0; bm < TL::FM; ++bm) {
 #pragma unroll
@@ -346,7 +370,7 @@ __device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL
         }
         const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g4, lane);
         const int chunk = (ml >> 2) ^ ((nl >> 4) & 1);
-        PackBf16::store4((uint16_t*)(lds + nl * GT_PITCH + chunk * 8), gv[0], gv[1], gv[2], gv[3]);
+        TL::store4((uint16_t*)(lds + nl * PITCH + chunk * 8), gv[0], gv[1], gv[2], gv[3]);
       }
     }
   }
@@ -356,9 +380,9 @@ __device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL
   // config 4 backward 22.6 -> 21.9 ms)
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   constexpr int VPR = TL::BM * 2 / 16;  // 16-byte vectors per tile row
-  for (int v = threadIdx.x; v < TL::BN * VPR; v += 256) {
+  for (int v = threadIdx.x; v < TL::BN * VPR; v += TL::NT) {
     const int row = v / VPR, cv = v - row * VPR;
-    u32x4 u = *(const u32x4*)(lds + row * GT_PITCH + cv * 16);
+    u32x4 u = *(const u32x4*)(lds + row * PITCH + cv * 16);
     if ((row >> 4) & 1) u = u32x4{u.z, u.w, u.x, u.y};  // undo the chunk swizzle
     __builtin_nontemporal_store(u, (u32x4*)(GTb + (int64_t)row * bs + cv * 8));
   }
@@ -375,19 +399,21 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
                                             char* lds, float* s_rx, float* s_ry, float* s_ir, float* s_ic) {
   const int64_t n64 = N;
   const int t = threadIdx.x;
-  typename TL::Op A{X + (int64_t)i0 * ldx, ldx, min(N - i0, TL::BM), kmax};
-  typename TL::Op B{Y + (int64_t)j0 * ldy, ldy, min(N - j0, TL::BN), kmax};
+  const auto A = tile_op<TL>(X + (int64_t)i0 * ldx, ldx, min(N - i0, TL::BM), kmax);
+  const auto B = tile_op<TL>(Y + (int64_t)j0 * ldy, ldy, min(N - j0, TL::BN), kmax);
   f32x16 acc[TL::FM][TL::FN];
   TL::template run<VEC, VEC>(A, B, D, lds, acc);
-  for (int u = t; u < TL::BM; u += 256) {
+  // 1/R_i and 1/C_j carry the storage scale of G' (a power of two: exact)
+  constexpr float GS = GScale<T>::value;
+  for (int u = t; u < TL::BM; u += TL::NT) {
     const bool ok = i0 + u < N;
     s_rx[u] = (NORM && ok) ? ws[WS_RX * n64 + i0 + u] : 1.f;
-    s_ir[u] = ok ? ws[WS_INV_ROW * n64 + i0 + u] : 0.f;
+    s_ir[u] = ok ? GS * ws[WS_INV_ROW * n64 + i0 + u] : 0.f;
   }
-  for (int u = t; u < TL::BN; u += 256) {
+  for (int u = t; u < TL::BN; u += TL::NT) {
     const bool ok = j0 + u < N;
     s_ry[u] = (NORM && ok) ? ws[WS_RY * n64 + j0 + u] : 1.f;
-    s_ic[u] = (!LIT && ok) ? ws[WS_INV_COL * n64 + j0 + u] : 0.f;
+    s_ic[u] = (!LIT && ok) ? GS * ws[WS_INV_COL * n64 + j0 + u] : 0.f;
   }
   __syncthreads();
   const bool diag = i0 < j0 + TL::BN && j0 < i0 + TL::BM;
@@ -426,8 +452,8 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
   // entries of G' and XT/YT at k in [qn, round8(qn)) are stored zeros
   const int kq = (qn + 7) & ~7;
   // A: rows tm*BM.. of the block (K-major), or columns tm*BM.. of a transposed block
-  typename TC::Op A{Gblk + (TC::TA ? (int64_t)(tm * TC::BM) : (int64_t)(tm * TC::BM) * bg.bs), bg.bs, TC::BM, kq};
-  typename TC::Op B{OT + (int64_t)d0 * ldt + q0, ldt, min(D - d0, TC::BN), kq};
+  const auto A = tile_op<TC>(Gblk + (TC::TA ? (int64_t)(tm * TC::BM) : (int64_t)(tm * TC::BM) * bg.bs), bg.bs, TC::BM, kq);
+  const auto B = tile_op<TC>(OT + (int64_t)d0 * ldt + q0, ldt, min(D - d0, TC::BN), kq);
   f32x16 acc[TC::FM][TC::FN];
   TC::template run<true, true>(A, B, kq, lds, acc);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TC::WN, wn = w % TC::WN;
@@ -444,10 +470,11 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
           // a fire-and-forget add in L2 instead of a load-add-store round trip;
           // the tile has one owner per launch, so the summation order (launch
           // order) and the result are deterministic
+          const float v = acc[bm][bn][r] * (1.f / GScale<T>::value);
           if (accumulate)
-            __hip_atomic_fetch_add(p, acc[bm][bn][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           else
-            *p = acc[bm][bn][r];
+            *p = v;
         }
       }
     }
@@ -502,18 +529,17 @@ __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int
 // One pipeline step: G' tiles of diagonal diag_g and, for fp32, the
 // contractions of diagonal diag_c (bf16 runs those in k_grad_contract).
 template <typename T, bool LIT, bool NORM, bool VEC>
-__global__ __launch_bounds__(256, Occ<T>::bwd) void k_grad_step(const T* __restrict__ X, int64_t ldx,
+__global__ __launch_bounds__((FwdTile<T, VEC>::NT), Occ<T>::bwd) void k_grad_step(const T* __restrict__ X, int64_t ldx,
                                                                const T* __restrict__ Y, int64_t ldy, int N, int D,
                                                                int kmax, float c, const float* __restrict__ ws,
                                                                GradBufs gb, BlockGrid bg, StepPlan sp,
                                                                float* __restrict__ acc_x, float* __restrict__ acc_y) {
   using TF = FwdTile<T, VEC>;
-  static_assert(TF::WM == 2 && TF::WN == 2, "epilogues assume 2 x 2 waves");
   constexpr bool FUSED = !GtOnly<T>::value;  // contractions in this kernel
   using TCX = typename std::conditional<FUSED, ConTileX<T>, TF>::type;
   using TCY = typename std::conditional<FUSED, ConTileY<T>, TF>::type;
-  static_assert(TF::NT == 256 && TCX::NT == 256 && TCY::NT == 256, "256-thread tiles");
-  constexpr int GT_LDS = GtOnly<T>::value ? TF::BN * GT_PITCH : 0;
+  static_assert(TCX::NT == TF::NT && TCY::NT == TF::NT, "one workgroup size per launch");
+  constexpr int GT_LDS = GtOnly<T>::value ? TF::BN * gt_pitch(TF::BM) : 0;
   __shared__ __attribute__((aligned(1024)))
   char lds[CMax<CMax<TF::LDS_BYTES, GT_LDS>::value, CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value>::value];
   __shared__ float s_rx[TF::BM], s_ry[TF::BN], s_ir[TF::BM], s_ic[TF::BN];

@@ -11,9 +11,13 @@ template <> struct Elem<float> {
   static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
   static __device__ __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
 };
-template <> struct Elem<uint16_t> {
+template <> struct Elem<uint16_t> {  // bf16 bits
   static __device__ __forceinline__ float load(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
   static __device__ __forceinline__ void store(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+};
+template <> struct Elem<_Float16> {
+  static __device__ __forceinline__ float load(const _Float16* p, int64_t i) { return (float)p[i]; }
+  static __device__ __forceinline__ void store(_Float16* p, int64_t i, float v) { p[i] = (_Float16)v; }
 };
 
 // Per row i: rx = 1/max(||x_i||, 1e-12) (or 1), ry likewise, diag = x_i . y_i.

@@ -1,15 +1,15 @@
 // Tile geometry of the MFMA kernels, shared by host and device code.
 //
 //   fp32                      128 x 128 tiles everywhere (mec_gemm_f32.h)
-//   bf16, 16-byte vectors     forward sums and gradient-matrix tiles 128 x 256
-//                             (x rows x y rows), direct global->LDS loads
-//                             (mec_gemm_bf16_dma.h); contractions 256 x 256
+//   bf16 / fp16, 16-byte      forward sums and gradient-matrix tiles 128 x 256
+//   vectors                   (x rows x y rows), direct global->LDS loads
+//                             (mec_gemm_16_dma.h); contractions 256 x 256
 //                             (output rows x feature columns, 8 waves) in a
 //                             kernel of their own
-//   bf16, other layouts       forward sums and gradient-matrix tiles 128 x 128
-//                             staged through registers (mec_gemm_bf16.h);
-//                             the contractions read internal buffers, which
-//                             are always 16-byte vectors, so they keep 256 x 256
+//   bf16 / fp16, other        forward sums and gradient-matrix tiles 128 x 128
+//   layouts                   staged through registers (mec_gemm_16.h); the
+//                             contractions read internal buffers, which are
+//                             always 16-byte vectors, so they keep 256 x 256
 //
 // The backward's block decomposition uses blocks of a multiple of
 // block_quantum(dtype) rows, so that every tile kind divides a block.
@@ -24,11 +24,12 @@ struct TileDims {
 
 constexpr int kDtypeF32 = 0;
 constexpr int kDtypeBF16 = 1;
+constexpr int kDtypeF16 = 2;
 
 // forward sums and gradient-matrix tiles (x rows x y rows)
 inline TileDims fwd_tile_dims(int dtype, bool vec) {
-  if (dtype == kDtypeF32) return {128, 128};
-  return vec ? TileDims{128, 256} : TileDims{128, 128};
+  if (dtype == kDtypeF32 || !vec) return {128, 128};
+  return {128, 256};
 }
 // contraction tiles (output rows x feature columns)
 inline TileDims con_tile_dims(int dtype) {

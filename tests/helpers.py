@@ -39,6 +39,7 @@ def max_rel(g, ref):
 TOL = {
     torch.float32: dict(loss=1e-4, grad=1e-3),
     torch.bfloat16: dict(loss=1e-2, grad=1e-2),
+    torch.float16: dict(loss=1e-2, grad=1e-2),
 }
 
 

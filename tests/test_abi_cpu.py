@@ -38,11 +38,11 @@ def test_sizes():
     assert lib.mec_workspace_floats(1025) == 8 * 1025 + 4
     assert lib.mec_workspace_floats(0) < 0
     # scratch is O(n*d): two block diagonals of the N x N gradient matrix (fp32:
-    # in both layouts; bf16: transposed only), plus transposed copies of the two
-    # inputs; blocks are a multiple of 128 rows (fp32) or 256 rows (bf16: its
-    # tiles are 128 x 256 and 256 x 128)
+    # in both layouts; bf16 and fp16: transposed only), plus transposed copies of
+    # the two inputs; blocks are a multiple of 128 rows (fp32) or 256 rows (the
+    # 16-bit types: their tiles are 128 x 256 and 256 x 256)
     for n, d in [(1024, 512), (32768, 1152), (65536, 768), (262144, 1152), (1000, 3), (777, 1152)]:
-        for dt, elem, q, copies in [(0, 4, 128, 4), (1, 2, 256, 2)]:
+        for dt, elem, q, copies in [(0, 4, 128, 4), (1, 2, 256, 2), (2, 2, 256, 2)]:
             b = lib.mec_grad_scratch_bytes(n, d, dt)
             bs, nb = _lib.grad_blocking(n, d, dt)
             assert bs % q == 0 and nb * bs >= n > (nb - 1) * bs, (n, d, dt, bs, nb)
@@ -56,7 +56,7 @@ def test_sizes():
 def test_blocking_prefers_exact_divisors():
     # the headline and bf16 shapes split into equal blocks (no short last block)
     for n, d in [(32768, 1152), (65536, 768), (262144, 1152), (1024, 512)]:
-        for dt in (0, 1):
+        for dt in (0, 1, 2):
             bs, nb = _lib.grad_blocking(n, d, dt)
             assert nb * bs == n, (n, d, dt, bs, nb)
     assert _lib.grad_blocking(32768, 1152, 0) == (2048, 16)
@@ -82,6 +82,21 @@ def test_sumexp_rejects_invalid_arguments(field, value, needle):
                         a["temperature"], 16, None)
     assert rc == _lib.MEC_ERR_INVALID
     assert needle in _lib.last_error()
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_16bit_size_limit(dtype):
+    # the 16-bit contractions address transposed panels with 32-bit offsets
+    lib = _lib.load()
+    a = dict(VALID, dtype=dtype)
+    for n, want in [((1 << 22) + 1, _lib.MEC_ERR_UNSUPPORTED), (1 << 22, None)]:
+        rc = lib.mec_sumexp(a["x"], a["ldx"], a["y"], a["ldy"], n, a["d"], dtype, a["mode"], a["normalize"],
+                            a["temperature"], None, None)
+        if want is None:
+            # passes the size check and stops at the null workspace, before any launch
+            assert rc == _lib.MEC_ERR_INVALID and "workspace" in _lib.last_error()
+        else:
+            assert rc == want and "2^22" in _lib.last_error()
 
 
 def test_grad_rejects_small_scratch_and_missing_outputs():

@@ -84,6 +84,7 @@ def test_check_inputs_shape_and_dtype_rules():
     with pytest.raises(TypeError, match="dtype mismatch"):
         check_inputs(fake((4, 8)), fake((4, 8), torch.bfloat16))
     check_inputs(fake((4, 8), torch.bfloat16), fake((4, 8), torch.bfloat16))
+    check_inputs(fake((4, 8), torch.float16), fake((4, 8), torch.float16))
 
 
 def test_product_path_does_not_import_oracle():
