@@ -31,11 +31,14 @@
  *     x is the row side of S = x^ y^T: image for CLIP, text for LiT.
  *   - dtype: MEC_DTYPE_F32 (float), MEC_DTYPE_BF16 (uint16 bfloat16 bits) or
  *     MEC_DTYPE_F16 (uint16 IEEE binary16 bits).  All arithmetic accumulates
- *     in fp32 (sums and loss in fp64).  Sizes: 1 <= d <= 2^20; 1 <= n <= 2^30
+ *     in fp32; the loss is reduced in fp64.  Sizes: 1 <= d <= 2^20; 1 <= n <= 2^30
  *     for fp32 and n <= 2^22 for the 16-bit types (MEC_ERR_UNSUPPORTED
  *     beyond).  16-bit rows that are 16-byte aligned (x, y 16-byte aligned, d,
  *     ldx, ldy multiples of 8) use the direct-to-LDS tiles; other layouts are
  *     supported at lower speed.
+ *   - mode: MEC_MODE_CLIP or MEC_MODE_LIT, optionally OR
+ *     MEC_FLAG_DETERMINISTIC.  Every function accepts the flag; only the
+ *     forward sums (mec_sumexp, mec_forward) depend on it.
  *   - All work is enqueued on `stream` (a hipStream_t; NULL = default
  *     stream).  No function synchronises the host and none allocates device
  *     memory: the workspace and the gradient scratch are caller-owned.
@@ -62,6 +65,13 @@ extern "C" {
 
 #define MEC_MODE_CLIP 0 /* symmetric image<->text loss, gradients for x and y */
 #define MEC_MODE_LIT 1  /* text->image only (x = text), gradient for x only */
+#define MEC_MODE_MASK 0xff
+/* OR into `mode`: the forward sums are formed without atomics across
+ * workgroups, in a fixed order, so the loss and (through the sums) the
+ * gradients are bitwise reproducible for the same inputs on the same device.
+ * The backward is deterministic in either mode.  Costs one extra pass over
+ * the similarity tiles for CLIP (the column sums). */
+#define MEC_FLAG_DETERMINISTIC 0x100
 
 /* Thread-local message for the last error on this thread ("" if none). */
 const char* mec_last_error(void);
@@ -72,10 +82,11 @@ const char* mec_version(void);
 /* Number of floats of the per-call workspace: 8 vectors of length n
  * (inverse norms rx, ry; raw diagonal x_i.y_i; off-diagonal row/column sums
  * of E = exp((S-1)/T); 1/R; 1/C; diagonal gradient coefficient), then
- * ceil(n/1024) doubles of loss partials (mec_finalize).  The workspace must
- * be 8-byte aligned.  The same workspace must be passed to mec_forward and
- * the matching mec_backward (it replaces ctx.save_for_backward of the sums,
- * clip_loss.py:199). */
+ * ceil(n/1024) doubles of loss partials (mec_finalize), then 8 x n floats
+ * of partial sums (the deterministic forward, MEC_FLAG_DETERMINISTIC).  The
+ * workspace must be 8-byte aligned.  The same workspace must be passed to
+ * mec_forward and the matching mec_backward (it replaces
+ * ctx.save_for_backward of the sums, clip_loss.py:199). */
 int64_t mec_workspace_floats(int64_t n);
 
 /* Bytes of gradient scratch needed by mec_grad / mec_grad_step /

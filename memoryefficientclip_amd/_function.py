@@ -11,7 +11,10 @@ This mirrors the glue of the reference's autograd Functions
 * the optional L2 normalisation is fused (``normalize=True``) instead of
   running ``F.normalize`` (``clip_loss.py:266-268``) as separate PyTorch ops;
 * any N >= 1 and D >= 1 is accepted, with exact masking of ragged tiles, and
-  inputs with a row stride are read in place (no ``.contiguous()`` copy).
+  inputs with a row stride are read in place (no ``.contiguous()`` copy);
+* under ``torch.use_deterministic_algorithms(True)`` the loss and gradients
+  are bitwise reproducible (the reference's relaxed atomics are not,
+  ``clip_loss.py:63-64,155-156``).
 """
 from __future__ import annotations
 
@@ -70,7 +73,10 @@ def forward(ctx, x: torch.Tensor, y: torch.Tensor, temperature: float, mode: int
     with torch.cuda.device(dev):
         ws = torch.empty(_lib.load().mec_workspace_floats(n), dtype=torch.float32, device=dev)
         loss = torch.empty((), dtype=torch.float32, device=dev)
-        _lib.call("mec_forward", x.data_ptr(), ldx, y.data_ptr(), ldy, n, d, dt, mode, int(normalize),
+        # under torch.use_deterministic_algorithms(True) the forward sums are
+        # formed without atomics (the backward is deterministic either way)
+        fmode = mode | (_lib.FLAG_DETERMINISTIC if torch.are_deterministic_algorithms_enabled() else 0)
+        _lib.call("mec_forward", x.data_ptr(), ldx, y.data_ptr(), ldy, n, d, dt, fmode, int(normalize),
                   temperature, ws.data_ptr(), loss.data_ptr(), _stream(dev))
     ctx.save_for_backward(x, y, ws)
     ctx.mec = (ldx, ldy, n, d, dt, mode, bool(normalize), temperature,

@@ -23,6 +23,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 MODE_CLIP = 0
 MODE_LIT = 1
+FLAG_DETERMINISTIC = 0x100  # OR into the mode of mec_sumexp / mec_forward
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64

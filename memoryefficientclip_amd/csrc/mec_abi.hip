@@ -59,8 +59,11 @@ int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   return MEC_OK;
 }
 
+// mode = MEC_MODE_CLIP or MEC_MODE_LIT, optionally OR MEC_FLAG_DETERMINISTIC
 int check_mode(int mode) {
-  if (mode != MEC_MODE_CLIP && mode != MEC_MODE_LIT) return fail(MEC_ERR_INVALID, "unknown mode %d", mode);
+  const int base = mode & MEC_MODE_MASK, flags = mode & ~MEC_MODE_MASK;
+  if ((base != MEC_MODE_CLIP && base != MEC_MODE_LIT) || (flags & ~MEC_FLAG_DETERMINISTIC))
+    return fail(MEC_ERR_INVALID, "unknown mode %d", mode);
   return MEC_OK;
 }
 
@@ -68,6 +71,13 @@ int check_temperature(float t) {
   if (!(t > 0.f) || !std::isfinite(t)) return fail(MEC_ERR_INVALID, "temperature must be finite and > 0");
   return MEC_OK;
 }
+
+bool is_lit(int mode) { return (mode & MEC_MODE_MASK) == MEC_MODE_LIT; }
+
+// workspace: WS_NSLOTS vectors of n floats, the fp64 loss partials, then the
+// DET_SPLITS x n partial sums of the deterministic forward
+int64_t loss_partials_floats(int64_t n) { return 2 * ((n + FIN_ROWS - 1) / FIN_ROWS); }
+int64_t det_partials_offset(int64_t n) { return (int64_t)WS_NSLOTS * n + loss_partials_floats(n); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -185,7 +195,7 @@ const char* mec_version(void) { return "memoryefficientclip_amd 0.1.0 gfx950"; }
 
 int64_t mec_workspace_floats(int64_t n) {
   if (n < 1 || n > kMaxN) return -1;
-  return (int64_t)WS_NSLOTS * n + 2 * ((n + FIN_ROWS - 1) / FIN_ROWS);
+  return det_partials_offset(n) + (int64_t)DET_SPLITS * n;
 }
 
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype) {
@@ -225,7 +235,28 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   const int64_t nwg = (int64_t)tiles_m * tiles_n;
   if (nwg > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "forward grid too large");
   dim3 grid((unsigned)nwg);
-  const bool lit = mode == MEC_MODE_LIT;
+  const bool lit = is_lit(mode);
+  if (mode & MEC_FLAG_DETERMINISTIC) {
+    // row sums, then (CLIP) the column sums as the row sums of the swapped problem
+    const int64_t n64 = n;
+    float* part = workspace + det_partials_offset(n);
+    const int64_t nwg_det = (int64_t)tiles_m * DET_SPLITS;
+    if (nwg_det > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "forward grid too large");
+    const unsigned sum_grid = (unsigned)((n + 255) / 256);
+    DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, {
+      k_sumexp_rows_det<T, NORM, VEC><<<(unsigned)nwg_det, FwdTile<T, VEC>::NT, 0, s>>>(
+          (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace + WS_RX * n64, workspace + WS_RY * n64, part,
+          tiles_m, tiles_n);
+      k_det_sum<<<sum_grid, 256, 0, s>>>(part, N, workspace + WS_ROW_OFF * n64);
+      if (!lit) {
+        k_sumexp_rows_det<T, NORM, VEC><<<(unsigned)nwg_det, FwdTile<T, VEC>::NT, 0, s>>>(
+            (const T*)y, ldy, (const T*)x, ldx, N, D, D, c, workspace + WS_RY * n64, workspace + WS_RX * n64,
+            part, tiles_m, tiles_n);
+        k_det_sum<<<sum_grid, 256, 0, s>>>(part, N, workspace + WS_COL_OFF * n64);
+      }
+    })));
+    return check_launch("sumexp (deterministic)");
+  }
   DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
       k_sumexp<T, LIT, NORM, VEC><<<grid, FwdTile<T, VEC>::NT, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, D,
                                                                       c, workspace, tiles_m, tiles_n)))));
@@ -245,7 +276,7 @@ int mec_finalize(int64_t n, int mode, float temperature, float* workspace, float
   const int nparts = (int)((n + FIN_ROWS - 1) / FIN_ROWS);
   // partials after the 8 slots (8 n floats: 8-byte aligned when the workspace is)
   double* partial = (double*)(workspace + (int64_t)WS_NSLOTS * n);
-  if (mode == MEC_MODE_LIT) {
+  if (is_lit(mode)) {
     k_finalize_rows<true><<<nparts, FIN_ROWS, 0, s>>>((int)n, inv_t, workspace, partial);
     k_finalize_sum<true><<<1, 1024, 0, s>>>((int)n, nparts, partial, loss);
   } else {
@@ -289,7 +320,7 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
   if (!rc) rc = check_mode(mode);
   if (!rc) rc = check_temperature(temperature);
   if (rc) return rc;
-  const bool lit = mode == MEC_MODE_LIT;
+  const bool lit = is_lit(mode);
   if (lit) acc_y = nullptr;
   if (!workspace || !scratch) return fail(MEC_ERR_INVALID, "workspace and scratch must be non-null");
   if (!acc_x && !acc_y) return fail(MEC_ERR_INVALID, "no gradient requested (acc_x%s null)", lit ? "" : " and acc_y");
@@ -401,7 +432,7 @@ int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   if (!rc) rc = check_mode(mode);
   if (rc) return rc;
   if (!std::isfinite(grad_scale)) return fail(MEC_ERR_INVALID, "grad_scale must be finite");
-  const bool lit = mode == MEC_MODE_LIT;
+  const bool lit = is_lit(mode);
   if (lit) acc_y = nullptr, dy = nullptr;
   if (!workspace) return fail(MEC_ERR_INVALID, "workspace must be non-null");
   if ((acc_x == nullptr) != (dx == nullptr) || (acc_y == nullptr) != (dy == nullptr))

@@ -30,6 +30,9 @@ enum WsSlot {
   WS_INV_ROW = 5, WS_INV_COL = 6, WS_KAPPA = 7, WS_NSLOTS = 8
 };
 constexpr int FIN_ROWS = 1024;  // rows per workgroup of the loss finalize
+// deterministic forward: column splits per row tile, whose DET_SPLITS x n
+// partial row sums follow the loss partials in the workspace
+constexpr int DET_SPLITS = 8;
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 

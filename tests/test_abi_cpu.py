@@ -34,8 +34,9 @@ def test_library_exports_every_declared_symbol():
 
 def test_sizes():
     lib = _lib.load()
-    assert lib.mec_workspace_floats(1000) == 8000 + 2      # 8 vectors + one fp64 loss partial
-    assert lib.mec_workspace_floats(1025) == 8 * 1025 + 4
+    # 8 vectors, ceil(n / 1024) fp64 loss partials, 8 vectors of deterministic partial sums
+    assert lib.mec_workspace_floats(1000) == 8000 + 2 + 8000
+    assert lib.mec_workspace_floats(1025) == 8 * 1025 + 4 + 8 * 1025
     assert lib.mec_workspace_floats(0) < 0
     # scratch is O(n*d): two block diagonals of the N x N gradient matrix (fp32:
     # in both layouts; bf16 and fp16: transposed only), plus transposed copies of
@@ -82,6 +83,20 @@ def test_sumexp_rejects_invalid_arguments(field, value, needle):
                         a["temperature"], 16, None)
     assert rc == _lib.MEC_ERR_INVALID
     assert needle in _lib.last_error()
+
+
+@pytest.mark.parametrize("mode,ok", [(0, True), (1, True), (0x100, True), (0x101, True), (2, False),
+                                     (0x102, False), (0x200, False), (0x300, False), (-1, False)])
+def test_mode_and_deterministic_flag(mode, ok):
+    # validation only: a null workspace stops every valid call before any launch
+    lib = _lib.load()
+    a = dict(VALID, mode=mode)
+    rc = lib.mec_sumexp(a["x"], a["ldx"], a["y"], a["ldy"], a["n"], a["d"], a["dtype"], mode, a["normalize"],
+                        a["temperature"], None, None)
+    assert rc == _lib.MEC_ERR_INVALID
+    assert ("workspace" if ok else "mode") in _lib.last_error()
+    rc = lib.mec_finalize(10, mode, 0.07, None, None, None)
+    assert rc == _lib.MEC_ERR_INVALID and (("non-null" if ok else "mode") in _lib.last_error())
 
 
 @pytest.mark.parametrize("dtype", [1, 2])
