@@ -15,7 +15,23 @@
 #include <hip/hip_bf16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace mec {
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time (the
+// index can then be a template argument, e.g. an instruction's immediate offset)
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for_from(F& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for_from<I + 1, N>(f);
+  }
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_from<0, N>(f);
+}
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));

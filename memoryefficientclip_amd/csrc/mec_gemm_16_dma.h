@@ -156,10 +156,28 @@ struct Frags {
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
+// Operand reads from LDS, as inline asm.  The compiler cannot tell these
+// reads from the global->LDS loads still in flight into the other stages,
+// and in some loop shapes it waits for every outstanding load (vmcnt(0))
+// before each group of reads, which serialises the prefetch ring.  In asm
+// they carry no such wait; the mainloop awaits their completion explicitly
+// (lgkm_wait) before the MFMAs that use them, and wait_barrier orders them
+// against the loads that refill their stage.
+__device__ __forceinline__ uint32_t lds_off(const char* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+template <int OFF>
+__device__ __forceinline__ i16x8 lds_read_b128(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536 && OFF % 16 == 0, "ds_read_b128 offset");
+  i16x8 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+  return v;
+}
 // 4 k-rows of one column per lane (see the transposed-A note above)
 __device__ __forceinline__ i16x4_t read_tr4(const char* p) {
-  return __builtin_bit_cast(
-      i16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)p));
+  i16x4_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(lds_off(p)) : "memory");
+  return v;
 }
 
 template <class G>
@@ -188,11 +206,30 @@ __device__ __forceinline__ void read_frags(const char* stage, int s, Frags<G>& f
       f.a[i] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   } else {
-#pragma unroll
-    for (int i = 0; i < G::FM; ++i) f.a[i] = *(const i16x8*)(stage + (wm * G::TM + i * 32 + q) * ROWB + off);
+    const uint32_t abase = lds_off(stage + (wm * G::TM + q) * ROWB + off);
+    static_for<G::FM>([&](auto i) { f.a[i] = lds_read_b128<i * 32 * ROWB>(abase); });
   }
+  const uint32_t bbase = lds_off(stage + (G::BM + wn * G::TN + q) * ROWB + off);
+  static_for<G::FN>([&](auto j) { f.b[j] = lds_read_b128<j * 32 * ROWB>(bbase); });
+}
+
+// LDS reads per read_frags call
+template <class G>
+constexpr int frag_reads() {
+  return (G::TA ? 2 * G::FM : G::FM) + G::FN;
+}
+
+// at most N LDS operations outstanding (the reads of `f` were issued before
+// the last N), then f's registers are tied to the wait so that no MFMA using
+// them is scheduled above it
+template <int N, class G>
+__device__ __forceinline__ void lgkm_wait(Frags<G>& f) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
 #pragma unroll
-  for (int j = 0; j < G::FN; ++j) f.b[j] = *(const i16x8*)(stage + (G::BM + wn * G::TN + j * 32 + q) * ROWB + off);
+  for (int i = 0; i < G::FM; ++i) asm volatile("" : "+v"(f.a[i]));
+#pragma unroll
+  for (int j = 0; j < G::FN; ++j) asm volatile("" : "+v"(f.b[j]));
 }
 
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
@@ -274,12 +311,15 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
     }
     sched_fence();
     read_frags<G>(cs, 1, f1);
+    lgkm_wait<frag_reads<G>()>(f0);  // f0 landed; f1's reads may still be in flight
     sched_fence();
     mfma_step<G, G::LPS, G::IPW>(f0, acc, lp, ld, k0, fs);
     sched_fence();
     cur = cur + 1 == S ? 0 : cur + 1;
     fre = fre + 1 == S ? 0 : fre + 1;
   }
+  lgkm_wait<0>(f1);
+  sched_fence();
   mfma_step<G, 0, 0>(f1, acc, lp, false, 0, lds);
 }
 
