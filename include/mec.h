@@ -92,9 +92,10 @@ int64_t mec_workspace_floats(int64_t n);
 /* Bytes of gradient scratch needed by mec_grad / mec_grad_step /
  * mec_backward for (n, d, dtype), all in the input dtype: two buffers holding
  * one block diagonal of the off-diagonal gradient matrix each (nb blocks of
- * bs x bs, bs ~ 2d for fp32 and ~8d for the 16-bit types), for fp32 the same
- * blocks transposed as well, and transposed normalised copies of x and y
- * ([d][n rounded up to 128]); O(n*d) in total.  Returns < 0 on bad args. */
+ * bs x bs; bs ~ 2d for fp32, ~8d but at most 32512 for the 16-bit types),
+ * for fp32 the same blocks transposed as well, and transposed normalised
+ * copies of x and y ([d][n rounded up to 128]); O(n*d) in total.  Returns
+ * < 0 on bad args. */
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype);
 
 /* Block decomposition of the backward for (n, d, dtype): the n x n gradient

@@ -81,11 +81,20 @@ int64_t det_partials_offset(int64_t n) { return (int64_t)WS_NSLOTS * n + loss_pa
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The 16-bit direct-to-LDS core addresses each operand panel with 32-bit
+// byte offsets and masks with the offset 2^31, so a panel (at most 256 rows)
+// must span less than 2^31 bytes: (rows - 1) * ld + kmax < 2^30 elements.
+constexpr int64_t kDmaMaxElems = (int64_t(1) << 30) - 1;
+constexpr int64_t kDmaRows = 256;
+
 // 16-byte vector loads are legal when every row start is 16-byte aligned and
-// rows hold a whole number of vectors.
+// rows hold a whole number of vectors; for the 16-bit types this also selects
+// the direct-to-LDS core, whose panels must fit its 32-bit offsets.
 bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, int dtype) {
   const int64_t per = dtype == MEC_DTYPE_F32 ? 4 : 8;
-  return aligned16(x) && aligned16(y) && d % per == 0 && ldx % per == 0 && ldy % per == 0;
+  if (!(aligned16(x) && aligned16(y) && d % per == 0 && ldx % per == 0 && ldy % per == 0)) return false;
+  const int64_t ld = ldx > ldy ? ldx : ldy;
+  return dtype == MEC_DTYPE_F32 || (kDmaRows - 1) * ld + d <= kDmaMaxElems;
 }
 
 // Block decomposition of the N x N gradient matrix for the backward: nb
@@ -104,18 +113,22 @@ bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, i
 void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
   const int64_t q = block_quantum(dtype);
   const int64_t tiles = (n + q - 1) / q;
+  // 16-bit: a transposed gradient-matrix block is a direct-to-LDS operand
+  // ((bs - 1) * bs + 256 elements within kDmaMaxElems): bs <= 127 * 256
+  const int64_t cap = dtype == MEC_DTYPE_F32 ? tiles : 127;
   int64_t target = ((dtype == MEC_DTYPE_F32 ? 2 : 8) * d + q - 1) / q;
   if (target < 1024 / q) target = 1024 / q;
   if (const char* env = std::getenv("MEC_GRAD_BLOCK_TILES")) {
     long v = std::strtol(env, nullptr, 10);
     if (v >= 1 && v <= 4096) target = v;
   }
+  if (target > cap) target = cap;
   int64_t tb;
   if (target >= tiles) {
     tb = tiles;
   } else {
     int64_t best = -1;
-    for (int64_t c = (target + 1) / 2; c <= 2 * target && c <= tiles; ++c) {
+    for (int64_t c = (target + 1) / 2; c <= 2 * target && c <= tiles && c <= cap; ++c) {
       if (tiles % c) continue;
       const int64_t dc = c > target ? c - target : target - c;
       const int64_t db = best > target ? best - target : target - best;

@@ -94,13 +94,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_t(const Operand& op)
 }
 
 // This wave's IPW loads of every chunk: per-lane byte offset at k = 0, the
-// lane's k-vector start, and the 1 KB LDS block each load fills.
+// lane's k-vector start, and the 1 KB LDS block each load fills.  Load i of
+// wave w fills block b = i * NW + w, so blocks [0, BM / 16) (operand A) are
+// the loads i < A_LOADS of every wave: which operand a load reads is known at
+// compile time.
 template <class G>
 struct LoadPlan {
+  static constexpr int A_BLOCKS = G::BM / RPB;  // 1 KB blocks of A per stage (transposed A too)
+  static_assert(A_BLOCKS % G::NW == 0, "every wave loads whole rows of A blocks");
+  static constexpr int A_LOADS = A_BLOCKS / G::NW;
   __amdgpu_buffer_rsrc_t ra, rb;
   uint32_t voff[G::IPW];
   int kv;          // k of this lane's 16-byte vector within a chunk (K-major operands)
   int kr;          // k-row of this lane within a 1 KB block (transposed A: 0 or 1)
+  int w;           // wave index (uniform)
   int kmax_a, kmax_b;
   int64_t lda;     // transposed A: bytes per k-row
   __device__ __forceinline__ void init(const Operand& A, const Operand& B) {
@@ -109,42 +116,42 @@ struct LoadPlan {
     kmax_a = A.kmax;
     kmax_b = B.kmax;
     lda = A.ld * 2;
-    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rib = lane >> 2, phys = lane & 3;
     // rows of one load block are b*16 .. b*16+15, so swz(r) = (rib >> 2) & 3
     kv = (phys ^ swz(rib)) * 8;
     kr = lane >> 5;
 #pragma unroll
     for (int i = 0; i < G::IPW; ++i) {
-      const int b = w * G::IPW + i;
-      const bool isa = b * RPB < G::BM;
-      if (G::TA && isa) {
+      const int b = i * G::NW + w;
+      if (G::TA && i < A_LOADS) {
         // block b holds k-rows 2b, 2b+1 (within the chunk); lane l fills slot l % 32 of k-row 2b + l / 32
         const int krow = 2 * b + kr;
         const int slot = (lane & 31) ^ (4 * (krow & 3));
         voff[i] = (uint32_t)((int64_t)krow * A.ld + slot * 8) * 2;
       } else {
         const int r = b * RPB + rib;
-        voff[i] = (uint32_t)(((isa ? (int64_t)r * A.ld : (int64_t)(r - G::BM) * B.ld) + kv) * 2);
+        voff[i] = (uint32_t)(((i < A_LOADS ? (int64_t)r * A.ld : (int64_t)(r - G::BM) * B.ld) + kv) * 2);
       }
     }
   }
-  // load i of the chunk starting at k0 into `stage`
-  __device__ __forceinline__ void issue(int i, int k0, char* stage) const {
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int b = w * G::IPW + i;
-    const bool isa = b * RPB < G::BM;
+  // load i of the chunk starting at k0 into `stage`.  Chunks at or past kmax
+  // read as zeros (out-of-range offsets), so loads may run past the last chunk.
+  template <int I>
+  __device__ __forceinline__ void issue(int k0, char* stage) const {
+    constexpr bool isa = I < A_LOADS;
     uint32_t off, soff;
     if (G::TA && isa) {
-      off = (k0 + 2 * b + kr < kmax_a) ? voff[i] : OOB;
+      off = (k0 + 2 * (I * G::NW + w) + kr < kmax_a) ? voff[I] : OOB;
       soff = (uint32_t)(k0 * lda);
     } else {
-      off = (k0 + kv < (isa ? kmax_a : kmax_b)) ? voff[i] : OOB;
+      off = (k0 + kv < (isa ? kmax_a : kmax_b)) ? voff[I] : OOB;
       soff = (uint32_t)k0 * 2;
     }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(isa ? ra : rb,
-                                             (__attribute__((address_space(3))) void*)(stage + b * 1024), 16, off,
-                                             soff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        isa ? ra : rb, (__attribute__((address_space(3))) void*)(stage + (I * G::NW + w) * 1024), 16, off, soff, 0,
+        0);
   }
 };
 
@@ -249,27 +256,31 @@ __device__ __forceinline__ void wait_barrier() {
 // MFMAs of one k-step with loads [L0, L1) interleaved, in program order.
 template <class G, int L0, int L1>
 __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const LoadPlan<G>& lp,
-                                          bool do_load, int k0, char* stage) {
+                                          int k0, char* stage) {
   constexpr int NL = L1 - L0;
   static_assert(NL <= G::NMF, "at most one load per MFMA");
   // one load after every EVERY-th MFMA: floor(NMF / EVERY) >= NL slots
   constexpr int EVERY = NL > 0 ? G::NMF / (NL > 0 ? NL : 1) : G::NMF + 1;
-#pragma unroll
-  for (int m = 0; m < G::NMF; ++m) {
-    const int i = m / G::FN, j = m % G::FN;
-    acc[i][j] = mfma16_32x32x16<G::F16>(f.a[i], f.b[j], acc[i][j]);
-    if (NL > 0 && (m % EVERY) == EVERY - 1 && L0 + m / EVERY < L1) {
+  static_for<G::NMF>([&](auto mc) {
+    constexpr int m = mc;
+    acc[m / G::FN][m % G::FN] = mfma16_32x32x16<G::F16>(f.a[m / G::FN], f.b[m % G::FN], acc[m / G::FN][m % G::FN]);
+    if constexpr (NL > 0 && (m % EVERY) == EVERY - 1 && L0 + m / EVERY < L1) {
       sched_fence();
-      if (do_load) lp.issue(L0 + m / EVERY, k0, stage);
+      lp.template issue<L0 + m / EVERY>(k0, stage);
       sched_fence();
     }
-  }
+  });
 }
 
 // acc[i][j] (this wave's sub-tile) = sum_k A(m, k) * B(n, k) over k in [0, K),
 // K > 0 (chunks past kmax read as zero).  Uses LDS_BYTES of `lds`; ends with
-// every wave past its last LDS read of the ring (callers may reuse it after a
-// barrier).
+// every wave past its last LDS read of the ring and its loads landed
+// (callers may reuse the ring after a barrier).
+//
+// Every iteration issues the loads of chunk kt+S-1, also past the last chunk
+// (they read zeros into a stage nobody reads again): the loop has no branches
+// around its loads and the number of loads in flight at each wait is the
+// same, IPW * (S - 2).
 template <class G>
 __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int K, char* lds,
                                          f32x16 (&acc)[G::FM][G::FN]) {
@@ -284,43 +295,37 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
   lp.init(A, B);
   // prologue: chunks 0 .. S-2 in flight
 #pragma unroll
-  for (int c = 0; c + 1 < S; ++c)
-    if (c < nk) {
-#pragma unroll
-      for (int i = 0; i < G::IPW; ++i) lp.issue(i, c * BK, lds + c * G::STAGE);
-    }
+  for (int c = 0; c + 1 < S; ++c) static_for<G::IPW>([&](auto i) { lp.template issue<i>(c * BK, lds + c * G::STAGE); });
   Frags<G> f0, f1;
   int cur = 0;      // stage of chunk kt
   int fre = S - 1;  // stage of chunk kt-1 = stage of chunk kt+S-1
   for (int kt = 0; kt < nk; ++kt) {
-    // chunk kt landed: min(S-2, nk-1-kt) newer chunks may still be in flight
-    if (kt + S - 2 < nk) wait_barrier<G::IPW*(S - 2)>();
-    else wait_barrier<0>();
+    wait_barrier<G::IPW*(S - 2)>();  // chunk kt landed (chunks kt+1 .. kt+S-2 may be in flight)
     char* cs = lds + cur * G::STAGE;
     char* fs = lds + fre * G::STAGE;
-    const bool ld = kt + S - 1 < nk;
     const int k0 = (kt + S - 1) * BK;
     read_frags<G>(cs, 0, f0);
     sched_fence();
     // the previous chunk's last k-step (its operands are already in registers)
     if (kt > 0) {
-      mfma_step<G, 0, G::LPS>(f1, acc, lp, ld, k0, fs);
-    } else if (ld) {
-#pragma unroll
-      for (int i = 0; i < G::LPS; ++i) lp.issue(i, k0, fs);
+      mfma_step<G, 0, G::LPS>(f1, acc, lp, k0, fs);
+    } else {
+      static_for<G::LPS>([&](auto i) { lp.template issue<i>(k0, fs); });
     }
     sched_fence();
     read_frags<G>(cs, 1, f1);
     lgkm_wait<frag_reads<G>()>(f0);  // f0 landed; f1's reads may still be in flight
     sched_fence();
-    mfma_step<G, G::LPS, G::IPW>(f0, acc, lp, ld, k0, fs);
+    mfma_step<G, G::LPS, G::IPW>(f0, acc, lp, k0, fs);
     sched_fence();
     cur = cur + 1 == S ? 0 : cur + 1;
     fre = fre + 1 == S ? 0 : fre + 1;
   }
   lgkm_wait<0>(f1);
   sched_fence();
-  mfma_step<G, 0, 0>(f1, acc, lp, false, 0, lds);
+  mfma_step<G, 0, 0>(f1, acc, lp, 0, lds);
+  // the zero loads past the last chunk land before the caller reuses the ring
+  __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));
 }
 
 }  // namespace g16d

@@ -54,6 +54,18 @@ def test_sizes():
     assert lib.mec_grad_scratch_bytes(10, 10, 7) < 0
 
 
+def test_16bit_blocks_fit_the_32bit_operand_range():
+    # the direct-to-LDS core reads a transposed gradient-matrix block with 32-bit
+    # byte offsets masked at 2^31: (bs - 1) * bs + 256 elements of 2 bytes < 2^31
+    for n, d in [(65536, 8192), (65536, 4096), (33000, 4352), (2 ** 22, 1024), (40000, 100000)]:
+        for dt in (1, 2):
+            bs, nb = _lib.grad_blocking(n, d, dt)
+            assert bs <= 32512 and ((bs - 1) * bs + 256) * 2 < 2 ** 31, (n, d, bs)
+            assert nb * bs >= n > (nb - 1) * bs
+    # fp32 addresses with 64-bit pointers and keeps its ~2d blocks
+    assert _lib.grad_blocking(65536, 32768, 0)[0] == 65536
+
+
 def test_blocking_prefers_exact_divisors():
     # the headline and bf16 shapes split into equal blocks (no short last block)
     for n, d in [(32768, 1152), (65536, 768), (262144, 1152), (1024, 512)]:

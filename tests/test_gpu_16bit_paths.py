@@ -186,3 +186,40 @@ def test_f16_tiny_gradient_matrix_entries():
     ex, ey = max_rel(acc_x.cpu(), gp @ xh), max_rel(acc_y.cpu(), gp.T @ xh)
     say(f"  median entry {med:.2e}; acc_x max-rel {ex:.2e} acc_y max-rel {ey:.2e}")
     assert ex < TOL and ey < TOL
+
+
+def test_bf16_large_d_caps_the_block_size():
+    """D = 4352: the ~8D-row block target (34816 rows) would make a transposed
+    gradient-matrix block exceed the direct-to-LDS core's 2^31-byte operand
+    range; the blocking caps it (here: two blocks of 16640 rows).  Reference:
+    the dense definition in fp64, chunked over rows on the GPU."""
+    n, d, t = 33000, 4352, 0.07
+    bs, nb = _lib.grad_blocking(n, d, _lib.DTYPE_BF16)
+    assert bs <= 32512 and nb >= 2, (bs, nb)
+    a, b = correlated_pair(n, d, seed=17, dtype=torch.bfloat16)
+    say(f"bf16 CLIP n={n} d={d} blocks {nb} x {bs}")
+    loss, da, db = grads_of(MemoryEfficientCLIPLoss(t, True), a, b)
+    rl, rda, rdb = ref_fp64(a.to(DEV), b.to(DEV), t, False, True, 2048)
+    check(f"bf16 clip n={n} d={d}", loss, rl.cpu(), [("d_img", da, rda.cpu()), ("d_txt", db, rdb.cpu())])
+
+
+def test_bf16_row_stride_beyond_the_direct_core_range():
+    """A row stride of 2^23 elements puts a 256-row panel past the direct-to-LDS
+    core's 2^31-byte range: such inputs run on the register-staged core."""
+    n, d, ld = 300, 64, 1 << 23
+    # rows of width d at stride ld inside one flat buffer per input (5 GB each)
+    a, b = randn_pair(n, d, seed=23, dtype=torch.bfloat16)
+    flat_a = torch.zeros((n - 1) * ld + d, dtype=torch.bfloat16, device=DEV)
+    flat_b = torch.zeros((n - 1) * ld + d, dtype=torch.bfloat16, device=DEV)
+    ga = flat_a.as_strided((n, d), (ld, 1))
+    gb = flat_b.as_strided((n, d), (ld, 1))
+    ga.copy_(a.to(DEV))
+    gb.copy_(b.to(DEV))
+    ga.requires_grad_(True)
+    gb.requires_grad_(True)
+    say(f"bf16 CLIP n={n} d={d} row stride {ld}")
+    loss = MemoryEfficientCLIPLoss(0.07)(ga, gb)
+    loss.backward()
+    rl, rda, rdb = oracle.clip_loss_and_grads(a.float(), b.float(), 0.07)
+    check(f"bf16 stride {ld}", loss.detach().cpu(), rl,
+          [("d_img", ga.grad.cpu(), rda), ("d_txt", gb.grad.cpu(), rdb)])
