@@ -81,20 +81,22 @@ int64_t det_partials_offset(int64_t n) { return (int64_t)WS_NSLOTS * n + loss_pa
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// The 16-bit direct-to-LDS core addresses each operand panel with 32-bit
-// byte offsets and masks with the offset 2^31, so a panel (at most 256 rows)
-// must span less than 2^31 bytes: (rows - 1) * ld + kmax < 2^30 elements.
-constexpr int64_t kDmaMaxElems = (int64_t(1) << 30) - 1;
-constexpr int64_t kDmaRows = 256;
+// The direct-to-LDS core addresses each operand panel with 32-bit byte
+// offsets and masks with the offset 2^31, so a panel must span less than 2^31
+// bytes: (rows - 1) * ld + kmax elements of esz bytes.  Panels have at most
+// 256 rows (16-bit) or 128 rows (fp32).
+int64_t dma_max_elems(int dtype) { return ((int64_t(1) << 31) - 1) / (dtype == MEC_DTYPE_F32 ? 4 : 2); }
+int64_t dma_rows(int dtype) { return dtype == MEC_DTYPE_F32 ? 128 : 256; }
 
 // 16-byte vector loads are legal when every row start is 16-byte aligned and
-// rows hold a whole number of vectors; for the 16-bit types this also selects
-// the direct-to-LDS core, whose panels must fit its 32-bit offsets.
+// rows hold a whole number of vectors; this also selects the direct-to-LDS
+// core for the forward and gradient-matrix tiles, whose panels must fit its
+// 32-bit offsets.
 bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, int dtype) {
   const int64_t per = dtype == MEC_DTYPE_F32 ? 4 : 8;
   if (!(aligned16(x) && aligned16(y) && d % per == 0 && ldx % per == 0 && ldy % per == 0)) return false;
   const int64_t ld = ldx > ldy ? ldx : ldy;
-  return dtype == MEC_DTYPE_F32 || (kDmaRows - 1) * ld + d <= kDmaMaxElems;
+  return (dma_rows(dtype) - 1) * ld + d <= dma_max_elems(dtype);
 }
 
 // Block decomposition of the N x N gradient matrix for the backward: nb
@@ -114,7 +116,7 @@ void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
   const int64_t q = block_quantum(dtype);
   const int64_t tiles = (n + q - 1) / q;
   // 16-bit: a transposed gradient-matrix block is a direct-to-LDS operand
-  // ((bs - 1) * bs + 256 elements within kDmaMaxElems): bs <= 127 * 256
+  // ((bs - 1) * bs + 256 elements within dma_max_elems): bs <= 127 * 256
   const int64_t cap = dtype == MEC_DTYPE_F32 ? tiles : 127;
   int64_t target = ((dtype == MEC_DTYPE_F32 ? 2 : 8) * d + q - 1) / q;
   if (target < 1024 / q) target = 1024 / q;
@@ -171,6 +173,17 @@ ScratchLayout scratch_layout(int64_t n, int64_t d, int dtype) {
 int64_t scratch_bytes_for(int64_t n, int64_t d, int dtype) { return scratch_layout(n, d, dtype).total; }
 
 int round8(int v) { return (v + 7) & ~7; }
+
+// fp32 contractions run on the direct-to-LDS core when a transposed input
+// panel (128 rows of pitch ldt) and a gradient-matrix block panel (128 rows of
+// pitch bs) fit its 32-bit offsets, i.e. up to n of about 4.2M; beyond that on
+// the register-staged core.  MEC_F32_CONTRACT_DMA=0 forces the latter (tests).
+bool f32_contract_dma(int64_t ldt, int64_t bs) {
+  if (const char* env = std::getenv("MEC_F32_CONTRACT_DMA"))
+    if (env[0] == '0') return false;
+  const int64_t pitch = ldt > bs ? ldt : bs;
+  return (dma_rows(MEC_DTYPE_F32) - 1) * pitch + bs <= dma_max_elems(MEC_DTYPE_F32);
+}
 
 // T = element type of dtype: float, bf16 bits (uint16_t) or fp16 (_Float16)
 #define DISPATCH_DTYPE(dtype, T, ...)   \
@@ -349,6 +362,7 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
   const int N = (int)n, D = (int)d;
   const float c = (float)(1.4426950408889634 / (double)temperature);
   const bool vec = vec_ok(x, ldx, y, ldy, d, dtype);
+  const bool cdma = f32_contract_dma(L.ldt, bs);
   const TileDims tf = fwd_tile_dims(dtype, vec), tc = con_tile_dims(dtype);
   BlockGrid bg{bs, nb, bs / tf.bm, bs / tf.bn, bs / tc.bm, (D + tc.bn - 1) / tc.bn};
   StepPlan sp{};
@@ -411,10 +425,15 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
       }
     }
     if (!rc && grid > 0) {
-      DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-          k_grad_step<T, LIT, NORM, VEC><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
-              (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, split ? sp_g : sp, acc_x,
-              acc_y))));
+      if constexpr (Is16<T>::value) {
+        DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
+            k_grad_step<T, LIT, NORM, VEC, true><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
+                (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp_g, acc_x, acc_y))));
+      } else {
+        DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, DISPATCH_BOOL(cdma, CDMA,
+            k_grad_step<T, LIT, NORM, VEC, CDMA><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
+                (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y)))));
+      }
     }
   });
   if (rc) return rc;

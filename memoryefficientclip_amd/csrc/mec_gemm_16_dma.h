@@ -47,19 +47,27 @@
 namespace mec {
 namespace g16d {
 
-constexpr int BK = 32;            // k per chunk
 constexpr int S = 3;              // LDS stages
-constexpr int ROWB = BK * 2;      // bytes per staged row
+constexpr int ROWB = 64;          // bytes per staged row of a chunk (BK = 64 / element size)
 constexpr int RPB = 16;           // rows per 1 KB load block
-constexpr int NS = BK / 16;       // MFMA k-steps per chunk
+constexpr int NS = 2;             // k-steps per chunk (one 16-byte vector per lane half each)
 constexpr uint32_t OOB = 0x80000000u;  // buffer offset that reads as zero
 
-template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, bool F16_ = false>
+// element kinds: bf16 and fp16 (v_mfma_f32_32x32x16_*, one MFMA per k-step
+// and block) and fp32 (v_mfma_f32_32x32x2_f32, four per k-step and block)
+enum Kind { K_BF16 = 0, K_F16 = 1, K_F32 = 2 };
+
+template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_;
-  static constexpr bool F16 = F16_;                    // fp16 MFMAs (else bf16)
+  static constexpr int KIND = KIND_;
+  static constexpr bool F16 = KIND == K_F16;           // fp16 MFMAs (16-bit kinds)
+  static constexpr int ESZ = KIND == K_F32 ? 4 : 2;    // bytes per element
+  static constexpr int EPV = 16 / ESZ;                 // elements per 16-byte vector
+  static constexpr int BK = ROWB / ESZ;                // k per chunk
+  static constexpr int MPB = KIND == K_F32 ? 4 : 1;    // MFMAs per block and k-step
   static constexpr bool TA = TA_;                      // A stored k-row-major
-  static_assert(!TA || BM == 256, "transposed A: 512-byte k-rows (BM = 256)");
+  static_assert(!TA || (BM == 256 && ESZ == 2), "transposed A: 16-bit, 512-byte k-rows (BM = 256)");
   static constexpr int WM = WM_, WN = WN_, NW = WM * WN, NT = 64 * NW;
   static constexpr int TM = BM / WM, TN = BN / WN;     // wave sub-tile
   static constexpr int FM = TM / 32, FN = TN / 32;     // 32x32 MFMA blocks per wave
@@ -67,26 +75,27 @@ struct Geo {
   static constexpr int STAGE = ROWS * ROWB;
   static constexpr int LDS_BYTES = S * STAGE;
   static constexpr int IPW = ROWS / RPB / NW;          // load instructions per wave per chunk
-  static constexpr int NMF = FM * FN;                  // MFMAs per k-step
+  static constexpr int NMF = FM * FN * MPB;            // MFMAs per k-step
   static constexpr int LPS = (IPW + NS - 1) / NS;      // loads interleaved per k-step
   static_assert(ROWS % (RPB * NW) == 0 && BM % RPB == 0, "load split");
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave sub-tile of 32x32 blocks");
 };
 
 struct Operand {
-  const uint16_t* base;  // element (row, k) at base[row * ld + k] (transposed A: base[k * ld + row])
+  const void* base;  // element (row, k) at base[row * ld + k] (transposed A: base[k * ld + row])
   int64_t ld;
-  int rows;              // valid rows from base (rows beyond read as 0; transposed A: all BM rows readable)
-  int kmax;              // valid k range [0, kmax), a multiple of 8
+  int rows;          // valid rows from base (rows beyond read as 0; transposed A: all BM rows readable)
+  int kmax;          // valid k range [0, kmax), a multiple of the elements per 16-byte vector
 };
 
 __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
+template <int ESZ>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& op) {
   const int64_t elems = op.rows > 0 ? (int64_t)(op.rows - 1) * op.ld + op.kmax : 0;
-  return __builtin_amdgcn_make_buffer_rsrc((void*)op.base, 0, (int)(elems * 2), 0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)op.base, 0, (int)(elems * ESZ), 0x00020000);
 }
-// transposed A: k-rows [0, kmax) of BM elements
+// transposed A (16-bit): k-rows [0, kmax) of BM elements
 template <int BM>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_t(const Operand& op) {
   const int64_t elems = op.kmax > 0 ? (int64_t)(op.kmax - 1) * op.ld + BM : 0;
@@ -111,8 +120,8 @@ struct LoadPlan {
   int kmax_a, kmax_b;
   int64_t lda;     // transposed A: bytes per k-row
   __device__ __forceinline__ void init(const Operand& A, const Operand& B) {
-    ra = G::TA ? make_rsrc_t<G::BM>(A) : make_rsrc(A);
-    rb = make_rsrc(B);
+    ra = G::TA ? make_rsrc_t<G::BM>(A) : make_rsrc<G::ESZ>(A);
+    rb = make_rsrc<G::ESZ>(B);
     kmax_a = A.kmax;
     kmax_b = B.kmax;
     lda = A.ld * 2;
@@ -120,7 +129,7 @@ struct LoadPlan {
     w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rib = lane >> 2, phys = lane & 3;
     // rows of one load block are b*16 .. b*16+15, so swz(r) = (rib >> 2) & 3
-    kv = (phys ^ swz(rib)) * 8;
+    kv = (phys ^ swz(rib)) * G::EPV;
     kr = lane >> 5;
 #pragma unroll
     for (int i = 0; i < G::IPW; ++i) {
@@ -132,7 +141,7 @@ struct LoadPlan {
         voff[i] = (uint32_t)((int64_t)krow * A.ld + slot * 8) * 2;
       } else {
         const int r = b * RPB + rib;
-        voff[i] = (uint32_t)(((i < A_LOADS ? (int64_t)r * A.ld : (int64_t)(r - G::BM) * B.ld) + kv) * 2);
+        voff[i] = (uint32_t)(((i < A_LOADS ? (int64_t)r * A.ld : (int64_t)(r - G::BM) * B.ld) + kv) * G::ESZ);
       }
     }
   }
@@ -147,7 +156,7 @@ struct LoadPlan {
       soff = (uint32_t)(k0 * lda);
     } else {
       off = (k0 + kv < (isa ? kmax_a : kmax_b)) ? voff[I] : OOB;
-      soff = (uint32_t)k0 * 2;
+      soff = (uint32_t)k0 * G::ESZ;
     }
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         isa ? ra : rb, (__attribute__((address_space(3))) void*)(stage + (I * G::NW + w) * 1024), 16, off, soff, 0,
@@ -263,7 +272,15 @@ __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM
   constexpr int EVERY = NL > 0 ? G::NMF / (NL > 0 ? NL : 1) : G::NMF + 1;
   static_for<G::NMF>([&](auto mc) {
     constexpr int m = mc;
-    acc[m / G::FN][m % G::FN] = mfma16_32x32x16<G::F16>(f.a[m / G::FN], f.b[m % G::FN], acc[m / G::FN][m % G::FN]);
+    if constexpr (G::KIND == K_F32) {
+      // block (i, j), sub-step t: lane half h supplies k = 16-byte vector's element t
+      constexpr int blk = m / 4, t = m % 4, i = blk / G::FN, j = blk % G::FN;
+      acc[i][j] = mfma_f32_32x32x2(__builtin_bit_cast(f32x4, f.a[i])[t], __builtin_bit_cast(f32x4, f.b[j])[t],
+                                   acc[i][j]);
+    } else {
+      acc[m / G::FN][m % G::FN] =
+          mfma16_32x32x16<G::F16>(f.a[m / G::FN], f.b[m % G::FN], acc[m / G::FN][m % G::FN]);
+    }
     if constexpr (NL > 0 && (m % EVERY) == EVERY - 1 && L0 + m / EVERY < L1) {
       sched_fence();
       lp.template issue<L0 + m / EVERY>(k0, stage);
@@ -290,6 +307,7 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
     for (int j = 0; j < G::FN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  constexpr int BK = G::BK;
   const int nk = (K + BK - 1) / BK;
   LoadPlan<G> lp;
   lp.init(A, B);

@@ -76,14 +76,24 @@ struct Tile16V : Pack16<F16> {
   }
 };
 
-// bf16 / fp16, BM_ x BN_, direct global->LDS loads (16-byte aligned rows, ld
-// and kmax multiples of 8); TA_: A stored k-row-major (a transposed
+struct PackF32 {
+  static __device__ __forceinline__ float pack(float v) { return v; }
+  static __device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+    *(f32x4*)p = f32x4{a, b, c, d};
+  }
+};
+template <int KIND> struct PackOf { using type = Pack16<KIND == g16d::K_F16>; };
+template <> struct PackOf<g16d::K_F32> { using type = PackF32; };
+
+// BM_ x BN_, direct global->LDS loads (16-byte aligned rows, ld and kmax
+// multiples of the elements per 16-byte vector), element kind KIND (bf16,
+// fp16 or fp32); TA_: A stored k-row-major (a transposed 16-bit
 // gradient-matrix block)
-template <int BM_, int BN_, bool TA_, int WM_, int WN_, bool F16>
-struct Tile16D : Pack16<F16> {
-  using Elem = uint16_t;
+template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND>
+struct TileD : PackOf<KIND>::type {
+  using Elem = typename std::conditional<KIND == g16d::K_F32, float, uint16_t>::type;
   using Op = g16d::Operand;
-  using G = g16d::Geo<BM_, BN_, TA_, WM_, WN_, F16>;
+  using G = g16d::Geo<BM_, BN_, TA_, WM_, WN_, KIND>;
   static constexpr bool TA = TA_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
@@ -99,26 +109,33 @@ struct Tile16D : Pack16<F16> {
 template <typename T> struct Is16 { static constexpr bool value = false, f16 = false; };
 template <> struct Is16<uint16_t> { static constexpr bool value = true, f16 = false; };
 template <> struct Is16<_Float16> { static constexpr bool value = true, f16 = true; };
+template <typename T> constexpr int kind16() { return Is16<T>::f16 ? g16d::K_F16 : g16d::K_BF16; }
 
 // forward sums and gradient-matrix tiles; contractions (see mec_tiles.h)
 template <typename T, bool VEC, bool IS16 = Is16<T>::value> struct FwdTileSel;
-template <typename T, bool VEC> struct FwdTileSel<T, VEC, false> { using type = TileF32; };
-template <typename T> struct FwdTileSel<T, true, true> { using type = Tile16D<128, 256, false, 2, 2, Is16<T>::f16>; };
+template <typename T> struct FwdTileSel<T, false, false> { using type = TileF32; };
+template <typename T> struct FwdTileSel<T, true, false> { using type = TileD<128, 128, false, 2, 2, g16d::K_F32>; };
+template <typename T> struct FwdTileSel<T, true, true> { using type = TileD<128, 256, false, 2, 2, kind16<T>()>; };
 template <typename T> struct FwdTileSel<T, false, true> { using type = Tile16V<Is16<T>::f16>; };
 template <typename T, bool VEC> using FwdTile = typename FwdTileSel<T, VEC>::type;
 // Contractions.  fp32 stores the gradient-matrix blocks in both layouts (G'
-// for the x side, G'^T for the y side) and runs them inside k_grad_step; the
-// 16-bit types store only G'^T, which the y side reads K-major and the x side
-// reads transposed through LDS, in a kernel of their own (k_grad_contract)
-// with 256 x 256 tiles of 8 waves.
-template <typename T, bool IS16 = Is16<T>::value> struct ConTileSel;
-template <typename T> struct ConTileSel<T, false> { using x = TileF32; using y = TileF32; };
-template <typename T> struct ConTileSel<T, true> {
-  using x = Tile16D<256, 256, true, 4, 2, Is16<T>::f16>;
-  using y = Tile16D<256, 256, false, 4, 2, Is16<T>::f16>;
+// for the x side, G'^T for the y side) and runs them inside k_grad_step, on
+// the direct-to-LDS core when its 32-bit offsets reach across a transposed
+// input panel (DMA; 128 rows of pitch ~N), else on the register-staged one.
+// The 16-bit types store only G'^T, which the y side reads K-major and the x
+// side reads transposed through LDS, in a kernel of their own
+// (k_grad_contract) with 256 x 256 tiles of 8 waves.
+template <typename T, bool DMA = true, bool IS16 = Is16<T>::value> struct ConTileSel;
+template <typename T, bool DMA> struct ConTileSel<T, DMA, false> {
+  using x = typename std::conditional<DMA, TileD<128, 128, false, 2, 2, g16d::K_F32>, TileF32>::type;
+  using y = x;
 };
-template <typename T> using ConTileX = typename ConTileSel<T>::x;
-template <typename T> using ConTileY = typename ConTileSel<T>::y;
+template <typename T, bool DMA> struct ConTileSel<T, DMA, true> {
+  using x = TileD<256, 256, true, 4, 2, kind16<T>()>;
+  using y = TileD<256, 256, false, 4, 2, kind16<T>()>;
+};
+template <typename T, bool DMA = true> using ConTileX = typename ConTileSel<T, DMA>::x;
+template <typename T, bool DMA = true> using ConTileY = typename ConTileSel<T, DMA>::y;
 // the 16-bit types keep one layout of the gradient-matrix blocks (G'^T)
 template <typename T> struct GtOnly { static constexpr bool value = Is16<T>::value; };
 // Scale of the stored gradient-matrix entries.  0 < G'_ij <= 2 (E_ij <= 1,
@@ -621,8 +638,9 @@ __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int
 }
 
 // One pipeline step: G' tiles of diagonal diag_g and, for fp32, the
-// contractions of diagonal diag_c (bf16 runs those in k_grad_contract).
-template <typename T, bool LIT, bool NORM, bool VEC>
+// contractions of diagonal diag_c (bf16 runs those in k_grad_contract); CDMA
+// selects the fp32 contraction core.
+template <typename T, bool LIT, bool NORM, bool VEC, bool CDMA>
 __global__ __launch_bounds__((FwdTile<T, VEC>::NT), Occ<T>::bwd) void k_grad_step(const T* __restrict__ X, int64_t ldx,
                                                                const T* __restrict__ Y, int64_t ldy, int N, int D,
                                                                int kmax, float c, const float* __restrict__ ws,
@@ -630,8 +648,8 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), Occ<T>::bwd) void k_grad_ste
                                                                float* __restrict__ acc_x, float* __restrict__ acc_y) {
   using TF = FwdTile<T, VEC>;
   constexpr bool FUSED = !GtOnly<T>::value;  // contractions in this kernel
-  using TCX = typename std::conditional<FUSED, ConTileX<T>, TF>::type;
-  using TCY = typename std::conditional<FUSED, ConTileY<T>, TF>::type;
+  using TCX = typename std::conditional<FUSED, ConTileX<T, CDMA>, TF>::type;
+  using TCY = typename std::conditional<FUSED, ConTileY<T, CDMA>, TF>::type;
   static_assert(TCX::NT == TF::NT && TCY::NT == TF::NT, "one workgroup size per launch");
   constexpr int GT_LDS = GtOnly<T>::value ? TF::BN * gt_pitch(TF::BM) : 0;
   __shared__ __attribute__((aligned(1024)))

@@ -1,0 +1,85 @@
+"""GPU parity of the fp32 core choices, against the fp64 CPU oracle.
+
+fp32 inputs whose rows are 16-byte aligned run the forward and
+gradient-matrix tiles on the direct-to-LDS core, and the contractions too
+while a transposed input panel (128 rows of pitch ~N) fits its 32-bit
+offsets (N up to about 4.2M); otherwise on the register-staged core.  The
+second choice cannot be reached at test sizes, so MEC_F32_CONTRACT_DMA=0
+forces it here; a row stride past the 32-bit range exercises the first.
+"""
+import os
+
+import pytest
+import torch
+
+import oracle
+from helpers import max_rel, randn_pair, rel_err
+from memoryefficientclip_amd.clip_loss import MemoryEfficientCLIPLoss
+from memoryefficientclip_amd.lit_loss import MemoryEfficientLiTLoss
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TOL_LOSS, TOL_GRAD = 1e-4, 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def run(module, a, b, grad_b=True):
+    ga = a.to(DEV).requires_grad_(True)
+    gb = b.to(DEV).requires_grad_(grad_b)
+    loss = module(ga, gb)
+    loss.backward()
+    torch.cuda.synchronize()
+    return loss.detach().cpu(), ga.grad.cpu(), (gb.grad.cpu() if grad_b else None)
+
+
+@pytest.mark.parametrize("lit", [False, True], ids=["clip", "lit"])
+def test_f32_register_staged_contractions(lit):
+    n, d = 2300, 96  # two backward blocks of 2048 rows, the last one short
+    a, b = randn_pair(n, d, seed=31)
+    mod = MemoryEfficientLiTLoss(0.07) if lit else MemoryEfficientCLIPLoss(0.07)
+    say(f"fp32 {'LiT' if lit else 'CLIP'} n={n} d={d}: direct-to-LDS vs register-staged contractions")
+    l_dma, da_dma, db_dma = run(mod, a, b, grad_b=not lit)
+    os.environ["MEC_F32_CONTRACT_DMA"] = "0"
+    try:
+        l_reg, da_reg, db_reg = run(mod, a, b, grad_b=not lit)
+    finally:
+        del os.environ["MEC_F32_CONTRACT_DMA"]
+    if lit:
+        rl, rda = oracle.lit_loss_and_grads(a, b, 0.07)
+        pairs = [(da_dma, rda), (da_reg, rda)]
+    else:
+        rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+        pairs = [(da_dma, rda), (db_dma, rdb), (da_reg, rda), (db_reg, rdb)]
+    errs = [max_rel(g, r) for g, r in pairs]
+    say(f"  loss rel {rel_err(l_dma, rl):.2e} / {rel_err(l_reg, rl):.2e}; grads {['%.2e' % e for e in errs]}")
+    assert rel_err(l_dma, rl) <= TOL_LOSS and rel_err(l_reg, rl) <= TOL_LOSS
+    assert all(e <= TOL_GRAD for e in errs)
+    # the two cores sum the same products in different orders
+    assert max_rel(da_dma, da_reg) < 1e-5
+
+
+def test_f32_row_stride_beyond_the_direct_core_range():
+    """A row stride of 2^23 floats puts a 128-row panel past the direct-to-LDS
+    core's 2^31-byte range: the forward and gradient-matrix tiles then run on
+    the register-staged core."""
+    n, d, ld = 300, 64, 1 << 23
+    a, b = randn_pair(n, d, seed=37)
+    flat_a = torch.zeros((n - 1) * ld + d, device=DEV)
+    flat_b = torch.zeros((n - 1) * ld + d, device=DEV)
+    ga = flat_a.as_strided((n, d), (ld, 1))
+    gb = flat_b.as_strided((n, d), (ld, 1))
+    ga.copy_(a.to(DEV))
+    gb.copy_(b.to(DEV))
+    ga.requires_grad_(True)
+    gb.requires_grad_(True)
+    say(f"fp32 CLIP n={n} d={d} row stride {ld}")
+    loss = MemoryEfficientCLIPLoss(0.07)(ga, gb)
+    loss.backward()
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    ea, eb = max_rel(ga.grad.cpu(), rda), max_rel(gb.grad.cpu(), rdb)
+    say(f"  loss rel {rel_err(loss.detach().cpu(), rl):.2e} grads {ea:.2e} {eb:.2e}")
+    assert rel_err(loss.detach().cpu(), rl) <= TOL_LOSS
+    assert ea <= TOL_GRAD and eb <= TOL_GRAD
