@@ -1,36 +1,38 @@
-// 16-bit (bf16 or fp16) MFMA tile core for gfx950 with direct global->LDS
-// loads.
+// MFMA tile core for gfx950 with direct global->LDS loads, for bf16, fp16
+// and fp32 operands (Geo::KIND).
 //
 // Geometry: a BM x BN output tile per workgroup of WM x WN waves, each wave a
-// (BM/WM) x (BN/WN) sub-tile of v_mfma_f32_32x32x16_{bf16,f16} blocks (fp32
-// accumulate; Geo::F16 selects the format, the data movement is the same).
-// The forward and gradient-matrix tiles are 128 x 256 with 2 x 2 waves: two
-// workgroups share a CU (72 KB of LDS each), so one workgroup's epilogue
-// (exp, reductions, stores) runs while the other's MFMAs do.  The
-// contractions, whose epilogue is a few atomics, are 256 x 256 with 4 x 2
-// waves, one workgroup per CU: fewer operand bytes per MFMA through the
-// global->LDS path (≈64 B/clk per CU), which bounds these kernels.
+// (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks, fp32 accumulate:
+// v_mfma_f32_32x32x16_{bf16,f16} (one per block and k-step) or
+// v_mfma_f32_32x32x2_f32 (four per block and k-step).  The 16-bit forward and
+// gradient-matrix tiles are 128 x 256 with 2 x 2 waves: two workgroups share a
+// CU (72 KB of LDS each), so one workgroup's epilogue (exp, reductions,
+// stores) runs while the other's MFMAs do.  The 16-bit contractions, whose
+// epilogue is a few atomics, are 256 x 256 with 4 x 2 waves, one workgroup
+// per CU.  fp32 tiles are 128 x 128 with 2 x 2 waves (48 KB, three per CU).
 //
 // Operands are K-major (element (row, k) at base[row * ld + k]).  K is staged
-// in chunks of BK = 32 through a ring of S = 3 LDS stages ([row][32] bf16, 64
-// bytes per row).  Each chunk arrives by buffer_load_dwordx4 ... lds: every
-// lane of a wave moves 16 bytes and the wave writes one contiguous 1 KB block
-// (16 rows) of the stage; which 16-byte k-vector of a row a lane fetches is
-// XOR-swizzled (vector v of row r sits in slot v ^ ((r >> 2) & 3)) so that the
-// MFMA operand reads (ds_read_b128, lanes 0..15 on rows 0..15 at one k-vector)
-// hit 16 distinct 16-byte bank groups.  The loads of chunk kt+S-1 are spread
-// over the MFMAs of chunk kt; one barrier per chunk.
+// in chunks of 64 bytes per row (BK = 32 16-bit or 16 fp32 values) through a
+// ring of S = 3 LDS stages ([row][64 bytes]).  Each chunk arrives by
+// buffer_load_dwordx4 ... lds: every lane of a wave moves 16 bytes and the
+// wave writes one contiguous 1 KB block (16 rows) of the stage; which 16-byte
+// k-vector of a row a lane fetches is XOR-swizzled (vector v of row r sits in
+// slot v ^ ((r >> 2) & 3)) so that the MFMA operand reads (ds_read_b128,
+// lanes 0..15 on rows 0..15 at one k-vector) hit 16 distinct 16-byte bank
+// groups.  The loads of chunk kt+S-1 are spread over the MFMAs of chunk kt;
+// one barrier per chunk.
 //
 // Masking costs nothing in the loop: each operand's buffer descriptor covers
 // exactly its valid rows and k range, so rows beyond `rows` read as zero, and
 // lanes whose k-vector lies at or beyond kmax in the tail chunk get an
 // out-of-range offset (also zero).  Requirements (checked by the host):
-// 16-byte aligned base, ld % 8 == 0, kmax % 8 == 0, (rows - 1) * ld + kmax
-// < 2^31 elements / 2 (byte offsets are 32-bit).
+// 16-byte aligned base, ld and kmax multiples of the elements per 16-byte
+// vector, and (rows - 1) * ld + kmax elements within 2^31 - 1 bytes (byte
+// offsets are 32-bit, and the offset 2^31 must read as zero).
 //
-// Within a chunk the logical k fed to MFMA step s (0, 1) by lane half
-// h = lane / 32 is the 16-byte vector h * 2 + s for both operands, so the
-// contraction over the chunk is exact.
+// Within a chunk the 16-byte vector fed to k-step s (0, 1) by lane half
+// h = lane / 32 is vector h * 2 + s for both operands (fp32: its four values
+// feed four MFMAs in order), so the contraction over the chunk is exact.
 //
 // Transposed A (TA = true): A is stored k-row-major (element (m, k) at
 // base[k * ld + m], m contiguous), e.g. a transposed gradient-matrix block.
@@ -45,7 +47,7 @@
 #include "mec_common.h"
 
 namespace mec {
-namespace g16d {
+namespace gdma {
 
 constexpr int S = 3;              // LDS stages
 constexpr int ROWB = 64;          // bytes per staged row of a chunk (BK = 64 / element size)
@@ -346,5 +348,5 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
   __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));
 }
 
-}  // namespace g16d
+}  // namespace gdma
 }  // namespace mec

@@ -20,7 +20,7 @@
 
 #include "mec_gemm_f32.h"
 #include "mec_gemm_16.h"
-#include "mec_gemm_16_dma.h"
+#include "mec_gemm_dma.h"
 #include "mec_tiles.h"
 
 namespace mec {
@@ -82,8 +82,8 @@ struct PackF32 {
     *(f32x4*)p = f32x4{a, b, c, d};
   }
 };
-template <int KIND> struct PackOf { using type = Pack16<KIND == g16d::K_F16>; };
-template <> struct PackOf<g16d::K_F32> { using type = PackF32; };
+template <int KIND> struct PackOf { using type = Pack16<KIND == gdma::K_F16>; };
+template <> struct PackOf<gdma::K_F32> { using type = PackF32; };
 
 // BM_ x BN_, direct global->LDS loads (16-byte aligned rows, ld and kmax
 // multiples of the elements per 16-byte vector), element kind KIND (bf16,
@@ -91,16 +91,16 @@ template <> struct PackOf<g16d::K_F32> { using type = PackF32; };
 // gradient-matrix block)
 template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND>
 struct TileD : PackOf<KIND>::type {
-  using Elem = typename std::conditional<KIND == g16d::K_F32, float, uint16_t>::type;
-  using Op = g16d::Operand;
-  using G = g16d::Geo<BM_, BN_, TA_, WM_, WN_, KIND>;
+  using Elem = typename std::conditional<KIND == gdma::K_F32, float, uint16_t>::type;
+  using Op = gdma::Operand;
+  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND>;
   static constexpr bool TA = TA_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
   static constexpr int LDS_BYTES = G::LDS_BYTES;
   template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
-    g16d::mainloop<G>(a, b, K, (char*)lds, acc);
+    gdma::mainloop<G>(a, b, K, (char*)lds, acc);
   }
 };
 
@@ -109,12 +109,12 @@ struct TileD : PackOf<KIND>::type {
 template <typename T> struct Is16 { static constexpr bool value = false, f16 = false; };
 template <> struct Is16<uint16_t> { static constexpr bool value = true, f16 = false; };
 template <> struct Is16<_Float16> { static constexpr bool value = true, f16 = true; };
-template <typename T> constexpr int kind16() { return Is16<T>::f16 ? g16d::K_F16 : g16d::K_BF16; }
+template <typename T> constexpr int kind16() { return Is16<T>::f16 ? gdma::K_F16 : gdma::K_BF16; }
 
 // forward sums and gradient-matrix tiles; contractions (see mec_tiles.h)
 template <typename T, bool VEC, bool IS16 = Is16<T>::value> struct FwdTileSel;
 template <typename T> struct FwdTileSel<T, false, false> { using type = TileF32; };
-template <typename T> struct FwdTileSel<T, true, false> { using type = TileD<128, 128, false, 2, 2, g16d::K_F32>; };
+template <typename T> struct FwdTileSel<T, true, false> { using type = TileD<128, 128, false, 2, 2, gdma::K_F32>; };
 template <typename T> struct FwdTileSel<T, true, true> { using type = TileD<128, 256, false, 2, 2, kind16<T>()>; };
 template <typename T> struct FwdTileSel<T, false, true> { using type = Tile16V<Is16<T>::f16>; };
 template <typename T, bool VEC> using FwdTile = typename FwdTileSel<T, VEC>::type;
@@ -127,7 +127,7 @@ template <typename T, bool VEC> using FwdTile = typename FwdTileSel<T, VEC>::typ
 // (k_grad_contract) with 256 x 256 tiles of 8 waves.
 template <typename T, bool DMA = true, bool IS16 = Is16<T>::value> struct ConTileSel;
 template <typename T, bool DMA> struct ConTileSel<T, DMA, false> {
-  using x = typename std::conditional<DMA, TileD<128, 128, false, 2, 2, g16d::K_F32>, TileF32>::type;
+  using x = typename std::conditional<DMA, TileD<128, 128, false, 2, 2, gdma::K_F32>, TileF32>::type;
   using y = x;
 };
 template <typename T, bool DMA> struct ConTileSel<T, DMA, true> {

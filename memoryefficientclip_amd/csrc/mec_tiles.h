@@ -3,7 +3,7 @@
 //   fp32                      128 x 128 tiles everywhere (mec_gemm_f32.h)
 //   bf16 / fp16, 16-byte      forward sums and gradient-matrix tiles 128 x 256
 //   vectors                   (x rows x y rows), direct global->LDS loads
-//                             (mec_gemm_16_dma.h); contractions 256 x 256
+//                             (mec_gemm_dma.h); contractions 256 x 256
 //                             (output rows x feature columns, 8 waves) in a
 //                             kernel of their own
 //   bf16 / fp16, other        forward sums and gradient-matrix tiles 128 x 128
