@@ -1,4 +1,4 @@
-// MFMA tile kernels of the contrastive-loss hot path (fp32 and bf16 inputs;
+// MFMA tile kernels of the contrastive-loss hot path (fp32, bf16 and fp16 inputs;
 // the element type and layout select the MFMA core and tile shape, the
 // epilogues are shared):
 //   k_sumexp        forward: tiled S = X Y^T, E = exp2(S c - c), off-diagonal
@@ -14,7 +14,13 @@
 //                       contracting diagonal t-1 from the other buffer:
 //                       dX_I += G'_IJ Y^_J and dY_J += G'_IJ^T X^_I as plain MFMA
 //                       contractions without contending atomics
-//                       (clip_loss.py:127-156, lit_loss.py:123-148).
+//                       (clip_loss.py:127-156, lit_loss.py:123-148); fp32
+//                       runs both kinds of tile in this launch.
+//   k_grad_contract the 16-bit types' contractions of one pipeline step, in
+//                       a launch of their own with larger tiles.
+//   k_sumexp_rows_det, k_det_sum
+//                   the forward sums without atomics across workgroups
+//                       (deterministic mode).
 #pragma once
 #include <type_traits>
 
@@ -369,7 +375,7 @@ struct BlockGrid {
 // Scratch of the backward (all in the input dtype T, row-major):
 //   G[2]   two buffers of nb blocks of bs x bs: block I of buffer s&1 holds
 //          G'(I, (I+s) mod nb) of diagonal s (fp32 only);
-//   GT[2]  the same blocks transposed (fp32: CLIP only; bf16: always, the
+//   GT[2]  the same blocks transposed (fp32: CLIP only; 16-bit: always, the
 //          only copy);
 //   XT, YT the normalised inputs transposed, [D][ldt] with ldt = N rounded
 //          up to 128 and zero columns [N, ldt): element (d, i) = rx_i x_i[d].
@@ -438,7 +444,7 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN]
   }
 }
 
-// bf16: G'_ij of this wave's TM x TN accumulators, staged through LDS as
+// 16-bit: G'_ij of this wave's TM x TN accumulators, staged through LDS as
 // [j][i] (row pitch gt_pitch(BM) = 2 BM + 16 bytes; 4 consecutive i per 8-byte write), then
 // written to GTb (row pitch bs) as whole 256-byte tile rows, 16 bytes per
 // lane.  MASK zeroes the diagonal and entries outside [0, N).  Every row of
@@ -544,7 +550,7 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
 // One BM x BN output tile of a contraction: rows r0.. of block P, feature
 // columns d0..:
 //   x side: acc_x[i, d] (+)= sum_{j in Q} G'(P,Q)[i, j]  * YT[d, j]   (Q = P + s)
-//           (bf16: G'(P,Q)[i, j] read from the transposed block G'T(P,Q)[j, i])
+//           (16-bit: G'(P,Q)[i, j] read from the transposed block G'T(P,Q)[j, i])
 //   y side: acc_y[j, d] (+)= sum_{i in Q} G'T(Q,P)[j, i] * XT[d, i]   (Q = P - s)
 // Each output tile has one owner per launch: accumulation across launches
 // adds each element once per launch, in launch order (the reference instead
@@ -604,7 +610,7 @@ __device__ __forceinline__ void grad_contract_dispatch(int sub, int N, int D, co
   if (pid >= (is_x ? sp.cx_n : sp.cy_n)) return;
   int tmg, td;
   if constexpr (GtOnly<T>::value) {
-    // bf16: feature tiles fastest, so the tiles sharing one gradient-matrix
+    // 16-bit: feature tiles fastest, so the tiles sharing one gradient-matrix
     // panel run side by side on one XCD and the panel is fetched from HBM
     // about once (its contractions are bound by that traffic)
     tmg = pid / bg.ctd;
@@ -625,7 +631,7 @@ __device__ __forceinline__ void grad_contract_dispatch(int sub, int N, int D, co
   }
 }
 
-// bf16 contractions of one pipeline step (the x side of diagonal diag_c, then the y side).
+// 16-bit contractions of one pipeline step (the x side of diagonal diag_c, then the y side).
 template <typename T>
 __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int D, GradBufs gb, BlockGrid bg,
                                                                      StepPlan sp, float* __restrict__ acc_x,
@@ -638,7 +644,7 @@ __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int
 }
 
 // One pipeline step: G' tiles of diagonal diag_g and, for fp32, the
-// contractions of diagonal diag_c (bf16 runs those in k_grad_contract); CDMA
+// contractions of diagonal diag_c (the 16-bit types run those in k_grad_contract); CDMA
 // selects the fp32 contraction core.
 template <typename T, bool LIT, bool NORM, bool VEC, bool CDMA>
 __global__ __launch_bounds__((FwdTile<T, VEC>::NT), Occ<T>::bwd) void k_grad_step(const T* __restrict__ X, int64_t ldx,
