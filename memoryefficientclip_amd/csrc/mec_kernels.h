@@ -121,7 +121,7 @@ template <typename T> constexpr int kind16() { return Is16<T>::f16 ? gdma::K_F16
 template <typename T, bool VEC, bool IS16 = Is16<T>::value> struct FwdTileSel;
 template <typename T> struct FwdTileSel<T, false, false> { using type = TileF32; };
 template <typename T> struct FwdTileSel<T, true, false> { using type = TileD<128, 128, false, 2, 2, gdma::K_F32>; };
-template <typename T> struct FwdTileSel<T, true, true> { using type = TileD<128, 256, false, 2, 2, kind16<T>()>; };
+template <typename T> struct FwdTileSel<T, true, true> { using type = TileD<256, 256, false, 4, 2, kind16<T>()>; };
 template <typename T> struct FwdTileSel<T, false, true> { using type = Tile16V<Is16<T>::f16>; };
 template <typename T, bool VEC> using FwdTile = typename FwdTileSel<T, VEC>::type;
 // Contractions.  fp32 stores the gradient-matrix blocks in both layouts (G'
@@ -151,10 +151,10 @@ template <typename T> struct GtOnly { static constexpr bool value = Is16<T>::val
 template <typename T> struct GScale { static constexpr float value = 1.f; };
 template <> struct GScale<_Float16> { static constexpr float value = 16384.f; };
 
-// workgroups per CU the launch bounds promise (the 16-bit direct-load configs
-// use 72 KB of LDS: two workgroups, one's epilogue overlapping the other's MFMAs)
-template <typename T> struct Occ {
-  static constexpr int fwd = 2, bwd = Is16<T>::value ? 2 : 3;
+// workgroups per CU the launch bounds promise (the 16-bit direct-load tiles
+// use 96 KB of LDS or more: one per CU)
+template <typename T, bool VEC> struct Occ {
+  static constexpr int fwd = Is16<T>::value ? (VEC ? 1 : 2) : 2, bwd = Is16<T>::value ? (VEC ? 1 : 2) : 3;
 };
 
 // Operand of a tile core from a typed pointer (the 16-bit cores address bits)
@@ -200,7 +200,7 @@ __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::
 }
 
 template <typename T, bool LIT, bool NORM, bool VEC>
-__global__ __launch_bounds__((FwdTile<T, VEC>::NT), Occ<T>::fwd) void k_sumexp(const T* __restrict__ X, int64_t ldx,
+__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_sumexp(const T* __restrict__ X, int64_t ldx,
                                                             const T* __restrict__ Y, int64_t ldy, int N, int D,
                                                             int kmax, float c, float* __restrict__ ws, int tiles_m,
                                                             int tiles_n) {
@@ -302,7 +302,7 @@ __device__ __forceinline__ void rowsum_accumulate(const f32x16 (&acc)[TL::FM][TL
 }
 
 template <typename T, bool NORM, bool VEC>
-__global__ __launch_bounds__((FwdTile<T, VEC>::NT), Occ<T>::fwd) void k_sumexp_rows_det(
+__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_sumexp_rows_det(
     const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
     const float* __restrict__ rx, const float* __restrict__ ry, float* __restrict__ part, int tiles_m,
     int tiles_n) {
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int
 // contractions of diagonal diag_c (the 16-bit types run those in k_grad_contract); CDMA
 // selects the fp32 contraction core.
 template <typename T, bool LIT, bool NORM, bool VEC, bool CDMA>
-__global__ __launch_bounds__((FwdTile<T, VEC>::NT), Occ<T>::bwd) void k_grad_step(const T* __restrict__ X, int64_t ldx,
+__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::bwd)) void k_grad_step(const T* __restrict__ X, int64_t ldx,
                                                                const T* __restrict__ Y, int64_t ldy, int N, int D,
                                                                int kmax, float c, const float* __restrict__ ws,
                                                                GradBufs gb, BlockGrid bg, StepPlan sp,

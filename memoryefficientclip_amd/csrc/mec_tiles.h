@@ -1,9 +1,11 @@
 // Tile geometry of the MFMA kernels, shared by host and device code.
 //
-//   fp32                      128 x 128 tiles everywhere (mec_gemm_f32.h)
-//   bf16 / fp16, 16-byte      forward sums and gradient-matrix tiles 128 x 256
-//   vectors                   (x rows x y rows), direct global->LDS loads
-//                             (mec_gemm_dma.h); contractions 256 x 256
+//   fp32                      128 x 128 tiles everywhere; direct global->LDS
+//                             loads (mec_gemm_dma.h) for 16-byte vectors,
+//                             else staged through registers (mec_gemm_f32.h)
+//   bf16 / fp16, 16-byte      forward sums and gradient-matrix tiles 256 x 256
+//   vectors                   (x rows x y rows, 8 waves), direct global->LDS
+//                             loads (mec_gemm_dma.h); contractions 256 x 256
 //                             (output rows x feature columns, 8 waves) in a
 //                             kernel of their own
 //   bf16 / fp16, other        forward sums and gradient-matrix tiles 128 x 128
@@ -29,7 +31,7 @@ constexpr int kDtypeF16 = 2;
 // forward sums and gradient-matrix tiles (x rows x y rows)
 inline TileDims fwd_tile_dims(int dtype, bool vec) {
   if (dtype == kDtypeF32 || !vec) return {128, 128};
-  return {128, 256};
+  return {256, 256};
 }
 // contraction tiles (output rows x feature columns)
 inline TileDims con_tile_dims(int dtype) {

@@ -3,7 +3,7 @@ oracle on the same dtype-rounded inputs (tolerance 1e-2 on loss and gradient
 max-rel).
 
 16-bit inputs with 16-byte aligned rows (D and the row stride multiples of 8)
-run on the direct-to-LDS core (128 x 256 forward tiles); other layouts on the
+run on the direct-to-LDS core (256 x 256 forward tiles); other layouts on the
 register-staged 128 x 128 core.  The backward always keeps only the transposed
 gradient matrix: the y-side contraction reads it K-major, the x-side one (the
 only side LiT has) through transposing LDS loads.  fp16 stores that matrix
