@@ -186,18 +186,18 @@ bool f32_contract_dma(int64_t ldt, int64_t bs) {
 }
 
 // T = element type of dtype: float, bf16 bits (uint16_t) or fp16 (_Float16)
-#define DISPATCH_DTYPE(dtype, T, ...)   \
-  do {                                  \
-    if ((dtype) == MEC_DTYPE_F32) {     \
-      using T = float;                  \
-      __VA_ARGS__;                      \
+#define DISPATCH_DTYPE(dtype, T, ...)       \
+  do {                                      \
+    if ((dtype) == MEC_DTYPE_F32) {         \
+      using T = float;                      \
+      __VA_ARGS__;                          \
     } else if ((dtype) == MEC_DTYPE_BF16) { \
-      using T = uint16_t;               \
-      __VA_ARGS__;                      \
-    } else {                            \
-      using T = _Float16;               \
-      __VA_ARGS__;                      \
-    }                                   \
+      using T = uint16_t;                   \
+      __VA_ARGS__;                          \
+    } else {                                \
+      using T = _Float16;                   \
+      __VA_ARGS__;                          \
+    }                                       \
   } while (0)
 
 #define DISPATCH_BOOL(cond, NAME, ...) \

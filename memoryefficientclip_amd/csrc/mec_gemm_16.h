@@ -14,8 +14,8 @@
 #pragma once
 #include "mec_common.h"
 
-#ifndef MEC_BF16_STAGES
-#define MEC_BF16_STAGES 1
+#ifndef MEC_16BIT_STAGES
+#define MEC_16BIT_STAGES 1
 #endif
 
 namespace mec {
@@ -23,7 +23,7 @@ namespace g16 {
 
 constexpr int BM = 128;
 constexpr int NT = 256;
-constexpr int STAGES = MEC_BF16_STAGES;
+constexpr int STAGES = MEC_16BIT_STAGES;
 
 // Geometry of a core with K chunks of BK elements.
 template <int BK>

@@ -166,6 +166,8 @@ struct LoadPlan {
   }
 };
 
+// One k-step's operand fragments: per 32-row block, this lane's 16-byte
+// vector (8 16-bit or 4 fp32 values; the bits are moved as i16x8)
 template <class G>
 struct Frags {
   i16x8 a[G::FM], b[G::FN];
@@ -315,7 +317,8 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
   lp.init(A, B);
   // prologue: chunks 0 .. S-2 in flight
 #pragma unroll
-  for (int c = 0; c + 1 < S; ++c) static_for<G::IPW>([&](auto i) { lp.template issue<i>(c * BK, lds + c * G::STAGE); });
+  for (int c = 0; c + 1 < S; ++c)
+    static_for<G::IPW>([&](auto i) { lp.template issue<i>(c * BK, lds + c * G::STAGE); });
   Frags<G> f0, f1;
   int cur = 0;      // stage of chunk kt
   int fre = S - 1;  // stage of chunk kt-1 = stage of chunk kt+S-1

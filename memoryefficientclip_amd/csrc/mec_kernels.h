@@ -35,8 +35,8 @@ namespace mec {
 // Every config: BM x BN output tile per workgroup of WM x WN waves (NT
 // threads), each wave a TM x TN sub-tile of FM x FN 32x32 MFMA blocks whose
 // accumulator register r of lane l holds element (acc_row(r, l), l % 32).
-#ifndef MEC_BF16_BK_FWD
-#define MEC_BF16_BK_FWD 64
+#ifndef MEC_16BIT_BK
+#define MEC_16BIT_BK 64
 #endif
 
 // fp32, 128 x 128, operands staged through registers
@@ -75,10 +75,10 @@ struct Tile16V : Pack16<F16> {
   using Op = g16::Operand;
   static constexpr bool TA = false;
   static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2, WM = 2, WN = 2, NT = 256;
-  static constexpr int LDS_BYTES = g16::Cfg<MEC_BF16_BK_FWD>::LDS_ELEMS * 2;
+  static constexpr int LDS_BYTES = g16::Cfg<MEC_16BIT_BK>::LDS_ELEMS * 2;
   template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
-    g16::mainloop<MEC_BF16_BK_FWD, VECA, VECB, F16>(a, b, K, (uint16_t*)lds, acc);
+    g16::mainloop<MEC_16BIT_BK, VECA, VECB, F16>(a, b, K, (uint16_t*)lds, acc);
   }
 };
 
@@ -200,10 +200,9 @@ __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::
 }
 
 template <typename T, bool LIT, bool NORM, bool VEC>
-__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_sumexp(const T* __restrict__ X, int64_t ldx,
-                                                            const T* __restrict__ Y, int64_t ldy, int N, int D,
-                                                            int kmax, float c, float* __restrict__ ws, int tiles_m,
-                                                            int tiles_n) {
+__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_sumexp(
+    const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
+    float* __restrict__ ws, int tiles_m, int tiles_n) {
   using TL = FwdTile<T, VEC>;
   static_assert(TL::FM == 2, "row reduction assumes 64-row wave sub-tiles");
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
@@ -569,7 +568,8 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
   // entries of G' and XT/YT at k in [qn, round8(qn)) are stored zeros
   const int kq = (qn + 7) & ~7;
   // A: rows tm*BM.. of the block (K-major), or columns tm*BM.. of a transposed block
-  const auto A = tile_op<TC>(Gblk + (TC::TA ? (int64_t)(tm * TC::BM) : (int64_t)(tm * TC::BM) * bg.bs), bg.bs, TC::BM, kq);
+  const int64_t a_off = TC::TA ? (int64_t)(tm * TC::BM) : (int64_t)(tm * TC::BM) * bg.bs;
+  const auto A = tile_op<TC>(Gblk + a_off, bg.bs, TC::BM, kq);
   const auto B = tile_op<TC>(OT + (int64_t)d0 * ldt + q0, ldt, min(D - d0, TC::BN), kq);
   f32x16 acc[TC::FM][TC::FN];
   TC::template run<true, true>(A, B, kq, lds, acc);
@@ -647,11 +647,10 @@ __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int
 // contractions of diagonal diag_c (the 16-bit types run those in k_grad_contract); CDMA
 // selects the fp32 contraction core.
 template <typename T, bool LIT, bool NORM, bool VEC, bool CDMA>
-__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::bwd)) void k_grad_step(const T* __restrict__ X, int64_t ldx,
-                                                               const T* __restrict__ Y, int64_t ldy, int N, int D,
-                                                               int kmax, float c, const float* __restrict__ ws,
-                                                               GradBufs gb, BlockGrid bg, StepPlan sp,
-                                                               float* __restrict__ acc_x, float* __restrict__ acc_y) {
+__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::bwd)) void k_grad_step(
+    const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
+    const float* __restrict__ ws, GradBufs gb, BlockGrid bg, StepPlan sp, float* __restrict__ acc_x,
+    float* __restrict__ acc_y) {
   using TF = FwdTile<T, VEC>;
   constexpr bool FUSED = !GtOnly<T>::value;  // contractions in this kernel
   using TCX = typename std::conditional<FUSED, ConTileX<T, CDMA>, TF>::type;
