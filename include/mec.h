@@ -29,13 +29,14 @@
  *   - Pointers are device pointers.  x and y are row-major [n, d] with row
  *     strides ldx, ldy (in elements, >= d) and unit column stride.
  *     x is the row side of S = x^ y^T: image for CLIP, text for LiT.
- *   - dtype: MEC_DTYPE_F32 (float), MEC_DTYPE_BF16 (uint16 bfloat16 bits) or
- *     MEC_DTYPE_F16 (uint16 IEEE binary16 bits).  All arithmetic accumulates
- *     in fp32; the loss is reduced in fp64.  Sizes: 1 <= d <= 2^20; 1 <= n <= 2^30
- *     for fp32 and n <= 2^22 for the 16-bit types (MEC_ERR_UNSUPPORTED
- *     beyond).  16-bit rows that are 16-byte aligned (x, y 16-byte aligned, d,
- *     ldx, ldy multiples of 8) use the direct-to-LDS tiles; other layouts are
- *     supported at lower speed.
+ *   - dtype: MEC_DTYPE_F32 (float), MEC_DTYPE_BF16 (uint16 bfloat16 bits),
+ *     MEC_DTYPE_F16 (uint16 IEEE binary16 bits) or MEC_DTYPE_F32_BF16X3
+ *     (float data, products formed from bf16 terms, below).  All arithmetic
+ *     accumulates in fp32; the loss is reduced in fp64.  Sizes: 1 <= d <= 2^20;
+ *     1 <= n <= 2^30 for fp32 and n <= 2^22 for the other dtypes
+ *     (MEC_ERR_UNSUPPORTED beyond).  16-bit rows that are 16-byte aligned (x, y
+ *     16-byte aligned, d, ldx, ldy multiples of 8) use the direct-to-LDS
+ *     tiles; other layouts are supported at lower speed.
  *   - mode: MEC_MODE_CLIP or MEC_MODE_LIT, optionally OR
  *     MEC_FLAG_DETERMINISTIC.  Every function accepts the flag; only the
  *     forward sums (mec_sumexp, mec_forward) depend on it.
@@ -62,6 +63,19 @@ extern "C" {
 #define MEC_DTYPE_F32 0
 #define MEC_DTYPE_BF16 1
 #define MEC_DTYPE_F16 2
+/* fp32 inputs and outputs (as MEC_DTYPE_F32), with every product of the
+ * similarity GEMMs and the gradient contractions formed as
+ * hi_a hi_b + lo_a hi_b + hi_a lo_b on the bf16 MFMA, where hi = bf16(v) and
+ * lo = bf16(v - hi) (about 16 significant bits per operand; the error of one
+ * product is at most about 3 * 2^-16 of it), accumulated in fp32.  The norms,
+ * the diagonal and the post-pass stay in fp32.  This is PyTorch's "high"
+ * float32 matmul precision (torch.set_float32_matmul_precision), and plays
+ * the role of the TF32 dot products the reference gets from Triton on NVIDIA
+ * (clip_loss.py:53,113,148-149 pass no input_precision).  No counterpart
+ * dtype in the reference.  The workspace is larger (mec_workspace_floats_for)
+ * and must be 16-byte aligned; mec_sumexp and mec_grad_step read split copies
+ * of x and y that mec_prepass writes into it. */
+#define MEC_DTYPE_F32_BF16X3 3
 
 #define MEC_MODE_CLIP 0 /* symmetric image<->text loss, gradients for x and y */
 #define MEC_MODE_LIT 1  /* text->image only (x = text), gradient for x only */
@@ -86,16 +100,24 @@ const char* mec_version(void);
  * of partial sums (the deterministic forward, MEC_FLAG_DETERMINISTIC).  The
  * workspace must be 8-byte aligned.  The same workspace must be passed to
  * mec_forward and the matching mec_backward (it replaces
- * ctx.save_for_backward of the sums, clip_loss.py:199). */
+ * ctx.save_for_backward of the sums, clip_loss.py:199).  For every dtype
+ * except MEC_DTYPE_F32_BF16X3. */
 int64_t mec_workspace_floats(int64_t n);
+
+/* Number of floats of the workspace for (n, d, dtype): mec_workspace_floats(n)
+ * for fp32, bf16 and fp16; for MEC_DTYPE_F32_BF16X3 that, rounded up to 4
+ * floats, plus split copies of x and y (2 n rows of 3 * round8(d) bf16).
+ * Returns < 0 on bad args.  No counterpart in the reference. */
+int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype);
 
 /* Bytes of gradient scratch needed by mec_grad / mec_grad_step /
  * mec_backward for (n, d, dtype), all in the input dtype: two buffers holding
  * one block diagonal of the off-diagonal gradient matrix each (nb blocks of
- * bs x bs; bs ~ 2d for fp32, ~8d but at most 32512 for the 16-bit types),
+ * bs x bs; bs ~ 2d for fp32, ~8d but at most 32512 for the other dtypes),
  * for fp32 the same blocks transposed as well, and transposed normalised
- * copies of x and y ([d][n rounded up to 128]); O(n*d) in total.  Returns
- * < 0 on bad args. */
+ * copies of x and y ([d][n rounded up to 128]); O(n*d) in total.
+ * MEC_DTYPE_F32_BF16X3 holds bf16 hi and lo planes of the transposed blocks
+ * and of the transposed copies.  Returns < 0 on bad args. */
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype);
 
 /* Block decomposition of the backward for (n, d, dtype): the n x n gradient
@@ -105,7 +127,8 @@ int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype);
  * clip_loss.py:239-249); exposed so callers can size and drive the steps. */
 int mec_grad_blocking(int64_t n, int64_t d, int dtype, int64_t* block_rows, int64_t* num_blocks);
 
-/* rx, ry (1 if !normalize), diag; clears the sum accumulators. */
+/* rx, ry (1 if !normalize), diag; clears the sum accumulators.
+ * MEC_DTYPE_F32_BF16X3: also writes the split copies of x and y. */
 int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                 int dtype, int normalize, float* workspace, void* stream);
 

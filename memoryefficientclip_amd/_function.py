@@ -14,7 +14,14 @@ This mirrors the glue of the reference's autograd Functions
   inputs with a row stride are read in place (no ``.contiguous()`` copy);
 * under ``torch.use_deterministic_algorithms(True)`` the loss and gradients
   are bitwise reproducible (the reference's relaxed atomics are not,
-  ``clip_loss.py:63-64,155-156``).
+  ``clip_loss.py:63-64,155-156``);
+* fp32 inputs follow ``torch.get_float32_matmul_precision()``: "highest" (the
+  default) multiplies in IEEE fp32 on the fp32 MFMA; "high" and "medium" form
+  each product from bf16 terms (hi*hi + lo*hi + hi*lo, about 16 significant
+  bits per operand) on the bf16 MFMA, PyTorch's meaning of "high".  The
+  reference's fp32 dot products are TF32 on NVIDIA (``tl.dot`` without
+  ``input_precision``, ``clip_loss.py:53,113,148-149``); this mode is the
+  fast counterpart here and keeps the fp32 tolerances.
 """
 from __future__ import annotations
 
@@ -59,6 +66,16 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def compute_dtype(dtype: torch.dtype) -> int:
+    """C-ABI dtype code for inputs of `dtype` under the current
+    ``torch.get_float32_matmul_precision()`` (fp32 only: anything but
+    "highest" selects the three-term bf16 products)."""
+    code = _DTYPES[dtype]
+    if code == _lib.DTYPE_F32 and torch.get_float32_matmul_precision() != "highest":
+        return _lib.DTYPE_F32_BF16X3
+    return code
+
+
 def forward(ctx, x: torch.Tensor, y: torch.Tensor, temperature: float, mode: int, normalize: bool,
             stable: bool) -> torch.Tensor:
     check_inputs(x, y)
@@ -69,9 +86,9 @@ def forward(ctx, x: torch.Tensor, y: torch.Tensor, temperature: float, mode: int
     y, ldy = _rows(y)
     n, d = x.shape
     dev = x.device
-    dt = _DTYPES[x.dtype]
+    dt = compute_dtype(x.dtype)
     with torch.cuda.device(dev):
-        ws = torch.empty(_lib.load().mec_workspace_floats(n), dtype=torch.float32, device=dev)
+        ws = torch.empty(_lib.load().mec_workspace_floats_for(n, d, dt), dtype=torch.float32, device=dev)
         loss = torch.empty((), dtype=torch.float32, device=dev)
         # under torch.use_deterministic_algorithms(True) the forward sums are
         # formed without atomics (the backward is deterministic either way)
@@ -98,7 +115,7 @@ def backward(ctx, grad_output: torch.Tensor, need_x: bool, need_y: bool):
         go = grad_output.detach().to(device=dev, dtype=torch.float32).reshape(()).contiguous()
         acc_x = torch.empty((n, d), dtype=torch.float32, device=dev) if need_x else None
         acc_y = torch.empty((n, d), dtype=torch.float32, device=dev) if need_y else None
-        if dt == _lib.DTYPE_F32:
+        if dt in (_lib.DTYPE_F32, _lib.DTYPE_F32_BF16X3):
             dx, dy = acc_x, acc_y  # the post-pass runs in place
         else:
             dx = torch.empty((n, d), dtype=x.dtype, device=dev) if need_x else None

@@ -21,6 +21,7 @@ MEC_ERR_HIP = -3
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_F16 = 2
+DTYPE_F32_BF16X3 = 3  # fp32 data, products as three bf16 MFMA terms
 MODE_CLIP = 0
 MODE_LIT = 1
 FLAG_DETERMINISTIC = 0x100  # OR into the mode of mec_sumexp / mec_forward
@@ -35,6 +36,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mec_last_error": (ctypes.c_char_p, []),
     "mec_version": (ctypes.c_char_p, []),
     "mec_workspace_floats": (_i64, [_i64]),
+    "mec_workspace_floats_for": (_i64, [_i64, _i64, _int]),
     "mec_grad_scratch_bytes": (_i64, [_i64, _i64, _int]),
     "mec_grad_blocking": (_int, [_i64, _i64, _int, _vp, _vp]),
     "mec_prepass": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp]),

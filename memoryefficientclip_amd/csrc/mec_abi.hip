@@ -42,8 +42,12 @@ constexpr int64_t kMaxD = int64_t(1) << 20;
 constexpr int64_t kMaxN16 = int64_t(1) << 22;
 
 bool known_dtype(int dtype) {
-  return dtype == MEC_DTYPE_F32 || dtype == MEC_DTYPE_BF16 || dtype == MEC_DTYPE_F16;
+  return dtype == MEC_DTYPE_F32 || dtype == MEC_DTYPE_BF16 || dtype == MEC_DTYPE_F16 ||
+         dtype == MEC_DTYPE_F32_BF16X3;
 }
+bool is_x3(int dtype) { return dtype == MEC_DTYPE_F32_BF16X3; }
+// element type of the caller's x, y, dx, dy (the bf16x3 mode reads and writes fp32)
+int data_dtype(int dtype) { return is_x3(dtype) ? MEC_DTYPE_F32 : dtype; }
 
 int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                  int dtype) {
@@ -55,7 +59,7 @@ int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   if (!known_dtype(dtype)) return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
   if (x == nullptr || y == nullptr) return fail(MEC_ERR_INVALID, "x and y must be non-null");
   if (dtype != MEC_DTYPE_F32 && n > kMaxN16)
-    return fail(MEC_ERR_UNSUPPORTED, "bf16 and fp16 support n <= 2^22 (n=%lld)", (long long)n);
+    return fail(MEC_ERR_UNSUPPORTED, "bf16, fp16 and bf16x3 support n <= 2^22 (n=%lld)", (long long)n);
   return MEC_OK;
 }
 
@@ -78,6 +82,35 @@ bool is_lit(int mode) { return (mode & MEC_MODE_MASK) == MEC_MODE_LIT; }
 // DET_SPLITS x n partial sums of the deterministic forward
 int64_t loss_partials_floats(int64_t n) { return 2 * ((n + FIN_ROWS - 1) / FIN_ROWS); }
 int64_t det_partials_offset(int64_t n) { return (int64_t)WS_NSLOTS * n + loss_partials_floats(n); }
+int64_t base_workspace_floats(int64_t n) { return det_partials_offset(n) + (int64_t)DET_SPLITS * n; }
+
+// bf16x3: the split operands of the similarity GEMMs follow, 16-byte aligned:
+// A3 (x rows: hi | lo | hi) and B3 (y rows: hi | hi | lo), n rows of
+// ld3 = 3 dp bf16 each, dp = d rounded up to 8 (k_split3)
+int64_t split_dp(int64_t d) { return (d + 7) & ~int64_t(7); }
+int64_t split_ld(int64_t d) { return 3 * split_dp(d); }
+int64_t split_offset_floats(int64_t n) { return (base_workspace_floats(n) + 3) & ~int64_t(3); }
+int64_t workspace_floats_for(int64_t n, int64_t d, int dtype) {
+  if (!is_x3(dtype)) return base_workspace_floats(n);
+  return split_offset_floats(n) + n * split_ld(d);  // 2 n ld3 bf16 = n ld3 floats
+}
+const uint16_t* split_a(const float* ws, int64_t n) { return (const uint16_t*)(ws + split_offset_floats(n)); }
+const uint16_t* split_b(const float* ws, int64_t n, int64_t d) { return split_a(ws, n) + n * split_ld(d); }
+
+// operands of the similarity GEMMs (forward sums, gradient-matrix tiles)
+struct GemmOperands {
+  const void* x;
+  int64_t ldx;
+  const void* y;
+  int64_t ldy;
+  int64_t d;   // K
+  int dtype;   // element type of x, y
+};
+// bf16x3: the split copies in the workspace, a bf16 problem with K = 3 dp
+GemmOperands split_operands(const float* ws, int64_t n, int64_t d) {
+  const int64_t ld3 = split_ld(d);
+  return GemmOperands{split_a(ws, n), ld3, split_b(ws, n, d), ld3, ld3, MEC_DTYPE_BF16};
+}
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -147,14 +180,18 @@ void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
   *nb = (int)((tiles + tb - 1) / tb);
 }
 
-// Scratch layout of the backward (element type = input dtype):
-//   fp32: [G0 | G1 | GT0 | GT1 | XT | YT]     bf16, fp16: [GT0 | GT1 | XT | YT]
+// Scratch layout of the backward (element type = input dtype; bf16x3: bf16):
+//   fp32:        [G0 | G1 | GT0 | GT1 | XT | YT]
+//   bf16, fp16:  [GT0 | GT1 | XT | YT]
+//   bf16x3:      [GT0 | GT1 | GTlo0 | GTlo1 | XT | YT | XTlo | YTlo]
 // G0/G1 (and their transposes GT0/GT1) double-buffer one block diagonal of
-// G' (nb blocks of bs x bs; the 16-bit types keep only the transposed copy); XT/YT are
-// the normalised inputs transposed, [d][ldt] with ldt = n rounded up to 128.
+// G' (nb blocks of bs x bs; the 16-bit types keep only the transposed copy,
+// bf16x3 its hi and lo planes); XT/YT are the normalised inputs transposed,
+// [d][ldt] with ldt = n rounded up to 128 (bf16x3: hi and lo planes).
 struct ScratchLayout {
   int bs, nb;
-  int ncopies;                     // gradient-matrix buffers: 4 (G, GT double-buffered) or 2 (GT)
+  int ncopies;                     // gradient-matrix buffers: 4 or 2
+  int ntrans;                      // transposed-input buffers: 2 or 4
   int64_t ldt, gbuf, tbuf, total;  // bytes except ldt (elements)
 };
 
@@ -165,8 +202,9 @@ ScratchLayout scratch_layout(int64_t n, int64_t d, int dtype) {
   L.ldt = (n + 127) / 128 * 128;
   L.gbuf = (int64_t)L.nb * L.bs * L.bs * elem;
   L.tbuf = d * L.ldt * elem;
-  L.ncopies = dtype == MEC_DTYPE_F32 ? 4 : 2;
-  L.total = L.ncopies * L.gbuf + 2 * L.tbuf;
+  L.ncopies = (dtype == MEC_DTYPE_F32 || is_x3(dtype)) ? 4 : 2;
+  L.ntrans = is_x3(dtype) ? 4 : 2;
+  L.total = L.ncopies * L.gbuf + L.ntrans * L.tbuf;
   return L;
 }
 
@@ -185,7 +223,8 @@ bool f32_contract_dma(int64_t ldt, int64_t bs) {
   return (dma_rows(MEC_DTYPE_F32) - 1) * pitch + bs <= dma_max_elems(MEC_DTYPE_F32);
 }
 
-// T = element type of dtype: float, bf16 bits (uint16_t) or fp16 (_Float16)
+// T = element type of dtype: float, bf16 bits (uint16_t) or fp16 (_Float16);
+// callers map the bf16x3 mode to float first (data_dtype)
 #define DISPATCH_DTYPE(dtype, T, ...)       \
   do {                                      \
     if ((dtype) == MEC_DTYPE_F32) {         \
@@ -221,7 +260,12 @@ const char* mec_version(void) { return "memoryefficientclip_amd 0.1.0 gfx950"; }
 
 int64_t mec_workspace_floats(int64_t n) {
   if (n < 1 || n > kMaxN) return -1;
-  return det_partials_offset(n) + (int64_t)DET_SPLITS * n;
+  return base_workspace_floats(n);
+}
+
+int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype) {
+  if (n < 1 || n > kMaxN || d < 1 || d > kMaxD || !known_dtype(dtype)) return -1;
+  return workspace_floats_for(n, d, dtype);
 }
 
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype) {
@@ -236,11 +280,25 @@ int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
   int rc = check_common(x, ldx, y, ldy, n, d, dtype);
   if (rc) return rc;
   if (!workspace) return fail(MEC_ERR_INVALID, "workspace must be non-null");
+  if (is_x3(dtype) && !aligned16(workspace))
+    return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for bf16x3");
   hipStream_t s = (hipStream_t)stream;
   const int N = (int)n, D = (int)d;
   dim3 grid((unsigned)((n + 3) / 4));
-  DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM,
+  DISPATCH_DTYPE(data_dtype(dtype), T, DISPATCH_BOOL(normalize, NORM,
       k_prepass<T, NORM><<<grid, 256, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, workspace)));
+  if (is_x3(dtype)) {
+    // split copies of x and y for the similarity GEMMs (the norms and the
+    // diagonal above come from the fp32 inputs)
+    const int64_t dp = split_dp(d), ld3 = split_ld(d);
+    const int64_t nthr = n * (dp / 8);
+    if ((nthr + 255) / 256 > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "split grid too large");
+    const unsigned sgrid = (unsigned)((nthr + 255) / 256);
+    uint16_t* a3 = (uint16_t*)split_a(workspace, n);
+    uint16_t* b3 = (uint16_t*)split_b(workspace, n, d);
+    k_split3<0><<<sgrid, 256, 0, s>>>((const float*)x, ldx, N, D, (int)dp, a3, ld3);
+    k_split3<1><<<sgrid, 256, 0, s>>>((const float*)y, ldy, N, D, (int)dp, b3, ld3);
+  }
   return check_launch("prepass");
 }
 
@@ -253,8 +311,15 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   if (rc) return rc;
   if (!workspace) return fail(MEC_ERR_INVALID, "workspace must be non-null");
   hipStream_t s = (hipStream_t)stream;
-  const int N = (int)n, D = (int)d;
   const float c = (float)(1.4426950408889634 / (double)temperature);
+  // bf16x3: the bf16 sums over the split copies (K = 3 dp) that mec_prepass wrote
+  GemmOperands g{x, ldx, y, ldy, d, dtype};
+  if (is_x3(dtype)) {
+    if (!aligned16(workspace)) return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for bf16x3");
+    g = split_operands(workspace, n, d);
+  }
+  x = g.x, ldx = g.ldx, y = g.y, ldy = g.ldy, d = g.d, dtype = g.dtype;
+  const int N = (int)n, D = (int)d;
   const bool vec = vec_ok(x, ldx, y, ldy, d, dtype);
   const TileDims td = fwd_tile_dims(dtype, vec);
   const int tiles_m = (int)((n + td.bm - 1) / td.bm), tiles_n = (int)((n + td.bn - 1) / td.bn);
@@ -361,7 +426,12 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
     return fail(MEC_ERR_INVALID, "step %lld out of range [0, %d]", (long long)step, nb);
   const int N = (int)n, D = (int)d;
   const float c = (float)(1.4426950408889634 / (double)temperature);
-  const bool vec = vec_ok(x, ldx, y, ldy, d, dtype);
+  const bool x3 = is_x3(dtype);
+  if (x3 && !aligned16(workspace)) return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for bf16x3");
+  // operands of the gradient-matrix tiles (bf16x3: the split copies, K = 3 dp)
+  const GemmOperands go = x3 ? split_operands(workspace, n, d) : GemmOperands{x, ldx, y, ldy, d, dtype};
+  const bool vec = vec_ok(go.x, go.ldx, go.y, go.ldy, go.d, go.dtype);
+  if (x3 && !vec) return fail(MEC_ERR_UNSUPPORTED, "bf16x3 split operands beyond the direct-load range");
   const bool cdma = f32_contract_dma(L.ldt, bs);
   const TileDims tf = fwd_tile_dims(dtype, vec), tc = con_tile_dims(dtype);
   BlockGrid bg{bs, nb, bs / tf.bm, bs / tf.bn, bs / tc.bm, (D + tc.bn - 1) / tc.bn};
@@ -387,35 +457,70 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
   const int64_t grid_c = split ? (int64_t)sp.cx_pad + sp.cy_pad : 0;
   if (grid > 0x7fffffff || grid_c > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "backward grid too large");
   char* base = (char*)scratch;
-  GradBufs gb;
-  if (L.ncopies == 4) {
+  GradBufs gb{};
+  if (dtype == MEC_DTYPE_F32) {
     gb.g[0] = base;
     gb.g[1] = base + L.gbuf;
     gb.gt[0] = base + 2 * L.gbuf;
     gb.gt[1] = base + 3 * L.gbuf;
   } else {
-    gb.g[0] = gb.g[1] = nullptr;
     gb.gt[0] = base;
     gb.gt[1] = base + L.gbuf;
+    if (x3) {
+      gb.gt_lo[0] = base + 2 * L.gbuf;
+      gb.gt_lo[1] = base + 3 * L.gbuf;
+    }
   }
-  gb.xt = base + L.ncopies * L.gbuf;
-  gb.yt = base + L.ncopies * L.gbuf + L.tbuf;
+  char* tb = base + L.ncopies * L.gbuf;
+  gb.xt = tb;
+  gb.yt = tb + L.tbuf;
+  if (x3) {
+    gb.xt_lo = tb + 2 * L.tbuf;
+    gb.yt_lo = tb + 3 * L.tbuf;
+  }
   gb.ldt = L.ldt;
   hipStream_t s = (hipStream_t)stream;
   if (step == 0) {
     // transposed normalised operands of the contractions: YT for the x side, XT for the y side
     const int64_t n64 = n;
     dim3 tgrid((unsigned)(L.ldt / 64), (unsigned)((d + 63) / 64));
-    DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, {
-      if (acc_x)
-        k_transpose<T, NORM><<<tgrid, 256, 0, s>>>((const T*)y, ldy, N, D, workspace + WS_RY * n64, (T*)gb.yt,
-                                                   L.ldt);
-      if (acc_y)
-        k_transpose<T, NORM><<<tgrid, 256, 0, s>>>((const T*)x, ldx, N, D, workspace + WS_RX * n64, (T*)gb.xt,
-                                                   L.ldt);
-    }));
+    if (x3) {
+      DISPATCH_BOOL(normalize, NORM, {
+        if (acc_x)
+          k_transpose_split<NORM><<<tgrid, 256, 0, s>>>((const float*)y, ldy, N, D, workspace + WS_RY * n64,
+                                                        (uint16_t*)gb.yt, (uint16_t*)gb.yt_lo, L.ldt);
+        if (acc_y)
+          k_transpose_split<NORM><<<tgrid, 256, 0, s>>>((const float*)x, ldx, N, D, workspace + WS_RX * n64,
+                                                        (uint16_t*)gb.xt, (uint16_t*)gb.xt_lo, L.ldt);
+      });
+    } else {
+      DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, {
+        if (acc_x)
+          k_transpose<T, NORM><<<tgrid, 256, 0, s>>>((const T*)y, ldy, N, D, workspace + WS_RY * n64, (T*)gb.yt,
+                                                     L.ldt);
+        if (acc_y)
+          k_transpose<T, NORM><<<tgrid, 256, 0, s>>>((const T*)x, ldx, N, D, workspace + WS_RX * n64, (T*)gb.xt,
+                                                     L.ldt);
+      }));
+    }
     rc = check_launch("transpose");
     if (rc) return rc;
+  }
+  if (x3) {
+    // the bf16 kernels on the split operands, with hi/lo gradient-matrix planes
+    using T = uint16_t;
+    const int D3 = (int)go.d;
+    if (grid_c > 0) {
+      k_grad_contract<T, true><<<(unsigned)grid_c, ConTileX<T>::NT, 0, s>>>(N, D, gb, bg, sp_c, acc_x, acc_y);
+      rc = check_launch("grad_contract");
+      if (rc) return rc;
+    }
+    if (grid > 0)
+      DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM,
+          k_grad_step<T, LIT, NORM, true, true, true><<<(unsigned)grid, FwdTile<T, true>::NT, 0, s>>>(
+              (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, D3, D3, c, workspace, gb, bg, sp_g, acc_x,
+              acc_y)));
+    return check_launch("grad_step");
   }
   DISPATCH_DTYPE(dtype, T, {
     if (grid_c > 0) {
@@ -478,7 +583,7 @@ int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   const float* kap = workspace + WS_KAPPA * n64;
   const float a = (float)((double)grad_scale / (lit ? (double)n : 2.0 * (double)n));
   dim3 grid((unsigned)((n + 3) / 4));
-  DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, {
+  DISPATCH_DTYPE(data_dtype(dtype), T, DISPATCH_BOOL(normalize, NORM, {
     if (acc_x)
       k_postpass<T, NORM><<<grid, 256, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, rx, ry, kap, a,
                                                grad_output, acc_x, (T*)dx);

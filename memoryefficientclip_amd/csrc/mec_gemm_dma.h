@@ -293,24 +293,26 @@ __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM
   });
 }
 
-// acc[i][j] (this wave's sub-tile) = sum_k A(m, k) * B(n, k) over k in [0, K),
-// K > 0 (chunks past kmax read as zero).  Uses LDS_BYTES of `lds`; ends with
-// every wave past its last LDS read of the ring and its loads landed
-// (callers may reuse the ring after a barrier).
+// acc[i][j] (this wave's sub-tile) = sum_k A(m, k) * B(n, k) over k in [0, K)
+// (ZERO = false: added to acc), K > 0 (chunks past kmax read as zero).  Uses
+// LDS_BYTES of `lds`; ends with every wave past its last LDS read of the ring
+// and its loads landed (callers may reuse the ring after a barrier).
 //
 // Every iteration issues the loads of chunk kt+S-1, also past the last chunk
 // (they read zeros into a stage nobody reads again): the loop has no branches
 // around its loads and the number of loads in flight at each wait is the
 // same, IPW * (S - 2).
-template <class G>
+template <class G, bool ZERO = true>
 __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int K, char* lds,
                                          f32x16 (&acc)[G::FM][G::FN]) {
+  if constexpr (ZERO) {
 #pragma unroll
-  for (int i = 0; i < G::FM; ++i)
+    for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < G::FN; ++j)
+      for (int j = 0; j < G::FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  }
   constexpr int BK = G::BK;
   const int nk = (K + BK - 1) / BK;
   LoadPlan<G> lp;

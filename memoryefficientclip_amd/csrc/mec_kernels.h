@@ -104,9 +104,9 @@ struct TileD : PackOf<KIND>::type {
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
   static constexpr int LDS_BYTES = G::LDS_BYTES;
-  template <bool VECA, bool VECB>
+  template <bool VECA, bool VECB, bool ZERO = true>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
-    gdma::mainloop<G>(a, b, K, (char*)lds, acc);
+    gdma::mainloop<G, ZERO>(a, b, K, (char*)lds, acc);
   }
 };
 
@@ -378,13 +378,18 @@ struct BlockGrid {
 //          only copy);
 //   XT, YT the normalised inputs transposed, [D][ldt] with ldt = N rounded
 //          up to 128 and zero columns [N, ldt): element (d, i) = rx_i x_i[d].
-// Every contraction operand is then K-major (k contiguous).
+// Every contraction operand is then K-major (k contiguous).  The bf16x3 mode
+// keeps GT, XT and YT as bf16 hi planes (gt, xt, yt) and lo planes (gt_lo,
+// xt_lo, yt_lo), all null otherwise.
 struct GradBufs {
   void* g[2];
   void* gt[2];
   const void* xt;
   const void* yt;
   int64_t ldt;
+  void* gt_lo[2];
+  const void* xt_lo;
+  const void* yt_lo;
 };
 
 // One pipeline step of the backward (launch t = 0 .. nb):
@@ -445,8 +450,8 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN]
 
 // 16-bit: G'_ij of this wave's TM x TN accumulators, staged through LDS as
 // [j][i] (row pitch gt_pitch(BM) = 2 BM + 16 bytes; 4 consecutive i per 8-byte write), then
-// written to GTb (row pitch bs) as whole 256-byte tile rows, 16 bytes per
-// lane.  MASK zeroes the diagonal and entries outside [0, N).  Every row of
+// written to GTb (row pitch bs) as whole tile rows of 2 BM bytes, 16 bytes
+// per lane.  MASK zeroes the diagonal and entries outside [0, N).  Every row of
 // the tile is written (zeros for j >= N), so the contractions may read a
 // tile's rows and columns past N as zeros.  lds must hold BN * gt_pitch(BM) bytes
 // and be free (no wave still reading it).
@@ -454,13 +459,38 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN]
 // of a half-wave write one chunk of 32 consecutive rows, which then fall on
 // 32 distinct bank pairs (rows j and j + 16 would share them at this pitch).
 constexpr int gt_pitch(int bm) { return 2 * bm + 16; }
+
+// 4 consecutive i (tile rows ml .. ml+3) into staging row `row` (a tile
+// column j) of the [j][i] staging
+template <class TL>
+__device__ __forceinline__ void gt_stage4(char* lds, int ml, int row, float a, float b, float c, float d) {
+  const int chunk = (ml >> 2) ^ ((row >> 4) & 1);
+  TL::store4((uint16_t*)(lds + row * gt_pitch(TL::BM) + chunk * 8), a, b, c, d);
+}
+
+// the staged tile to GTb (row pitch bs) as whole tile rows, 16 bytes per lane.
+// Non-temporal stores: the block is read back from HBM by the next launch's
+// contractions and would only evict their operand panels from L2 (measured:
+// config 4 backward 22.6 -> 21.9 ms).
+template <class TL>
+__device__ __forceinline__ void gt_write_plane(const char* lds, uint16_t* __restrict__ GTb, int bs) {
+  constexpr int PITCH = gt_pitch(TL::BM);
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int VPR = TL::BM * 2 / 16;  // 16-byte vectors per tile row
+  for (int v = threadIdx.x; v < TL::BN * VPR; v += TL::NT) {
+    const int row = v / VPR, cv = v - row * VPR;
+    u32x4 u = *(const u32x4*)(lds + row * PITCH + cv * 16);
+    if ((row >> 4) & 1) u = u32x4{u.z, u.w, u.x, u.y};  // undo the chunk swizzle
+    __builtin_nontemporal_store(u, (u32x4*)(GTb + (int64_t)row * bs + cv * 8));
+  }
+}
+
 template <class TL, bool LIT, bool NORM, bool MASK>
 __device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0, int N,
                                                   uint16_t* __restrict__ GTb, int bs, const float* s_rx,
                                                   const float* s_ry, const float* s_ir, const float* s_ic,
                                                   char* lds) {
-  constexpr int PITCH = gt_pitch(TL::BM);
-  static_assert(PITCH % 256 == 16, "rows j and j + 16 share banks only as the swizzle assumes");
+  static_assert(gt_pitch(TL::BM) % 256 == 16, "rows j and j + 16 share banks only as the swizzle assumes");
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
 #pragma unroll
   for (int bm = 0; bm < TL::FM; ++bm) {
@@ -485,34 +515,96 @@ __device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL
           gv[e] = g;
         }
         const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g4, lane);
-        const int chunk = (ml >> 2) ^ ((nl >> 4) & 1);
-        TL::store4((uint16_t*)(lds + nl * PITCH + chunk * 8), gv[0], gv[1], gv[2], gv[3]);
+        gt_stage4<TL>(lds, ml, nl, gv[0], gv[1], gv[2], gv[3]);
       }
     }
   }
   __syncthreads();
-  // non-temporal stores: the block is read back from HBM by the next launch's
-  // contractions and would only evict their operand panels from L2 (measured:
-  // config 4 backward 22.6 -> 21.9 ms)
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  gt_write_plane<TL>(lds, GTb, bs);
+}
+
+// bf16x3: G'^T as a bf16 hi plane bf16(G') at GTh and a lo plane
+// bf16(G' - hi) at GTl.  Both planes of half the tile's columns fit the
+// staging area of one full plane, so the tile goes out in two halves: each
+// wave's column blocks bn < FN/2, then the rest.  Staging row s (of BN/2)
+// holds tile column nl(s) as in grad_gt_store_lds (same swizzle), the hi
+// plane in rows [0, BN/2), the lo plane after it.
+template <class TL>
+__device__ __forceinline__ int x3_stage_col(int srow, int half) {
+  constexpr int HT = TL::TN / 2;  // staged columns per wave and half
+  const int wn = srow / HT, rem = srow - wn * HT;
+  return wn * TL::TN + half * HT + rem;
+}
+template <class TL, bool LIT, bool NORM, bool MASK>
+__device__ __forceinline__ void grad_gt_store_lds_x3(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0,
+                                                     int N, uint16_t* __restrict__ GTh, uint16_t* __restrict__ GTl,
+                                                     int bs, const float* s_rx, const float* s_ry, const float* s_ir,
+                                                     const float* s_ic, char* lds) {
+  constexpr int PITCH = gt_pitch(TL::BM);
+  static_assert(PITCH % 256 == 16, "rows j and j + 16 share banks only as the swizzle assumes");
+  static_assert(TL::FN % 2 == 0, "two halves of whole column blocks");
+  constexpr int HB = TL::FN / 2, HT = TL::TN / 2, HROWS = TL::BN / 2;
   constexpr int VPR = TL::BM * 2 / 16;  // 16-byte vectors per tile row
-  for (int v = threadIdx.x; v < TL::BN * VPR; v += TL::NT) {
-    const int row = v / VPR, cv = v - row * VPR;
-    u32x4 u = *(const u32x4*)(lds + row * PITCH + cv * 16);
-    if ((row >> 4) & 1) u = u32x4{u.z, u.w, u.x, u.y};  // undo the chunk swizzle
-    __builtin_nontemporal_store(u, (u32x4*)(GTb + (int64_t)row * bs + cv * 8));
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
+  char* lds_lo = lds + HROWS * PITCH;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int bm = 0; bm < TL::FM; ++bm) {
+#pragma unroll
+      for (int bb = 0; bb < HB; ++bb) {
+        const int bn = half * HB + bb;
+        const int nl = wn * TL::TN + bn * 32 + (lane & 31);
+        const int srow = wn * HT + bb * 32 + (lane & 31);
+        const int j = j0 + nl;
+        const float cy = NORM ? c * s_ry[nl] : c;
+        const float icj = s_ic[nl];
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          float gv[4], lv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g4 + e;
+            const int ml = wm * TL::TM + bm * 32 + acc_row(r, lane);
+            const int i = i0 + ml;
+            const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
+            const float ex = fast_exp2(fmaf(sc, cy, -c));
+            float g = LIT ? ex * s_ir[ml] : ex * (s_ir[ml] + icj);
+            if (MASK) g = (i < N && j < N && i != j) ? g : 0.f;
+            gv[e] = g;
+            lv[e] = g - bf16_to_f32(f32_to_bf16(g));
+          }
+          const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g4, lane);
+          gt_stage4<TL>(lds, ml, srow, gv[0], gv[1], gv[2], gv[3]);
+          gt_stage4<TL>(lds_lo, ml, srow, lv[0], lv[1], lv[2], lv[3]);
+        }
+      }
+    }
+    __syncthreads();
+    for (int v = threadIdx.x; v < 2 * HROWS * VPR; v += TL::NT) {
+      const int prow = v / VPR, cv = v - prow * VPR;  // staged row over both planes
+      const int lo = prow >= HROWS, srow = prow - lo * HROWS;
+      u32x4 u = *(const u32x4*)(lds + prow * PITCH + cv * 16);
+      if ((srow >> 4) & 1) u = u32x4{u.z, u.w, u.x, u.y};  // undo the chunk swizzle
+      const int nl = x3_stage_col<TL>(srow, half);
+      __builtin_nontemporal_store(u, (u32x4*)((lo ? GTl : GTh) + (int64_t)nl * bs + cv * 8));
+    }
+    if (half == 0) __syncthreads();  // every wave is done reading the first half
   }
 }
 
 // Recompute the similarity tile (i0, j0) and store G'_ij = E_ij (1/R_i + 1/C_j)
 // (LiT: E_ij / R_i) for i != j, 0 on the diagonal and outside [0, N), into
-// the G' block at Gb (row pitch bs) and, for CLIP, transposed at GTb.
+// the G' block at Gb (row pitch bs) and, for CLIP, transposed at GTb (X3: its
+// bf16 hi plane at GTb and lo plane at GTl).
 // Follows clip_loss.py:96-124 / lit_loss.py:94-120.
-template <class TL, typename T, bool LIT, bool NORM, bool VEC>
+template <class TL, typename T, bool LIT, bool NORM, bool VEC, bool X3>
 __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y,
                                             int64_t ldy, int N, int D, int kmax, float c, const float* __restrict__ ws,
-                                            T* __restrict__ Gb, T* __restrict__ GTb, int bs, int i0, int j0,
-                                            char* lds, float* s_rx, float* s_ry, float* s_ir, float* s_ic) {
+                                            T* __restrict__ Gb, T* __restrict__ GTb, T* __restrict__ GTl, int bs,
+                                            int i0, int j0, char* lds, float* s_rx, float* s_ry, float* s_ir,
+                                            float* s_ic) {
   const int64_t n64 = N;
   const int t = threadIdx.x;
   const auto A = tile_op<TL>(X + (int64_t)i0 * ldx, ldx, min(N - i0, TL::BM), kmax);
@@ -533,7 +625,13 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
   }
   __syncthreads();
   const bool diag = i0 < j0 + TL::BN && j0 < i0 + TL::BM;
-  if constexpr (GtOnly<T>::value) {
+  if constexpr (X3) {
+    static_assert(std::is_same<T, uint16_t>::value, "bf16x3 runs on bf16 split operands");
+    if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
+      grad_gt_store_lds_x3<TL, LIT, NORM, false>(acc, c, i0, j0, N, GTb, GTl, bs, s_rx, s_ry, s_ir, s_ic, lds);
+    else
+      grad_gt_store_lds_x3<TL, LIT, NORM, true>(acc, c, i0, j0, N, GTb, GTl, bs, s_rx, s_ry, s_ir, s_ic, lds);
+  } else if constexpr (GtOnly<T>::value) {
     if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
       grad_gt_store_lds<TL, LIT, NORM, false>(acc, c, i0, j0, N, (uint16_t*)GTb, bs, s_rx, s_ry, s_ir, s_ic, lds);
     else
@@ -555,9 +653,12 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
 // adds each element once per launch, in launch order (the reference instead
 // lets every (row-tile, column-tile) program add into dX/dY with contending
 // atomics, clip_loss.py:148-156).
-template <class TC, typename T>
+// X3 (bf16x3): Gblk/OT are the hi planes and Glo/OTlo the lo planes; the
+// tile is hi.hi + hi.lo + lo.hi, three passes over K into one accumulator.
+template <class TC, typename T, bool X3 = false>
 __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __restrict__ Gblk,
-                                                   const T* __restrict__ OT, int64_t ldt, const BlockGrid& bg,
+                                                   const T* __restrict__ Glo, const T* __restrict__ OT,
+                                                   const T* __restrict__ OTlo, int64_t ldt, const BlockGrid& bg,
                                                    int P, int Q, int tm, int td, bool accumulate,
                                                    float* __restrict__ out, char* lds) {
   const int r0 = P * bg.bs + tm * TC::BM;
@@ -570,9 +671,16 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
   // A: rows tm*BM.. of the block (K-major), or columns tm*BM.. of a transposed block
   const int64_t a_off = TC::TA ? (int64_t)(tm * TC::BM) : (int64_t)(tm * TC::BM) * bg.bs;
   const auto A = tile_op<TC>(Gblk + a_off, bg.bs, TC::BM, kq);
-  const auto B = tile_op<TC>(OT + (int64_t)d0 * ldt + q0, ldt, min(D - d0, TC::BN), kq);
+  const int64_t b_off = (int64_t)d0 * ldt + q0;
+  const auto B = tile_op<TC>(OT + b_off, ldt, min(D - d0, TC::BN), kq);
   f32x16 acc[TC::FM][TC::FN];
   TC::template run<true, true>(A, B, kq, lds, acc);
+  if constexpr (X3) {
+    __syncthreads();  // every wave is past its last read of the ring
+    TC::template run<true, true, false>(A, tile_op<TC>(OTlo + b_off, ldt, min(D - d0, TC::BN), kq), kq, lds, acc);
+    __syncthreads();
+    TC::template run<true, true, false>(tile_op<TC>(Glo + a_off, bg.bs, TC::BM, kq), B, kq, lds, acc);
+  }
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TC::WN, wn = w % TC::WN;
 #pragma unroll
   for (int bm = 0; bm < TC::FM; ++bm) {
@@ -599,7 +707,7 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
 }
 
 // Contraction workgroup `sub` (in [0, cx_pad + cy_pad)) of one pipeline step.
-template <class TCX, class TCY, typename T>
+template <class TCX, class TCY, typename T, bool X3 = false>
 __device__ __forceinline__ void grad_contract_dispatch(int sub, int N, int D, const GradBufs& gb, const BlockGrid& bg,
                                                        const StepPlan& sp, float* __restrict__ acc_x,
                                                        float* __restrict__ acc_y, char* lds) {
@@ -623,16 +731,20 @@ __device__ __forceinline__ void grad_contract_dispatch(int sub, int N, int D, co
   if (is_x) {
     const int Q = (P + sp.diag_c) % bg.nb;
     const T* gx = (const T*)(GtOnly<T>::value ? gb.gt[buf] : gb.g[buf]) + P * blk;
-    grad_contract_tile<TCX, T>(N, D, gx, (const T*)gb.yt, gb.ldt, bg, P, Q, tm, td, sp.accumulate != 0, acc_x, lds);
+    const T* gxl = X3 ? (const T*)gb.gt_lo[buf] + P * blk : nullptr;
+    grad_contract_tile<TCX, T, X3>(N, D, gx, gxl, (const T*)gb.yt, (const T*)gb.yt_lo, gb.ldt, bg, P, Q, tm, td,
+                                   sp.accumulate != 0, acc_x, lds);
   } else {
     const int Q = (P - sp.diag_c + bg.nb) % bg.nb;
-    grad_contract_tile<TCY, T>(N, D, (const T*)gb.gt[buf] + Q * blk, (const T*)gb.xt, gb.ldt, bg, P, Q, tm, td,
-                               sp.accumulate != 0, acc_y, lds);
+    const T* gyl = X3 ? (const T*)gb.gt_lo[buf] + Q * blk : nullptr;
+    grad_contract_tile<TCY, T, X3>(N, D, (const T*)gb.gt[buf] + Q * blk, gyl, (const T*)gb.xt, (const T*)gb.xt_lo,
+                                   gb.ldt, bg, P, Q, tm, td, sp.accumulate != 0, acc_y, lds);
   }
 }
 
-// 16-bit contractions of one pipeline step (the x side of diagonal diag_c, then the y side).
-template <typename T>
+// 16-bit (and bf16x3) contractions of one pipeline step (the x side of
+// diagonal diag_c, then the y side).
+template <typename T, bool X3 = false>
 __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int D, GradBufs gb, BlockGrid bg,
                                                                      StepPlan sp, float* __restrict__ acc_x,
                                                                      float* __restrict__ acc_y) {
@@ -640,13 +752,14 @@ __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int
   using TCY = ConTileY<T>;
   static_assert(TCX::BM == TCY::BM && TCX::BN == TCY::BN && TCX::NT == TCY::NT, "one contraction tile shape");
   __shared__ __attribute__((aligned(1024))) char lds[CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value];
-  grad_contract_dispatch<TCX, TCY, T>(blockIdx.x, N, D, gb, bg, sp, acc_x, acc_y, lds);
+  grad_contract_dispatch<TCX, TCY, T, X3>(blockIdx.x, N, D, gb, bg, sp, acc_x, acc_y, lds);
 }
 
 // One pipeline step: G' tiles of diagonal diag_g and, for fp32, the
 // contractions of diagonal diag_c (the 16-bit types run those in k_grad_contract); CDMA
-// selects the fp32 contraction core.
-template <typename T, bool LIT, bool NORM, bool VEC, bool CDMA>
+// selects the fp32 contraction core.  X3: bf16 split operands (K = 3 dp),
+// G'^T written as hi and lo planes.
+template <typename T, bool LIT, bool NORM, bool VEC, bool CDMA, bool X3 = false>
 __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::bwd)) void k_grad_step(
     const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
     const float* __restrict__ ws, GradBufs gb, BlockGrid bg, StepPlan sp, float* __restrict__ acc_x,
@@ -677,10 +790,11 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::bwd)) void k_g
   if (i0 >= N || j0 >= N) return;  // never read by the contraction
   const int buf = sp.diag_g & 1;
   T* Gb = GtOnly<T>::value ? nullptr : (T*)gb.g[buf] + I * blk + (int64_t)(tm * TF::BM) * bg.bs + tn * TF::BN;
-  T* GTb = (LIT && !GtOnly<T>::value) ? nullptr
-                                      : (T*)gb.gt[buf] + I * blk + (int64_t)(tn * TF::BN) * bg.bs + tm * TF::BM;
-  grad_g_tile<TF, T, LIT, NORM, VEC>(X, ldx, Y, ldy, N, D, kmax, c, ws, Gb, GTb, bg.bs, i0, j0, lds, s_rx, s_ry,
-                                     s_ir, s_ic);
+  const int64_t gt_off = I * blk + (int64_t)(tn * TF::BN) * bg.bs + tm * TF::BM;
+  T* GTb = (LIT && !GtOnly<T>::value) ? nullptr : (T*)gb.gt[buf] + gt_off;
+  T* GTl = X3 ? (T*)gb.gt_lo[buf] + gt_off : nullptr;
+  grad_g_tile<TF, T, LIT, NORM, VEC, X3>(X, ldx, Y, ldy, N, D, kmax, c, ws, Gb, GTb, GTl, bg.bs, i0, j0, lds, s_rx,
+                                         s_ry, s_ir, s_ic);
 }
 
 }  // namespace mec

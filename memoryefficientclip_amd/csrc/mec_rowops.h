@@ -203,4 +203,79 @@ __global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ X, int6
   }
 }
 
+// ------------------------------------------------- three-term bf16 split
+// fp32 as the sum of two bf16 terms: hi = bf16(v), lo = bf16(v - hi), both
+// rounded to nearest even (v - hi is exact in fp32), so v = hi + lo + r with
+// |r| <= 2^-16 |v| (bf16 keeps 8 significant bits).  The bf16x3 mode forms
+// every product a*b of the hot loops as hi_a*hi_b + lo_a*hi_b + hi_a*lo_b on
+// the bf16 MFMA (fp32 accumulate); the dropped lo_a*lo_b and the two
+// remainders bound the error of one product by about 3 * 2^-16 |ab|.
+__device__ __forceinline__ void split2_bf16(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const uint16_t ha = f32_to_bf16(a), hb = f32_to_bf16(b);
+  hi = (uint32_t)ha | ((uint32_t)hb << 16);
+  lo = pack2_bf16(a - bf16_to_f32(ha), b - bf16_to_f32(hb));
+}
+
+// Split copies of the inputs for the similarity GEMMs of the bf16x3 mode.
+// Row i of out (pitch ld3 elements) holds three segments of dp = D rounded up
+// to 8 elements: ORDER 0 (x side) hi, lo, hi; ORDER 1 (y side) hi, hi, lo.
+// The dot product of an x row with a y row over the 3 dp elements is then
+// hi.hi + lo.hi + hi.lo, one bf16 GEMM with K = 3 dp.  Columns D .. dp-1 of
+// each segment are zero.  One thread per 8 columns; out and ld3 16-byte
+// aligned.
+template <int ORDER>
+__global__ __launch_bounds__(256) void k_split3(const float* __restrict__ X, int64_t ldx, int N, int D, int dp,
+                                                uint16_t* __restrict__ out, int64_t ld3) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int vpr = dp / 8;
+  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (v >= (int64_t)N * vpr) return;
+  const int i = (int)(v / vpr), d0 = (int)(v - (int64_t)i * vpr) * 8;
+  const float* x = X + (int64_t)i * ldx;
+  u32x4 hi, lo;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int d = d0 + 2 * e;
+    const float a = d < D ? x[d] : 0.f, b = d + 1 < D ? x[d + 1] : 0.f;
+    uint32_t h, l;
+    split2_bf16(a, b, h, l);
+    hi[e] = h;
+    lo[e] = l;
+  }
+  uint16_t* o = out + (int64_t)i * ld3 + d0;
+  *(u32x4*)o = hi;
+  *(u32x4*)(o + dp) = ORDER == 0 ? lo : hi;
+  *(u32x4*)(o + 2 * dp) = ORDER == 0 ? hi : lo;
+}
+
+// k_transpose<float, NORM> into two bf16 planes: XT_hi[d][i] = hi(v),
+// XT_lo[d][i] = lo(v) with v = scale_i x_i[d] (fp32), zero for N <= i < ldt.
+template <bool NORM>
+__global__ __launch_bounds__(256) void k_transpose_split(const float* __restrict__ X, int64_t ldx, int N, int D,
+                                                         const float* __restrict__ scale, uint16_t* __restrict__ XTh,
+                                                         uint16_t* __restrict__ XTl, int64_t ldt) {
+  __shared__ float tile[64][65];
+  const int i0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int i = i0 + r, d = d0 + tx;
+    float v = 0.f;
+    if (i < N && d < D) {
+      v = X[(int64_t)i * ldx + d];
+      if (NORM) v *= scale[i];
+    }
+    tile[r][tx] = v;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int d = d0 + r, i = i0 + tx;
+    if (d < D && i < ldt) {
+      const float v = tile[tx][r];
+      const uint16_t h = f32_to_bf16(v);
+      XTh[(int64_t)d * ldt + i] = h;
+      XTl[(int64_t)d * ldt + i] = f32_to_bf16(v - bf16_to_f32(h));
+    }
+  }
+}
+
 }  // namespace mec

@@ -98,3 +98,23 @@ def test_product_path_does_not_import_oracle():
                 assert not any(a.name.split(".")[0] == "oracle" for a in node.names), f
             if isinstance(node, ast.ImportFrom):
                 assert (node.module or "").split(".")[0] != "oracle", f
+
+
+def test_float32_matmul_precision_selects_the_bf16x3_mode():
+    # "highest" (PyTorch's default): IEEE fp32 products; "high"/"medium":
+    # products from bf16 terms (C-ABI dtype MEC_DTYPE_F32_BF16X3); 16-bit
+    # inputs are unaffected
+    from memoryefficientclip_amd import _lib
+    from memoryefficientclip_amd._function import compute_dtype
+
+    old = torch.get_float32_matmul_precision()
+    try:
+        torch.set_float32_matmul_precision("highest")
+        assert compute_dtype(torch.float32) == _lib.DTYPE_F32
+        for p in ("high", "medium"):
+            torch.set_float32_matmul_precision(p)
+            assert compute_dtype(torch.float32) == _lib.DTYPE_F32_BF16X3
+            assert compute_dtype(torch.bfloat16) == _lib.DTYPE_BF16
+            assert compute_dtype(torch.float16) == _lib.DTYPE_F16
+    finally:
+        torch.set_float32_matmul_precision(old)
