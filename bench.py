@@ -19,6 +19,13 @@ benchmark table for exploration.  Rank 0 prints ONE JSON line:
 * ``cpu_baseline``: the dense PyTorch loss (fp32) on the host cores, on a
   bounded sample of the same workload (smaller N, same D and generator),
   scaled to TFLOP/s with the same flop convention.
+
+``--precision high`` runs fp32 inputs under
+``torch.set_float32_matmul_precision("high")``: the products are formed from
+bf16 terms (hi*hi + lo*hi + hi*lo) on the bf16 MFMA.  ``dtype`` is then
+"bf16x3", ``value`` stays in algorithmic (fp32-equivalent) flop, and the
+roofline counts the three MFMA products per algorithmic one against the bf16
+peak.  The default, "highest", is IEEE fp32 on the fp32 MFMA.
 """
 from __future__ import annotations
 
@@ -98,8 +105,9 @@ def grad_step_flop(n, d, bs, nb, sides):
     return out
 
 
-def kernel_leg(x, y, mode, dt, normalize, temperature, reps):
-    """Times each C-ABI stage of the path on its own (same inputs, same stream).
+def kernel_leg(x, y, mode, dtc, normalize, temperature, reps):
+    """Times each C-ABI stage of the path on its own (same inputs, same stream);
+    dtc is the C-ABI dtype code.
 
     Returns {stage: (avg ms per launch, launches per step, algorithmic flop per launch)}."""
     import torch
@@ -107,10 +115,9 @@ def kernel_leg(x, y, mode, dt, normalize, temperature, reps):
     lib = _lib.load()
     n, d = x.shape
     m = _lib.MODE_CLIP if mode == "clip" else _lib.MODE_LIT
-    dtc = {"f32": _lib.DTYPE_F32, "bf16": _lib.DTYPE_BF16, "f16": _lib.DTYPE_F16}[dt]
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
-    ws = torch.empty(lib.mec_workspace_floats(n), device=x.device)
+    ws = torch.empty(lib.mec_workspace_floats_for(n, d, dtc), device=x.device)
     loss = torch.empty((), device=x.device)
     nbytes = lib.mec_grad_scratch_bytes(n, d, dtc)
     scratch = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
@@ -218,6 +225,9 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--dtype", choices=sorted(PEAK_TFLOPS), default=None,
                     help="input dtype instead of the config's own (e.g. --config 4 --dtype f16)")
+    ap.add_argument("--precision", choices=["highest", "high"], default="highest",
+                    help="float32 matmul precision for fp32 inputs: highest = IEEE fp32 MFMA, "
+                         "high = three bf16 MFMA products per fp32 product (bf16x3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-reps", type=int, default=0, help="launches per stage in the kernel leg (default: steps)")
     ap.add_argument("--probe", choices=["copy"], default=None,
@@ -251,7 +261,20 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     tdtype = getattr(torch, TORCH_DTYPE[dt])
-    log(f"bench: config {args.config} {mode} n={n} d={d} {dt} normalized_inputs={normalized} T={temperature}")
+    # arithmetic: the input dtype's MFMA, or bf16x3 (three bf16 products per fp32 product)
+    x3 = args.precision == "high"
+    if x3 and dt != "f32":
+        print("bench.py: --precision high applies to fp32 inputs only", file=sys.stderr)
+        sys.exit(2)
+    torch.set_float32_matmul_precision(args.precision)
+    arith = "bf16x3" if x3 else dt
+    mfma_per_flop = 3 if x3 else 1
+    peak = PEAK_TFLOPS["bf16" if x3 else dt]
+    dtc = {"f32": _lib.DTYPE_F32, "bf16": _lib.DTYPE_BF16, "f16": _lib.DTYPE_F16}[dt]
+    if x3:
+        dtc = _lib.DTYPE_F32_BF16X3
+    log(f"bench: config {args.config} {mode} n={n} d={d} {dt} normalized_inputs={normalized} T={temperature}"
+        f" arithmetic={arith}")
     a_h, b_h = make_inputs(n, d, gen, seed=0)
     a = a_h.to(dev, tdtype).requires_grad_(True)
     b = b_h.to(dev, tdtype).requires_grad_(mode == "clip")
@@ -302,22 +325,22 @@ def main():
     x = a.detach()
     y = b.detach()
     reps = args.kernel_reps or args.steps
-    stages, blocking = kernel_leg(x, y, mode, dt, not normalized, temperature, reps)
+    stages, blocking = kernel_leg(x, y, mode, dtc, not normalized, temperature, reps)
     for k, (t, nl, fl) in stages.items():
         log(f"bench: stage {k:9s} {t:9.3f} ms x {nl:3d}" + (f"  {fl / (t * 1e-3) / 1e12:8.2f} TFLOP/s" if fl else ""))
     log(f"bench: backward blocking {blocking}")
     # dominant kernel: k_grad_step (nb + 1 launches per step, about 3/4 of the step's flop)
+    # (bf16x3: MFMA flop = 3 x algorithmic flop, against the bf16 peak)
     t_k, nl_k, f_k = stages["grad_step"]
-    peak = PEAK_TFLOPS[dt]
-    achieved = f_k / (t_k * 1e-3) / 1e12
+    achieved = mfma_per_flop * f_k / (t_k * 1e-3) / 1e12
     roofline = {"bound": "mfma", "kernel": "k_grad_step", "achieved": round(achieved, 3), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
-                "traffic": measured_traffic(f"{mode}_n{n}_d{d}_{dt}", "k_grad_step"),
-                "launch_ms": round(t_k, 4), "flop_per_launch": f_k, "launches_per_step": nl_k}
+                "traffic": measured_traffic(f"{mode}_n{n}_d{d}_{arith}", "k_grad_step"),
+                "launch_ms": round(t_k, 4), "flop_per_launch": mfma_per_flop * f_k, "launches_per_step": nl_k}
     t_f, _, f_f = stages["sumexp"]
-    roofline_fwd = {"kernel": "k_sumexp", "achieved": round(f_f / (t_f * 1e-3) / 1e12, 3),
-                    "frac": round(f_f / (t_f * 1e-3) / 1e12 / peak, 4), "launch_ms": round(t_f, 4),
-                    "flop_per_launch": f_f}
+    roofline_fwd = {"kernel": "k_sumexp", "achieved": round(mfma_per_flop * f_f / (t_f * 1e-3) / 1e12, 3),
+                    "frac": round(mfma_per_flop * f_f / (t_f * 1e-3) / 1e12 / peak, 4), "launch_ms": round(t_f, 4),
+                    "flop_per_launch": mfma_per_flop * f_f}
 
     cpu = None
     if not args.no_cpu:
@@ -336,13 +359,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": dt,
+        "dtype": arith,
         "data": "synthetic",
         "config": {"workload": f"{mode}_loss_fwd_bwd", "n": n, "d": d, "temperature": temperature,
-                   "normalized_inputs": normalized, "input_dtype": dt, "parallelism": "none (1 GPU)"},
+                   "normalized_inputs": normalized, "input_dtype": dt, "float32_matmul_precision": args.precision,
+                   "parallelism": "none (1 GPU)"},
         "fwd_ms": round(fwd_ms, 4),
         "bwd_ms": round(bwd_ms, 4),
-        "frac_of_peak": round(tflops / peak, 4),
+        "frac_of_peak": round(mfma_per_flop * tflops / peak, 4),
         "peak_extra_hbm_bytes": int(peak_extra),
         "loss": loss_val,
         "stages_ms": {k: round(v[0], 4) for k, v in stages.items()},
