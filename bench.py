@@ -321,6 +321,25 @@ def main():
     log(f"bench: {args.steps} steps, {ms:.3f} ms/step (fwd {fwd_ms:.3f}, bwd {bwd_ms:.3f}), {tflops:.2f} TFLOP/s, "
         f"loss {loss_val:.6f}")
 
+    # fp32 inputs at "highest" precision: the same steps once more under "high"
+    # (bf16x3), reported beside the IEEE line (not as its value)
+    alt = None
+    if dt == "f32" and not x3:
+        torch.set_float32_matmul_precision("high")
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        ms_hi = (time.perf_counter() - t1) * 1e3 / args.steps
+        torch.set_float32_matmul_precision("highest")
+        alt = {"float32_matmul_precision": "high", "dtype": "bf16x3", "ms_per_step": round(ms_hi, 4),
+               "value": round(flop / (ms_hi * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+               "frac_of_bf16_peak": round(3 * flop / (ms_hi * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4)}
+        log(f"bench: float32 matmul precision high (bf16x3): {ms_hi:.3f} ms/step, {alt['value']:.2f} TFLOP/s")
+
     # kernel leg: per-stage launch times on the library's stream
     x = a.detach()
     y = b.detach()
@@ -373,6 +392,7 @@ def main():
         "roofline": roofline,
         "roofline_forward": roofline_fwd,
         "backward_blocking": blocking,
+        "precision_high": alt,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
