@@ -143,6 +143,34 @@ def test_parity_against_the_oracle(mode, n, d, normed, stable, t):
     assert le <= F32["loss"] and all(e <= F32["grad"] for e in ge.values())
 
 
+@pytest.mark.parametrize("n,d", [(1, 1), (2, 5), (3, 1), (257, 9)])
+def test_tiny_shapes(n, d):
+    a, b = randn_pair(n, d, seed=31 * n + d)
+    say(f"bf16x3 tiny n={n} d={d}")
+    with matmul_precision("high"):
+        loss, da, db = run(MemoryEfficientCLIPLoss(0.07), a, b)
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    assert abs(float(loss) - float(rl)) <= max(F32["loss"] * abs(float(rl)), 1e-6)
+    assert max_rel(da, rda) <= F32["grad"] and max_rel(db, rdb) <= F32["grad"]
+
+
+def test_frozen_tower_and_grad_output():
+    """CLIP with the text tower frozen (only the x side is contracted) and a
+    loss scaled by a non-unit grad_output."""
+    n, d = 1300, 72
+    a, b = randn_pair(n, d, seed=77)
+    ga = a.to(DEV).requires_grad_(True)
+    gb = b.to(DEV)
+    say(f"bf16x3 frozen text tower, grad_output -1.5, n={n} d={d}")
+    with matmul_precision("high"):
+        loss = MemoryEfficientCLIPLoss(0.07)(ga, gb)
+        (loss * -1.5).backward()
+    torch.cuda.synchronize()
+    rl, rda, _ = oracle.clip_loss_and_grads(a, b, 0.07, grad_output=-1.5)
+    assert rel_err(loss.detach().cpu(), rl) <= F32["loss"]
+    assert max_rel(ga.grad.cpu(), rda) <= F32["grad"]
+
+
 def test_mode_differs_from_ieee_and_strided_inputs():
     """Row-strided inputs are read in place; the result differs from the IEEE
     path's (the bf16 products ran) by less than the fp32 tolerance."""
