@@ -25,7 +25,8 @@ benchmark table for exploration.  Rank 0 prints ONE JSON line:
 bf16 terms (hi*hi + lo*hi + hi*lo) on the bf16 MFMA.  ``dtype`` is then
 "bf16x3", ``value`` stays in algorithmic (fp32-equivalent) flop, and the
 roofline counts the three MFMA products per algorithmic one against the bf16
-peak.  The default, "highest", is IEEE fp32 on the fp32 MFMA.
+peak.  ``--precision medium`` multiplies bf16-rounded values ("bf16").  The
+default, "highest", is IEEE fp32 on the fp32 MFMA.
 """
 from __future__ import annotations
 
@@ -225,9 +226,9 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--dtype", choices=sorted(PEAK_TFLOPS), default=None,
                     help="input dtype instead of the config's own (e.g. --config 4 --dtype f16)")
-    ap.add_argument("--precision", choices=["highest", "high"], default="highest",
+    ap.add_argument("--precision", choices=["highest", "high", "medium"], default="highest",
                     help="float32 matmul precision for fp32 inputs: highest = IEEE fp32 MFMA, "
-                         "high = three bf16 MFMA products per fp32 product (bf16x3)")
+                         "high = three bf16 MFMA products per fp32 product (bf16x3), medium = bf16 products")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-reps", type=int, default=0, help="launches per stage in the kernel leg (default: steps)")
     ap.add_argument("--probe", choices=["copy"], default=None,
@@ -261,18 +262,20 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     tdtype = getattr(torch, TORCH_DTYPE[dt])
-    # arithmetic: the input dtype's MFMA, or bf16x3 (three bf16 products per fp32 product)
+    # arithmetic: the input dtype's MFMA, or for fp32 inputs below "highest"
+    # precision bf16x3 (three bf16 products per fp32 product) or bf16
     x3 = args.precision == "high"
-    if x3 and dt != "f32":
-        print("bench.py: --precision high applies to fp32 inputs only", file=sys.stderr)
+    lowp = args.precision != "highest"
+    if lowp and dt != "f32":
+        print(f"bench.py: --precision {args.precision} applies to fp32 inputs only", file=sys.stderr)
         sys.exit(2)
     torch.set_float32_matmul_precision(args.precision)
-    arith = "bf16x3" if x3 else dt
+    arith = "bf16x3" if x3 else "bf16" if lowp else dt
     mfma_per_flop = 3 if x3 else 1
-    peak = PEAK_TFLOPS["bf16" if x3 else dt]
+    peak = PEAK_TFLOPS["bf16" if lowp else dt]
     dtc = {"f32": _lib.DTYPE_F32, "bf16": _lib.DTYPE_BF16, "f16": _lib.DTYPE_F16}[dt]
-    if x3:
-        dtc = _lib.DTYPE_F32_BF16X3
+    if lowp:
+        dtc = _lib.DTYPE_F32_BF16X3 if x3 else _lib.DTYPE_F32_BF16
     log(f"bench: config {args.config} {mode} n={n} d={d} {dt} normalized_inputs={normalized} T={temperature}"
         f" arithmetic={arith}")
     a_h, b_h = make_inputs(n, d, gen, seed=0)
@@ -324,7 +327,7 @@ def main():
     # fp32 inputs at "highest" precision: the same steps once more under "high"
     # (bf16x3), reported beside the IEEE line (not as its value)
     alt = None
-    if dt == "f32" and not x3:
+    if dt == "f32" and not lowp:
         torch.set_float32_matmul_precision("high")
         for _ in range(args.warmup):
             step()

@@ -30,8 +30,8 @@
  *     strides ldx, ldy (in elements, >= d) and unit column stride.
  *     x is the row side of S = x^ y^T: image for CLIP, text for LiT.
  *   - dtype: MEC_DTYPE_F32 (float), MEC_DTYPE_BF16 (uint16 bfloat16 bits),
- *     MEC_DTYPE_F16 (uint16 IEEE binary16 bits) or MEC_DTYPE_F32_BF16X3
- *     (float data, products formed from bf16 terms, below).  All arithmetic
+ *     MEC_DTYPE_F16 (uint16 IEEE binary16 bits), or float data with products
+ *     formed from bf16 terms: MEC_DTYPE_F32_BF16X3, MEC_DTYPE_F32_BF16 (below).  All arithmetic
  *     accumulates in fp32; the loss is reduced in fp64.  Sizes: 1 <= d <= 2^20;
  *     1 <= n <= 2^30 for fp32 and n <= 2^22 for the other dtypes
  *     (MEC_ERR_UNSUPPORTED beyond).  16-bit rows that are 16-byte aligned (x, y
@@ -76,6 +76,13 @@ extern "C" {
  * and must be 16-byte aligned; mec_sumexp and mec_grad_step read split copies
  * of x and y that mec_prepass writes into it. */
 #define MEC_DTYPE_F32_BF16X3 3
+/* fp32 inputs and outputs with the products of the similarity GEMMs and the
+ * contractions in plain bf16 (bf16(a) bf16(b), fp32 accumulate): PyTorch's
+ * "medium" float32 matmul precision.  Errors are those of bf16 inputs (the
+ * bf16 tolerances); the norms, the diagonal and the post-pass stay fp32.
+ * Workspace and scratch as for MEC_DTYPE_F32_BF16X3 (one term instead of
+ * three). */
+#define MEC_DTYPE_F32_BF16 4
 
 #define MEC_MODE_CLIP 0 /* symmetric image<->text loss, gradients for x and y */
 #define MEC_MODE_LIT 1  /* text->image only (x = text), gradient for x only */
@@ -105,9 +112,10 @@ const char* mec_version(void);
 int64_t mec_workspace_floats(int64_t n);
 
 /* Number of floats of the workspace for (n, d, dtype): mec_workspace_floats(n)
- * for fp32, bf16 and fp16; for MEC_DTYPE_F32_BF16X3 that, rounded up to 4
- * floats, plus split copies of x and y (2 n rows of 3 * round8(d) bf16).
- * Returns < 0 on bad args.  No counterpart in the reference. */
+ * for fp32, bf16 and fp16; for MEC_DTYPE_F32_BF16X3 (MEC_DTYPE_F32_BF16) that,
+ * rounded up to 4 floats, plus split copies of x and y: 2 n rows of
+ * 3 * round8(d) (round8(d)) bf16.  Returns < 0 on bad args.  No counterpart
+ * in the reference. */
 int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype);
 
 /* Bytes of gradient scratch needed by mec_grad / mec_grad_step /
@@ -115,9 +123,10 @@ int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype);
  * one block diagonal of the off-diagonal gradient matrix each (nb blocks of
  * bs x bs; bs ~ 2d for fp32, ~8d but at most 32512 for the other dtypes),
  * for fp32 the same blocks transposed as well, and transposed normalised
- * copies of x and y ([d][n rounded up to 128]); O(n*d) in total.
- * MEC_DTYPE_F32_BF16X3 holds bf16 hi and lo planes of the transposed blocks
- * and of the transposed copies.  Returns < 0 on bad args. */
+ * copies of x and y ([d][n rounded up to 128]); O(n*d) in total.  The
+ * fp32-data modes keep these in bf16; MEC_DTYPE_F32_BF16X3 holds hi and lo
+ * planes of the transposed blocks and of the transposed copies.  Returns < 0
+ * on bad args. */
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype);
 
 /* Block decomposition of the backward for (n, d, dtype): the n x n gradient
@@ -128,7 +137,8 @@ int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype);
 int mec_grad_blocking(int64_t n, int64_t d, int dtype, int64_t* block_rows, int64_t* num_blocks);
 
 /* rx, ry (1 if !normalize), diag; clears the sum accumulators.
- * MEC_DTYPE_F32_BF16X3: also writes the split copies of x and y. */
+ * MEC_DTYPE_F32_BF16X3, MEC_DTYPE_F32_BF16: also writes the bf16 (split)
+ * copies of x and y into the workspace. */
 int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                 int dtype, int normalize, float* workspace, void* stream);
 

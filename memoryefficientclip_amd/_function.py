@@ -16,12 +16,12 @@ This mirrors the glue of the reference's autograd Functions
   are bitwise reproducible (the reference's relaxed atomics are not,
   ``clip_loss.py:63-64,155-156``);
 * fp32 inputs follow ``torch.get_float32_matmul_precision()``: "highest" (the
-  default) multiplies in IEEE fp32 on the fp32 MFMA; "high" and "medium" form
-  each product from bf16 terms (hi*hi + lo*hi + hi*lo, about 16 significant
-  bits per operand) on the bf16 MFMA, PyTorch's meaning of "high".  The
-  reference's fp32 dot products are TF32 on NVIDIA (``tl.dot`` without
-  ``input_precision``, ``clip_loss.py:53,113,148-149``); this mode is the
-  fast counterpart here and keeps the fp32 tolerances.
+  default) multiplies in IEEE fp32 on the fp32 MFMA; "high" forms each product
+  from bf16 terms (hi*hi + lo*hi + hi*lo, about 16 significant bits per
+  operand) on the bf16 MFMA and keeps the fp32 tolerances; "medium" multiplies
+  bf16-rounded values (the bf16 tolerances).  These are PyTorch's meanings of
+  the three settings.  The reference's fp32 dot products are TF32 on NVIDIA
+  (``tl.dot`` without ``input_precision``, ``clip_loss.py:53,113,148-149``).
 """
 from __future__ import annotations
 
@@ -68,11 +68,15 @@ def _stream(dev: torch.device) -> int:
 
 def compute_dtype(dtype: torch.dtype) -> int:
     """C-ABI dtype code for inputs of `dtype` under the current
-    ``torch.get_float32_matmul_precision()`` (fp32 only: anything but
-    "highest" selects the three-term bf16 products)."""
+    ``torch.get_float32_matmul_precision()`` (fp32 only: "high" selects the
+    three-term bf16 products, "medium" plain bf16 products)."""
     code = _DTYPES[dtype]
-    if code == _lib.DTYPE_F32 and torch.get_float32_matmul_precision() != "highest":
-        return _lib.DTYPE_F32_BF16X3
+    if code == _lib.DTYPE_F32:
+        p = torch.get_float32_matmul_precision()
+        if p == "high":
+            return _lib.DTYPE_F32_BF16X3
+        if p == "medium":
+            return _lib.DTYPE_F32_BF16
     return code
 
 
@@ -115,7 +119,7 @@ def backward(ctx, grad_output: torch.Tensor, need_x: bool, need_y: bool):
         go = grad_output.detach().to(device=dev, dtype=torch.float32).reshape(()).contiguous()
         acc_x = torch.empty((n, d), dtype=torch.float32, device=dev) if need_x else None
         acc_y = torch.empty((n, d), dtype=torch.float32, device=dev) if need_y else None
-        if dt in (_lib.DTYPE_F32, _lib.DTYPE_F32_BF16X3):
+        if dt in (_lib.DTYPE_F32, _lib.DTYPE_F32_BF16X3, _lib.DTYPE_F32_BF16):
             dx, dy = acc_x, acc_y  # the post-pass runs in place
         else:
             dx = torch.empty((n, d), dtype=x.dtype, device=dev) if need_x else None

@@ -22,6 +22,7 @@ DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_F16 = 2
 DTYPE_F32_BF16X3 = 3  # fp32 data, products as three bf16 MFMA terms
+DTYPE_F32_BF16 = 4  # fp32 data, bf16 products
 MODE_CLIP = 0
 MODE_LIT = 1
 FLAG_DETERMINISTIC = 0x100  # OR into the mode of mec_sumexp / mec_forward

@@ -43,11 +43,17 @@ constexpr int64_t kMaxN16 = int64_t(1) << 22;
 
 bool known_dtype(int dtype) {
   return dtype == MEC_DTYPE_F32 || dtype == MEC_DTYPE_BF16 || dtype == MEC_DTYPE_F16 ||
-         dtype == MEC_DTYPE_F32_BF16X3;
+         dtype == MEC_DTYPE_F32_BF16X3 || dtype == MEC_DTYPE_F32_BF16;
 }
+// fp32 data with bf16 products: bf16 terms per operand value in the
+// similarity GEMMs (3: hi, lo; 1: hi), 0 for the other dtypes
+int split_terms(int dtype) {
+  return dtype == MEC_DTYPE_F32_BF16X3 ? 3 : dtype == MEC_DTYPE_F32_BF16 ? 1 : 0;
+}
+bool is_split(int dtype) { return split_terms(dtype) > 0; }
 bool is_x3(int dtype) { return dtype == MEC_DTYPE_F32_BF16X3; }
-// element type of the caller's x, y, dx, dy (the bf16x3 mode reads and writes fp32)
-int data_dtype(int dtype) { return is_x3(dtype) ? MEC_DTYPE_F32 : dtype; }
+// element type of the caller's x, y, dx, dy (the split modes read and write fp32)
+int data_dtype(int dtype) { return is_split(dtype) ? MEC_DTYPE_F32 : dtype; }
 
 int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                  int dtype) {
@@ -59,7 +65,7 @@ int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   if (!known_dtype(dtype)) return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
   if (x == nullptr || y == nullptr) return fail(MEC_ERR_INVALID, "x and y must be non-null");
   if (dtype != MEC_DTYPE_F32 && n > kMaxN16)
-    return fail(MEC_ERR_UNSUPPORTED, "bf16, fp16 and bf16x3 support n <= 2^22 (n=%lld)", (long long)n);
+    return fail(MEC_ERR_UNSUPPORTED, "dtypes other than fp32 support n <= 2^22 (n=%lld)", (long long)n);
   return MEC_OK;
 }
 
@@ -84,18 +90,21 @@ int64_t loss_partials_floats(int64_t n) { return 2 * ((n + FIN_ROWS - 1) / FIN_R
 int64_t det_partials_offset(int64_t n) { return (int64_t)WS_NSLOTS * n + loss_partials_floats(n); }
 int64_t base_workspace_floats(int64_t n) { return det_partials_offset(n) + (int64_t)DET_SPLITS * n; }
 
-// bf16x3: the split operands of the similarity GEMMs follow, 16-byte aligned:
-// A3 (x rows: hi | lo | hi) and B3 (y rows: hi | hi | lo), n rows of
-// ld3 = 3 dp bf16 each, dp = d rounded up to 8 (k_split3)
+// Split modes: the bf16 operands of the similarity GEMMs follow, 16-byte
+// aligned: A (x rows) and B (y rows), n rows of ld = terms * dp bf16 each,
+// dp = d rounded up to 8.  bf16x3: A rows hi | lo | hi, B rows hi | hi | lo
+// (k_split3); bf16: A, B rows hi (k_split1).
 int64_t split_dp(int64_t d) { return (d + 7) & ~int64_t(7); }
-int64_t split_ld(int64_t d) { return 3 * split_dp(d); }
+int64_t split_ld(int64_t d, int dtype) { return split_terms(dtype) * split_dp(d); }
 int64_t split_offset_floats(int64_t n) { return (base_workspace_floats(n) + 3) & ~int64_t(3); }
 int64_t workspace_floats_for(int64_t n, int64_t d, int dtype) {
-  if (!is_x3(dtype)) return base_workspace_floats(n);
-  return split_offset_floats(n) + n * split_ld(d);  // 2 n ld3 bf16 = n ld3 floats
+  if (!is_split(dtype)) return base_workspace_floats(n);
+  return split_offset_floats(n) + n * split_ld(d, dtype);  // 2 n ld bf16 = n ld floats
 }
 const uint16_t* split_a(const float* ws, int64_t n) { return (const uint16_t*)(ws + split_offset_floats(n)); }
-const uint16_t* split_b(const float* ws, int64_t n, int64_t d) { return split_a(ws, n) + n * split_ld(d); }
+const uint16_t* split_b(const float* ws, int64_t n, int64_t d, int dtype) {
+  return split_a(ws, n) + n * split_ld(d, dtype);
+}
 
 // operands of the similarity GEMMs (forward sums, gradient-matrix tiles)
 struct GemmOperands {
@@ -106,10 +115,10 @@ struct GemmOperands {
   int64_t d;   // K
   int dtype;   // element type of x, y
 };
-// bf16x3: the split copies in the workspace, a bf16 problem with K = 3 dp
-GemmOperands split_operands(const float* ws, int64_t n, int64_t d) {
-  const int64_t ld3 = split_ld(d);
-  return GemmOperands{split_a(ws, n), ld3, split_b(ws, n, d), ld3, ld3, MEC_DTYPE_BF16};
+// split modes: the copies in the workspace, a bf16 problem with K = terms * dp
+GemmOperands split_operands(const float* ws, int64_t n, int64_t d, int dtype) {
+  const int64_t ld = split_ld(d, dtype);
+  return GemmOperands{split_a(ws, n), ld, split_b(ws, n, d, dtype), ld, ld, MEC_DTYPE_BF16};
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -180,10 +189,10 @@ void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
   *nb = (int)((tiles + tb - 1) / tb);
 }
 
-// Scratch layout of the backward (element type = input dtype; bf16x3: bf16):
-//   fp32:        [G0 | G1 | GT0 | GT1 | XT | YT]
-//   bf16, fp16:  [GT0 | GT1 | XT | YT]
-//   bf16x3:      [GT0 | GT1 | GTlo0 | GTlo1 | XT | YT | XTlo | YTlo]
+// Scratch layout of the backward (element type = input dtype; split modes: bf16):
+//   fp32:                  [G0 | G1 | GT0 | GT1 | XT | YT]
+//   bf16, fp16, fp32/bf16: [GT0 | GT1 | XT | YT]
+//   bf16x3:                [GT0 | GT1 | GTlo0 | GTlo1 | XT | YT | XTlo | YTlo]
 // G0/G1 (and their transposes GT0/GT1) double-buffer one block diagonal of
 // G' (nb blocks of bs x bs; the 16-bit types keep only the transposed copy,
 // bf16x3 its hi and lo planes); XT/YT are the normalised inputs transposed,
@@ -224,7 +233,7 @@ bool f32_contract_dma(int64_t ldt, int64_t bs) {
 }
 
 // T = element type of dtype: float, bf16 bits (uint16_t) or fp16 (_Float16);
-// callers map the bf16x3 mode to float first (data_dtype)
+// callers map the split modes to float first (data_dtype)
 #define DISPATCH_DTYPE(dtype, T, ...)       \
   do {                                      \
     if ((dtype) == MEC_DTYPE_F32) {         \
@@ -280,24 +289,29 @@ int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
   int rc = check_common(x, ldx, y, ldy, n, d, dtype);
   if (rc) return rc;
   if (!workspace) return fail(MEC_ERR_INVALID, "workspace must be non-null");
-  if (is_x3(dtype) && !aligned16(workspace))
-    return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for bf16x3");
+  if (is_split(dtype) && !aligned16(workspace))
+    return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for the bf16-product modes");
   hipStream_t s = (hipStream_t)stream;
   const int N = (int)n, D = (int)d;
   dim3 grid((unsigned)((n + 3) / 4));
   DISPATCH_DTYPE(data_dtype(dtype), T, DISPATCH_BOOL(normalize, NORM,
       k_prepass<T, NORM><<<grid, 256, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, workspace)));
-  if (is_x3(dtype)) {
-    // split copies of x and y for the similarity GEMMs (the norms and the
-    // diagonal above come from the fp32 inputs)
-    const int64_t dp = split_dp(d), ld3 = split_ld(d);
+  if (is_split(dtype)) {
+    // bf16 (split) copies of x and y for the similarity GEMMs (the norms and
+    // the diagonal above come from the fp32 inputs)
+    const int64_t dp = split_dp(d), ld = split_ld(d, dtype);
     const int64_t nthr = n * (dp / 8);
     if ((nthr + 255) / 256 > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "split grid too large");
     const unsigned sgrid = (unsigned)((nthr + 255) / 256);
-    uint16_t* a3 = (uint16_t*)split_a(workspace, n);
-    uint16_t* b3 = (uint16_t*)split_b(workspace, n, d);
-    k_split3<0><<<sgrid, 256, 0, s>>>((const float*)x, ldx, N, D, (int)dp, a3, ld3);
-    k_split3<1><<<sgrid, 256, 0, s>>>((const float*)y, ldy, N, D, (int)dp, b3, ld3);
+    uint16_t* sa = (uint16_t*)split_a(workspace, n);
+    uint16_t* sb = (uint16_t*)split_b(workspace, n, d, dtype);
+    if (is_x3(dtype)) {
+      k_split3<0><<<sgrid, 256, 0, s>>>((const float*)x, ldx, N, D, (int)dp, sa, ld);
+      k_split3<1><<<sgrid, 256, 0, s>>>((const float*)y, ldy, N, D, (int)dp, sb, ld);
+    } else {
+      k_split1<<<sgrid, 256, 0, s>>>((const float*)x, ldx, N, D, (int)dp, sa, ld);
+      k_split1<<<sgrid, 256, 0, s>>>((const float*)y, ldy, N, D, (int)dp, sb, ld);
+    }
   }
   return check_launch("prepass");
 }
@@ -312,11 +326,12 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   if (!workspace) return fail(MEC_ERR_INVALID, "workspace must be non-null");
   hipStream_t s = (hipStream_t)stream;
   const float c = (float)(1.4426950408889634 / (double)temperature);
-  // bf16x3: the bf16 sums over the split copies (K = 3 dp) that mec_prepass wrote
+  // split modes: the bf16 sums over the copies (K = terms * dp) that mec_prepass wrote
   GemmOperands g{x, ldx, y, ldy, d, dtype};
-  if (is_x3(dtype)) {
-    if (!aligned16(workspace)) return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for bf16x3");
-    g = split_operands(workspace, n, d);
+  if (is_split(dtype)) {
+    if (!aligned16(workspace))
+      return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for the bf16-product modes");
+    g = split_operands(workspace, n, d, dtype);
   }
   x = g.x, ldx = g.ldx, y = g.y, ldy = g.ldy, d = g.d, dtype = g.dtype;
   const int N = (int)n, D = (int)d;
@@ -426,12 +441,13 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
     return fail(MEC_ERR_INVALID, "step %lld out of range [0, %d]", (long long)step, nb);
   const int N = (int)n, D = (int)d;
   const float c = (float)(1.4426950408889634 / (double)temperature);
-  const bool x3 = is_x3(dtype);
-  if (x3 && !aligned16(workspace)) return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for bf16x3");
-  // operands of the gradient-matrix tiles (bf16x3: the split copies, K = 3 dp)
-  const GemmOperands go = x3 ? split_operands(workspace, n, d) : GemmOperands{x, ldx, y, ldy, d, dtype};
+  const bool x3 = is_x3(dtype), split = is_split(dtype);
+  if (split && !aligned16(workspace))
+    return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for the bf16-product modes");
+  // operands of the gradient-matrix tiles (split modes: the copies, K = terms * dp)
+  const GemmOperands go = split ? split_operands(workspace, n, d, dtype) : GemmOperands{x, ldx, y, ldy, d, dtype};
   const bool vec = vec_ok(go.x, go.ldx, go.y, go.ldy, go.d, go.dtype);
-  if (x3 && !vec) return fail(MEC_ERR_UNSUPPORTED, "bf16x3 split operands beyond the direct-load range");
+  if (split && !vec) return fail(MEC_ERR_UNSUPPORTED, "split operands beyond the direct-load range");
   const bool cdma = f32_contract_dma(L.ldt, bs);
   const TileDims tf = fwd_tile_dims(dtype, vec), tc = con_tile_dims(dtype);
   BlockGrid bg{bs, nb, bs / tf.bm, bs / tf.bn, bs / tc.bm, (D + tc.bn - 1) / tc.bn};
@@ -447,14 +463,14 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
   sp.cy_pad = round8(sp.cy_n);
   // bf16: the contractions of diagonal t-1 run in k_grad_contract, before the
   // G' tiles of diagonal t (different scratch buffers, so either order works)
-  const bool split = separate_contractions(dtype);
+  const bool sep = separate_contractions(dtype);
   StepPlan sp_g = sp, sp_c = sp;
-  if (split) {
+  if (sep) {
     sp_g.cx_n = sp_g.cy_n = sp_g.cx_pad = sp_g.cy_pad = 0;
     sp_c.g_n = sp_c.g_pad = 0;
   }
-  const int64_t grid = split ? (int64_t)sp.g_pad : (int64_t)sp.g_pad + sp.cx_pad + sp.cy_pad;
-  const int64_t grid_c = split ? (int64_t)sp.cx_pad + sp.cy_pad : 0;
+  const int64_t grid = sep ? (int64_t)sp.g_pad : (int64_t)sp.g_pad + sp.cx_pad + sp.cy_pad;
+  const int64_t grid_c = sep ? (int64_t)sp.cx_pad + sp.cy_pad : 0;
   if (grid > 0x7fffffff || grid_c > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "backward grid too large");
   char* base = (char*)scratch;
   GradBufs gb{};
@@ -484,15 +500,15 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
     // transposed normalised operands of the contractions: YT for the x side, XT for the y side
     const int64_t n64 = n;
     dim3 tgrid((unsigned)(L.ldt / 64), (unsigned)((d + 63) / 64));
-    if (x3) {
-      DISPATCH_BOOL(normalize, NORM, {
+    if (split) {
+      DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(x3, LO, {
         if (acc_x)
-          k_transpose_split<NORM><<<tgrid, 256, 0, s>>>((const float*)y, ldy, N, D, workspace + WS_RY * n64,
-                                                        (uint16_t*)gb.yt, (uint16_t*)gb.yt_lo, L.ldt);
+          k_transpose_split<NORM, LO><<<tgrid, 256, 0, s>>>((const float*)y, ldy, N, D, workspace + WS_RY * n64,
+                                                            (uint16_t*)gb.yt, (uint16_t*)gb.yt_lo, L.ldt);
         if (acc_y)
-          k_transpose_split<NORM><<<tgrid, 256, 0, s>>>((const float*)x, ldx, N, D, workspace + WS_RX * n64,
-                                                        (uint16_t*)gb.xt, (uint16_t*)gb.xt_lo, L.ldt);
-      });
+          k_transpose_split<NORM, LO><<<tgrid, 256, 0, s>>>((const float*)x, ldx, N, D, workspace + WS_RX * n64,
+                                                            (uint16_t*)gb.xt, (uint16_t*)gb.xt_lo, L.ldt);
+      }));
     } else {
       DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, {
         if (acc_x)
@@ -506,20 +522,23 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
     rc = check_launch("transpose");
     if (rc) return rc;
   }
-  if (x3) {
-    // the bf16 kernels on the split operands, with hi/lo gradient-matrix planes
+  if (split) {
+    // the bf16 kernels on the split operands (bf16x3: with hi/lo planes of
+    // the gradient-matrix blocks and of the transposed inputs)
     using T = uint16_t;
-    const int D3 = (int)go.d;
-    if (grid_c > 0) {
-      k_grad_contract<T, true><<<(unsigned)grid_c, ConTileX<T>::NT, 0, s>>>(N, D, gb, bg, sp_c, acc_x, acc_y);
-      rc = check_launch("grad_contract");
-      if (rc) return rc;
-    }
-    if (grid > 0)
-      DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM,
-          k_grad_step<T, LIT, NORM, true, true, true><<<(unsigned)grid, FwdTile<T, true>::NT, 0, s>>>(
-              (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, D3, D3, c, workspace, gb, bg, sp_g, acc_x,
-              acc_y)));
+    const int DK = (int)go.d;
+    DISPATCH_BOOL(x3, X3, {
+      if (grid_c > 0) {
+        k_grad_contract<T, X3><<<(unsigned)grid_c, ConTileX<T>::NT, 0, s>>>(N, D, gb, bg, sp_c, acc_x, acc_y);
+        rc = check_launch("grad_contract");
+      }
+      if (!rc && grid > 0)
+        DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM,
+            k_grad_step<T, LIT, NORM, true, true, X3><<<(unsigned)grid, FwdTile<T, true>::NT, 0, s>>>(
+                (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g, acc_x,
+                acc_y)));
+    });
+    if (rc) return rc;
     return check_launch("grad_step");
   }
   DISPATCH_DTYPE(dtype, T, {

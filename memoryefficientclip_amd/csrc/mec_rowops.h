@@ -248,9 +248,30 @@ __global__ __launch_bounds__(256) void k_split3(const float* __restrict__ X, int
   *(u32x4*)(o + 2 * dp) = ORDER == 0 ? hi : lo;
 }
 
-// k_transpose<float, NORM> into two bf16 planes: XT_hi[d][i] = hi(v),
-// XT_lo[d][i] = lo(v) with v = scale_i x_i[d] (fp32), zero for N <= i < ldt.
-template <bool NORM>
+// bf16 copies of the inputs for the fp32-data / bf16-product mode: row i of
+// out (pitch ldo) is bf16(x_i) (round to nearest even), zero-padded to dp
+// columns.  One thread per 8 columns; out and ldo 16-byte aligned.
+__global__ __launch_bounds__(256) void k_split1(const float* __restrict__ X, int64_t ldx, int N, int D, int dp,
+                                                uint16_t* __restrict__ out, int64_t ldo) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int vpr = dp / 8;
+  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (v >= (int64_t)N * vpr) return;
+  const int i = (int)(v / vpr), d0 = (int)(v - (int64_t)i * vpr) * 8;
+  const float* x = X + (int64_t)i * ldx;
+  u32x4 hi;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int d = d0 + 2 * e;
+    hi[e] = pack2_bf16(d < D ? x[d] : 0.f, d + 1 < D ? x[d + 1] : 0.f);
+  }
+  *(u32x4*)(out + (int64_t)i * ldo + d0) = hi;
+}
+
+// k_transpose<float, NORM> into bf16 planes: XT_hi[d][i] = hi(v) and, when
+// LO, XT_lo[d][i] = lo(v), with v = scale_i x_i[d] (fp32), zero for
+// N <= i < ldt.
+template <bool NORM, bool LO>
 __global__ __launch_bounds__(256) void k_transpose_split(const float* __restrict__ X, int64_t ldx, int N, int D,
                                                          const float* __restrict__ scale, uint16_t* __restrict__ XTh,
                                                          uint16_t* __restrict__ XTl, int64_t ldt) {
@@ -273,7 +294,7 @@ __global__ __launch_bounds__(256) void k_transpose_split(const float* __restrict
       const float v = tile[tx][r];
       const uint16_t h = f32_to_bf16(v);
       XTh[(int64_t)d * ldt + i] = h;
-      XTl[(int64_t)d * ldt + i] = f32_to_bf16(v - bf16_to_f32(h));
+      if (LO) XTl[(int64_t)d * ldt + i] = f32_to_bf16(v - bf16_to_f32(h));
     }
   }
 }

@@ -12,8 +12,8 @@
 //   layouts                   staged through registers (mec_gemm_16.h); the
 //                             contractions read internal buffers, which are
 //                             always 16-byte vectors, so they keep 256 x 256
-//   fp32 as three bf16        the bf16 tiles on internal split copies of the
-//   products (bf16x3)         inputs (always 16-byte vectors)
+//   fp32 data with bf16       the bf16 tiles on internal bf16 / split copies
+//   products (bf16, bf16x3)   of the inputs (always 16-byte vectors)
 //
 // The backward's block decomposition uses blocks of a multiple of
 // block_quantum(dtype) rows, so that every tile kind divides a block.
@@ -29,11 +29,12 @@ struct TileDims {
 constexpr int kDtypeF32 = 0;
 constexpr int kDtypeBF16 = 1;
 constexpr int kDtypeF16 = 2;
-constexpr int kDtypeX3 = 3;  // fp32 data, products as three bf16 MFMA terms
+constexpr int kDtypeX3 = 3;   // fp32 data, products as three bf16 MFMA terms
+constexpr int kDtypeF32B = 4;  // fp32 data, bf16 products
 
 // forward sums and gradient-matrix tiles (x rows x y rows)
 inline TileDims fwd_tile_dims(int dtype, bool vec) {
-  if (dtype == kDtypeX3) return {256, 256};
+  if (dtype == kDtypeX3 || dtype == kDtypeF32B) return {256, 256};
   if (dtype == kDtypeF32 || !vec) return {128, 128};
   return {256, 256};
 }

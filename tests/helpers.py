@@ -1,4 +1,7 @@
 """Shared helpers for the test suite (input generators, error metrics)."""
+import contextlib
+
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -91,3 +94,38 @@ def ref_fp64(a, b, t, lit, normalized, chunk):
         return (dvh - vh * (vh * dvh).sum(dim=1, keepdim=True)) / nrm
 
     return loss, norm_bwd(x, dxh), (None if lit else norm_bwd(y, dyh))
+
+
+@contextlib.contextmanager
+def matmul_precision(p):
+    """torch.set_float32_matmul_precision(p) within the block."""
+    old = torch.get_float32_matmul_precision()
+    torch.set_float32_matmul_precision(p)
+    try:
+        yield
+    finally:
+        torch.set_float32_matmul_precision(old)
+
+
+def bf16_rne(v: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even (finite inputs)."""
+    u = v.astype(np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def split_rows(x: np.ndarray, order: int) -> np.ndarray:
+    """bf16 copies of fp32 rows as the bf16-product modes lay them out, each
+    segment d rounded up to 8 wide with zero padding: [hi | lo | hi] (order
+    0, x side of bf16x3), [hi | hi | lo] (order 1, y side) or [hi] (order 2,
+    plain bf16 products)."""
+    n, d = x.shape
+    dp = (d + 7) // 8 * 8
+    hi = np.zeros((n, dp), np.uint16)
+    lo = np.zeros((n, dp), np.uint16)
+    hi[:, :d] = bf16_rne(x)
+    lo[:, :d] = bf16_rne(x - bf16_to_f32(hi[:, :d]))
+    return np.concatenate({0: [hi, lo, hi], 1: [hi, hi, lo], 2: [hi]}[order], axis=1)

@@ -54,26 +54,30 @@ def test_sizes():
     assert lib.mec_grad_scratch_bytes(10, 10, 7) < 0
 
 
-def test_bf16x3_sizes():
+def test_bf16_product_mode_sizes():
     # fp32 data with bf16 split products: the workspace carries split copies of
     # x and y (rows of 3 segments of d rounded up to 8 bf16), the backward uses
     # the bf16 blocking with hi and lo planes of the transposed blocks and inputs
+    # (MEC_DTYPE_F32_BF16: one bf16 copy per input, the bf16 scratch layout)
     lib = _lib.load()
-    x3 = _lib.DTYPE_F32_BF16X3
+    x3, x1 = _lib.DTYPE_F32_BF16X3, _lib.DTYPE_F32_BF16
     for n, d in [(1000, 3), (32768, 1152), (777, 130), (65536, 768)]:
         base = lib.mec_workspace_floats(n)
         for dt in (0, 1, 2):
             assert lib.mec_workspace_floats_for(n, d, dt) == base
         dp = (d + 7) // 8 * 8
         assert lib.mec_workspace_floats_for(n, d, x3) == (base + 3) // 4 * 4 + n * 3 * dp
-        assert _lib.grad_blocking(n, d, x3) == _lib.grad_blocking(n, d, 1)
-        bs, nb = _lib.grad_blocking(n, d, x3)
+        assert lib.mec_workspace_floats_for(n, d, x1) == (base + 3) // 4 * 4 + n * dp
         ldt = (n + 127) // 128 * 128
-        assert lib.mec_grad_scratch_bytes(n, d, x3) == (4 * nb * bs * bs + 4 * d * ldt) * 2
+        for dt, planes in ((x3, 4), (x1, 2)):
+            assert _lib.grad_blocking(n, d, dt) == _lib.grad_blocking(n, d, 1)
+            bs, nb = _lib.grad_blocking(n, d, dt)
+            assert lib.mec_grad_scratch_bytes(n, d, dt) == (planes * nb * bs * bs + planes * d * ldt) * 2
     assert lib.mec_workspace_floats_for(10, 0, x3) < 0 and lib.mec_workspace_floats_for(10, 10, 7) < 0
     # the split copies need a 16-byte aligned workspace; rejected before any launch
-    rc = lib.mec_prepass(16, 64, 16, 64, 10, 64, x3, 1, 8, None)
-    assert rc == _lib.MEC_ERR_INVALID and "16-byte" in _lib.last_error()
+    for dt in (x3, x1):
+        rc = lib.mec_prepass(16, 64, 16, 64, 10, 64, dt, 1, 8, None)
+        assert rc == _lib.MEC_ERR_INVALID and "16-byte" in _lib.last_error()
 
 
 def test_16bit_blocks_fit_the_32bit_operand_range():
@@ -133,7 +137,7 @@ def test_mode_and_deterministic_flag(mode, ok):
     assert rc == _lib.MEC_ERR_INVALID and (("non-null" if ok else "mode") in _lib.last_error())
 
 
-@pytest.mark.parametrize("dtype", [1, 2, 3])
+@pytest.mark.parametrize("dtype", [1, 2, 3, 4])
 def test_16bit_size_limit(dtype):
     # the 16-bit contractions address transposed panels with 32-bit offsets
     lib = _lib.load()

@@ -100,20 +100,19 @@ def test_product_path_does_not_import_oracle():
                 assert (node.module or "").split(".")[0] != "oracle", f
 
 
-def test_float32_matmul_precision_selects_the_bf16x3_mode():
-    # "highest" (PyTorch's default): IEEE fp32 products; "high"/"medium":
-    # products from bf16 terms (C-ABI dtype MEC_DTYPE_F32_BF16X3); 16-bit
-    # inputs are unaffected
+def test_float32_matmul_precision_selects_the_product_mode():
+    # "highest" (PyTorch's default): IEEE fp32 products; "high": three bf16
+    # terms per product (MEC_DTYPE_F32_BF16X3); "medium": bf16 products
+    # (MEC_DTYPE_F32_BF16); 16-bit inputs are unaffected
     from memoryefficientclip_amd import _lib
     from memoryefficientclip_amd._function import compute_dtype
 
     old = torch.get_float32_matmul_precision()
     try:
-        torch.set_float32_matmul_precision("highest")
-        assert compute_dtype(torch.float32) == _lib.DTYPE_F32
-        for p in ("high", "medium"):
+        for p, code in (("highest", _lib.DTYPE_F32), ("high", _lib.DTYPE_F32_BF16X3),
+                        ("medium", _lib.DTYPE_F32_BF16)):
             torch.set_float32_matmul_precision(p)
-            assert compute_dtype(torch.float32) == _lib.DTYPE_F32_BF16X3
+            assert compute_dtype(torch.float32) == code
             assert compute_dtype(torch.bfloat16) == _lib.DTYPE_BF16
             assert compute_dtype(torch.float16) == _lib.DTYPE_F16
     finally:

@@ -11,7 +11,6 @@ as hi*hi + lo*hi + hi*lo from bf16 terms on the bf16 MFMA.
   this package's kernels) at the benchmark's fp32 sizes.
 * The mode really runs: its gradients differ from the IEEE fp32 path's.
 """
-import contextlib
 import math
 
 import numpy as np
@@ -19,7 +18,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import TOL, max_rel, randn_pair, ref_fp64, rel_err
+from helpers import TOL, matmul_precision, max_rel, randn_pair, ref_fp64, rel_err, split_rows
 from memoryefficientclip_amd import _lib
 from memoryefficientclip_amd.clip_loss import MemoryEfficientCLIPLoss, StableMemoryEfficientCLIPLoss
 from memoryefficientclip_amd.lit_loss import MemoryEfficientLiTLoss, StableMemoryEfficientLiTLoss
@@ -31,38 +30,6 @@ F32 = TOL[torch.float32]
 
 def say(*a):
     print(*a, flush=True)
-
-
-@contextlib.contextmanager
-def matmul_precision(p):
-    old = torch.get_float32_matmul_precision()
-    torch.set_float32_matmul_precision(p)
-    try:
-        yield
-    finally:
-        torch.set_float32_matmul_precision(old)
-
-
-def bf16_rne(v: np.ndarray) -> np.ndarray:
-    """fp32 -> bf16 bits, round to nearest even (finite inputs)."""
-    u = v.astype(np.float32).view(np.uint32).astype(np.uint64)
-    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-
-
-def bf16_to_f32(h: np.ndarray) -> np.ndarray:
-    return (h.astype(np.uint32) << 16).view(np.float32)
-
-
-def split_rows(x: np.ndarray, order: int) -> np.ndarray:
-    """Rows [hi | lo | hi] (order 0) or [hi | hi | lo] (order 1), each segment
-    d rounded up to 8 wide with zero padding."""
-    n, d = x.shape
-    dp = (d + 7) // 8 * 8
-    hi = np.zeros((n, dp), np.uint16)
-    lo = np.zeros((n, dp), np.uint16)
-    hi[:, :d] = bf16_rne(x)
-    lo[:, :d] = bf16_rne(x - bf16_to_f32(hi[:, :d]))
-    return np.concatenate([hi, lo, hi] if order == 0 else [hi, hi, lo], axis=1)
 
 
 def run(module, a, b, grad_b=True):
