@@ -4,12 +4,10 @@
 // Geometry: a BM x BN output tile per workgroup of WM x WN waves, each wave a
 // (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks, fp32 accumulate:
 // v_mfma_f32_32x32x16_{bf16,f16} (one per block and k-step) or
-// v_mfma_f32_32x32x2_f32 (four per block and k-step).  The 16-bit forward and
-// gradient-matrix tiles are 128 x 256 with 2 x 2 waves: two workgroups share a
-// CU (72 KB of LDS each), so one workgroup's epilogue (exp, reductions,
-// stores) runs while the other's MFMAs do.  The 16-bit contractions, whose
-// epilogue is a few atomics, are 256 x 256 with 4 x 2 waves, one workgroup
-// per CU.  fp32 tiles are 128 x 128 with 2 x 2 waves (48 KB, three per CU).
+// v_mfma_f32_32x32x2_f32 (four per block and k-step).  The 16-bit tiles
+// (forward, gradient matrix, contractions) are 256 x 256 with 4 x 2 waves,
+// one workgroup per CU (96 KB of ring); fp32 tiles are 128 x 128 with 2 x 2
+// waves (48 KB), two (forward) or three (backward) workgroups per CU.
 //
 // Operands are K-major (element (row, k) at base[row * ld + k]).  K is staged
 // in chunks of 64 bytes per row (BK = 32 16-bit or 16 fp32 values) through a
@@ -20,7 +18,8 @@
 // slot v ^ ((r >> 2) & 3)) so that the MFMA operand reads (ds_read_b128,
 // lanes 0..15 on rows 0..15 at one k-vector) hit 16 distinct 16-byte bank
 // groups.  The loads of chunk kt+S-1 are spread over the MFMAs of chunk kt;
-// one barrier per chunk.
+// one barrier per chunk.  For the 16-bit kinds with K-major A the operand
+// reads of each k-step are also spread over the MFMAs of the step before.
 //
 // Masking costs nothing in the loop: each operand's buffer descriptor covers
 // exactly its valid rows and k range, so rows beyond `rows` read as zero, and
@@ -239,6 +238,28 @@ constexpr int frag_reads() {
   return (G::TA ? 2 * G::FM : G::FM) + G::FN;
 }
 
+// read_frags (K-major A) one read at a time: read R of a k-step's fragments
+template <class G>
+struct FragReader {
+  uint32_t abase, bbase;
+  __device__ __forceinline__ FragReader(const char* stage, int s) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int wm = w / G::WN, wn = w % G::WN;
+    const int q = lane & 31, h = lane >> 5;
+    const int off = (((h * NS + s) ^ swz(q)) << 4);
+    abase = lds_off(stage + (wm * G::TM + q) * ROWB + off);
+    bbase = lds_off(stage + (G::BM + wn * G::TN + q) * ROWB + off);
+  }
+  template <int R>
+  __device__ __forceinline__ void read(Frags<G>& f) const {
+    static_assert(!G::TA, "K-major A");
+    if constexpr (R < G::FM)
+      f.a[R] = lds_read_b128<R * 32 * ROWB>(abase);
+    else
+      f.b[R - G::FM] = lds_read_b128<(R - G::FM) * 32 * ROWB>(bbase);
+  }
+};
+
 // at most N LDS operations outstanding (the reads of `f` were issued before
 // the last N), then f's registers are tied to the wait so that no MFMA using
 // them is scheduled above it
@@ -293,6 +314,34 @@ __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM
   });
 }
 
+// mfma_step (16-bit kinds) with the LDS reads of the next fragment set `nf`
+// interleaved: two reads after each of the first MFMAs, so that the reads
+// land during the step and the next step's MFMAs need not wait for them.
+template <class G, int L0, int L1>
+__device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const LoadPlan<G>& lp,
+                                             int k0, char* stage, const FragReader<G>& rd, Frags<G>& nf) {
+  static_assert(G::KIND != K_F32, "16-bit kinds (one MFMA per block and k-step)");
+  constexpr int NL = L1 - L0;
+  constexpr int NR = frag_reads<G>();
+  static_assert(NL <= G::NMF && (NR + 1) / 2 <= G::NMF, "slots");
+  constexpr int EVERY = NL > 0 ? G::NMF / (NL > 0 ? NL : 1) : G::NMF + 1;
+  static_for<G::NMF>([&](auto mc) {
+    constexpr int m = mc;
+    acc[m / G::FN][m % G::FN] = mfma16_32x32x16<G::F16>(f.a[m / G::FN], f.b[m % G::FN], acc[m / G::FN][m % G::FN]);
+    if constexpr (2 * m < NR) {
+      sched_fence();
+      rd.template read<2 * m>(nf);
+      if constexpr (2 * m + 1 < NR) rd.template read<2 * m + 1>(nf);
+      sched_fence();
+    }
+    if constexpr (NL > 0 && (m % EVERY) == EVERY - 1 && L0 + m / EVERY < L1) {
+      sched_fence();
+      lp.template issue<L0 + m / EVERY>(k0, stage);
+      sched_fence();
+    }
+  });
+}
+
 // acc[i][j] (this wave's sub-tile) = sum_k A(m, k) * B(n, k) over k in [0, K)
 // (ZERO = false: added to acc), K > 0 (chunks past kmax read as zero).  Uses
 // LDS_BYTES of `lds`; ends with every wave past its last LDS read of the ring
@@ -324,6 +373,39 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
   Frags<G> f0, f1;
   int cur = 0;      // stage of chunk kt
   int fre = S - 1;  // stage of chunk kt-1 = stage of chunk kt+S-1
+  // 16-bit kinds, K-major A: each k-step's operand reads are spread over the
+  // first MFMAs of the step before (measured: config 4 forward 6.48 -> 6.29
+  // ms; the fp32 backward, three workgroups per CU, was 0.6% slower this way)
+  if constexpr (!G::TA && G::KIND != K_F32) {
+    for (int kt = 0; kt < nk; ++kt) {
+      wait_barrier<G::IPW*(S - 2)>();
+      // the previous step's reads into f1 have landed: tie f1 to that wait so
+      // that no MFMA using f1 is scheduled above it
+      lgkm_wait<0>(f1);
+      sched_fence();
+      char* cs = lds + cur * G::STAGE;
+      char* fs = lds + fre * G::STAGE;
+      const int k0 = (kt + S - 1) * BK;
+      const FragReader<G> r0(cs, 0), r1(cs, 1);
+      if (kt > 0) {
+        mfma_step_rd<G, 0, G::LPS>(f1, acc, lp, k0, fs, r0, f0);
+      } else {
+        read_frags<G>(cs, 0, f0);
+        static_for<G::LPS>([&](auto i) { lp.template issue<i>(k0, fs); });
+      }
+      lgkm_wait<0>(f0);
+      sched_fence();
+      mfma_step_rd<G, G::LPS, G::IPW>(f0, acc, lp, k0, fs, r1, f1);
+      sched_fence();
+      cur = cur + 1 == S ? 0 : cur + 1;
+      fre = fre + 1 == S ? 0 : fre + 1;
+    }
+    lgkm_wait<0>(f1);
+    sched_fence();
+    mfma_step<G, 0, 0>(f1, acc, lp, 0, lds);
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));
+    return;
+  }
   for (int kt = 0; kt < nk; ++kt) {
     wait_barrier<G::IPW*(S - 2)>();  // chunk kt landed (chunks kt+1 .. kt+S-2 may be in flight)
     char* cs = lds + cur * G::STAGE;
