@@ -238,10 +238,13 @@ constexpr int frag_reads() {
   return (G::TA ? 2 * G::FM : G::FM) + G::FN;
 }
 
-// read_frags (K-major A) one read at a time: read R of a k-step's fragments
+// read_frags one read at a time: read R (of frag_reads) of a k-step's
+// fragments.  Transposed A takes two reads per fragment (its low and high
+// four k-values), written into the halves of f.a[i].
 template <class G>
 struct FragReader {
   uint32_t abase, bbase;
+  uint32_t ta[G::TA ? G::FM : 1][2];  // transposed A: per fragment and half
   __device__ __forceinline__ FragReader(const char* stage, int s) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wm = w / G::WN, wn = w % G::WN;
@@ -249,14 +252,39 @@ struct FragReader {
     const int off = (((h * NS + s) ^ swz(q)) << 4);
     abase = lds_off(stage + (wm * G::TM + q) * ROWB + off);
     bbase = lds_off(stage + (G::BM + wn * G::TN + q) * ROWB + off);
+    if constexpr (G::TA) {
+      // the addresses of read_frags' transposed-A branch
+      const int g = lane >> 4, j = lane & 15;
+      const int kb = ((g >> 1) * NS + s) * 8;
+#pragma unroll
+      for (int i = 0; i < G::FM; ++i) {
+        const int m = wm * G::TM + i * 32 + 16 * (g & 1) + 4 * (j & 3);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int krow = kb + 4 * half + (j >> 2);
+          const int slot = (m >> 3) ^ (4 * (krow & 3));
+          ta[i][half] = lds_off(stage + krow * (G::BM * 2) + slot * 16 + (m & 7) * 2);
+        }
+      }
+    }
   }
   template <int R>
   __device__ __forceinline__ void read(Frags<G>& f) const {
-    static_assert(!G::TA, "K-major A");
-    if constexpr (R < G::FM)
-      f.a[R] = lds_read_b128<R * 32 * ROWB>(abase);
-    else
-      f.b[R - G::FM] = lds_read_b128<(R - G::FM) * 32 * ROWB>(bbase);
+    constexpr int NA = G::TA ? 2 * G::FM : G::FM;
+    if constexpr (R < NA) {
+      if constexpr (G::TA) {
+        i16x4_t v;
+        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(ta[R / 2][R % 2]) : "memory");
+        if constexpr (R % 2 == 0)
+          f.a[R / 2].lo = v;
+        else
+          f.a[R / 2].hi = v;
+      } else {
+        f.a[R] = lds_read_b128<R * 32 * ROWB>(abase);
+      }
+    } else {
+      f.b[R - NA] = lds_read_b128<(R - NA) * 32 * ROWB>(bbase);
+    }
   }
 };
 
@@ -373,10 +401,10 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
   Frags<G> f0, f1;
   int cur = 0;      // stage of chunk kt
   int fre = S - 1;  // stage of chunk kt-1 = stage of chunk kt+S-1
-  // 16-bit kinds, K-major A: each k-step's operand reads are spread over the
-  // first MFMAs of the step before (measured: config 4 forward 6.48 -> 6.29
-  // ms; the fp32 backward, three workgroups per CU, was 0.6% slower this way)
-  if constexpr (!G::TA && G::KIND != K_F32) {
+  // 16-bit kinds: each k-step's operand reads are spread over the first MFMAs
+  // of the step before (measured: config 4 forward 6.48 -> 6.29 ms; the fp32
+  // backward, three workgroups per CU, was 0.6% slower this way)
+  if constexpr (G::KIND != K_F32) {
     for (int kt = 0; kt < nk; ++kt) {
       wait_barrier<G::IPW*(S - 2)>();
       // the previous step's reads into f1 have landed: tie f1 to that wait so
