@@ -10,16 +10,19 @@
 // waves (48 KB), two (forward) or three (backward) workgroups per CU.
 //
 // Operands are K-major (element (row, k) at base[row * ld + k]).  K is staged
-// in chunks of 64 bytes per row (BK = 32 16-bit or 16 fp32 values) through a
-// ring of S = 3 LDS stages ([row][64 bytes]).  Each chunk arrives by
-// buffer_load_dwordx4 ... lds: every lane of a wave moves 16 bytes and the
-// wave writes one contiguous 1 KB block (16 rows) of the stage; which 16-byte
-// k-vector of a row a lane fetches is XOR-swizzled (vector v of row r sits in
-// slot v ^ ((r >> 2) & 3)) so that the MFMA operand reads (ds_read_b128,
-// lanes 0..15 on rows 0..15 at one k-vector) hit 16 distinct 16-byte bank
-// groups.  The loads of chunk kt+S-1 are spread over the MFMAs of chunk kt;
-// one barrier per chunk.  For the 16-bit kinds with K-major A the operand
-// reads of each k-step are also spread over the MFMAs of the step before.
+// in chunks of ROWB bytes per row through a ring of LDS stages ([row][ROWB]):
+//   fp32: 64-byte rows (BK = 16), 3 stages; the loads of chunk kt+2 are
+//         spread over the MFMAs of chunk kt.
+//   16-bit: 128-byte rows (BK = 64, whole cache lines: half the L2 requests
+//         of 64-byte rows), 2 stages of 64 KB; the loads of chunk kt+1 are
+//         spread over the first two of chunk kt's four k-steps, and each
+//         k-step's operand reads over the MFMAs of the step before.
+// One barrier per chunk.  Each chunk arrives by buffer_load_dwordx4 ... lds:
+// every lane of a wave moves 16 bytes and the wave writes one contiguous 1 KB
+// block (1024 / ROWB rows) of the stage; which 16-byte k-vector of a row a
+// lane fetches is XOR-swizzled (vector v of row r sits in slot v ^ swz(r))
+// so that the MFMA operand reads (ds_read_b128, lanes 0..15 on rows 0..15 at
+// one k-vector) hit 16 distinct 16-byte bank groups.
 //
 // Masking costs nothing in the loop: each operand's buffer descriptor covers
 // exactly its valid rows and k range, so rows beyond `rows` read as zero, and
@@ -29,13 +32,13 @@
 // vector, and (rows - 1) * ld + kmax elements within 2^31 - 1 bytes (byte
 // offsets are 32-bit, and the offset 2^31 must read as zero).
 //
-// Within a chunk the 16-byte vector fed to k-step s (0, 1) by lane half
-// h = lane / 32 is vector h * 2 + s for both operands (fp32: its four values
+// Within a chunk the 16-byte vector fed to k-step s (0 .. NS-1) by lane half
+// h = lane / 32 is vector h * NS + s for both operands (fp32: its four values
 // feed four MFMAs in order), so the contraction over the chunk is exact.
 //
 // Transposed A (TA = true): A is stored k-row-major (element (m, k) at
 // base[k * ld + m], m contiguous), e.g. a transposed gradient-matrix block.
-// Its stage region is [32 k-rows][BM m] (2 k-rows per 1 KB load block, the
+// Its stage region is [BK k-rows][BM m] (2 k-rows per 1 KB load block, the
 // 16-byte slot of m-vector v in k-row r at v ^ 4 (r & 3)), and each MFMA
 // fragment (8 consecutive k at one m) is assembled from two
 // ds_read_b64_tr_b16: within each group of 16 lanes, source lane j points at
@@ -48,24 +51,32 @@
 namespace mec {
 namespace gdma {
 
-constexpr int S = 3;              // LDS stages
-constexpr int ROWB = 64;          // bytes per staged row of a chunk (BK = 64 / element size)
-constexpr int RPB = 16;           // rows per 1 KB load block
-constexpr int NS = 2;             // k-steps per chunk (one 16-byte vector per lane half each)
 constexpr uint32_t OOB = 0x80000000u;  // buffer offset that reads as zero
 
 // element kinds: bf16 and fp16 (v_mfma_f32_32x32x16_*, one MFMA per k-step
 // and block) and fp32 (v_mfma_f32_32x32x2_f32, four per k-step and block)
 enum Kind { K_BF16 = 0, K_F16 = 1, K_F32 = 2 };
 
-template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16>
+template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16, int ROWB_ = 64>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_;
   static constexpr int KIND = KIND_;
   static constexpr bool F16 = KIND == K_F16;           // fp16 MFMAs (16-bit kinds)
   static constexpr int ESZ = KIND == K_F32 ? 4 : 2;    // bytes per element
   static constexpr int EPV = 16 / ESZ;                 // elements per 16-byte vector
+  // ring: chunks of ROWB bytes per row; 64-byte rows in 3 stages (the loads of
+  // chunk kt+2 spread over chunk kt), or 128-byte rows (whole cache lines) in
+  // 2 stages (the loads of chunk kt+1 issued when chunk kt starts)
+  static constexpr int ROWB = ROWB_;
+  static_assert(ROWB == 64 || ROWB == 128, "64- or 128-byte rows");
+  static constexpr int S = ROWB == 64 ? 3 : 2;         // LDS stages
+  static constexpr int RPB = 1024 / ROWB;              // rows per 1 KB load block
+  static constexpr int SLOTS = ROWB / 16;              // 16-byte vectors per row
+  static constexpr int NS = ROWB / 32;                 // k-steps per chunk (one vector per lane half each)
   static constexpr int BK = ROWB / ESZ;                // k per chunk
+  // bank-conflict swizzle: vector v of row r sits in slot v ^ swz(r), so that
+  // 16 consecutive rows at one vector hit 16 distinct 16-byte bank groups
+  static __device__ __forceinline__ int swz(int r) { return ROWB == 64 ? (r >> 2) & 3 : (r >> 1) & 7; }
   static constexpr int MPB = KIND == K_F32 ? 4 : 1;    // MFMAs per block and k-step
   static constexpr bool TA = TA_;                      // A stored k-row-major
   static_assert(!TA || (BM == 256 && ESZ == 2), "transposed A: 16-bit, 512-byte k-rows (BM = 256)");
@@ -79,6 +90,7 @@ struct Geo {
   static constexpr int NMF = FM * FN * MPB;            // MFMAs per k-step
   static constexpr int LPS = (IPW + NS - 1) / NS;      // loads interleaved per k-step
   static_assert(ROWS % (RPB * NW) == 0 && BM % RPB == 0, "load split");
+  static_assert((NW * RPB) % 16 == 0, "the loads of one wave share the row swizzle");
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave sub-tile of 32x32 blocks");
 };
 
@@ -89,7 +101,6 @@ struct Operand {
   int kmax;          // valid k range [0, kmax), a multiple of the elements per 16-byte vector
 };
 
-__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
 template <int ESZ>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& op) {
@@ -110,7 +121,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_t(const Operand& op)
 // compile time.
 template <class G>
 struct LoadPlan {
-  static constexpr int A_BLOCKS = G::BM / RPB;  // 1 KB blocks of A per stage (transposed A too)
+  static constexpr int A_BLOCKS = G::BM / G::RPB;  // 1 KB blocks of A per stage (transposed A too)
   static_assert(A_BLOCKS % G::NW == 0, "every wave loads whole rows of A blocks");
   static constexpr int A_LOADS = A_BLOCKS / G::NW;
   __amdgpu_buffer_rsrc_t ra, rb;
@@ -128,9 +139,10 @@ struct LoadPlan {
     lda = A.ld * 2;
     const int lane = threadIdx.x & 63;
     w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int rib = lane >> 2, phys = lane & 3;
-    // rows of one load block are b*16 .. b*16+15, so swz(r) = (rib >> 2) & 3
-    kv = (phys ^ swz(rib)) * G::EPV;
+    const int rib = lane / G::SLOTS, phys = lane % G::SLOTS;
+    // every load of this wave fills rows b * RPB + rib with b = i * NW + w,
+    // whose swizzle does not depend on i
+    kv = (phys ^ G::swz(w * G::RPB + rib)) * G::EPV;
     kr = lane >> 5;
 #pragma unroll
     for (int i = 0; i < G::IPW; ++i) {
@@ -141,7 +153,7 @@ struct LoadPlan {
         const int slot = (lane & 31) ^ (4 * (krow & 3));
         voff[i] = (uint32_t)((int64_t)krow * A.ld + slot * 8) * 2;
       } else {
-        const int r = b * RPB + rib;
+        const int r = b * G::RPB + rib;
         voff[i] = (uint32_t)(((i < A_LOADS ? (int64_t)r * A.ld : (int64_t)(r - G::BM) * B.ld) + kv) * G::ESZ);
       }
     }
@@ -204,12 +216,12 @@ __device__ __forceinline__ void read_frags(const char* stage, int s, Frags<G>& f
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w / G::WN, wn = w % G::WN;
   const int q = lane & 31, h = lane >> 5;
-  const int off = (((h * NS + s) ^ swz(q)) << 4);
+  const int off = (((h * G::NS + s) ^ G::swz(q)) << 4);
   if (G::TA) {
     // fragment of 32 m x 16 k: lane group g = lane / 16 covers m0 + 16 (g & 1) .. + 15 and
-    // logical k-vector (g >> 1) * 2 + s; source lane j reads k-row kb + j / 4, m-quad j % 4
+    // logical k-vector (g >> 1) * NS + s; source lane j reads k-row kb + j / 4, m-quad j % 4
     const int g = lane >> 4, j = lane & 15;
-    const int kb = ((g >> 1) * NS + s) * 8;
+    const int kb = ((g >> 1) * G::NS + s) * 8;
 #pragma unroll
     for (int i = 0; i < G::FM; ++i) {
       const int m = wm * G::TM + i * 32 + 16 * (g & 1) + 4 * (j & 3);
@@ -225,11 +237,11 @@ __device__ __forceinline__ void read_frags(const char* stage, int s, Frags<G>& f
       f.a[i] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   } else {
-    const uint32_t abase = lds_off(stage + (wm * G::TM + q) * ROWB + off);
-    static_for<G::FM>([&](auto i) { f.a[i] = lds_read_b128<i * 32 * ROWB>(abase); });
+    const uint32_t abase = lds_off(stage + (wm * G::TM + q) * G::ROWB + off);
+    static_for<G::FM>([&](auto i) { f.a[i] = lds_read_b128<i * 32 * G::ROWB>(abase); });
   }
-  const uint32_t bbase = lds_off(stage + (G::BM + wn * G::TN + q) * ROWB + off);
-  static_for<G::FN>([&](auto j) { f.b[j] = lds_read_b128<j * 32 * ROWB>(bbase); });
+  const uint32_t bbase = lds_off(stage + (G::BM + wn * G::TN + q) * G::ROWB + off);
+  static_for<G::FN>([&](auto j) { f.b[j] = lds_read_b128<j * 32 * G::ROWB>(bbase); });
 }
 
 // LDS reads per read_frags call
@@ -249,13 +261,13 @@ struct FragReader {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wm = w / G::WN, wn = w % G::WN;
     const int q = lane & 31, h = lane >> 5;
-    const int off = (((h * NS + s) ^ swz(q)) << 4);
-    abase = lds_off(stage + (wm * G::TM + q) * ROWB + off);
-    bbase = lds_off(stage + (G::BM + wn * G::TN + q) * ROWB + off);
+    const int off = (((h * G::NS + s) ^ G::swz(q)) << 4);
+    abase = lds_off(stage + (wm * G::TM + q) * G::ROWB + off);
+    bbase = lds_off(stage + (G::BM + wn * G::TN + q) * G::ROWB + off);
     if constexpr (G::TA) {
       // the addresses of read_frags' transposed-A branch
       const int g = lane >> 4, j = lane & 15;
-      const int kb = ((g >> 1) * NS + s) * 8;
+      const int kb = ((g >> 1) * G::NS + s) * 8;
 #pragma unroll
       for (int i = 0; i < G::FM; ++i) {
         const int m = wm * G::TM + i * 32 + 16 * (g & 1) + 4 * (j & 3);
@@ -280,10 +292,10 @@ struct FragReader {
         else
           f.a[R / 2].hi = v;
       } else {
-        f.a[R] = lds_read_b128<R * 32 * ROWB>(abase);
+        f.a[R] = lds_read_b128<R * 32 * G::ROWB>(abase);
       }
     } else {
-      f.b[R - NA] = lds_read_b128<(R - NA) * 32 * ROWB>(bbase);
+      f.b[R - NA] = lds_read_b128<(R - NA) * 32 * G::ROWB>(bbase);
     }
   }
 };
@@ -368,6 +380,7 @@ __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G:
       sched_fence();
     }
   });
+  sched_fence();  // the step's MFMAs stay above the caller's next wait
 }
 
 // acc[i][j] (this wave's sub-tile) = sum_k A(m, k) * B(n, k) over k in [0, K)
@@ -394,26 +407,71 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
   const int nk = (K + BK - 1) / BK;
   LoadPlan<G> lp;
   lp.init(A, B);
+  if constexpr (G::S == 2) {
+    // 128-byte rows, 2 stages: chunk kt+1 loads into the other stage, freed
+    // by the barrier at the start of chunk kt; the NS k-steps of chunk kt
+    // alternate fragment sets f0 / f1, each step's reads spread over the
+    // MFMAs of the step before
+    static_assert(G::KIND != K_F32 && G::NS == 4, "16-bit kinds, four k-steps per chunk");
+    static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, lds); });
+    Frags<G> f0, f1;
+    for (int kt = 0; kt < nk; ++kt) {
+      wait_barrier<0>();  // chunk kt landed; every wave is done with the other stage
+      lgkm_wait<0>(f1);   // f1 (the last step of chunk kt-1) landed before its MFMAs
+      sched_fence();
+      char* cs = lds + (kt & 1) * G::STAGE;
+      char* ns = lds + ((kt & 1) ^ 1) * G::STAGE;
+      const int k1 = (kt + 1) * BK;
+      // loads of chunk kt+1: spread over the first NSP k-steps (measured: all
+      // at the start of the chunk or over all four steps were slower)
+      constexpr int NSP = 2, PER = G::IPW / NSP;
+      static_assert(G::IPW % NSP == 0 && NSP <= 4, "even load split");
+      constexpr int L1a = PER, L2a = NSP > 1 ? 2 * PER : PER, L3a = NSP > 2 ? 3 * PER : L2a,
+                    L4a = NSP > 3 ? 4 * PER : L3a;
+      const FragReader<G> r0(cs, 0), r1(cs, 1), r2(cs, 2), r3(cs, 3);
+      if (kt > 0) {
+        mfma_step_rd<G, 0, L1a>(f1, acc, lp, k1, ns, r0, f0);
+      } else {
+        read_frags<G>(cs, 0, f0);
+        static_for<L1a>([&](auto i) { lp.template issue<i>(k1, ns); });
+      }
+      lgkm_wait<0>(f0);
+      sched_fence();
+      mfma_step_rd<G, L1a, L2a>(f0, acc, lp, k1, ns, r1, f1);
+      lgkm_wait<0>(f1);
+      sched_fence();
+      mfma_step_rd<G, L2a, L3a>(f1, acc, lp, k1, ns, r2, f0);
+      lgkm_wait<0>(f0);
+      sched_fence();
+      mfma_step_rd<G, L3a, L4a>(f0, acc, lp, k1, ns, r3, f1);
+      sched_fence();
+    }
+    lgkm_wait<0>(f1);
+    sched_fence();
+    mfma_step<G, 0, 0>(f1, acc, lp, 0, lds);
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));
+    return;
+  }
   // prologue: chunks 0 .. S-2 in flight
 #pragma unroll
-  for (int c = 0; c + 1 < S; ++c)
+  for (int c = 0; c + 1 < G::S; ++c)
     static_for<G::IPW>([&](auto i) { lp.template issue<i>(c * BK, lds + c * G::STAGE); });
   Frags<G> f0, f1;
   int cur = 0;      // stage of chunk kt
-  int fre = S - 1;  // stage of chunk kt-1 = stage of chunk kt+S-1
+  int fre = G::S - 1;  // stage of chunk kt-1 = stage of chunk kt+S-1
   // 16-bit kinds: each k-step's operand reads are spread over the first MFMAs
   // of the step before (measured: config 4 forward 6.48 -> 6.29 ms; the fp32
   // backward, three workgroups per CU, was 0.6% slower this way)
   if constexpr (G::KIND != K_F32) {
     for (int kt = 0; kt < nk; ++kt) {
-      wait_barrier<G::IPW*(S - 2)>();
+      wait_barrier<G::IPW*(G::S - 2)>();
       // the previous step's reads into f1 have landed: tie f1 to that wait so
       // that no MFMA using f1 is scheduled above it
       lgkm_wait<0>(f1);
       sched_fence();
       char* cs = lds + cur * G::STAGE;
       char* fs = lds + fre * G::STAGE;
-      const int k0 = (kt + S - 1) * BK;
+      const int k0 = (kt + G::S - 1) * BK;
       const FragReader<G> r0(cs, 0), r1(cs, 1);
       if (kt > 0) {
         mfma_step_rd<G, 0, G::LPS>(f1, acc, lp, k0, fs, r0, f0);
@@ -425,8 +483,8 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
       sched_fence();
       mfma_step_rd<G, G::LPS, G::IPW>(f0, acc, lp, k0, fs, r1, f1);
       sched_fence();
-      cur = cur + 1 == S ? 0 : cur + 1;
-      fre = fre + 1 == S ? 0 : fre + 1;
+      cur = cur + 1 == G::S ? 0 : cur + 1;
+      fre = fre + 1 == G::S ? 0 : fre + 1;
     }
     lgkm_wait<0>(f1);
     sched_fence();
@@ -435,10 +493,10 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
     return;
   }
   for (int kt = 0; kt < nk; ++kt) {
-    wait_barrier<G::IPW*(S - 2)>();  // chunk kt landed (chunks kt+1 .. kt+S-2 may be in flight)
+    wait_barrier<G::IPW*(G::S - 2)>();  // chunk kt landed (chunks kt+1 .. kt+S-2 may be in flight)
     char* cs = lds + cur * G::STAGE;
     char* fs = lds + fre * G::STAGE;
-    const int k0 = (kt + S - 1) * BK;
+    const int k0 = (kt + G::S - 1) * BK;
     read_frags<G>(cs, 0, f0);
     sched_fence();
     // the previous chunk's last k-step (its operands are already in registers)
@@ -453,8 +511,8 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
     sched_fence();
     mfma_step<G, G::LPS, G::IPW>(f0, acc, lp, k0, fs);
     sched_fence();
-    cur = cur + 1 == S ? 0 : cur + 1;
-    fre = fre + 1 == S ? 0 : fre + 1;
+    cur = cur + 1 == G::S ? 0 : cur + 1;
+    fre = fre + 1 == G::S ? 0 : fre + 1;
   }
   lgkm_wait<0>(f1);
   sched_fence();

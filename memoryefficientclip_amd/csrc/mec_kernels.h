@@ -95,11 +95,13 @@ template <> struct PackOf<gdma::K_F32> { using type = PackF32; };
 // multiples of the elements per 16-byte vector), element kind KIND (bf16,
 // fp16 or fp32); TA_: A stored k-row-major (a transposed 16-bit
 // gradient-matrix block)
+// (ring rows: 64 bytes for fp32, whose tiles run two or three per CU; 128
+// bytes for the 16-bit kinds, one 256 x 256 tile per CU)
 template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND>
 struct TileD : PackOf<KIND>::type {
   using Elem = typename std::conditional<KIND == gdma::K_F32, float, uint16_t>::type;
   using Op = gdma::Operand;
-  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND>;
+  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, KIND == gdma::K_F32 ? 64 : 128>;
   static constexpr bool TA = TA_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
