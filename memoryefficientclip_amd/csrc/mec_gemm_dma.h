@@ -354,20 +354,26 @@ __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM
   });
 }
 
-// mfma_step (16-bit kinds) with the LDS reads of the next fragment set `nf`
-// interleaved: two reads after each of the first MFMAs, so that the reads
+// mfma_step with the LDS reads of the next fragment set `nf` interleaved: two reads after each of the first MFMAs, so that the reads
 // land during the step and the next step's MFMAs need not wait for them.
 template <class G, int L0, int L1>
 __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const LoadPlan<G>& lp,
                                              int k0, char* stage, const FragReader<G>& rd, Frags<G>& nf) {
-  static_assert(G::KIND != K_F32, "16-bit kinds (one MFMA per block and k-step)");
   constexpr int NL = L1 - L0;
   constexpr int NR = frag_reads<G>();
   static_assert(NL <= G::NMF && (NR + 1) / 2 <= G::NMF, "slots");
   constexpr int EVERY = NL > 0 ? G::NMF / (NL > 0 ? NL : 1) : G::NMF + 1;
   static_for<G::NMF>([&](auto mc) {
     constexpr int m = mc;
-    acc[m / G::FN][m % G::FN] = mfma16_32x32x16<G::F16>(f.a[m / G::FN], f.b[m % G::FN], acc[m / G::FN][m % G::FN]);
+    if constexpr (G::KIND == K_F32) {
+      // consecutive MFMAs on different blocks (the fences below keep program order)
+      constexpr int NB = G::FM * G::FN, blk = m % NB, t = m / NB, i = blk / G::FN, j = blk % G::FN;
+      acc[i][j] = mfma_f32_32x32x2(__builtin_bit_cast(f32x4, f.a[i])[t], __builtin_bit_cast(f32x4, f.b[j])[t],
+                                   acc[i][j]);
+    } else {
+      acc[m / G::FN][m % G::FN] =
+          mfma16_32x32x16<G::F16>(f.a[m / G::FN], f.b[m % G::FN], acc[m / G::FN][m % G::FN]);
+    }
     if constexpr (2 * m < NR) {
       sched_fence();
       rd.template read<2 * m>(nf);
@@ -412,7 +418,7 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
     // by the barrier at the start of chunk kt; the NS k-steps of chunk kt
     // alternate fragment sets f0 / f1, each step's reads spread over the
     // MFMAs of the step before
-    static_assert(G::KIND != K_F32 && G::NS == 4, "16-bit kinds, four k-steps per chunk");
+    static_assert(G::NS == 4, "four k-steps per chunk");
     static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, lds); });
     Frags<G> f0, f1;
     for (int kt = 0; kt < nk; ++kt) {

@@ -95,13 +95,11 @@ template <> struct PackOf<gdma::K_F32> { using type = PackF32; };
 // multiples of the elements per 16-byte vector), element kind KIND (bf16,
 // fp16 or fp32); TA_: A stored k-row-major (a transposed 16-bit
 // gradient-matrix block)
-// (ring rows: 64 bytes for fp32, whose tiles run two or three per CU; 128
-// bytes for the 16-bit kinds, one 256 x 256 tile per CU)
 template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND>
 struct TileD : PackOf<KIND>::type {
   using Elem = typename std::conditional<KIND == gdma::K_F32, float, uint16_t>::type;
   using Op = gdma::Operand;
-  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, KIND == gdma::K_F32 ? 64 : 128>;
+  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND>;
   static constexpr bool TA = TA_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
@@ -156,7 +154,7 @@ template <> struct GScale<_Float16> { static constexpr float value = 16384.f; };
 // workgroups per CU the launch bounds promise (the 16-bit direct-load tiles
 // use 96 KB of LDS or more: one per CU)
 template <typename T, bool VEC> struct Occ {
-  static constexpr int fwd = Is16<T>::value ? (VEC ? 1 : 2) : 2, bwd = Is16<T>::value ? (VEC ? 1 : 2) : 3;
+  static constexpr int fwd = Is16<T>::value ? (VEC ? 1 : 2) : 2, bwd = Is16<T>::value ? (VEC ? 1 : 2) : 2;
 };
 
 // Operand of a tile core from a typed pointer (the 16-bit cores address bits)
