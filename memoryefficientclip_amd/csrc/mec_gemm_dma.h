@@ -57,26 +57,24 @@ constexpr uint32_t OOB = 0x80000000u;  // buffer offset that reads as zero
 // and block) and fp32 (v_mfma_f32_32x32x2_f32, four per k-step and block)
 enum Kind { K_BF16 = 0, K_F16 = 1, K_F32 = 2 };
 
-template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16, int ROWB_ = 64>
+template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_;
   static constexpr int KIND = KIND_;
   static constexpr bool F16 = KIND == K_F16;           // fp16 MFMAs (16-bit kinds)
   static constexpr int ESZ = KIND == K_F32 ? 4 : 2;    // bytes per element
   static constexpr int EPV = 16 / ESZ;                 // elements per 16-byte vector
-  // ring: chunks of ROWB bytes per row; 64-byte rows in 3 stages (the loads of
-  // chunk kt+2 spread over chunk kt), or 128-byte rows (whole cache lines) in
-  // 2 stages (the loads of chunk kt+1 issued when chunk kt starts)
-  static constexpr int ROWB = ROWB_;
-  static_assert(ROWB == 64 || ROWB == 128, "64- or 128-byte rows");
-  static constexpr int S = ROWB == 64 ? 3 : 2;         // LDS stages
+  // ring: chunks of 128 bytes per operand row (whole cache lines) in 2 stages
+  static constexpr int ROWB = 128;                     // bytes per staged row of a chunk
+  static constexpr int S = 2;                          // LDS stages
   static constexpr int RPB = 1024 / ROWB;              // rows per 1 KB load block
   static constexpr int SLOTS = ROWB / 16;              // 16-byte vectors per row
   static constexpr int NS = ROWB / 32;                 // k-steps per chunk (one vector per lane half each)
   static constexpr int BK = ROWB / ESZ;                // k per chunk
   // bank-conflict swizzle: vector v of row r sits in slot v ^ swz(r), so that
   // 16 consecutive rows at one vector hit 16 distinct 16-byte bank groups
-  static __device__ __forceinline__ int swz(int r) { return ROWB == 64 ? (r >> 2) & 3 : (r >> 1) & 7; }
+  // (rows r and r + 2 share banks at this pitch)
+  static __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
   static constexpr int MPB = KIND == K_F32 ? 4 : 1;    // MFMAs per block and k-step
   static constexpr bool TA = TA_;                      // A stored k-row-major
   static_assert(!TA || (BM == 256 && ESZ == 2), "transposed A: 16-bit, 512-byte k-rows (BM = 256)");
@@ -88,7 +86,6 @@ struct Geo {
   static constexpr int LDS_BYTES = S * STAGE;
   static constexpr int IPW = ROWS / RPB / NW;          // load instructions per wave per chunk
   static constexpr int NMF = FM * FN * MPB;            // MFMAs per k-step
-  static constexpr int LPS = (IPW + NS - 1) / NS;      // loads interleaved per k-step
   static_assert(ROWS % (RPB * NW) == 0 && BM % RPB == 0, "load split");
   static_assert((NW * RPB) % 16 == 0, "the loads of one wave share the row swizzle");
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave sub-tile of 32x32 blocks");
@@ -394,13 +391,17 @@ __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G:
 // LDS_BYTES of `lds`; ends with every wave past its last LDS read of the ring
 // and its loads landed (callers may reuse the ring after a barrier).
 //
-// Every iteration issues the loads of chunk kt+S-1, also past the last chunk
-// (they read zeros into a stage nobody reads again): the loop has no branches
-// around its loads and the number of loads in flight at each wait is the
-// same, IPW * (S - 2).
+// Chunk kt+1 loads into the other stage, freed by the barrier at the start of
+// chunk kt, spread over the first two of chunk kt's four k-steps (measured:
+// issuing them all at the start of the chunk, or over all four steps, was
+// slower).  The k-steps alternate fragment sets f0 / f1, each step's reads
+// spread over the MFMAs of the step before.  Every iteration issues its
+// loads, also past the last chunk (they read zeros into a stage nobody reads
+// again), so the loop has no branches around them.
 template <class G, bool ZERO = true>
 __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int K, char* lds,
                                          f32x16 (&acc)[G::FM][G::FN]) {
+  static_assert(G::S == 2 && G::NS == 4, "two stages, four k-steps per chunk");
   if constexpr (ZERO) {
 #pragma unroll
     for (int i = 0; i < G::FM; ++i)
@@ -410,115 +411,37 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   }
   constexpr int BK = G::BK;
+  constexpr int L1 = G::IPW / 2, L2 = G::IPW;  // loads issued in k-steps 0 and 1
+  static_assert(G::IPW % 2 == 0, "even load split");
   const int nk = (K + BK - 1) / BK;
   LoadPlan<G> lp;
   lp.init(A, B);
-  if constexpr (G::S == 2) {
-    // 128-byte rows, 2 stages: chunk kt+1 loads into the other stage, freed
-    // by the barrier at the start of chunk kt; the NS k-steps of chunk kt
-    // alternate fragment sets f0 / f1, each step's reads spread over the
-    // MFMAs of the step before
-    static_assert(G::NS == 4, "four k-steps per chunk");
-    static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, lds); });
-    Frags<G> f0, f1;
-    for (int kt = 0; kt < nk; ++kt) {
-      wait_barrier<0>();  // chunk kt landed; every wave is done with the other stage
-      lgkm_wait<0>(f1);   // f1 (the last step of chunk kt-1) landed before its MFMAs
-      sched_fence();
-      char* cs = lds + (kt & 1) * G::STAGE;
-      char* ns = lds + ((kt & 1) ^ 1) * G::STAGE;
-      const int k1 = (kt + 1) * BK;
-      // loads of chunk kt+1: spread over the first NSP k-steps (measured: all
-      // at the start of the chunk or over all four steps were slower)
-      constexpr int NSP = 2, PER = G::IPW / NSP;
-      static_assert(G::IPW % NSP == 0 && NSP <= 4, "even load split");
-      constexpr int L1a = PER, L2a = NSP > 1 ? 2 * PER : PER, L3a = NSP > 2 ? 3 * PER : L2a,
-                    L4a = NSP > 3 ? 4 * PER : L3a;
-      const FragReader<G> r0(cs, 0), r1(cs, 1), r2(cs, 2), r3(cs, 3);
-      if (kt > 0) {
-        mfma_step_rd<G, 0, L1a>(f1, acc, lp, k1, ns, r0, f0);
-      } else {
-        read_frags<G>(cs, 0, f0);
-        static_for<L1a>([&](auto i) { lp.template issue<i>(k1, ns); });
-      }
-      lgkm_wait<0>(f0);
-      sched_fence();
-      mfma_step_rd<G, L1a, L2a>(f0, acc, lp, k1, ns, r1, f1);
-      lgkm_wait<0>(f1);
-      sched_fence();
-      mfma_step_rd<G, L2a, L3a>(f1, acc, lp, k1, ns, r2, f0);
-      lgkm_wait<0>(f0);
-      sched_fence();
-      mfma_step_rd<G, L3a, L4a>(f0, acc, lp, k1, ns, r3, f1);
-      sched_fence();
-    }
-    lgkm_wait<0>(f1);
-    sched_fence();
-    mfma_step<G, 0, 0>(f1, acc, lp, 0, lds);
-    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));
-    return;
-  }
-  // prologue: chunks 0 .. S-2 in flight
-#pragma unroll
-  for (int c = 0; c + 1 < G::S; ++c)
-    static_for<G::IPW>([&](auto i) { lp.template issue<i>(c * BK, lds + c * G::STAGE); });
+  static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, lds); });
   Frags<G> f0, f1;
-  int cur = 0;      // stage of chunk kt
-  int fre = G::S - 1;  // stage of chunk kt-1 = stage of chunk kt+S-1
-  // 16-bit kinds: each k-step's operand reads are spread over the first MFMAs
-  // of the step before (measured: config 4 forward 6.48 -> 6.29 ms; the fp32
-  // backward, three workgroups per CU, was 0.6% slower this way)
-  if constexpr (G::KIND != K_F32) {
-    for (int kt = 0; kt < nk; ++kt) {
-      wait_barrier<G::IPW*(G::S - 2)>();
-      // the previous step's reads into f1 have landed: tie f1 to that wait so
-      // that no MFMA using f1 is scheduled above it
-      lgkm_wait<0>(f1);
-      sched_fence();
-      char* cs = lds + cur * G::STAGE;
-      char* fs = lds + fre * G::STAGE;
-      const int k0 = (kt + G::S - 1) * BK;
-      const FragReader<G> r0(cs, 0), r1(cs, 1);
-      if (kt > 0) {
-        mfma_step_rd<G, 0, G::LPS>(f1, acc, lp, k0, fs, r0, f0);
-      } else {
-        read_frags<G>(cs, 0, f0);
-        static_for<G::LPS>([&](auto i) { lp.template issue<i>(k0, fs); });
-      }
-      lgkm_wait<0>(f0);
-      sched_fence();
-      mfma_step_rd<G, G::LPS, G::IPW>(f0, acc, lp, k0, fs, r1, f1);
-      sched_fence();
-      cur = cur + 1 == G::S ? 0 : cur + 1;
-      fre = fre + 1 == G::S ? 0 : fre + 1;
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_barrier<0>();  // chunk kt landed; every wave is done with the other stage
+    lgkm_wait<0>(f1);   // f1 (the last step of chunk kt-1) landed before its MFMAs
+    sched_fence();
+    char* cs = lds + (kt & 1) * G::STAGE;
+    char* ns = lds + ((kt & 1) ^ 1) * G::STAGE;
+    const int k1 = (kt + 1) * BK;
+    const FragReader<G> r0(cs, 0), r1(cs, 1), r2(cs, 2), r3(cs, 3);
+    if (kt > 0) {
+      mfma_step_rd<G, 0, L1>(f1, acc, lp, k1, ns, r0, f0);
+    } else {
+      read_frags<G>(cs, 0, f0);
+      static_for<L1>([&](auto i) { lp.template issue<i>(k1, ns); });
     }
+    lgkm_wait<0>(f0);
+    sched_fence();
+    mfma_step_rd<G, L1, L2>(f0, acc, lp, k1, ns, r1, f1);
     lgkm_wait<0>(f1);
     sched_fence();
-    mfma_step<G, 0, 0>(f1, acc, lp, 0, lds);
-    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));
-    return;
-  }
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_barrier<G::IPW*(G::S - 2)>();  // chunk kt landed (chunks kt+1 .. kt+S-2 may be in flight)
-    char* cs = lds + cur * G::STAGE;
-    char* fs = lds + fre * G::STAGE;
-    const int k0 = (kt + G::S - 1) * BK;
-    read_frags<G>(cs, 0, f0);
+    mfma_step_rd<G, 0, 0>(f1, acc, lp, 0, lds, r2, f0);
+    lgkm_wait<0>(f0);
     sched_fence();
-    // the previous chunk's last k-step (its operands are already in registers)
-    if (kt > 0) {
-      mfma_step<G, 0, G::LPS>(f1, acc, lp, k0, fs);
-    } else {
-      static_for<G::LPS>([&](auto i) { lp.template issue<i>(k0, fs); });
-    }
+    mfma_step_rd<G, 0, 0>(f0, acc, lp, 0, lds, r3, f1);
     sched_fence();
-    read_frags<G>(cs, 1, f1);
-    lgkm_wait<frag_reads<G>()>(f0);  // f0 landed; f1's reads may still be in flight
-    sched_fence();
-    mfma_step<G, G::LPS, G::IPW>(f0, acc, lp, k0, fs);
-    sched_fence();
-    cur = cur + 1 == G::S ? 0 : cur + 1;
-    fre = fre + 1 == G::S ? 0 : fre + 1;
   }
   lgkm_wait<0>(f1);
   sched_fence();
