@@ -230,6 +230,8 @@ def main():
                     help="float32 matmul precision for fp32 inputs: highest = IEEE fp32 MFMA, "
                          "high = three bf16 MFMA products per fp32 product (bf16x3), medium = bf16 products")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-alt", action="store_true",
+                    help="skip the fp32 'high' precision side leg (e.g. for per-kernel profiles of the IEEE path)")
     ap.add_argument("--kernel-reps", type=int, default=0, help="launches per stage in the kernel leg (default: steps)")
     ap.add_argument("--probe", choices=["copy"], default=None,
                     help="copy: only run 5 plain device copies of 1 GiB (calibrates the rocprofv3 byte counters)")
@@ -327,7 +329,7 @@ def main():
     # fp32 inputs at "highest" precision: the same steps once more under "high"
     # (bf16x3), reported beside the IEEE line (not as its value)
     alt = None
-    if dt == "f32" and not lowp:
+    if dt == "f32" and not lowp and not args.no_alt:
         torch.set_float32_matmul_precision("high")
         for _ in range(args.warmup):
             step()
