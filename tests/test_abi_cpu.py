@@ -49,7 +49,7 @@ def test_sizes():
             assert bs % q == 0 and nb * bs >= n > (nb - 1) * bs, (n, d, dt, bs, nb)
             ldt = (n + 127) // 128 * 128
             assert b == (copies * nb * bs * bs + 2 * d * ldt) * elem, (n, d, dt)
-            bs_max = 2 * max(1024, (2 if dt == 0 else 8) * d + q)
+            bs_max = 2 * max(1024, (2 if dt == 0 else 16) * d + q)
             assert bs <= bs_max and b <= elem * (4 * (n + bs_max) * bs_max + 2 * d * (n + 128)), (n, d, dt, b)
     assert lib.mec_grad_scratch_bytes(10, 10, 7) < 0
 
@@ -99,8 +99,10 @@ def test_blocking_prefers_exact_divisors():
             bs, nb = _lib.grad_blocking(n, d, dt)
             assert nb * bs == n, (n, d, dt, bs, nb)
     assert _lib.grad_blocking(32768, 1152, 0) == (2048, 16)
-    assert _lib.grad_blocking(65536, 768, 1) == (8192, 8)
+    # 16-bit: ~16d rows while 8d would give fewer than 16 blocks, else ~8d
+    assert _lib.grad_blocking(65536, 768, 1) == (16384, 4)
     assert _lib.grad_blocking(262144, 1152, 1) == (8192, 32)
+    assert _lib.grad_blocking(32768, 1152, _lib.DTYPE_F32_BF16X3) == (16384, 2)
     assert _lib.grad_blocking(1000, 64, 0) == (1024, 1)
     assert _lib.grad_blocking(1000, 64, 1) == (1024, 1)
 
