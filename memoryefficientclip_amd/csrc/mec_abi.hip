@@ -143,27 +143,26 @@ bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, i
 
 // Block decomposition of the N x N gradient matrix for the backward: nb
 // blocks of tb quanta of q rows (q = block_quantum: 128 for fp32, 256 for
-// the 16-bit types, so every tile kind divides a block).  The target is
-// bs ~ 2d rows for fp32 and ~8d for the bf16 kernels (at least 1024 rows),
-// ~16d for the latter when n >= 8192 and 8d would give fewer than 16 blocks
-// (measured: n = 65536, d = 768: backward 19.0 -> 18.2 ms with 16384-row
-// blocks; n = 262144, d = 1152: 440 ms either way, so the smaller scratch is
-// kept), which keeps the scratch at O(n d).  Longer blocks mean fewer pipeline launches and
-// fewer fp32 accumulator updates through HBM (one per launch); bf16, whose MFMAs are 16x
-// faster, is bound by that traffic (backward at n = 65536, d = 768: 24.5 ms
-// with 4096-row blocks, 22.7 ms with 8192; at n = 262144, d = 1152: 561 vs
-// 553 ms), fp32 is not (57.9 vs 58.1 ms at the headline shape with 2048- and
-// 4096-row blocks).  An exact divisor of
-// the quantum count within a factor of two of the target is preferred (no
-// short last block, whose contractions would have a short K); otherwise the
-// quanta are balanced over the blocks.
+// the bf16 kernels, so every tile kind divides a block).  Longer blocks mean
+// fewer pipeline launches and fewer fp32 accumulator updates through HBM
+// (one per launch); the scratch grows as n * bs.  Targets (at least 1024
+// rows), measured on the 128-byte ring:
+//   fp32: bs ~ 4d (headline shape: backward 53.2 ms with 2048-row blocks,
+//         52.4 ms with 4096);
+//   bf16 kernels: bs ~ 8d, or ~16d when n >= 8192 and 8d would give fewer
+//         than 16 blocks (n = 65536, d = 768: backward 19.0 -> 18.2 ms with
+//         16384-row blocks; n = 262144, d = 1152: 440 ms either way, so the
+//         smaller scratch is kept).
+// An exact divisor of the quantum count within a factor of two of the
+// target is preferred (no short last block, whose contractions would have a
+// short K); otherwise the quanta are balanced over the blocks.
 void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
   const int64_t q = block_quantum(dtype);
   const int64_t tiles = (n + q - 1) / q;
   // 16-bit: a transposed gradient-matrix block is a direct-to-LDS operand
   // ((bs - 1) * bs + 256 elements within dma_max_elems): bs <= 127 * 256
   const int64_t cap = dtype == MEC_DTYPE_F32 ? tiles : 127;
-  int64_t mult = dtype == MEC_DTYPE_F32 ? 2 : 8;
+  int64_t mult = dtype == MEC_DTYPE_F32 ? 4 : 8;
   if (dtype != MEC_DTYPE_F32 && n >= 8192 && n < 16 * 8 * d) mult = 16;
   int64_t target = (mult * d + q - 1) / q;
   if (target < 1024 / q) target = 1024 / q;

@@ -49,7 +49,7 @@ def test_sizes():
             assert bs % q == 0 and nb * bs >= n > (nb - 1) * bs, (n, d, dt, bs, nb)
             ldt = (n + 127) // 128 * 128
             assert b == (copies * nb * bs * bs + 2 * d * ldt) * elem, (n, d, dt)
-            bs_max = 2 * max(1024, (2 if dt == 0 else 16) * d + q)
+            bs_max = 2 * max(1024, (4 if dt == 0 else 16) * d + q)
             assert bs <= bs_max and b <= elem * (4 * (n + bs_max) * bs_max + 2 * d * (n + 128)), (n, d, dt, b)
     assert lib.mec_grad_scratch_bytes(10, 10, 7) < 0
 
@@ -88,7 +88,7 @@ def test_16bit_blocks_fit_the_32bit_operand_range():
             bs, nb = _lib.grad_blocking(n, d, dt)
             assert bs <= 32512 and ((bs - 1) * bs + 256) * 2 < 2 ** 31, (n, d, bs)
             assert nb * bs >= n > (nb - 1) * bs
-    # fp32 addresses with 64-bit pointers and keeps its ~2d blocks
+    # fp32 addresses with 64-bit pointers and keeps its ~4d blocks
     assert _lib.grad_blocking(65536, 32768, 0)[0] == 65536
 
 
@@ -98,7 +98,7 @@ def test_blocking_prefers_exact_divisors():
         for dt in (0, 1, 2):
             bs, nb = _lib.grad_blocking(n, d, dt)
             assert nb * bs == n, (n, d, dt, bs, nb)
-    assert _lib.grad_blocking(32768, 1152, 0) == (2048, 16)
+    assert _lib.grad_blocking(32768, 1152, 0) == (4096, 8)
     # 16-bit: ~16d rows while 8d would give fewer than 16 blocks, else ~8d
     assert _lib.grad_blocking(65536, 768, 1) == (16384, 4)
     assert _lib.grad_blocking(262144, 1152, 1) == (8192, 32)
