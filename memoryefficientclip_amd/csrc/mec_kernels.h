@@ -204,7 +204,7 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_s
     const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
     float* __restrict__ ws, int tiles_m, int tiles_n) {
   using TL = FwdTile<T, VEC>;
-  static_assert(TL::FM == 2, "row reduction assumes 64-row wave sub-tiles");
+  static_assert(TL::FM % 2 == 0, "the row reduction takes 64-row halves of the wave sub-tile");
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
   __shared__ float s_rx[TL::BM], s_ry[TL::BN], s_row[TL::BM], s_col[TL::BN];
   const int64_t n64 = N;
@@ -236,10 +236,11 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_s
     sumexp_epilogue<TL, NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
   else
     sumexp_epilogue<TL, NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
-  const float rs = transpose_reduce32(rowv, lane);
-  {
+#pragma unroll
+  for (int h = 0; h < TL::FM / 2; ++h) {
+    const float rs = transpose_reduce32(*reinterpret_cast<float(*)[32]>(&rowv[32 * h]), lane);
     const int q = lane & 31;
-    const int ml = wm * TL::TM + (q >> 4) * 32 + acc_row(q & 15, lane);
+    const int ml = wm * TL::TM + h * 64 + (q >> 4) * 32 + acc_row(q & 15, lane);
     __hip_atomic_fetch_add(&s_row[ml], rs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   if (!LIT) {
