@@ -29,6 +29,23 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+// Compute units of the current device (cached per device).
+int compute_units(int* cus) {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(MEC_ERR_HIP, "hipGetDevice failed");
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) {
+    *cus = cache[dev];
+    return MEC_OK;
+  }
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1)
+    return fail(MEC_ERR_HIP, "hipDeviceGetAttribute(MultiprocessorCount) failed");
+  if (dev >= 0 && dev < 64) cache[dev] = v;
+  *cus = v;
+  return MEC_OK;
+}
+
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MEC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
@@ -367,9 +384,18 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
     })));
     return check_launch("sumexp (deterministic)");
   }
-  DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-      k_sumexp<T, LIT, NORM, VEC><<<grid, FwdTile<T, VEC>::NT, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, D,
-                                                                      c, workspace, tiles_m, tiles_n)))));
+  int cus = 0;
+  if (vec) {
+    rc = compute_units(&cus);
+    if (rc) return rc;
+  }
+  DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, {
+    // the chained (direct-to-LDS) tiles: one resident workgroup per slot
+    const int64_t slots = (int64_t)cus * Occ<T, VEC>::fwd;
+    if (FwdChain<T, VEC, NORM>::value && nwg > slots) grid.x = (unsigned)slots;
+    k_sumexp<T, LIT, NORM, VEC><<<grid, FwdTile<T, VEC>::NT, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, D,
+                                                                    c, workspace, tiles_m, tiles_n);
+  }))));
   return check_launch("sumexp");
 }
 

@@ -128,9 +128,13 @@ struct LoadPlan {
   int w;           // wave index (uniform)
   int kmax_a, kmax_b;
   int64_t lda;     // transposed A: bytes per k-row
+  static __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_a(const Operand& A) {
+    return G::TA ? make_rsrc_t<G::BM>(A) : make_rsrc<G::ESZ>(A);
+  }
+  static __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_b(const Operand& B) { return make_rsrc<G::ESZ>(B); }
   __device__ __forceinline__ void init(const Operand& A, const Operand& B) {
-    ra = G::TA ? make_rsrc_t<G::BM>(A) : make_rsrc<G::ESZ>(A);
-    rb = make_rsrc<G::ESZ>(B);
+    ra = rsrc_a(A);
+    rb = rsrc_b(B);
     kmax_a = A.kmax;
     kmax_b = B.kmax;
     lda = A.ld * 2;
@@ -398,9 +402,31 @@ __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G:
 // spread over the MFMAs of the step before.  Every iteration issues its
 // loads, also past the last chunk (they read zeros into a stage nobody reads
 // again), so the loop has no branches around them.
-template <class G, bool ZERO = true>
-__device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int K, char* lds,
-                                         f32x16 (&acc)[G::FM][G::FN]) {
+
+// Chunk 0 of a tile into stage 0: the loads before the first mainloop.
+template <class G>
+__device__ __forceinline__ void prologue(const Operand& A, const Operand& B, char* lds, LoadPlan<G>& lp) {
+  lp.init(A, B);
+  static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, lds); });
+}
+
+// The k-loop of one tile whose chunk 0 was issued into stage p0 (chunk kt
+// lives in stage (kt + p0) & 1).  With CHAIN and has_next, the last chunk's
+// loads, which would otherwise read zeros past the end, fetch chunk 0 of the
+// next tile instead: only the buffer descriptors differ between tiles of one
+// launch (the per-lane offsets depend on the leading dimensions alone).  lp
+// then describes the next tile and p0 names the stage its chunk 0 goes to;
+// those loads are still in flight on return, and the caller keeps the ring
+// untouched (and waits with wait_barrier, not __syncthreads) until the next
+// call.  hook() runs once, after the first chunk's barrier: work issued there
+// (the previous tile's global stores) is not waited for by that barrier.
+struct NoHook {
+  __device__ __forceinline__ void operator()() const {}
+};
+template <class G, bool ZERO, bool CHAIN, class Hook = NoHook>
+__device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_rsrc_t ra_next,
+                                              __amdgpu_buffer_rsrc_t rb_next, bool has_next, int K, char* lds,
+                                              int& p0, f32x16 (&acc)[G::FM][G::FN], const Hook& hook = Hook()) {
   static_assert(G::S == 2 && G::NS == 4, "two stages, four k-steps per chunk");
   if constexpr (ZERO) {
 #pragma unroll
@@ -414,23 +440,28 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
   constexpr int L1 = G::IPW / 2, L2 = G::IPW;  // loads issued in k-steps 0 and 1
   static_assert(G::IPW % 2 == 0, "even load split");
   const int nk = (K + BK - 1) / BK;
-  LoadPlan<G> lp;
-  lp.init(A, B);
-  static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, lds); });
   Frags<G> f0, f1;
   for (int kt = 0; kt < nk; ++kt) {
     wait_barrier<0>();  // chunk kt landed; every wave is done with the other stage
     lgkm_wait<0>(f1);   // f1 (the last step of chunk kt-1) landed before its MFMAs
     sched_fence();
-    char* cs = lds + (kt & 1) * G::STAGE;
-    char* ns = lds + ((kt & 1) ^ 1) * G::STAGE;
-    const int k1 = (kt + 1) * BK;
+    char* cs = lds + ((kt + p0) & 1) * G::STAGE;
+    char* ns = lds + ((kt + p0 + 1) & 1) * G::STAGE;
+    int k1 = (kt + 1) * BK;
+    if constexpr (CHAIN) {
+      if (kt + 1 == nk && has_next) {
+        lp.ra = ra_next;
+        lp.rb = rb_next;
+        k1 = 0;
+      }
+    }
     const FragReader<G> r0(cs, 0), r1(cs, 1), r2(cs, 2), r3(cs, 3);
     if (kt > 0) {
       mfma_step_rd<G, 0, L1>(f1, acc, lp, k1, ns, r0, f0);
     } else {
       read_frags<G>(cs, 0, f0);
       static_for<L1>([&](auto i) { lp.template issue<i>(k1, ns); });
+      hook();
     }
     lgkm_wait<0>(f0);
     sched_fence();
@@ -446,8 +477,25 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
   lgkm_wait<0>(f1);
   sched_fence();
   mfma_step<G, 0, 0>(f1, acc, lp, 0, lds);
-  // the zero loads past the last chunk land before the caller reuses the ring
+  if constexpr (CHAIN) p0 = (p0 + nk) & 1;
+}
+
+// every outstanding global->LDS load landed (before the ring is reused for
+// anything else, and before the workgroup ends)
+__device__ __forceinline__ void drain_loads() {
   __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));
+}
+
+// One tile: chunk 0 into stage 0, the k-loop, and the zero loads past the
+// last chunk awaited before the caller reuses the ring.
+template <class G, bool ZERO = true>
+__device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int K, char* lds,
+                                         f32x16 (&acc)[G::FM][G::FN]) {
+  LoadPlan<G> lp;
+  prologue<G>(A, B, lds, lp);
+  int p0 = 0;
+  mainloop_core<G, ZERO, false>(lp, lp.ra, lp.rb, false, K, lds, p0, acc);
+  drain_loads();
 }
 
 }  // namespace gdma

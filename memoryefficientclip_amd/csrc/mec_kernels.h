@@ -46,6 +46,7 @@ struct TileF32 {
   static constexpr bool TA = false;
   static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2, WM = 2, WN = 2, NT = 256;
   static constexpr int LDS_BYTES = g32::LDS_FLOATS * 4;
+  static constexpr bool CHAIN = false;
   template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
     g32::mainloop<VECA, VECB>(a, b, K, (float*)lds, acc);
@@ -76,6 +77,7 @@ struct Tile16V : Pack16<F16> {
   static constexpr bool TA = false;
   static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2, WM = 2, WN = 2, NT = 256;
   static constexpr int LDS_BYTES = g16::Cfg<MEC_16BIT_BK>::LDS_ELEMS * 2;
+  static constexpr bool CHAIN = false;
   template <bool VECA, bool VECB>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
     g16::mainloop<MEC_16BIT_BK, VECA, VECB, F16>(a, b, K, (uint16_t*)lds, acc);
@@ -104,9 +106,23 @@ struct TileD : PackOf<KIND>::type {
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
   static constexpr int LDS_BYTES = G::LDS_BYTES;
+  static constexpr bool CHAIN = true;
   template <bool VECA, bool VECB, bool ZERO = true>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
     gdma::mainloop<G, ZERO>(a, b, K, (char*)lds, acc);
+  }
+  // Tiles in a chain (a persistent workgroup): start() issues the first
+  // tile's chunk 0; chain() runs one tile and, with has_next, leaves chunk 0
+  // of the tile (an, bn) in flight for the next call.
+  using Plan = gdma::LoadPlan<G>;
+  static __device__ __forceinline__ void start(const Op& a, const Op& b, void* lds, Plan& lp) {
+    gdma::prologue<G>(a, b, (char*)lds, lp);
+  }
+  template <class Hook>
+  static __device__ __forceinline__ void chain(Plan& lp, const Op& an, const Op& bn, bool has_next, int K, void* lds,
+                                               int& p0, f32x16 (&acc)[FM][FN], const Hook& hook) {
+    gdma::mainloop_core<G, true, true>(lp, Plan::rsrc_a(an), Plan::rsrc_b(bn), has_next, K, (char*)lds, p0, acc,
+                                       hook);
   }
 };
 
@@ -199,34 +215,32 @@ __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::
   }
 }
 
-template <typename T, bool LIT, bool NORM, bool VEC>
-__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_sumexp(
-    const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
-    float* __restrict__ ws, int tiles_m, int tiles_n) {
-  using TL = FwdTile<T, VEC>;
-  static_assert(TL::FM % 2 == 0, "the row reduction takes 64-row halves of the wave sub-tile");
-  __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
-  __shared__ float s_rx[TL::BM], s_ry[TL::BN], s_row[TL::BM], s_col[TL::BN];
-  const int64_t n64 = N;
-  int tm, tn;
-  tile_swizzle(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
-  const int m0 = tm * TL::BM, n0 = tn * TL::BN;
+// Workgroup barrier for the epilogues' own LDS arrays: their LDS operations
+// complete (lgkmcnt), then s_barrier.  __syncthreads() would also wait for the
+// next tile's global->LDS loads in flight into the ring.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// Row and column sums of E over one tile: thread t gets the sums of row m0 + t
+// (rs) and column n0 + t (cs), which sums_flush adds into ws.  rxv / ryv:
+// 1/|x| of row m0 + t and 1/|y| of column n0 + t (NORM).
+template <class TL, bool LIT, bool NORM>
+__device__ __forceinline__ void sumexp_tile(const f32x16 (&acc)[TL::FM][TL::FN], float c, int m0, int n0, int N,
+                                            float rxv, float ryv, float* s_rx, float* s_ry, float* s_row,
+                                            float* s_col, float& rs_out, float& cs_out) {
+  static_assert(TL::NT >= TL::BM && TL::NT >= TL::BN, "one row and one column per thread");
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / TL::WN, wn = w % TL::WN;
-
-  const auto A = tile_op<TL>(X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax);
-  const auto B = tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax);
-  f32x16 acc[TL::FM][TL::FN];
-  TL::template run<VEC, VEC>(A, B, D, lds, acc);
-
-  for (int u = t; u < TL::BM; u += TL::NT) {
-    s_rx[u] = (NORM && m0 + u < N) ? ws[WS_RX * n64 + m0 + u] : 1.f;
-    s_row[u] = 0.f;
+  if (t < TL::BM) {
+    s_rx[t] = rxv;
+    s_row[t] = 0.f;
   }
-  for (int u = t; u < TL::BN; u += TL::NT) {
-    s_ry[u] = (NORM && n0 + u < N) ? ws[WS_RY * n64 + n0 + u] : 1.f;
-    s_col[u] = 0.f;
+  if (t < TL::BN) {
+    s_ry[t] = ryv;
+    s_col[t] = 0.f;
   }
-  __syncthreads();
+  lds_barrier();
 
   float rowv[TL::FM * 16];
   float colv[TL::FN];
@@ -252,15 +266,95 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_s
                                __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
-  __syncthreads();
-  for (int u = t; u < TL::BM; u += TL::NT)
-    if (m0 + u < N)
-      __hip_atomic_fetch_add(&ws[WS_ROW_OFF * n64 + m0 + u], s_row[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (!LIT) {
-    for (int u = t; u < TL::BN; u += TL::NT)
-      if (n0 + u < N)
-        __hip_atomic_fetch_add(&ws[WS_COL_OFF * n64 + n0 + u], s_col[u], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+  lds_barrier();
+  rs_out = t < TL::BM ? s_row[t] : 0.f;
+  cs_out = (!LIT && t < TL::BN) ? s_col[t] : 0.f;
+}
+template <class TL, bool LIT>
+__device__ __forceinline__ void sums_flush(float* __restrict__ ws, int m0, int n0, int N, float rs, float cs) {
+  const int64_t n64 = N;
+  const int t = threadIdx.x;
+  if (t < TL::BM && m0 + t < N)
+    __hip_atomic_fetch_add(&ws[WS_ROW_OFF * n64 + m0 + t], rs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (!LIT && t < TL::BN && n0 + t < N)
+    __hip_atomic_fetch_add(&ws[WS_COL_OFF * n64 + n0 + t], cs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Forward tiles that chain (FwdChain): the 16-bit direct-to-LDS tiles
+// without the norm scaling.  Measured: the 16-bit forward (one workgroup per
+// CU, nothing else to overlap its epilogue) is 7% faster chained; fp32 (two
+// workgroups per CU, one's epilogue already overlaps the other's k-loop) was
+// 4% slower; the normalized 16-bit epilogue spills registers in the loop.
+template <typename T, bool VEC, bool NORM> struct FwdChain {
+  static constexpr bool value = FwdTile<T, VEC>::CHAIN && Is16<T>::value && !NORM;
+};
+
+// Forward sums.  Tiles t = blockIdx.x + i * gridDim.x of the tiles_m x
+// tiles_n grid (XCD-grouped order).  Chained tiles: a workgroup stays
+// resident (the launch covers the CUs once) and the last chunk of each
+// tile's k-loop loads chunk 0 of its next tile, which lands during the
+// epilogue; each tile's sums go to ws after the next tile's first barrier, so
+// that barrier does not wait for them.  Otherwise one tile per workgroup.
+template <typename T, bool LIT, bool NORM, bool VEC>
+__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_sumexp(
+    const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
+    float* __restrict__ ws, int tiles_m, int tiles_n) {
+  using TL = FwdTile<T, VEC>;
+  static_assert(TL::FM % 2 == 0, "the row reduction takes 64-row halves of the wave sub-tile");
+  __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
+  __shared__ float s_rx[TL::BM], s_ry[TL::BN], s_row[TL::BM], s_col[TL::BN];
+  const int64_t n64 = N;
+  const int ntiles = tiles_m * tiles_n;
+  const int t = threadIdx.x;
+  auto coords = [&](int tile, int& m0, int& n0) {
+    int tm, tn;
+    tile_swizzle(tile, ntiles, tiles_m, tiles_n, 8, tm, tn);
+    m0 = tm * TL::BM;
+    n0 = tn * TL::BN;
+  };
+  auto op_a = [&](int m0) { return tile_op<TL>(X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax); };
+  auto op_b = [&](int n0) { return tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax); };
+  auto rx_of = [&](int m0) { return (NORM && t < TL::BM && m0 + t < N) ? ws[WS_RX * n64 + m0 + t] : 1.f; };
+  auto ry_of = [&](int n0) { return (NORM && t < TL::BN && n0 + t < N) ? ws[WS_RY * n64 + n0 + t] : 1.f; };
+  f32x16 acc[TL::FM][TL::FN];
+  int tile = blockIdx.x, m0, n0;
+  coords(tile, m0, n0);
+  if constexpr (FwdChain<T, VEC, NORM>::value) {
+    typename TL::Plan lp;
+    float rxv = rx_of(m0), ryv = ry_of(n0);
+    TL::start(op_a(m0), op_b(n0), lds, lp);
+    int p0 = 0;
+    bool pending = false;  // sums of the previous tile (pm0, pn0) not yet in ws
+    int pm0 = 0, pn0 = 0;
+    float prs = 0.f, pcs = 0.f;
+    for (;;) {
+      const int next = tile + (int)gridDim.x;
+      const bool has_next = next < ntiles;
+      int m1 = m0, n1 = n0;
+      if (has_next) coords(next, m1, n1);
+      TL::chain(lp, op_a(m1), op_b(n1), has_next, D, lds, p0, acc, [&] {
+        if (pending) sums_flush<TL, LIT>(ws, pm0, pn0, N, prs, pcs);
+      });
+      // the next tile's norms, needed after its k-loop
+      const float rxn = has_next ? rx_of(m1) : 1.f, ryn = has_next ? ry_of(n1) : 1.f;
+      sumexp_tile<TL, LIT, NORM>(acc, c, m0, n0, N, rxv, ryv, s_rx, s_ry, s_row, s_col, prs, pcs);
+      pending = true;
+      pm0 = m0;
+      pn0 = n0;
+      if (!has_next) break;
+      tile = next;
+      m0 = m1;
+      n0 = n1;
+      rxv = rxn;
+      ryv = ryn;
+    }
+    sums_flush<TL, LIT>(ws, pm0, pn0, N, prs, pcs);
+    gdma::drain_loads();
+  } else {
+    TL::template run<VEC, VEC>(op_a(m0), op_b(n0), D, lds, acc);
+    float rs, cs;
+    sumexp_tile<TL, LIT, NORM>(acc, c, m0, n0, N, rx_of(m0), ry_of(n0), s_rx, s_ry, s_row, s_col, rs, cs);
+    sums_flush<TL, LIT>(ws, m0, n0, N, rs, cs);
   }
 }
 
