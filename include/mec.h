@@ -121,7 +121,8 @@ int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype);
 /* Bytes of gradient scratch needed by mec_grad / mec_grad_step /
  * mec_backward for (n, d, dtype), all in the input dtype: two buffers holding
  * one block diagonal of the off-diagonal gradient matrix each (nb blocks of
- * bs x bs; bs ~ 2d for fp32, ~8d but at most 32512 for the other dtypes),
+ * bs x bs; bs ~ 4d for fp32; ~8d for the other dtypes, ~16d when n >= 8192
+ * and 8d would give fewer than 16 blocks, at most 32512 rows),
  * for fp32 the same blocks transposed as well, and transposed normalised
  * copies of x and y ([d][n rounded up to 128]); O(n*d) in total.  The
  * fp32-data modes keep these in bf16; MEC_DTYPE_F32_BF16X3 holds hi and lo
