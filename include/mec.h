@@ -41,8 +41,10 @@
  *     MEC_FLAG_DETERMINISTIC.  Every function accepts the flag; only the
  *     forward sums (mec_sumexp, mec_forward) depend on it.
  *   - All work is enqueued on `stream` (a hipStream_t; NULL = default
- *     stream).  No function synchronises the host and none allocates device
- *     memory: the workspace and the gradient scratch are caller-owned.
+ *     stream), which must belong to the current HIP device (the device of
+ *     the data; the forward sizes its persistent launches by that device's
+ *     compute units).  No function synchronises the host and none allocates
+ *     device memory: the workspace and the gradient scratch are caller-owned.
  *   - Argument validation is pure host code; invalid arguments are reported
  *     before anything touches the GPU.
  */
