@@ -137,7 +137,9 @@ __global__ __launch_bounds__(1024) void k_finalize_sum(int N, int nparts, const 
 //            = r_i d_own^_i                                           (if ||own_i|| <= eps)
 //   out_i    = grad_output * d_own_i                                 (clip_loss.py:252-254)
 // out may alias acc (fp32 outputs): every element is read before it is written
-// by the same lane.
+// by the same lane.  One wave per row; rows of D <= 64 * POST_REG are read
+// once (held in registers across the reduction), longer rows twice.
+constexpr int POST_REG = 32;
 template <typename T, bool NORM>
 __global__ __launch_bounds__(256) void k_postpass(const T* __restrict__ own, int64_t ld_own,
                                                   const T* __restrict__ oth, int64_t ld_oth, int N, int D,
@@ -157,12 +159,34 @@ __global__ __launch_bounds__(256) void k_postpass(const T* __restrict__ own, int
   const float go = grad_output ? *grad_output : 1.f;
   if (NORM) {
     float dot = 0.f;
+    const bool clamped = ro >= 1e12f;
+    if (D <= 64 * POST_REG) {
+      // the row stays in registers between the reduction and the stores
+      float g[POST_REG], xr[POST_REG];
+#pragma unroll
+      for (int k = 0; k < POST_REG; ++k) {
+        const int d = lane + 64 * k;
+        g[k] = 0.f;
+        xr[k] = 0.f;
+        if (d < D) {
+          g[k] = a * fmaf(kq, Elem<T>::load(yo, d), ac[d]);
+          xr[k] = Elem<T>::load(xo, d) * ro;
+          dot = fmaf(xr[k], g[k], dot);
+        }
+      }
+      dot = wave_sum(dot);
+#pragma unroll
+      for (int k = 0; k < POST_REG; ++k) {
+        const int d = lane + 64 * k;
+        if (d < D) Elem<T>::store(o, d, go * (clamped ? ro * g[k] : ro * (g[k] - xr[k] * dot)));
+      }
+      return;
+    }
     for (int d = lane; d < D; d += 64) {
       float g = a * fmaf(kq, Elem<T>::load(yo, d), ac[d]);
       dot = fmaf(Elem<T>::load(xo, d) * ro, g, dot);
     }
     dot = wave_sum(dot);
-    const bool clamped = ro >= 1e12f;
     for (int d = lane; d < D; d += 64) {
       float g = a * fmaf(kq, Elem<T>::load(yo, d), ac[d]);
       float v = clamped ? ro * g : ro * (g - Elem<T>::load(xo, d) * ro * dot);
