@@ -1,6 +1,7 @@
 // C-ABI entry points (include/mec.h): argument validation in plain host code,
 // then stream-ordered kernel launches.  Nothing here allocates device memory
 // or synchronises the host.
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -29,19 +30,24 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; callers on any
+// thread may fill the cache, always with the same value).
 int compute_units(int* cus) {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(MEC_ERR_HIP, "hipGetDevice failed");
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) {
-    *cus = cache[dev];
-    return MEC_OK;
+  const bool cached = dev >= 0 && dev < 64;
+  if (cached) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) {
+      *cus = v;
+      return MEC_OK;
+    }
   }
   int v = 0;
   if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1)
     return fail(MEC_ERR_HIP, "hipDeviceGetAttribute(MultiprocessorCount) failed");
-  if (dev >= 0 && dev < 64) cache[dev] = v;
+  if (cached) cache[dev].store(v, std::memory_order_relaxed);
   *cus = v;
   return MEC_OK;
 }
