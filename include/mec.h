@@ -32,9 +32,12 @@
  *   - dtype: MEC_DTYPE_F32 (float), MEC_DTYPE_BF16 (uint16 bfloat16 bits),
  *     MEC_DTYPE_F16 (uint16 IEEE binary16 bits), or float data with products
  *     formed from bf16 terms: MEC_DTYPE_F32_BF16X3, MEC_DTYPE_F32_BF16 (below).  All arithmetic
- *     accumulates in fp32; the loss is reduced in fp64.  Sizes: 1 <= d <= 2^20;
- *     1 <= n <= 2^30 for fp32 and n <= 2^22 for the other dtypes
- *     (MEC_ERR_UNSUPPORTED beyond).  16-bit rows that are 16-byte aligned (x, y
+ *     accumulates in fp32; the loss is reduced in fp64.  Sizes: 1 <= d <= 2^20
+ *     (MEC_ERR_INVALID beyond) and 1 <= n <= 2^22 for every dtype
+ *     (MEC_ERR_UNSUPPORTED beyond, returned before any launch).  Memory
+ *     bounds n further: the caller holds the inputs, the workspace, two fp32
+ *     n x d accumulators and the gradient scratch (mec_grad_scratch_bytes;
+ *     about 54 GB at n = 2^21, d = 1152, fp32).  16-bit rows that are 16-byte aligned (x, y
  *     16-byte aligned, d, ldx, ldy multiples of 8) use the direct-to-LDS
  *     tiles; other layouts are supported at lower speed.
  *   - mode: MEC_MODE_CLIP or MEC_MODE_LIT, optionally OR
@@ -109,8 +112,11 @@ const char* mec_version(void);
  * of partial sums (the deterministic forward, MEC_FLAG_DETERMINISTIC).  The
  * workspace must be 8-byte aligned.  The same workspace must be passed to
  * mec_forward and the matching mec_backward (it replaces
- * ctx.save_for_backward of the sums, clip_loss.py:199).  For every dtype
- * except MEC_DTYPE_F32_BF16X3. */
+ * ctx.save_for_backward of the sums, clip_loss.py:199).  Enough for
+ * MEC_DTYPE_F32, MEC_DTYPE_BF16 and MEC_DTYPE_F16 only: the two bf16-product
+ * dtypes (MEC_DTYPE_F32_BF16X3, MEC_DTYPE_F32_BF16) keep bf16 copies of x and
+ * y in the workspace as well and need mec_workspace_floats_for(n, d, dtype),
+ * which is correct for every dtype.  Returns < 0 for n outside [1, 2^22]. */
 int64_t mec_workspace_floats(int64_t n);
 
 /* Number of floats of the workspace for (n, d, dtype): mec_workspace_floats(n)
@@ -121,15 +127,20 @@ int64_t mec_workspace_floats(int64_t n);
 int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype);
 
 /* Bytes of gradient scratch needed by mec_grad / mec_grad_step /
- * mec_backward for (n, d, dtype), all in the input dtype: two buffers holding
- * one block diagonal of the off-diagonal gradient matrix each (nb blocks of
- * bs x bs; bs ~ 4d for fp32; ~8d for the other dtypes, ~16d when n >= 8192
- * and 8d would give fewer than 16 blocks, at most 32512 rows),
- * for fp32 the same blocks transposed as well, and transposed normalised
- * copies of x and y ([d][n rounded up to 128]); O(n*d) in total.  The
- * fp32-data modes keep these in bf16; MEC_DTYPE_F32_BF16X3 holds hi and lo
- * planes of the transposed blocks and of the transposed copies.  Returns < 0
- * on bad args. */
+ * mec_backward for (n, d, dtype), all in the input dtype:
+ *   - the gradient-matrix buffers: two buffers holding one block diagonal of
+ *     the off-diagonal gradient matrix each (nb blocks of bs x bs), for fp32
+ *     the same blocks transposed as well (4 copies; bf16x3: hi and lo planes,
+ *     4 copies; the other dtypes 2 copies);
+ *   - transposed normalised copies of x and y ([d][n rounded up to 128];
+ *     bf16x3: hi and lo planes of each).
+ * bs targets ~4d rows for fp32 and ~8d for the other dtypes (~16d when
+ * n >= 8192 and 8d would give fewer than 16 blocks; at most 32512 rows), and
+ * is shortened until the gradient-matrix buffers fit the smaller of 16 GiB
+ * and the bytes of a dense fp32 n x n logit matrix (n^2 x 4), but not below
+ * 1024 rows.  The total is therefore about copies x n x bs x elem +
+ * 2 x d x n x elem: O(n*d).  The fp32-data modes keep these in bf16.
+ * Returns < 0 on bad args or n outside [1, 2^22]. */
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype);
 
 /* Block decomposition of the backward for (n, d, dtype): the n x n gradient
@@ -189,8 +200,12 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
  * times *grad_output (device fp32 scalar, NULL = 1), cast to dtype.
  * grad_scale is 1/T for the standard loss and sqrt(n/T) for the Stable
  * variants (clip_loss.py:182, :299).  dx/dy are row-major [n, d] (row
- * stride d) and may alias acc_x/acc_y when dtype is F32.  A side is skipped
- * when both its accumulator and its output are NULL (LiT: always y). */
+ * stride d) and may alias acc_x/acc_y when the data are fp32, i.e. for
+ * MEC_DTYPE_F32, MEC_DTYPE_F32_BF16X3 and MEC_DTYPE_F32_BF16 (one wave
+ * handles a row and reads each accumulator element before it writes that
+ * element of the output).  A
+ * side is skipped when both its accumulator and its output are NULL (LiT:
+ * always y). */
 int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                  int dtype, int mode, int normalize, float grad_scale, const float* workspace,
                  const float* grad_output, const float* acc_x, const float* acc_y, void* dx,

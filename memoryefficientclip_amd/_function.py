@@ -66,6 +66,18 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def refuse_graph_capture() -> None:
+    """Raise instead of enqueueing work into a CUDA/HIP graph capture.
+
+    Capturing a step that calls this loss ended in a host segmentation fault
+    inside ``torch.cuda.graph``'s ``capture_end`` on the MI355X box, with no
+    cause found in this library's launches; a clear error is better than a
+    crashed training process."""
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("MemoryEfficientCLIP: the fused loss does not support CUDA/HIP graph capture; "
+                           "call it outside the captured region")
+
+
 def compute_dtype(dtype: torch.dtype) -> int:
     """C-ABI dtype code for inputs of `dtype` under the current
     ``torch.get_float32_matmul_precision()`` (fp32 only: "high" selects the
@@ -83,6 +95,7 @@ def compute_dtype(dtype: torch.dtype) -> int:
 def forward(ctx, x: torch.Tensor, y: torch.Tensor, temperature: float, mode: int, normalize: bool,
             stable: bool) -> torch.Tensor:
     check_inputs(x, y)
+    refuse_graph_capture()
     temperature = float(temperature)
     if not (temperature > 0.0 and math.isfinite(temperature)):
         raise ValueError(f"temperature must be finite and > 0, got {temperature}")
@@ -107,6 +120,7 @@ def forward(ctx, x: torch.Tensor, y: torch.Tensor, temperature: float, mode: int
 
 def backward(ctx, grad_output: torch.Tensor, need_x: bool, need_y: bool):
     """Returns (dx, dy); a side that is not needed comes back as None."""
+    refuse_graph_capture()
     x, y, ws = ctx.saved_tensors
     ldx, ldy, n, d, dt, mode, normalize, temperature, grad_scale = ctx.mec
     if mode == _lib.MODE_LIT:

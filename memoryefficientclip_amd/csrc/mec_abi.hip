@@ -58,11 +58,12 @@ int check_launch(const char* what) {
   return MEC_OK;
 }
 
-constexpr int64_t kMaxN = int64_t(1) << 30;
+// Largest supported n, every dtype.  The 16-bit contractions address a
+// 256-row panel of the transposed inputs ([d][ldt], ldt ~ n) with 32-bit
+// buffer offsets, and the forward's grid of 128 x 128 fp32 tiles,
+// (n / 128)^2 = 2^30 workgroups at this n, stays below 2^31.
+constexpr int64_t kMaxN = int64_t(1) << 22;
 constexpr int64_t kMaxD = int64_t(1) << 20;
-// the 16-bit contractions address a 256-row panel of the transposed inputs
-// ([d][ldt], ldt ~ n) with 32-bit buffer offsets
-constexpr int64_t kMaxN16 = int64_t(1) << 22;
 
 bool known_dtype(int dtype) {
   return dtype == MEC_DTYPE_F32 || dtype == MEC_DTYPE_BF16 || dtype == MEC_DTYPE_F16 ||
@@ -80,15 +81,14 @@ int data_dtype(int dtype) { return is_split(dtype) ? MEC_DTYPE_F32 : dtype; }
 
 int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                  int dtype) {
-  if (n < 1 || n > kMaxN) return fail(MEC_ERR_INVALID, "n=%lld out of range [1, 2^30]", (long long)n);
+  if (n < 1) return fail(MEC_ERR_INVALID, "n=%lld must be >= 1", (long long)n);
+  if (n > kMaxN) return fail(MEC_ERR_UNSUPPORTED, "n=%lld exceeds the supported maximum 2^22", (long long)n);
   if (d < 1 || d > kMaxD) return fail(MEC_ERR_INVALID, "d=%lld out of range [1, 2^20]", (long long)d);
   if (ldx < d || ldy < d)
     return fail(MEC_ERR_INVALID, "row strides ldx=%lld ldy=%lld must be >= d=%lld", (long long)ldx,
                 (long long)ldy, (long long)d);
   if (!known_dtype(dtype)) return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
   if (x == nullptr || y == nullptr) return fail(MEC_ERR_INVALID, "x and y must be non-null");
-  if (dtype != MEC_DTYPE_F32 && n > kMaxN16)
-    return fail(MEC_ERR_UNSUPPORTED, "dtypes other than fp32 support n <= 2^22 (n=%lld)", (long long)n);
   return MEC_OK;
 }
 
@@ -179,16 +179,49 @@ bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, i
 // An exact divisor of the quantum count within a factor of two of the
 // target is preferred (no short last block, whose contractions would have a
 // short K); otherwise the quanta are balanced over the blocks.
-void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
+//
+// Memory bound: the gradient-matrix buffers (copies x nb x bs^2 elements,
+// about copies x n x bs) are kept within `gbudget` bytes by shortening the
+// blocks, down to a floor of 1024 rows, which wins over the budget (below
+// it the pipeline's launches and accumulator updates dominate).
+constexpr int64_t kFloorRows = 1024;
+int g_copies(int dtype) { return (dtype == MEC_DTYPE_F32 || is_x3(dtype)) ? 4 : 2; }
+int64_t g_elem(int dtype) { return dtype == MEC_DTYPE_F32 ? 4 : 2; }
+// bytes of the gradient-matrix buffers for blocks of tb quanta
+int64_t g_bytes(int64_t tiles, int64_t q, int64_t tb, int dtype) {
+  const int64_t nb = (tiles + tb - 1) / tb, bs = tb * q;
+  return (int64_t)g_copies(dtype) * nb * bs * bs * g_elem(dtype);
+}
+// Default budget of the gradient-matrix buffers: the bytes of a dense fp32
+// n x n logit matrix (what the memory-efficient path exists to avoid), and
+// at most 16 GiB.  Neither binds at the benchmark shapes.
+constexpr int64_t kGradBudgetCap = int64_t(16) << 30;
+int64_t default_gbudget(int64_t n) {
+  const int64_t dense = n * n * 4;
+  return dense < kGradBudgetCap ? dense : kGradBudgetCap;
+}
+void grad_blocks_budget(int64_t n, int64_t d, int dtype, int64_t gbudget, int* bs, int* nb) {
   const int64_t q = block_quantum(dtype);
   const int64_t tiles = (n + q - 1) / q;
+  const int64_t floor_tb = (kFloorRows + q - 1) / q;
   // 16-bit: a transposed gradient-matrix block is a direct-to-LDS operand
   // ((bs - 1) * bs + 256 elements within dma_max_elems): bs <= 127 * 256
-  const int64_t cap = dtype == MEC_DTYPE_F32 ? tiles : 127;
+  int64_t cap = dtype == MEC_DTYPE_F32 ? tiles : 127;
+  // the largest block within the budget (never below the floor)
+  {
+    // g_bytes(tb) >= copies * tiles * tb * q^2 * elem bounds tb from above; the
+    // rounding of the last block is then settled by a short walk down
+    const int64_t per_tb = (int64_t)g_copies(dtype) * tiles * q * q * g_elem(dtype);
+    int64_t tb = cap < tiles ? cap : tiles;
+    if (gbudget / per_tb < tb) tb = gbudget / per_tb;
+    if (tb < floor_tb) tb = floor_tb;
+    while (tb > floor_tb && g_bytes(tiles, q, tb, dtype) > gbudget) --tb;
+    cap = tb;
+  }
   int64_t mult = dtype == MEC_DTYPE_F32 ? 4 : 8;
   if (dtype != MEC_DTYPE_F32 && n >= 8192 && n < 16 * 8 * d) mult = 16;
   int64_t target = (mult * d + q - 1) / q;
-  if (target < 1024 / q) target = 1024 / q;
+  if (target < floor_tb) target = floor_tb;
   if (const char* env = std::getenv("MEC_GRAD_BLOCK_TILES")) {
     long v = std::strtol(env, nullptr, 10);
     if (v >= 1 && v <= 4096) target = v;
@@ -212,8 +245,13 @@ void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
       tb = (tiles + nbv - 1) / nbv;
     }
   }
+  // balanced blocks may round past the budget: shorten them (not below the floor)
+  while (tb > 1 && tb > floor_tb && g_bytes(tiles, q, tb, dtype) > gbudget) --tb;
   *bs = (int)(tb * q);
   *nb = (int)((tiles + tb - 1) / tb);
+}
+void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
+  grad_blocks_budget(n, d, dtype, default_gbudget(n), bs, nb);
 }
 
 // Scratch layout of the backward (element type = input dtype; split modes: bf16):
@@ -231,17 +269,27 @@ struct ScratchLayout {
   int64_t ldt, gbuf, tbuf, total;  // bytes except ldt (elements)
 };
 
-ScratchLayout scratch_layout(int64_t n, int64_t d, int dtype) {
+// transposed-input bytes of the scratch
+int64_t trans_bytes(int64_t n, int64_t d, int dtype) {
+  return (is_x3(dtype) ? 4 : 2) * d * ((n + 127) / 128 * 128) * g_elem(dtype);
+}
+ScratchLayout scratch_layout_blocks(int64_t n, int64_t d, int dtype, int bs, int nb) {
   ScratchLayout L;
-  grad_blocks(n, d, dtype, &L.bs, &L.nb);
-  const int64_t elem = dtype == MEC_DTYPE_F32 ? 4 : 2;
+  L.bs = bs;
+  L.nb = nb;
+  const int64_t elem = g_elem(dtype);
   L.ldt = (n + 127) / 128 * 128;
   L.gbuf = (int64_t)L.nb * L.bs * L.bs * elem;
   L.tbuf = d * L.ldt * elem;
-  L.ncopies = (dtype == MEC_DTYPE_F32 || is_x3(dtype)) ? 4 : 2;
+  L.ncopies = g_copies(dtype);
   L.ntrans = is_x3(dtype) ? 4 : 2;
   L.total = L.ncopies * L.gbuf + L.ntrans * L.tbuf;
   return L;
+}
+ScratchLayout scratch_layout(int64_t n, int64_t d, int dtype) {
+  int bs, nb;
+  grad_blocks(n, d, dtype, &bs, &nb);
+  return scratch_layout_blocks(n, d, dtype, bs, nb);
 }
 
 int64_t scratch_bytes_for(int64_t n, int64_t d, int dtype) { return scratch_layout(n, d, dtype).total; }
@@ -407,7 +455,8 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
 
 int mec_finalize(int64_t n, int mode, float temperature, float* workspace, float* loss, void* stream) {
   g_err.clear();
-  if (n < 1 || n > kMaxN) return fail(MEC_ERR_INVALID, "n=%lld out of range", (long long)n);
+  if (n < 1) return fail(MEC_ERR_INVALID, "n=%lld must be >= 1", (long long)n);
+  if (n > kMaxN) return fail(MEC_ERR_UNSUPPORTED, "n=%lld exceeds the supported maximum 2^22", (long long)n);
   int rc = check_mode(mode);
   if (!rc) rc = check_temperature(temperature);
   if (rc) return rc;
@@ -444,7 +493,8 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
 
 int mec_grad_blocking(int64_t n, int64_t d, int dtype, int64_t* block_rows, int64_t* num_blocks) {
   g_err.clear();
-  if (n < 1 || n > kMaxN || d < 1 || d > kMaxD) return fail(MEC_ERR_INVALID, "n or d out of range");
+  if (n < 1 || d < 1 || d > kMaxD) return fail(MEC_ERR_INVALID, "n or d out of range");
+  if (n > kMaxN) return fail(MEC_ERR_UNSUPPORTED, "n=%lld exceeds the supported maximum 2^22", (long long)n);
   if (!known_dtype(dtype)) return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
   if (!block_rows || !num_blocks) return fail(MEC_ERR_INVALID, "block_rows and num_blocks must be non-null");
   int bs, nb;
@@ -454,32 +504,55 @@ int mec_grad_blocking(int64_t n, int64_t d, int dtype, int64_t* block_rows, int6
   return MEC_OK;
 }
 
-int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
-                  int mode, int normalize, float temperature, const float* workspace, int64_t step, void* scratch,
-                  int64_t scratch_bytes, float* acc_x, float* acc_y, void* stream) {
-  g_err.clear();
-  int rc = check_common(x, ldx, y, ldy, n, d, dtype);
-  if (!rc) rc = check_mode(mode);
-  if (!rc) rc = check_temperature(temperature);
+// Arguments of one backward pipeline step, checked by the entry points.
+struct StepArgs {
+  const void* x;
+  int64_t ldx;
+  const void* y;
+  int64_t ldy;
+  int64_t n, d;
+  int dtype, mode, normalize;
+  float temperature;
+  const float* workspace;
+  float* acc_x;  // null: side skipped (LiT: acc_y always null)
+  float* acc_y;
+};
+
+// Validation shared by mec_grad_step, mec_grad and mec_backward_noalloc:
+// problem, mode, temperature, workspace and at least one accumulator (LiT
+// drops acc_y).
+static int check_step_args(StepArgs& a) {
+  int rc = check_common(a.x, a.ldx, a.y, a.ldy, a.n, a.d, a.dtype);
+  if (!rc) rc = check_mode(a.mode);
+  if (!rc) rc = check_temperature(a.temperature);
   if (rc) return rc;
+  const bool lit = is_lit(a.mode);
+  if (lit) a.acc_y = nullptr;
+  if (!a.workspace) return fail(MEC_ERR_INVALID, "workspace must be non-null");
+  if (!a.acc_x && !a.acc_y)
+    return fail(MEC_ERR_INVALID, "no gradient requested (acc_x%s null)", lit ? "" : " and acc_y");
+  if (is_split(a.dtype) && !aligned16(a.workspace))
+    return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for the bf16-product modes");
+  return MEC_OK;
+}
+
+// Pipeline step `step` of a checked problem on the scratch at `scratch`
+// (16-byte aligned, laid out as L: L.total bytes).
+static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L, void* scratch, void* stream) {
+  const void *x = a.x, *y = a.y;
+  const int64_t ldx = a.ldx, ldy = a.ldy, n = a.n, d = a.d;
+  const int dtype = a.dtype, mode = a.mode, normalize = a.normalize;
+  const float temperature = a.temperature;
+  const float* workspace = a.workspace;
+  float *acc_x = a.acc_x, *acc_y = a.acc_y;
   const bool lit = is_lit(mode);
-  if (lit) acc_y = nullptr;
-  if (!workspace || !scratch) return fail(MEC_ERR_INVALID, "workspace and scratch must be non-null");
-  if (!acc_x && !acc_y) return fail(MEC_ERR_INVALID, "no gradient requested (acc_x%s null)", lit ? "" : " and acc_y");
-  const int64_t need = scratch_bytes_for(n, d, dtype);
-  if (scratch_bytes < need)
-    return fail(MEC_ERR_INVALID, "scratch holds %lld bytes, %lld needed", (long long)scratch_bytes,
-                (long long)need);
-  if (!aligned16(scratch)) return fail(MEC_ERR_INVALID, "scratch must be 16-byte aligned");
-  const ScratchLayout L = scratch_layout(n, d, dtype);
+  int rc = MEC_OK;
   const int bs = L.bs, nb = L.nb;
   if (step < 0 || step > nb)
     return fail(MEC_ERR_INVALID, "step %lld out of range [0, %d]", (long long)step, nb);
   const int N = (int)n, D = (int)d;
   const float c = (float)(1.4426950408889634 / (double)temperature);
   const bool x3 = is_x3(dtype), split = is_split(dtype);
-  if (split && !aligned16(workspace))
-    return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for the bf16-product modes");
   // operands of the gradient-matrix tiles (split modes: the copies, K = terms * dp)
   const GemmOperands go = split ? split_operands(workspace, n, d, dtype) : GemmOperands{x, ldx, y, ldy, d, dtype};
   const bool vec = vec_ok(go.x, go.ldx, go.y, go.ldy, go.d, go.dtype);
@@ -600,17 +673,40 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
   return check_launch("grad_step");
 }
 
+// the caller's scratch against the default layout
+static int check_scratch(const StepArgs& a, void* scratch, int64_t scratch_bytes, ScratchLayout* L) {
+  if (!scratch) return fail(MEC_ERR_INVALID, "scratch must be non-null");
+  if (!aligned16(scratch)) return fail(MEC_ERR_INVALID, "scratch must be 16-byte aligned");
+  *L = scratch_layout(a.n, a.d, a.dtype);
+  if (scratch_bytes < L->total)
+    return fail(MEC_ERR_INVALID, "scratch holds %lld bytes, %lld needed", (long long)scratch_bytes,
+                (long long)L->total);
+  return MEC_OK;
+}
+
+int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
+                  int mode, int normalize, float temperature, const float* workspace, int64_t step, void* scratch,
+                  int64_t scratch_bytes, float* acc_x, float* acc_y, void* stream) {
+  g_err.clear();
+  StepArgs a{x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, acc_x, acc_y};
+  int rc = check_step_args(a);
+  ScratchLayout L;
+  if (!rc) rc = check_scratch(a, scratch, scratch_bytes, &L);
+  if (rc) return rc;
+  return grad_step_run(a, step, L, scratch, stream);
+}
+
 int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
              int mode, int normalize, float temperature, const float* workspace, void* scratch,
              int64_t scratch_bytes, float* acc_x, float* acc_y, void* stream) {
   g_err.clear();
-  int rc = check_common(x, ldx, y, ldy, n, d, dtype);
+  StepArgs a{x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, acc_x, acc_y};
+  int rc = check_step_args(a);
+  ScratchLayout L;
+  if (!rc) rc = check_scratch(a, scratch, scratch_bytes, &L);
   if (rc) return rc;
-  int bs, nb;
-  grad_blocks(n, d, dtype, &bs, &nb);
-  for (int t = 0; t <= nb; ++t) {
-    rc = mec_grad_step(x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, t, scratch,
-                       scratch_bytes, acc_x, acc_y, stream);
+  for (int t = 0; t <= L.nb; ++t) {
+    rc = grad_step_run(a, t, L, scratch, stream);
     if (rc) return rc;
   }
   return MEC_OK;

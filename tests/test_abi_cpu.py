@@ -88,8 +88,9 @@ def test_16bit_blocks_fit_the_32bit_operand_range():
             bs, nb = _lib.grad_blocking(n, d, dt)
             assert bs <= 32512 and ((bs - 1) * bs + 256) * 2 < 2 ** 31, (n, d, bs)
             assert nb * bs >= n > (nb - 1) * bs
-    # fp32 addresses with 64-bit pointers and keeps its ~4d blocks
-    assert _lib.grad_blocking(65536, 32768, 0)[0] == 65536
+    # fp32 addresses with 64-bit pointers; its ~4d target (131072 rows here)
+    # gives way to the memory budget of the gradient-matrix buffers (16 GiB)
+    assert _lib.grad_blocking(65536, 32768, 0) == (16384, 4)
 
 
 def test_blocking_prefers_exact_divisors():
@@ -139,6 +140,69 @@ def test_mode_and_deterministic_flag(mode, ok):
     assert rc == _lib.MEC_ERR_INVALID and (("non-null" if ok else "mode") in _lib.last_error())
 
 
+def gbuf_bytes(n, d, dt):
+    """Bytes of the gradient-matrix buffers: 4 copies (fp32: both layouts,
+    double-buffered; bf16x3: hi and lo planes) or 2 copies of nb blocks of bs^2."""
+    bs, nb = _lib.grad_blocking(n, d, dt)
+    copies = 4 if dt in (0, 3) else 2
+    elem = 4 if dt == 0 else 2
+    return copies * nb * bs * bs * elem, bs
+
+
+@pytest.mark.parametrize("dt", [0, 1, 2, 3, 4])
+def test_scratch_stays_within_its_budget(dt):
+    """The gradient-matrix buffers stay within the bytes of a dense fp32 n x n
+    logit matrix and within 16 GiB, unless the 1024-row block floor alone
+    exceeds that; the transposed input copies add 2 (bf16x3: 4) n x d planes."""
+    lib = _lib.load()
+    for n in (1024, 3000, 4096, 8192, 16384, 32768, 65536, 262144, 1 << 21, 1 << 22):
+        for d in (64, 512, 768, 1152, 2048, 4096, 8192):
+            g, bs = gbuf_bytes(n, d, dt)
+            budget = min(n * n * 4, 16 << 30)
+            q = 128 if dt == 0 else 256
+            floor_rows = max(1024, q)
+            elem = 4 if dt == 0 else 2
+            copies = 4 if dt in (0, 3) else 2
+            nb_floor = -(-n // floor_rows)
+            floor_bytes = copies * nb_floor * floor_rows * floor_rows * elem
+            assert g <= budget or (bs == floor_rows and g <= floor_bytes), (n, d, dt, bs, g, budget)
+            ldt = (n + 127) // 128 * 128
+            planes = 4 if dt == 3 else 2
+            assert lib.mec_grad_scratch_bytes(n, d, dt) == g + planes * d * ldt * elem
+
+
+def test_scratch_at_two_million_rows():
+    # n = 2^21 pairs at the headline width: 1024-row blocks, about 54 GB of
+    # scratch (34 GB gradient-matrix buffers + 19 GB transposed inputs), within
+    # the 288 GB of one MI355X beside the inputs and gradients (4 x 9.7 GB)
+    lib = _lib.load()
+    assert _lib.grad_blocking(1 << 21, 1152, 0) == (1024, 2048)
+    assert lib.mec_grad_scratch_bytes(2097152, 1152, 0) <= 60 * 10 ** 9
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2, 3, 4])
+def test_size_limit(dtype):
+    # every dtype supports n <= 2^22: the 16-bit contractions address transposed
+    # panels with 32-bit offsets, and the fp32 forward grid of 128 x 128 tiles
+    # ((n / 128)^2 workgroups) must stay below 2^31; beyond, every entry point
+    # returns MEC_ERR_UNSUPPORTED before any launch
+    lib = _lib.load()
+    assert lib.mec_workspace_floats((1 << 22) + 1) < 0
+    assert lib.mec_grad_scratch_bytes((1 << 22) + 1, 64, dtype) < 0
+    assert lib.mec_workspace_floats_for(1 << 22, 64, dtype) > 0
+    n_big = (1 << 22) + 1
+    for rc in (lib.mec_forward(16, 64, 16, 64, n_big, 64, dtype, 0, 1, 0.07, 16, 16, None),
+               lib.mec_prepass(16, 64, 16, 64, n_big, 64, dtype, 1, 16, None),
+               lib.mec_finalize(n_big, 0, 0.07, 16, 16, None),
+               lib.mec_grad(16, 64, 16, 64, n_big, 64, dtype, 0, 1, 0.07, 16, 16, 1 << 40, 16, 16, None),
+               lib.mec_postpass(16, 64, 16, 64, n_big, 64, dtype, 0, 1, 1.0, 16, None, 16, 16, 16, 16, None),
+               lib.mec_backward(16, 64, 16, 64, n_big, 64, dtype, 0, 1, 0.07, 1.0, 16, None, 16, 1 << 40, 16,
+                                16, 16, 16, None)):
+        assert rc == _lib.MEC_ERR_UNSUPPORTED and "2^22" in _lib.last_error()
+    with pytest.raises(_lib.MecError, match="2\\^22"):
+        _lib.grad_blocking(n_big, 64, dtype)
+
+
 @pytest.mark.parametrize("dtype", [1, 2, 3, 4])
 def test_16bit_size_limit(dtype):
     # the 16-bit contractions address transposed panels with 32-bit offsets
@@ -174,6 +238,10 @@ def test_grad_step_validation():
     assert rc == _lib.MEC_ERR_INVALID and "step" in _lib.last_error()
     with pytest.raises(_lib.MecError, match="out of range"):
         _lib.grad_blocking(0, 64, 0)
+    # the step counter is checked against the blocking of this shape
+    bs, nb = _lib.grad_blocking(10, 64, 0)
+    rc = lib.mec_grad_step(16, 64, 16, 64, 10, 64, 0, 0, 1, 0.07, 16, nb + 1, 16, need, 16, 16, None)
+    assert rc == _lib.MEC_ERR_INVALID and "step" in _lib.last_error()
 
 
 def test_postpass_and_finalize_validation():

@@ -117,3 +117,19 @@ def test_float32_matmul_precision_selects_the_product_mode():
             assert compute_dtype(torch.float16) == _lib.DTYPE_F16
     finally:
         torch.set_float32_matmul_precision(old)
+
+
+def test_graph_capture_is_refused(monkeypatch):
+    """Forward and backward raise RuntimeError, before touching any tensor,
+    while the current stream is capturing a CUDA/HIP graph (capture of the
+    loss crashed the host process in capture_end on the GPU box)."""
+    from memoryefficientclip_amd import _function
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    monkeypatch.setattr(_function, "check_inputs", lambda x, y: None)
+    x = torch.zeros(4, 8)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        _function.forward(None, x, x, 0.07, 0, True, False)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        _function.backward(None, torch.ones(()), True, True)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    _function.refuse_graph_capture()  # no capture: no error

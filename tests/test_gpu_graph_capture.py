@@ -17,7 +17,8 @@ pytestmark = [
     pytest.mark.gpu,
     pytest.mark.skip(reason="the first case ended in a host segmentation fault inside torch.cuda.graph's "
                             "capture_end (stream-capture end / graph instantiation) on the MI355X box; the cause "
-                            "is not identified, so the test stays off the GPU"),
+                            "is not identified, so the test stays off the GPU and the module refuses capture "
+                            "with a RuntimeError (tests/test_api_cpu.py::test_graph_capture_is_refused)"),
 ]
 DEV = "cuda:0"
 
