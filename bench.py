@@ -16,9 +16,15 @@ benchmark table for exploration.  Rank 0 prints ONE JSON line:
   average launch time, measured with HIP events on the stream the library
   launches on (torch's current stream), against the dense MFMA peak of the
   input dtype;
-* ``cpu_baseline``: the dense PyTorch loss (fp32) on the host cores, on a
-  bounded sample of the same workload (smaller N, same D and generator),
-  scaled to TFLOP/s with the same flop convention.
+* ``cpu_baseline``: the dense PyTorch loss (fp32) on the host cores at the
+  same workload (same N, D and generator; a smaller N only with
+  ``--cpu-n``), timed forward and backward, reported as the flop the dense
+  path performs (6 N^2 D for CLIP: logits, then the two gradient products;
+  4 N^2 D for LiT) per second, with the core count and CPU model;
+* ``configs``: every benchmark configuration (1-5) timed for a few steps
+  through the same module (the headline's row repeats its numbers), with
+  forward / backward / step ms, TFLOP/s, fraction of the input dtype's MFMA
+  peak and peak extra HBM bytes (``--no-table`` skips the other four).
 
 ``--precision high`` runs fp32 inputs under
 ``torch.set_float32_matmul_precision("high")``: the products are formed from
@@ -47,14 +53,18 @@ METRIC = "CLIP fwd+bwd ms & TFLOP/s (% MFMA peak) at N=32768 D=1152, 1 MI355X"
 PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6, "f16": 2516.6}
 TORCH_DTYPE = {"f32": "float32", "bf16": "bfloat16", "f16": "float16"}
 
-# config -> (mode, n, d, dtype, normalized_inputs, temperature, generator, cpu sample n)
+# config -> (mode, n, d, dtype, normalized_inputs, temperature, generator, CPU baseline n)
+# (the CPU baseline runs dense at the configuration's own N up to 32768; the
+# 4.3 GB logits of N = 32768 take about 10 s per fwd+bwd on 16 host threads)
 CONFIGS = {
     1: ("clip", 1024, 512, "f32", False, 0.07, "randn", 1024),
-    2: ("clip", 32768, 1152, "f32", False, 0.07, "randn", 8192),
-    3: ("lit", 32768, 1152, "f32", False, 0.07, "randn", 8192),
-    4: ("clip", 65536, 768, "bf16", True, 0.07, "correlated", 8192),
-    5: ("clip", 262144, 1152, "bf16", True, 0.05, "correlated", 8192),
+    2: ("clip", 32768, 1152, "f32", False, 0.07, "randn", 32768),
+    3: ("lit", 32768, 1152, "f32", False, 0.07, "randn", 32768),
+    4: ("clip", 65536, 768, "bf16", True, 0.07, "correlated", 32768),
+    5: ("clip", 262144, 1152, "bf16", True, 0.05, "correlated", 32768),
 }
+# steps, warm-up steps of each configuration in the table
+TABLE_STEPS = {1: (30, 5), 2: (5, 2), 3: (5, 2), 4: (5, 2), 5: (3, 1)}
 
 
 def log(*a):
@@ -189,8 +199,26 @@ def measured_traffic(workload, kernel):
         return None
 
 
-def cpu_baseline(mode, d, dt, normalized, temperature, gen, n_cpu, budget_s=20.0):
-    """Dense PyTorch loss on the host cores on an (n_cpu, d) sample of the workload."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def dense_flop(mode, n, d):
+    """Flop the dense PyTorch path performs: the logits (2 N^2 D) and, in the
+    backward, dX = G Y (2 N^2 D) and for CLIP dY = G^T X (2 N^2 D)."""
+    return (6.0 if mode == "clip" else 4.0) * n * n * d
+
+
+def cpu_baseline(mode, d, dt, normalized, temperature, gen, n_cpu, runs=3):
+    """Dense PyTorch loss on the host cores at (n_cpu, d) of the workload:
+    one warm-up, then the median of `runs` timed fwd+bwd steps."""
     import torch
     from oracle.cpu_baseline import dense_step
     a, b = make_inputs(n_cpu, d, gen, seed=0)
@@ -198,24 +226,89 @@ def cpu_baseline(mode, d, dt, normalized, temperature, gen, n_cpu, budget_s=20.0
         tdt = getattr(torch, TORCH_DTYPE[dt])
         a, b = a.to(tdt).float(), b.to(tdt).float()
     dense_step(a, b, temperature, mode == "lit", normalized)  # warm-up
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < budget_s * 0.5 and len(times) < 10):
+    times, fwd, bwd = [], [], []
+    for _ in range(runs):
+        t = {}
         t0 = time.perf_counter()
-        dense_step(a, b, temperature, mode == "lit", normalized)
+        dense_step(a, b, temperature, mode == "lit", normalized, times=t)
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s:
-            break
+        fwd.append(t["fwd"])
+        bwd.append(t["bwd"])
+        log(f"bench: CPU baseline step {len(times)}: {times[-1] * 1e3:.0f} ms")
     med = statistics.median(times)
     return {
-        "value": round(algo_flop(mode, n_cpu, d) / med / 1e12, 4),
+        "value": round(dense_flop(mode, n_cpu, d) / med / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"dense fp32 PyTorch {mode.upper()} fwd+bwd (F.normalize, logits, cross_entropy, autograd) "
-                   f"at N={n_cpu}, D={d}, same generator; median of {len(times)} runs = {med * 1e3:.1f} ms; "
-                   f"flop {('8' if mode == 'clip' else '6')}*N^2*D"),
+                   f"at N={n_cpu}, D={d}, same generator; 1 warm-up, median of {runs} runs; value counts the "
+                   f"{'6' if mode == 'clip' else '4'}*N^2*D flop the dense path performs"),
+        "n": n_cpu,
+        "ms_per_step": round(med * 1e3, 1),
+        "fwd_ms": round(statistics.median(fwd) * 1e3, 1),
+        "bwd_ms": round(statistics.median(bwd) * 1e3, 1),
+        "value_8n2d": round(algo_flop(mode, n_cpu, d) / med / 1e12, 4),
+        "threads": torch.get_num_threads(),
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": cpu_model(),
     }
+
+
+def measure(cfg, dt, steps, warmup, with_events=True):
+    """Times `steps` fwd+bwd steps of configuration `cfg` (input dtype dt)
+    through the drop-in module, after `warmup` steps.  Returns (row, a, b)
+    with the device inputs a, b."""
+    import torch
+    from memoryefficientclip_amd import MemoryEfficientCLIPLoss, MemoryEfficientLiTLoss
+    mode, n, d, _, normalized, temperature, gen, _ = CONFIGS[cfg]
+    dev = torch.device("cuda:0")
+    tdtype = getattr(torch, TORCH_DTYPE[dt])
+    a_h, b_h = make_inputs(n, d, gen, seed=0)
+    a = a_h.to(dev, tdtype).requires_grad_(True)
+    b = b_h.to(dev, tdtype).requires_grad_(mode == "clip")
+    del a_h, b_h
+    module = (MemoryEfficientCLIPLoss if mode == "clip" else MemoryEfficientLiTLoss)(temperature, normalized)
+
+    def step(evs=None):
+        if evs is not None:
+            evs[0].record()
+        loss = module(a, b)
+        if evs is not None:
+            evs[1].record()
+        loss.backward()
+        if evs is not None:
+            evs[2].record()
+        a.grad = None
+        b.grad = None
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    loss = step()
+    torch.cuda.synchronize()
+    peak_extra = torch.cuda.max_memory_allocated(dev) - base
+    loss_val = float(loss.detach())
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        step(evs[k] if with_events else None)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = wall * 1e3 / steps
+    row = {"config": cfg, "workload": f"{mode}_loss_fwd_bwd", "n": n, "d": d, "dtype": dt,
+           "normalized_inputs": normalized, "temperature": temperature, "steps": steps,
+           "ms_per_step": round(ms, 4),
+           "tflops": round(algo_flop(mode, n, d) / (ms * 1e-3) / 1e12, 3),
+           "peak_extra_hbm_bytes": int(peak_extra), "loss": loss_val}
+    if with_events:
+        row["fwd_ms"] = round(statistics.median(e[0].elapsed_time(e[1]) for e in evs), 4)
+        row["bwd_ms"] = round(statistics.median(e[1].elapsed_time(e[2]) for e in evs), 4)
+    return row, a, b
 
 
 def main():
@@ -230,6 +323,9 @@ def main():
                     help="float32 matmul precision for fp32 inputs: highest = IEEE fp32 MFMA, "
                          "high = three bf16 MFMA products per fp32 product (bf16x3), medium = bf16 products")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-n", type=int, default=0,
+                    help="N of the CPU baseline sample (default: the configuration's own N, at most 32768)")
+    ap.add_argument("--no-table", action="store_true", help="skip timing the other benchmark configurations")
     ap.add_argument("--no-alt", action="store_true",
                     help="skip the fp32 'high' precision side leg (e.g. for per-kernel profiles of the IEEE path)")
     ap.add_argument("--kernel-reps", type=int, default=0, help="launches per stage in the kernel leg (default: steps)")
@@ -263,7 +359,6 @@ def main():
     dt = args.dtype or dt
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    tdtype = getattr(torch, TORCH_DTYPE[dt])
     # arithmetic: the input dtype's MFMA, or for fp32 inputs below "highest"
     # precision bf16x3 (three bf16 products per fp32 product) or bf16
     x3 = args.precision == "high"
@@ -280,47 +375,9 @@ def main():
         dtc = _lib.DTYPE_F32_BF16X3 if x3 else _lib.DTYPE_F32_BF16
     log(f"bench: config {args.config} {mode} n={n} d={d} {dt} normalized_inputs={normalized} T={temperature}"
         f" arithmetic={arith}")
-    a_h, b_h = make_inputs(n, d, gen, seed=0)
-    a = a_h.to(dev, tdtype).requires_grad_(True)
-    b = b_h.to(dev, tdtype).requires_grad_(mode == "clip")
-    del a_h, b_h
-    module = (MemoryEfficientCLIPLoss if mode == "clip" else MemoryEfficientLiTLoss)(temperature, normalized)
-
-    def step(evs=None):
-        if evs is not None:
-            evs[0].record()
-        loss = module(a, b)
-        if evs is not None:
-            evs[1].record()
-        loss.backward()
-        if evs is not None:
-            evs[2].record()
-        a.grad = None
-        b.grad = None
-        return loss
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    log("bench: warm-up done")
-
-    base = torch.cuda.memory_allocated(dev)
-    torch.cuda.reset_peak_memory_stats(dev)
-    loss = step()
-    torch.cuda.synchronize()
-    peak_extra = torch.cuda.max_memory_allocated(dev) - base
-    loss_val = float(loss.detach())
-
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        step(evs[k])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    fwd_ms = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
-    bwd_ms = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
-    ms = wall * 1e3 / args.steps
+    head, a, b = measure(args.config, dt, args.steps, args.warmup)
+    ms, fwd_ms, bwd_ms = head["ms_per_step"], head["fwd_ms"], head["bwd_ms"]
+    peak_extra, loss_val = head["peak_extra_hbm_bytes"], head["loss"]
     flop = algo_flop(mode, n, d)
     tflops = flop / (ms * 1e-3) / 1e12
     log(f"bench: {args.steps} steps, {ms:.3f} ms/step (fwd {fwd_ms:.3f}, bwd {bwd_ms:.3f}), {tflops:.2f} TFLOP/s, "
@@ -331,15 +388,9 @@ def main():
     alt = None
     if dt == "f32" and not lowp and not args.no_alt:
         torch.set_float32_matmul_precision("high")
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        ms_hi = (time.perf_counter() - t1) * 1e3 / args.steps
+        hi, _, _ = measure(args.config, dt, args.steps, args.warmup, with_events=False)
         torch.set_float32_matmul_precision("highest")
+        ms_hi = hi["ms_per_step"]
         alt = {"float32_matmul_precision": "high", "dtype": "bf16x3", "ms_per_step": round(ms_hi, 4),
                "value": round(flop / (ms_hi * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
                "frac_of_bf16_peak": round(3 * flop / (ms_hi * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4)}
@@ -366,11 +417,34 @@ def main():
                     "frac": round(mfma_per_flop * f_f / (t_f * 1e-3) / 1e12 / peak, 4), "launch_ms": round(t_f, 4),
                     "flop_per_launch": mfma_per_flop * f_f}
 
+    del a, b
+    torch.cuda.empty_cache()
+
+    # every benchmark configuration (the headline's own row from the run above)
+    table = None
+    if not args.no_table and args.precision == "highest":
+        table = []
+        for cfg in sorted(CONFIGS):
+            if cfg == args.config and dt == CONFIGS[cfg][3]:
+                row = dict(head)
+            else:
+                st, wu = TABLE_STEPS[cfg]
+                row, ta, tb = measure(cfg, CONFIGS[cfg][3], st, wu)
+                del ta, tb
+                torch.cuda.empty_cache()
+            row["frac_of_peak"] = round(row["tflops"] / PEAK_TFLOPS[row["dtype"]], 4)
+            table.append(row)
+            log(f"bench: table config {cfg}: {row['ms_per_step']:.3f} ms/step (fwd {row['fwd_ms']:.3f}, "
+                f"bwd {row['bwd_ms']:.3f}), {row['tflops']:.1f} TFLOP/s, {100 * row['frac_of_peak']:.1f}% of "
+                f"{row['dtype']} peak, extra HBM {row['peak_extra_hbm_bytes'] / 1e9:.2f} GB")
+
     cpu = None
     if not args.no_cpu:
+        n_cpu = args.cpu_n or n_cpu
         log(f"bench: CPU baseline at n={n_cpu} ...")
         cpu = cpu_baseline(mode, d, dt, normalized, temperature, gen, n_cpu)
-        log(f"bench: CPU baseline {cpu['value']} TFLOP/s on {cpu['cores']} threads")
+        log(f"bench: CPU baseline {cpu['ms_per_step']} ms/step, {cpu['value']} TFLOP/s on {cpu['cores']} threads "
+            f"({cpu['os_cpu_count']} CPUs, {cpu['cpu_model']})")
 
     out = {
         "metric": METRIC,
@@ -399,6 +473,7 @@ def main():
         "backward_blocking": blocking,
         "precision_high": alt,
         "cpu_baseline": cpu,
+        "configs": table,
     }
     print(json.dumps(out), flush=True)
 

@@ -17,13 +17,19 @@ Its values are checked against the fp64 oracle in ``tests/test_oracle.py``.
 """
 from __future__ import annotations
 
+import time
+
 import torch
 import torch.nn.functional as F
 
 
-def dense_step(a: torch.Tensor, b: torch.Tensor, temperature: float, lit: bool, normalized_inputs: bool):
+def dense_step(a: torch.Tensor, b: torch.Tensor, temperature: float, lit: bool, normalized_inputs: bool,
+               times: dict | None = None):
     """One fwd+bwd of the dense loss on CPU tensors ``a`` (image for CLIP, text
-    for LiT) and ``b``.  Returns (loss, grad_a, grad_b or None)."""
+    for LiT) and ``b``.  Returns (loss, grad_a, grad_b or None).  With
+    ``times``, the forward and backward seconds are stored under "fwd" and
+    "bwd"."""
+    t0 = time.perf_counter()
     a = a.detach().float().requires_grad_(True)
     b = b.detach().float().requires_grad_(not lit)
     xh = a if normalized_inputs else F.normalize(a, dim=1)
@@ -33,5 +39,10 @@ def dense_step(a: torch.Tensor, b: torch.Tensor, temperature: float, lit: bool, 
     loss = F.cross_entropy(s, lab)
     if not lit:
         loss = 0.5 * (loss + F.cross_entropy(s.T, lab))
+    t1 = time.perf_counter()
     loss.backward()
+    t2 = time.perf_counter()
+    if times is not None:
+        times["fwd"] = t1 - t0
+        times["bwd"] = t2 - t1
     return loss.detach(), a.grad, (None if lit else b.grad)
