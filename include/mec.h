@@ -218,6 +218,26 @@ int mec_backward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
                  int64_t scratch_bytes, float* acc_x, float* acc_y, void* dx, void* dy,
                  void* stream);
 
+/* Bytes of the gradient scratch array of mec_backward_noalloc (256 MiB). */
+#define MEC_NOALLOC_SCRATCH_BYTES (256LL << 20)
+
+/* mec_backward without caller scratch and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The gradient scratch is a file-scope device array of
+ * MEC_NOALLOC_SCRATCH_BYTES on each GPU the library runs on, held until the
+ * process ends; its address is resolved once per device on the first call.
+ * The blocking is mec_backward's when its scratch fits the array, else
+ * shorter blocks (down to 1024 rows); problems whose scratch does not fit even
+ * then (e.g. more than about 2^15 rows at d = 1152) return
+ * MEC_ERR_UNSUPPORTED before any launch.  Nothing in the array needs to start
+ * at zero.  Every call on one GPU uses the same array: calls that overlap on
+ * one GPU (other streams, other threads) race and must be serialised by the
+ * caller.  Arguments and results otherwise as mec_backward. */
+int mec_backward_noalloc(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
+                         int mode, int normalize, float temperature, float grad_scale, const float* workspace,
+                         const float* grad_output, float* acc_x, float* acc_y, void* dx, void* dy, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

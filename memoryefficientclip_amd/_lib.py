@@ -52,7 +52,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                             _vp, _vp]),
     "mec_backward": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _int, _f32, _f32, _vp, _vp, _vp, _i64,
                             _vp, _vp, _vp, _vp, _vp]),
+    "mec_backward_noalloc": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _int, _f32, _f32, _vp, _vp,
+                                    _vp, _vp, _vp, _vp, _vp]),
 }
+NOALLOC_SCRATCH_BYTES = 256 << 20  # MEC_NOALLOC_SCRATCH_BYTES
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

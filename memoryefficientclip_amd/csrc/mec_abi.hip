@@ -52,6 +52,37 @@ int compute_units(int* cus) {
   return MEC_OK;
 }
 
+// Gradient scratch of mec_backward_noalloc: one array per GPU, held until the
+// process ends.  Host code never uses the name itself (on the host it is a
+// stand-in, not a device address): noalloc_scratch() resolves this device's
+// copy with hipGetSymbolAddress once per device.
+constexpr int64_t kNoAllocScratch = MEC_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratch];
+
+// Address of the current device's `scratch` (resolved on the first call on
+// each device; callers on any thread may fill the cache, always with the
+// same value).
+int noalloc_scratch(void** out) {
+  static std::atomic<void*> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(MEC_ERR_HIP, "hipGetDevice failed");
+  const bool cached = dev >= 0 && dev < 64;
+  if (cached) {
+    void* p = cache[dev].load(std::memory_order_acquire);
+    if (p) {
+      *out = p;
+      return MEC_OK;
+    }
+  }
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr)
+    return fail(MEC_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+  if (cached) cache[dev].store(p, std::memory_order_release);
+  *out = p;
+  return MEC_OK;
+}
+
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MEC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
@@ -710,6 +741,41 @@ int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, 
     if (rc) return rc;
   }
   return MEC_OK;
+}
+
+int mec_backward_noalloc(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
+                         int mode, int normalize, float temperature, float grad_scale, const float* workspace,
+                         const float* grad_output, float* acc_x, float* acc_y, void* dx, void* dy, void* stream) {
+  g_err.clear();
+  StepArgs a{x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, acc_x, acc_y};
+  int rc = check_step_args(a);
+  if (rc) return rc;
+  if (!std::isfinite(grad_scale)) return fail(MEC_ERR_INVALID, "grad_scale must be finite");
+  if (is_lit(mode)) dy = nullptr;
+  if ((a.acc_x == nullptr) != (dx == nullptr) || (a.acc_y == nullptr) != (dy == nullptr))
+    return fail(MEC_ERR_INVALID, "each side needs both its accumulator and its output (or neither)");
+  // the default blocking when it fits the array, else shorter blocks (not
+  // below 1024 rows) within what the transposed inputs leave of it
+  const int64_t trans = trans_bytes(n, d, dtype);
+  int64_t gbudget = kNoAllocScratch - trans;
+  if (gbudget > default_gbudget(n)) gbudget = default_gbudget(n);
+  int bs = 0, nb = 0;
+  if (gbudget > 0) grad_blocks_budget(n, d, dtype, gbudget, &bs, &nb);
+  const ScratchLayout L = scratch_layout_blocks(n, d, dtype, bs, nb);
+  if (gbudget <= 0 || L.total > kNoAllocScratch)
+    return fail(MEC_ERR_UNSUPPORTED,
+                "the backward of n=%lld d=%lld needs %lld bytes of scratch; mec_backward_noalloc holds %lld "
+                "(use mec_backward with caller scratch)",
+                (long long)n, (long long)d, (long long)(gbudget > 0 ? L.total : trans), (long long)kNoAllocScratch);
+  void* buf = nullptr;
+  rc = noalloc_scratch(&buf);
+  if (rc) return rc;
+  for (int t = 0; t <= L.nb; ++t) {
+    rc = grad_step_run(a, t, L, buf, stream);
+    if (rc) return rc;
+  }
+  return mec_postpass(x, ldx, y, ldy, n, d, dtype, mode, normalize, grad_scale, workspace, grad_output, a.acc_x,
+                      a.acc_y, dx, dy, stream);
 }
 
 int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,

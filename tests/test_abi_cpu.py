@@ -273,3 +273,24 @@ def test_error_string_is_thread_local():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="not built"):
         _lib.load(tmp_path / "nope.so")
+
+
+def test_noalloc_rejects_problems_beyond_its_array():
+    # mec_backward_noalloc holds its scratch in a 256 MiB device array: a
+    # problem whose scratch does not fit even with 1024-row blocks is refused
+    # in host code, before any HIP call (no device here)
+    lib = _lib.load()
+    n, d = 65536, 768  # config 4 (bf16): the transposed inputs alone are 201 MB
+    rc = lib.mec_backward_noalloc(16, d, 16, d, n, d, _lib.DTYPE_BF16, 0, 0, 0.07, 1.0 / 0.07, 16, None, 16, 16,
+                                  16, 16, None)
+    assert rc == _lib.MEC_ERR_UNSUPPORTED and "mec_backward_noalloc holds" in _lib.last_error()
+    n, d = 1 << 20, 1024  # fp32: 8 GB of transposed inputs
+    rc = lib.mec_backward_noalloc(16, d, 16, d, n, d, 0, 0, 1, 0.07, 1.0 / 0.07, 16, None, 16, 16, 16, 16, None)
+    assert rc == _lib.MEC_ERR_UNSUPPORTED
+    # argument errors as mec_backward
+    rc = lib.mec_backward_noalloc(16, 64, 16, 64, 10, 64, 0, 0, 1, 0.07, 1.0 / 0.07, 16, None, None, None, None,
+                                  None, None)
+    assert rc == _lib.MEC_ERR_INVALID and "no gradient" in _lib.last_error()
+    rc = lib.mec_backward_noalloc(16, 64, 16, 64, 10, 64, 0, 0, 1, 0.07, float("nan"), 16, None, 16, 16, 16, 16,
+                                  None)
+    assert rc == _lib.MEC_ERR_INVALID and "grad_scale" in _lib.last_error()
