@@ -187,14 +187,16 @@ def kernel_leg(x, y, mode, dtc, normalize, temperature, reps):
     return res, {"block_rows": bs, "num_blocks": nb, "step_ms": [round(v, 4) for v in per_step]}
 
 
-def measured_traffic(workload, kernel):
-    """HBM bytes per launch of `kernel` at `workload` from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/traffic_<workload>.md,
-    machine-readable copy in profiles/traffic.json), or None if not measured."""
+def measured_traffic(workload, kernels):
+    """HBM bytes of one launch of each of `kernels` at `workload`, summed, from
+    the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summaries
+    (profiles/traffic_<workload>.md, machine-readable copy in
+    profiles/traffic.json), or None if not measured."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f)[workload][kernel]["bytes"]
+            t = json.load(f)[workload]
+        return sum(t[k]["bytes"] for k in kernels)
     except (OSError, KeyError, ValueError):
         return None
 
@@ -329,8 +331,10 @@ def main():
     ap.add_argument("--no-alt", action="store_true",
                     help="skip the fp32 'high' precision side leg (e.g. for per-kernel profiles of the IEEE path)")
     ap.add_argument("--kernel-reps", type=int, default=0, help="launches per stage in the kernel leg (default: steps)")
-    ap.add_argument("--probe", choices=["copy"], default=None,
-                    help="copy: only run 5 plain device copies of 1 GiB (calibrates the rocprofv3 byte counters)")
+    ap.add_argument("--probe", choices=["copy", "gemm"], default=None,
+                    help="copy: only run 5 plain device copies of 1 GiB (calibrates the rocprofv3 byte counters); "
+                         "gemm: only time the vendor library's bf16 GEMM (torch.matmul, hipBLASLt) at the "
+                         "contraction and similarity shapes (calibrates the MFMA rate)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -351,6 +355,27 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"probe": "copy", "bytes_read_per_copy": src.numel() * 4,
                           "bytes_written_per_copy": dst.numel() * 4}), flush=True)
+        return
+    if args.probe == "gemm":
+        res = []
+        for m, nn, k in [(16384, 768, 16384), (16384, 2304, 16384), (16384, 16384, 4096), (32768, 32768, 768)]:
+            a = torch.randn(m, k, device="cuda:0", dtype=torch.bfloat16)
+            b = torch.randn(k, nn, device="cuda:0", dtype=torch.bfloat16)
+            for _ in range(2):
+                c = a @ b
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(6):
+                c = a @ b
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / 6
+            res.append({"m": m, "n": nn, "k": k, "ms": round(ms, 4), "tflops": round(2 * m * nn * k / ms / 1e9, 1)})
+            log(f"bench: probe gemm bf16 {m}x{nn}x{k}: {ms:.3f} ms, {res[-1]['tflops']} TFLOP/s")
+            del a, b, c
+        print(json.dumps({"probe": "gemm", "dtype": "bf16", "library": "torch.matmul (hipBLASLt)", "shapes": res}),
+              flush=True)
         return
     from memoryefficientclip_amd import MemoryEfficientCLIPLoss, MemoryEfficientLiTLoss, _lib
     _lib.load()  # fail loudly if the HIP library is missing
@@ -404,13 +429,21 @@ def main():
     for k, (t, nl, fl) in stages.items():
         log(f"bench: stage {k:9s} {t:9.3f} ms x {nl:3d}" + (f"  {fl / (t * 1e-3) / 1e12:8.2f} TFLOP/s" if fl else ""))
     log(f"bench: backward blocking {blocking}")
-    # dominant kernel: k_grad_step (nb + 1 launches per step, about 3/4 of the step's flop)
+    # dominant kernel: the backward pipeline step, nb + 1 launches of mec_grad_step per
+    # step, about 3/4 of the step's flop: k_grad_step (fp32: gradient-matrix tiles and
+    # contractions in one kernel; 16-bit: the gradient-matrix tiles, with the
+    # contractions in k_grad_contract before it)
     # (bf16x3: MFMA flop = 3 x algorithmic flop, against the bf16 peak)
     t_k, nl_k, f_k = stages["grad_step"]
     achieved = mfma_per_flop * f_k / (t_k * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": "k_grad_step", "achieved": round(achieved, 3), "peak": peak,
-                "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
-                "traffic": measured_traffic(f"{mode}_n{n}_d{d}_{arith}", "k_grad_step"),
+    kernels = ["k_grad_step"] if arith == "f32" else ["k_grad_contract", "k_grad_step"]
+    traffic = measured_traffic(f"{mode}_n{n}_d{d}_{arith}", kernels)
+    if traffic is not None and len(kernels) > 1:
+        # each kernel runs in nb of the nb + 1 pipeline launches
+        nbk = blocking["num_blocks"]
+        traffic = int(traffic * nbk / (nbk + 1))
+    roofline = {"bound": "mfma", "kernel": "+".join(kernels), "achieved": round(achieved, 3), "peak": peak,
+                "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                 "launch_ms": round(t_k, 4), "flop_per_launch": mfma_per_flop * f_k, "launches_per_step": nl_k}
     t_f, _, f_f = stages["sumexp"]
     roofline_fwd = {"kernel": "k_sumexp", "achieved": round(mfma_per_flop * f_f / (t_f * 1e-3) / 1e12, 3),

@@ -92,3 +92,36 @@ def test_full_size_clip_symmetry():
     assert rel_err(l1, l2) < 1e-5
     assert max_rel(da1, db2) < 1e-4 and max_rel(db1, da2) < 1e-4
     assert math.isfinite(l1)
+
+
+@pytest.mark.parametrize("lit", [False, True], ids=["clip", "lit"])
+def test_stable_variant_at_config5_scale(lit):
+    """The Stable modules at config 5's shape (N = 262144, D = 1152, bf16,
+    normalized inputs, T = 0.05), the scale the reference's docstring claims
+    for them ("300k+ works just fine", clip_loss.py:380, lit_loss.py:369):
+    the same loss as the standard module, and gradients sqrt(N T) times the
+    standard ones (grad scale sqrt(N/T) in place of 1/T, clip_loss.py:299,
+    lit_loss.py:289).  Both gradients are rounded to bf16 (unit roundoff
+    2^-8), so they may differ by 2^-7 of an element: bar 1e-2 of the largest."""
+    from memoryefficientclip_amd import StableMemoryEfficientCLIPLoss, StableMemoryEfficientLiTLoss
+    n, d, t = 262144, 1152, 0.05
+    a, b = correlated_pair(n, d, seed=0, dtype=torch.float32)
+    say(f"Stable {'LiT' if lit else 'CLIP'} at n={n} d={d} bf16 T={t}")
+    out = []
+    for cls in ((MemoryEfficientLiTLoss, StableMemoryEfficientLiTLoss) if lit else
+                (MemoryEfficientCLIPLoss, StableMemoryEfficientCLIPLoss)):
+        ga = a.to(DEV, torch.bfloat16).requires_grad_(True)
+        gb = b.to(DEV, torch.bfloat16).requires_grad_(not lit)
+        loss = cls(t, True)(ga, gb)
+        loss.backward()
+        torch.cuda.synchronize()
+        out.append((loss.item(), ga.grad.float(), None if lit else gb.grad.float()))
+        del ga, gb
+    (l0, da0, db0), (l1, da1, db1) = out
+    s = math.sqrt(n * t)
+    le = rel_err(l1, l0)
+    ea = max_rel(da1, s * da0)
+    eb = 0.0 if lit else max_rel(db1, s * db0)
+    say(f"  loss {l0:.6f} vs {l1:.6f} (rel {le:.1e}); grads vs sqrt(N T) x standard: {ea:.2e} {eb:.2e}")
+    assert le < 1e-6 and ea < 1e-2 and eb < 1e-2
+    assert da1.abs().max() > 100 * da0.abs().max()  # the scale is applied (sqrt(N T) = 114.5)
