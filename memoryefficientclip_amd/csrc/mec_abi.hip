@@ -578,6 +578,7 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   float *acc_x = a.acc_x, *acc_y = a.acc_y;
   const bool lit = is_lit(mode);
   int rc = MEC_OK;
+  int cus = 0;  // compute units, for the persistent gradient-matrix launch
   const int bs = L.bs, nb = L.nb;
   if (step < 0 || step > nb)
     return fail(MEC_ERR_INVALID, "step %lld out of range [0, %d]", (long long)step, nb);
@@ -672,11 +673,21 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
         k_grad_contract<T, X3><<<(unsigned)grid_c, ConTileX<T>::NT, 0, s>>>(N, D, gb, bg, sp_c, acc_x, acc_y);
         rc = check_launch("grad_contract");
       }
-      if (!rc && grid > 0)
-        DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM,
-            k_grad_step<T, LIT, NORM, true, true, X3><<<(unsigned)grid, FwdTile<T, true>::NT, 0, s>>>(
-                (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g, acc_x,
-                acc_y)));
+      if (!rc && grid > 0) {
+        if (!X3 && !normalize) {
+          // chained tiles (the normalising epilogue would spill registers in the tile loop)
+          rc = compute_units(&cus);
+          if (!rc)
+            DISPATCH_BOOL(lit, LIT,
+                k_grad_g_chain<T, LIT, false><<<(unsigned)(grid < cus ? grid : cus), FwdTile<T, true>::NT, 0, s>>>(
+                    (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g));
+        } else {
+          DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM,
+              k_grad_step<T, LIT, NORM, true, true, X3><<<(unsigned)grid, FwdTile<T, true>::NT, 0, s>>>(
+                  (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g, acc_x,
+                  acc_y)));
+        }
+      }
     });
     if (rc) return rc;
     return check_launch("grad_step");
@@ -690,9 +701,19 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
     }
     if (!rc && grid > 0) {
       if constexpr (Is16<T>::value) {
-        DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-            k_grad_step<T, LIT, NORM, VEC, true><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
-                (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp_g, acc_x, acc_y))));
+        if (vec && !normalize) {
+          // direct-to-LDS tiles: persistent workgroups, one per CU, chained tiles
+          // (the normalising epilogue would spill registers in the tile loop)
+          rc = compute_units(&cus);
+          if (!rc)
+            DISPATCH_BOOL(lit, LIT,
+                k_grad_g_chain<T, LIT, false><<<(unsigned)(grid < cus ? grid : cus), FwdTile<T, true>::NT, 0, s>>>(
+                    (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp_g));
+        } else {
+          DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
+              k_grad_step<T, LIT, NORM, VEC, true><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
+                  (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp_g, acc_x, acc_y))));
+        }
       } else {
         DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, DISPATCH_BOOL(cdma, CDMA,
             k_grad_step<T, LIT, NORM, VEC, CDMA><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(

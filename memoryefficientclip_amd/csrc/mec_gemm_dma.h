@@ -420,13 +420,19 @@ __device__ __forceinline__ void prologue(const Operand& A, const Operand& B, cha
 // untouched (and waits with wait_barrier, not __syncthreads) until the next
 // call.  hook() runs once, after the first chunk's barrier: work issued there
 // (the previous tile's global stores) is not waited for by that barrier.
+// With VMF > 0 and vmf_first, the first chunk's barrier waits only until at
+// most VMF vector-memory operations are outstanding: the caller issued at
+// least VMF of them (the previous tile's global stores) after this tile's
+// chunk-0 loads, and vector-memory operations complete in issue order, so the
+// loads have landed while the stores still drain.
 struct NoHook {
   __device__ __forceinline__ void operator()() const {}
 };
-template <class G, bool ZERO, bool CHAIN, class Hook = NoHook>
+template <class G, bool ZERO, bool CHAIN, class Hook = NoHook, int VMF = 0>
 __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_rsrc_t ra_next,
                                               __amdgpu_buffer_rsrc_t rb_next, bool has_next, int K, char* lds,
-                                              int& p0, f32x16 (&acc)[G::FM][G::FN], const Hook& hook = Hook()) {
+                                              int& p0, f32x16 (&acc)[G::FM][G::FN], const Hook& hook = Hook(),
+                                              bool vmf_first = false) {
   static_assert(G::S == 2 && G::NS == 4, "two stages, four k-steps per chunk");
   if constexpr (ZERO) {
 #pragma unroll
@@ -442,7 +448,11 @@ __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_r
   const int nk = (K + BK - 1) / BK;
   Frags<G> f0, f1;
   for (int kt = 0; kt < nk; ++kt) {
-    wait_barrier<0>();  // chunk kt landed; every wave is done with the other stage
+    // chunk kt landed; every wave is done with the other stage
+    if (VMF > 0 && kt == 0 && vmf_first)
+      wait_barrier<VMF>();
+    else
+      wait_barrier<0>();
     lgkm_wait<0>(f1);   // f1 (the last step of chunk kt-1) landed before its MFMAs
     sched_fence();
     char* cs = lds + ((kt + p0) & 1) * G::STAGE;

@@ -118,12 +118,14 @@ struct TileD : PackOf<KIND>::type {
   static __device__ __forceinline__ void start(const Op& a, const Op& b, void* lds, Plan& lp) {
     gdma::prologue<G>(a, b, (char*)lds, lp);
   }
-  template <class Hook>
+  template <class Hook, int VMF = 0>
   static __device__ __forceinline__ void chain(Plan& lp, const Op& an, const Op& bn, bool has_next, int K, void* lds,
-                                               int& p0, f32x16 (&acc)[FM][FN], const Hook& hook) {
-    gdma::mainloop_core<G, true, true>(lp, Plan::rsrc_a(an), Plan::rsrc_b(bn), has_next, K, (char*)lds, p0, acc,
-                                       hook);
+                                               int& p0, f32x16 (&acc)[FM][FN], const Hook& hook,
+                                               bool vmf_first = false) {
+    gdma::mainloop_core<G, true, true, Hook, VMF>(lp, Plan::rsrc_a(an), Plan::rsrc_b(bn), has_next, K, (char*)lds,
+                                                  p0, acc, hook, vmf_first);
   }
+  static constexpr int STAGE_BYTES = G::STAGE;  // one ring stage
 };
 
 // Input element types: float, bf16 bits (uint16_t), fp16 (_Float16).  The
@@ -689,6 +691,72 @@ __device__ __forceinline__ void grad_gt_store_lds_x3(const f32x16 (&acc)[TL::FM]
   }
 }
 
+// Chained 16-bit gradient-matrix tiles (k_grad_g_chain): G'^T staged half a
+// tile at a time in the ring stage the next tile's loads leave free (64 KB).
+// Half h holds tile columns j of blocks bn = 2h, 2h + 1 of each wave column:
+// staging row s = wn * 64 + (bn - 2h) * 32 + l % 32 (512 bytes, no padding),
+// with the 8-byte chunk c (4 consecutive i) of row s at c ^ (s % 32), so that
+// the 32 lanes writing one chunk of 32 rows hit 32 distinct bank pairs and a
+// half-wave reading one row covers it once.  Each staged row is one 512-byte
+// row of G'^T, written as 32 16-byte stores; 16 per lane per tile.
+template <class TL>
+constexpr int gt_chain_stores() {
+  return 2 * (TL::BN / 2) * (TL::BM * 2 / 16) / TL::NT;
+}
+template <class TL, bool LIT, bool NORM, bool MASK, int GSC>
+__device__ __forceinline__ void grad_gt_store_chain(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0,
+                                                    int N, uint16_t* __restrict__ GTb, int bs, const float* s_rx,
+                                                    const float* s_ry, const float* s_ir, const float* s_ic,
+                                                    char* stage) {
+  static_assert(TL::BM == 256 && TL::WN == 2 && TL::FN == 4 && TL::TN == 128, "256 x 256 tiles, 2 wave columns");
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      const int bn = 2 * half + bb;
+      const int nl = wn * TL::TN + bn * 32 + (lane & 31);
+      const int j = j0 + nl;
+      const int srow = wn * 64 + bb * 32 + (lane & 31);
+      const float cy = NORM ? c * s_ry[nl] : c;
+      const float icj = s_ic[nl];
+#pragma unroll
+      for (int bm = 0; bm < TL::FM; ++bm) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          float gv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g4 + e;
+            const int ml = wm * TL::TM + bm * 32 + acc_row(r, lane);
+            const int i = i0 + ml;
+            const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
+            const float ex = fast_exp2(fmaf(sc, cy, -c));
+            float g = LIT ? ex * s_ir[ml] : ex * (s_ir[ml] + icj);
+            if (GSC != 1) g *= (float)GSC;  // storage scale (exact: a power of two)
+            if (MASK) g = (i < N && j < N && i != j) ? g : 0.f;
+            gv[e] = g;
+          }
+          const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g4, lane);
+          const int pos = (ml >> 2) ^ (srow & 31);
+          TL::store4((uint16_t*)(stage + srow * 512 + pos * 8), gv[0], gv[1], gv[2], gv[3]);
+        }
+      }
+    }
+    lds_barrier();
+    // the staged half: row s is tile column wn * TN + half * 64 + s % 64
+    for (int v = threadIdx.x; v < (TL::BN / 2) * 32; v += TL::NT) {
+      const int srow = v >> 5, cv = v & 31, k = srow & 31;
+      u32x4 u = *(const u32x4*)(stage + srow * 512 + ((cv ^ (k >> 1)) << 4));
+      if (k & 1) u = u32x4{u.z, u.w, u.x, u.y};
+      const int nl = (srow >> 6) * TL::TN + half * 64 + (srow & 63);
+      __builtin_nontemporal_store(u, (u32x4*)(GTb + (int64_t)nl * bs + cv * 8));
+    }
+    if (half == 0) lds_barrier();  // every wave done reading before the second half is staged
+  }
+}
+
 // Recompute the similarity tile (i0, j0) and store G'_ij = E_ij (1/R_i + 1/C_j)
 // (LiT: E_ij / R_i) for i != j, 0 on the diagonal and outside [0, N), into
 // the G' block at Gb (row pitch bs) and, for CLIP, transposed at GTb (X3: its
@@ -890,6 +958,117 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::bwd)) void k_g
   T* GTl = X3 ? (T*)gb.gt_lo[buf] + gt_off : nullptr;
   grad_g_tile<TF, T, LIT, NORM, VEC, X3>(X, ldx, Y, ldy, N, D, kmax, c, ws, Gb, GTb, GTl, bg.bs, i0, j0, lds, s_rx,
                                          s_ry, s_ir, s_ic);
+}
+
+// 16-bit gradient-matrix tiles of diagonal sp.diag_g on the direct-to-LDS
+// 256 x 256 tiles, chained like the forward: persistent workgroups walk the
+// tiles t = blockIdx.x + i * gridDim.x (XCD-grouped order), and the last
+// chunk of each tile's k-loop loads chunk 0 of the next, which lands while
+// the tile's G'^T is staged (in the other ring stage) and stored
+// (grad_gt_store_chain).  The next tile's first barrier waits only for those
+// loads, not for the stores.  The per-row and per-column vectors of a tile
+// (rx, ry, 1/R, 1/C) reach LDS by direct loads into one of two buffers,
+// issued right after the previous tile's first barrier (when every wave is
+// done with that buffer).
+template <typename T, bool LIT, bool NORM>
+__global__ __launch_bounds__((FwdTile<T, true>::NT), 1) void k_grad_g_chain(
+    const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
+    const float* __restrict__ ws, GradBufs gb, BlockGrid bg, StepPlan sp) {
+  using TL = FwdTile<T, true>;
+  static_assert(TL::CHAIN && GtOnly<T>::value, "chained 16-bit direct-to-LDS tiles");
+  static_assert(TL::BM == 256 && TL::BN == 256 && TL::NT == 512, "one 64-float quarter per vector load, 8 waves");
+  static_assert(TL::STAGE_BYTES >= (TL::BN / 2) * 512, "a staged half fits one ring stage");
+  enum { V_RX = 0, V_RY = 1, V_IR = 2, V_IC = 3 };
+  __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) float s_vec[2][4][TL::BM];
+  constexpr int NST = gt_chain_stores<TL>();
+  const int64_t n64 = N;
+  const int64_t blk = (int64_t)bg.bs * bg.bs;
+  const int buf = sp.diag_g & 1;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  // tile -> (i0, j0, its place in the G'^T block); false for padding ids and tiles wholly past N
+  auto coords = [&](int tile, int& i0, int& j0, uint16_t*& gt) {
+    const int pid = xcd_remap(tile, sp.g_pad);
+    if (pid >= sp.g_n) return false;
+    int tmg, tn;
+    group_tile(pid, bg.nb * bg.gtm, bg.gtn, 8, tmg, tn);
+    const int I = tmg / bg.gtm, tm = tmg - I * bg.gtm;
+    const int J = (I + sp.diag_g) % bg.nb;
+    i0 = I * bg.bs + tm * TL::BM;
+    j0 = J * bg.bs + tn * TL::BN;
+    gt = (uint16_t*)gb.gt[buf] + I * blk + (int64_t)(tn * TL::BN) * bg.bs + tm * TL::BM;
+    return i0 < N && j0 < N;
+  };
+  auto next_valid = [&](int tile, int& i0, int& j0, uint16_t*& gt) {
+    for (; tile < sp.g_pad; tile += (int)gridDim.x)
+      if (coords(tile, i0, j0, gt)) return tile;
+    return sp.g_pad;
+  };
+  auto op_a = [&](int i0) { return tile_op<TL>(X + (int64_t)i0 * ldx, ldx, min(N - i0, TL::BM), kmax); };
+  auto op_b = [&](int j0) { return tile_op<TL>(Y + (int64_t)j0 * ldy, ldy, min(N - j0, TL::BN), kmax); };
+  // The vectors of tile (i0, j0) into s_vec[b]: load k (of 16) fills quarter
+  // k % 4 of vector k / 4; wave w issues loads w and w + 8.  Entries past N
+  // read as 0 (the buffer descriptor ends at N); 1/R and 1/C carry the
+  // storage scale of G' in the epilogue.
+  auto vec_loads = [&](int i0, int j0, int b) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int k = w + 8 * u, v = k >> 2, qr = k & 3;
+      const bool need = v == V_IR || (v == V_IC && !LIT) || ((v == V_RX || v == V_RY) && NORM);
+      if (!need) continue;
+      const int slot = v == V_RX ? WS_RX : v == V_RY ? WS_RY : v == V_IR ? WS_INV_ROW : WS_INV_COL;
+      const int o = (v == V_RX || v == V_IR) ? i0 : j0;
+      const __amdgpu_buffer_rsrc_t r =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(ws + slot * n64 + o), 0, (N - o) * 4, 0x00020000);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (__attribute__((address_space(3))) void*)&s_vec[b][v][qr * 64], 4, (uint32_t)(qr * 64 + lane) * 4, 0,
+          0, 0);
+    }
+  };
+  int i0, j0;
+  uint16_t* gt;
+  int tile = next_valid(blockIdx.x, i0, j0, gt);
+  if (tile >= sp.g_pad) return;
+  vec_loads(i0, j0, 0);
+  typename TL::Plan lp;
+  TL::start(op_a(i0), op_b(j0), lds, lp);
+  int p0 = 0, vb = 0;
+  bool first = true;
+  f32x16 acc[TL::FM][TL::FN];
+  for (;;) {
+    int i1 = i0, j1 = j0;
+    uint16_t* gt1 = gt;
+    const int next = next_valid(tile + (int)gridDim.x, i1, j1, gt1);
+    const bool has_next = next < sp.g_pad;
+    // the next tile's vectors go out after this tile's first barrier; the
+    // first tile's chunk 0 has no stores behind it: its barrier waits for all
+    auto hook = [&] {
+      if (has_next) vec_loads(i1, j1, vb ^ 1);
+    };
+    TL::template chain<decltype(hook), NST>(lp, op_a(i1), op_b(j1), has_next, D, lds, p0, acc, hook, !first);
+    first = false;
+    // every wave is past its last read of the stage the staging reuses (the
+    // one the next tile's chunk 0 does not go to)
+    lds_barrier();
+    char* stage = lds + (p0 ^ 1) * TL::STAGE_BYTES;
+    const float* sv = &s_vec[vb][0][0];
+    const bool diag = i0 < j0 + TL::BN && j0 < i0 + TL::BM;
+    if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
+      grad_gt_store_chain<TL, LIT, NORM, false, (int)GScale<T>::value>(
+          acc, c, i0, j0, N, gt, bg.bs, sv + V_RX * TL::BM, sv + V_RY * TL::BM, sv + V_IR * TL::BM,
+          sv + V_IC * TL::BM, stage);
+    else
+      grad_gt_store_chain<TL, LIT, NORM, true, (int)GScale<T>::value>(
+          acc, c, i0, j0, N, gt, bg.bs, sv + V_RX * TL::BM, sv + V_RY * TL::BM, sv + V_IR * TL::BM,
+          sv + V_IC * TL::BM, stage);
+    if (!has_next) break;
+    tile = next;
+    i0 = i1;
+    j0 = j1;
+    gt = gt1;
+    vb ^= 1;
+  }
+  gdma::drain_loads();
 }
 
 }  // namespace mec
