@@ -57,7 +57,7 @@ constexpr uint32_t OOB = 0x80000000u;  // buffer offset that reads as zero
 // and block) and fp32 (v_mfma_f32_32x32x2_f32, four per k-step and block)
 enum Kind { K_BF16 = 0, K_F16 = 1, K_F32 = 2 };
 
-template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16>
+template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16, int SA_ = 2>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_;
   static constexpr int KIND = KIND_;
@@ -83,7 +83,19 @@ struct Geo {
   static constexpr int FM = TM / 32, FN = TN / 32;     // 32x32 MFMA blocks per wave
   static constexpr int ROWS = BM + BN;
   static constexpr int STAGE = ROWS * ROWB;
-  static constexpr int LDS_BYTES = S * STAGE;
+  // A stages: 2 (the ring's stages hold A and B of one chunk each), or 3 (A
+  // gets a ring of its own, one chunk deeper than B's, for an A streamed from
+  // HBM; not chained): then A stages s = 0..2 come first, B's two after them
+  static constexpr int SA = SA_;
+  static_assert(SA == 2 || SA == 3, "two or three A stages");
+  static constexpr int A_STAGE = BM * ROWB, B_STAGE = BN * ROWB;
+  static constexpr int LDS_BYTES = SA == 2 ? S * STAGE : 3 * A_STAGE + 2 * B_STAGE;
+  static __device__ __forceinline__ char* a_stage(char* lds, int s) {
+    return SA == 2 ? lds + s * STAGE : lds + s * A_STAGE;
+  }
+  static __device__ __forceinline__ char* b_stage(char* lds, int s) {
+    return SA == 2 ? lds + s * STAGE + A_STAGE : lds + 3 * A_STAGE + s * B_STAGE;
+  }
   static constexpr int IPW = ROWS / RPB / NW;          // load instructions per wave per chunk
   static constexpr int NMF = FM * FN * MPB;            // MFMAs per k-step
   static_assert(ROWS % (RPB * NW) == 0 && BM % RPB == 0, "load split");
@@ -159,10 +171,11 @@ struct LoadPlan {
       }
     }
   }
-  // load i of the chunk starting at k0 into `stage`.  Chunks at or past kmax
-  // read as zeros (out-of-range offsets), so loads may run past the last chunk.
+  // load i of the chunk starting at k0 into the A stage ad (loads i <
+  // A_LOADS) or the B stage bd.  Chunks at or past kmax read as zeros
+  // (out-of-range offsets), so loads may run past the last chunk.
   template <int I>
-  __device__ __forceinline__ void issue(int k0, char* stage) const {
+  __device__ __forceinline__ void issue(int k0, char* ad, char* bd) const {
     constexpr bool isa = I < A_LOADS;
     uint32_t off, soff;
     if (G::TA && isa) {
@@ -172,9 +185,9 @@ struct LoadPlan {
       off = (k0 + kv < (isa ? kmax_a : kmax_b)) ? voff[I] : OOB;
       soff = (uint32_t)k0 * G::ESZ;
     }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        isa ? ra : rb, (__attribute__((address_space(3))) void*)(stage + (I * G::NW + w) * 1024), 16, off, soff, 0,
-        0);
+    char* dst = isa ? ad + (I * G::NW + w) * 1024 : bd + (I * G::NW + w - A_BLOCKS) * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(isa ? ra : rb, (__attribute__((address_space(3))) void*)dst, 16, off,
+                                             soff, 0, 0);
   }
 };
 
@@ -213,7 +226,7 @@ __device__ __forceinline__ i16x4_t read_tr4(const char* p) {
 }
 
 template <class G>
-__device__ __forceinline__ void read_frags(const char* stage, int s, Frags<G>& f) {
+__device__ __forceinline__ void read_frags(const char* stage, const char* bstage, int s, Frags<G>& f) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w / G::WN, wn = w % G::WN;
   const int q = lane & 31, h = lane >> 5;
@@ -241,7 +254,7 @@ __device__ __forceinline__ void read_frags(const char* stage, int s, Frags<G>& f
     const uint32_t abase = lds_off(stage + (wm * G::TM + q) * G::ROWB + off);
     static_for<G::FM>([&](auto i) { f.a[i] = lds_read_b128<i * 32 * G::ROWB>(abase); });
   }
-  const uint32_t bbase = lds_off(stage + (G::BM + wn * G::TN + q) * G::ROWB + off);
+  const uint32_t bbase = lds_off(bstage + (wn * G::TN + q) * G::ROWB + off);
   static_for<G::FN>([&](auto j) { f.b[j] = lds_read_b128<j * 32 * G::ROWB>(bbase); });
 }
 
@@ -258,13 +271,13 @@ template <class G>
 struct FragReader {
   uint32_t abase, bbase;
   uint32_t ta[G::TA ? G::FM : 1][2];  // transposed A: per fragment and half
-  __device__ __forceinline__ FragReader(const char* stage, int s) {
+  __device__ __forceinline__ FragReader(const char* stage, const char* bstage, int s) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wm = w / G::WN, wn = w % G::WN;
     const int q = lane & 31, h = lane >> 5;
     const int off = (((h * G::NS + s) ^ G::swz(q)) << 4);
     abase = lds_off(stage + (wm * G::TM + q) * G::ROWB + off);
-    bbase = lds_off(stage + (G::BM + wn * G::TN + q) * G::ROWB + off);
+    bbase = lds_off(bstage + (wn * G::TN + q) * G::ROWB + off);
     if constexpr (G::TA) {
       // the addresses of read_frags' transposed-A branch
       const int g = lane >> 4, j = lane & 15;
@@ -331,7 +344,7 @@ __device__ __forceinline__ void wait_barrier() {
 // MFMAs of one k-step with loads [L0, L1) interleaved, in program order.
 template <class G, int L0, int L1>
 __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const LoadPlan<G>& lp,
-                                          int k0, char* stage) {
+                                          int k0, char* ad, char* bd) {
   constexpr int NL = L1 - L0;
   static_assert(NL <= G::NMF, "at most one load per MFMA");
   // one load after every EVERY-th MFMA: floor(NMF / EVERY) >= NL slots
@@ -349,7 +362,7 @@ __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM
     }
     if constexpr (NL > 0 && (m % EVERY) == EVERY - 1 && L0 + m / EVERY < L1) {
       sched_fence();
-      lp.template issue<L0 + m / EVERY>(k0, stage);
+      lp.template issue<L0 + m / EVERY>(k0, ad, bd);
       sched_fence();
     }
   });
@@ -359,7 +372,7 @@ __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM
 // land during the step and the next step's MFMAs need not wait for them.
 template <class G, int L0, int L1>
 __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const LoadPlan<G>& lp,
-                                             int k0, char* stage, const FragReader<G>& rd, Frags<G>& nf) {
+                                             int k0, char* ad, char* bd, const FragReader<G>& rd, Frags<G>& nf) {
   constexpr int NL = L1 - L0;
   constexpr int NR = frag_reads<G>();
   static_assert(NL <= G::NMF && (NR + 1) / 2 <= G::NMF, "slots");
@@ -383,7 +396,7 @@ __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G:
     }
     if constexpr (NL > 0 && (m % EVERY) == EVERY - 1 && L0 + m / EVERY < L1) {
       sched_fence();
-      lp.template issue<L0 + m / EVERY>(k0, stage);
+      lp.template issue<L0 + m / EVERY>(k0, ad, bd);
       sched_fence();
     }
   });
@@ -407,7 +420,10 @@ __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G:
 template <class G>
 __device__ __forceinline__ void prologue(const Operand& A, const Operand& B, char* lds, LoadPlan<G>& lp) {
   lp.init(A, B);
-  static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, lds); });
+  static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, G::a_stage(lds, 0), G::b_stage(lds, 0)); });
+  // three A stages: A's chunk 1 as well, issued last (the first barrier waits for all but it)
+  if constexpr (G::SA == 3)
+    static_for<LoadPlan<G>::A_LOADS>([&](auto i) { lp.template issue<i>(G::BK, G::a_stage(lds, 1), nullptr); });
 }
 
 // The k-loop of one tile whose chunk 0 was issued into stage p0 (chunk kt
@@ -434,6 +450,7 @@ __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_r
                                               int& p0, f32x16 (&acc)[G::FM][G::FN], const Hook& hook = Hook(),
                                               bool vmf_first = false) {
   static_assert(G::S == 2 && G::NS == 4, "two stages, four k-steps per chunk");
+  static_assert(G::SA == 2 || !CHAIN, "three A stages: one tile per call");
   if constexpr (ZERO) {
 #pragma unroll
     for (int i = 0; i < G::FM; ++i)
@@ -443,20 +460,39 @@ __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_r
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   }
   constexpr int BK = G::BK;
+  constexpr int LA = LoadPlan<G>::A_LOADS;
   constexpr int L1 = G::IPW / 2, L2 = G::IPW;  // loads issued in k-steps 0 and 1
-  static_assert(G::IPW % 2 == 0, "even load split");
+  static_assert(G::IPW % 2 == 0 && (G::SA == 2 || LA == L1), "even load split");
+  // Two A stages: chunk kt + 1's A loads in k-step 0, its B loads in k-step 1.
+  // Three: chunk kt + 1's B loads in k-step 0, then chunk kt + 2's A loads in
+  // k-step 1 (A streams from HBM: one chunk more of lead time).
+  constexpr int S0A = G::SA == 2 ? 0 : LA, S0B = G::SA == 2 ? L1 : L2;
+  constexpr int S1A = G::SA == 2 ? L1 : 0, S1B = G::SA == 2 ? L2 : LA;
   const int nk = (K + BK - 1) / BK;
   Frags<G> f0, f1;
   for (int kt = 0; kt < nk; ++kt) {
-    // chunk kt landed; every wave is done with the other stage
-    if (VMF > 0 && kt == 0 && vmf_first)
+    // chunk kt landed (three A stages: all but the A loads of chunk kt + 1,
+    // issued last); every wave is done with the stages refilled below
+    if constexpr (G::SA == 3)
+      wait_barrier<LA>();
+    else if (VMF > 0 && kt == 0 && vmf_first)
       wait_barrier<VMF>();
     else
       wait_barrier<0>();
     lgkm_wait<0>(f1);   // f1 (the last step of chunk kt-1) landed before its MFMAs
     sched_fence();
-    char* cs = lds + ((kt + p0) & 1) * G::STAGE;
-    char* ns = lds + ((kt + p0 + 1) & 1) * G::STAGE;
+    char *ca, *cb, *na, *nb;
+    if constexpr (G::SA == 2) {
+      ca = G::a_stage(lds, (kt + p0) & 1);
+      cb = G::b_stage(lds, (kt + p0) & 1);
+      na = G::a_stage(lds, (kt + p0 + 1) & 1);
+      nb = G::b_stage(lds, (kt + p0 + 1) & 1);
+    } else {
+      ca = G::a_stage(lds, kt % 3);
+      cb = G::b_stage(lds, kt & 1);
+      na = G::a_stage(lds, (kt + 2) % 3);
+      nb = G::b_stage(lds, (kt + 1) & 1);
+    }
     int k1 = (kt + 1) * BK;
     if constexpr (CHAIN) {
       if (kt + 1 == nk && has_next) {
@@ -465,28 +501,29 @@ __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_r
         k1 = 0;
       }
     }
-    const FragReader<G> r0(cs, 0), r1(cs, 1), r2(cs, 2), r3(cs, 3);
+    const int k2 = G::SA == 2 ? k1 : (kt + 2) * BK;  // the chunk k-step 1 loads
+    const FragReader<G> r0(ca, cb, 0), r1(ca, cb, 1), r2(ca, cb, 2), r3(ca, cb, 3);
     if (kt > 0) {
-      mfma_step_rd<G, 0, L1>(f1, acc, lp, k1, ns, r0, f0);
+      mfma_step_rd<G, S0A, S0B>(f1, acc, lp, k1, na, nb, r0, f0);
     } else {
-      read_frags<G>(cs, 0, f0);
-      static_for<L1>([&](auto i) { lp.template issue<i>(k1, ns); });
+      read_frags<G>(ca, cb, 0, f0);
+      static_for<S0B - S0A>([&](auto i) { lp.template issue<S0A + i>(k1, na, nb); });
       hook();
     }
     lgkm_wait<0>(f0);
     sched_fence();
-    mfma_step_rd<G, L1, L2>(f0, acc, lp, k1, ns, r1, f1);
+    mfma_step_rd<G, S1A, S1B>(f0, acc, lp, k2, na, nb, r1, f1);
     lgkm_wait<0>(f1);
     sched_fence();
-    mfma_step_rd<G, 0, 0>(f1, acc, lp, 0, lds, r2, f0);
+    mfma_step_rd<G, 0, 0>(f1, acc, lp, 0, lds, lds, r2, f0);
     lgkm_wait<0>(f0);
     sched_fence();
-    mfma_step_rd<G, 0, 0>(f0, acc, lp, 0, lds, r3, f1);
+    mfma_step_rd<G, 0, 0>(f0, acc, lp, 0, lds, lds, r3, f1);
     sched_fence();
   }
   lgkm_wait<0>(f1);
   sched_fence();
-  mfma_step<G, 0, 0>(f1, acc, lp, 0, lds);
+  mfma_step<G, 0, 0>(f1, acc, lp, 0, lds, lds);
   if constexpr (CHAIN) p0 = (p0 + nk) & 1;
 }
 

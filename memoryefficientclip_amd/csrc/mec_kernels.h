@@ -97,11 +97,11 @@ template <> struct PackOf<gdma::K_F32> { using type = PackF32; };
 // multiples of the elements per 16-byte vector), element kind KIND (bf16,
 // fp16 or fp32); TA_: A stored k-row-major (a transposed 16-bit
 // gradient-matrix block)
-template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND>
+template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND, int SA_ = 2>
 struct TileD : PackOf<KIND>::type {
   using Elem = typename std::conditional<KIND == gdma::K_F32, float, uint16_t>::type;
   using Op = gdma::Operand;
-  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND>;
+  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, SA_>;
   static constexpr bool TA = TA_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
@@ -154,9 +154,10 @@ template <typename T, bool DMA> struct ConTileSel<T, DMA, false> {
   using x = typename std::conditional<DMA, TileD<128, 128, false, 2, 2, gdma::K_F32>, TileF32>::type;
   using y = x;
 };
+// (the gradient-matrix operand streams from HBM: three A stages, 160 KB of LDS)
 template <typename T, bool DMA> struct ConTileSel<T, DMA, true> {
-  using x = TileD<256, 256, true, 4, 2, kind16<T>()>;
-  using y = TileD<256, 256, false, 4, 2, kind16<T>()>;
+  using x = TileD<256, 256, true, 4, 2, kind16<T>(), 3>;
+  using y = TileD<256, 256, false, 4, 2, kind16<T>(), 3>;
 };
 template <typename T, bool DMA = true> using ConTileX = typename ConTileSel<T, DMA>::x;
 template <typename T, bool DMA = true> using ConTileY = typename ConTileSel<T, DMA>::y;
