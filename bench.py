@@ -431,12 +431,15 @@ def main():
     log(f"bench: backward blocking {blocking}")
     # dominant kernel: the backward pipeline step, nb + 1 launches of mec_grad_step per
     # step, about 3/4 of the step's flop: k_grad_step (fp32: gradient-matrix tiles and
-    # contractions in one kernel; 16-bit: the gradient-matrix tiles, with the
-    # contractions in k_grad_contract before it)
+    # contractions in one kernel; 16-bit: the gradient-matrix tiles, chained in
+    # k_grad_g_chain for normalized inputs, with the contractions in k_grad_contract
+    # before them)
     # (bf16x3: MFMA flop = 3 x algorithmic flop, against the bf16 peak)
     t_k, nl_k, f_k = stages["grad_step"]
     achieved = mfma_per_flop * f_k / (t_k * 1e-3) / 1e12
-    kernels = ["k_grad_step"] if arith == "f32" else ["k_grad_contract", "k_grad_step"]
+    # (16-bit data with normalized inputs: the gradient-matrix tiles run chained, in k_grad_g_chain)
+    gkern = "k_grad_g_chain" if (normalized and not x3) else "k_grad_step"
+    kernels = ["k_grad_step"] if arith == "f32" else ["k_grad_contract", gkern]
     traffic = measured_traffic(f"{mode}_n{n}_d{d}_{arith}", kernels)
     if traffic is not None and len(kernels) > 1:
         # each kernel runs in nb of the nb + 1 pipeline launches
