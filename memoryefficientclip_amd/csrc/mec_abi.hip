@@ -331,6 +331,15 @@ int round8(int v) { return (v + 7) & ~7; }
 // panel (128 rows of pitch ldt) and a gradient-matrix block panel (128 rows of
 // pitch bs) fit its 32-bit offsets, i.e. up to n of about 4.2M; beyond that on
 // the register-staged core.  MEC_F32_CONTRACT_DMA=0 forces the latter (tests).
+// 64 x 64 fp32 tiles (f32_small_n; MEC_F32_SMALL_TILES=0 or 1 overrides, for tests)
+bool f32_small_tiles(int64_t n) {
+  if (const char* env = std::getenv("MEC_F32_SMALL_TILES")) {
+    if (env[0] == '0') return false;
+    if (env[0] == '1') return true;
+  }
+  return f32_small_n(n);
+}
+
 bool f32_contract_dma(int64_t ldt, int64_t bs) {
   if (const char* env = std::getenv("MEC_F32_CONTRACT_DMA"))
     if (env[0] == '0') return false;
@@ -442,7 +451,9 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   x = g.x, ldx = g.ldx, y = g.y, ldy = g.ldy, d = g.d, dtype = g.dtype;
   const int N = (int)n, D = (int)d;
   const bool vec = vec_ok(x, ldx, y, ldy, d, dtype);
-  const TileDims td = fwd_tile_dims(dtype, vec);
+  // (the deterministic sums keep the 128 x 128 tiles)
+  const bool small = dtype == MEC_DTYPE_F32 && vec && !(mode & MEC_FLAG_DETERMINISTIC) && f32_small_tiles(n);
+  const TileDims td = fwd_tile_dims(dtype, vec, small);
   const int tiles_m = (int)((n + td.bm - 1) / td.bm), tiles_n = (int)((n + td.bn - 1) / td.bn);
   const int64_t nwg = (int64_t)tiles_m * tiles_n;
   if (nwg > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "forward grid too large");
@@ -478,8 +489,14 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
     // the chained (direct-to-LDS) tiles: one resident workgroup per slot
     const int64_t slots = (int64_t)cus * Occ<T, VEC>::fwd;
     if (FwdChain<T, VEC, NORM>::value && nwg > slots) grid.x = (unsigned)slots;
-    k_sumexp<T, LIT, NORM, VEC><<<grid, FwdTile<T, VEC>::NT, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, D,
-                                                                    c, workspace, tiles_m, tiles_n);
+    if (small) {
+      if constexpr (std::is_same<T, float>::value && VEC)
+        k_sumexp<T, LIT, NORM, VEC, true><<<grid, GemmTile<T, VEC, true>::NT, 0, s>>>(
+            (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, tiles_m, tiles_n);
+    } else {
+      k_sumexp<T, LIT, NORM, VEC><<<grid, FwdTile<T, VEC>::NT, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, D,
+                                                                      c, workspace, tiles_m, tiles_n);
+    }
   }))));
   return check_launch("sumexp");
 }
@@ -498,13 +515,14 @@ int mec_finalize(int64_t n, int mode, float temperature, float* workspace, float
   const int nparts = (int)((n + FIN_ROWS - 1) / FIN_ROWS);
   // partials after the 8 slots (8 n floats: 8-byte aligned when the workspace is)
   double* partial = (double*)(workspace + (int64_t)WS_NSLOTS * n);
-  if (is_lit(mode)) {
-    k_finalize_rows<true><<<nparts, FIN_ROWS, 0, s>>>((int)n, inv_t, workspace, partial);
-    k_finalize_sum<true><<<1, 1024, 0, s>>>((int)n, nparts, partial, loss);
-  } else {
-    k_finalize_rows<false><<<nparts, FIN_ROWS, 0, s>>>((int)n, inv_t, workspace, partial);
-    k_finalize_sum<false><<<1, 1024, 0, s>>>((int)n, nparts, partial, loss);
-  }
+  DISPATCH_BOOL(is_lit(mode), LIT, {
+    if (nparts <= FIN_SINGLE) {
+      k_finalize_rows<LIT, true><<<1, FIN_ROWS, 0, s>>>((int)n, inv_t, workspace, partial, loss);
+    } else {
+      k_finalize_rows<LIT, false><<<nparts, FIN_ROWS, 0, s>>>((int)n, inv_t, workspace, partial, loss);
+      k_finalize_sum<LIT><<<1, 1024, 0, s>>>((int)n, nparts, partial, loss);
+    }
+  });
   return check_launch("finalize");
 }
 
@@ -590,7 +608,8 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   const bool vec = vec_ok(go.x, go.ldx, go.y, go.ldy, go.d, go.dtype);
   if (split && !vec) return fail(MEC_ERR_UNSUPPORTED, "split operands beyond the direct-load range");
   const bool cdma = f32_contract_dma(L.ldt, bs);
-  const TileDims tf = fwd_tile_dims(dtype, vec), tc = con_tile_dims(dtype);
+  const bool small = dtype == MEC_DTYPE_F32 && vec && cdma && f32_small_tiles(n);
+  const TileDims tf = fwd_tile_dims(dtype, vec, small), tc = con_tile_dims(dtype, small);
   BlockGrid bg{bs, nb, bs / tf.bm, bs / tf.bn, bs / tc.bm, (D + tc.bn - 1) / tc.bn};
   StepPlan sp{};
   sp.diag_g = step < nb ? (int)step : -1;
@@ -640,24 +659,22 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   if (step == 0) {
     // transposed normalised operands of the contractions: YT for the x side, XT for the y side
     const int64_t n64 = n;
-    dim3 tgrid((unsigned)(L.ldt / 64), (unsigned)((d + 63) / 64));
+    // one launch for both sides (blockIdx.z): YT when the x side is wanted,
+    // XT when the y side is
+    const unsigned nsides = (acc_x ? 1u : 0u) + (acc_y ? 1u : 0u);
+    dim3 tgrid((unsigned)(L.ldt / 64), (unsigned)((d + 63) / 64), nsides);
     if (split) {
-      DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(x3, LO, {
-        if (acc_x)
-          k_transpose_split<NORM, LO><<<tgrid, 256, 0, s>>>((const float*)y, ldy, N, D, workspace + WS_RY * n64,
-                                                            (uint16_t*)gb.yt, (uint16_t*)gb.yt_lo, L.ldt);
-        if (acc_y)
-          k_transpose_split<NORM, LO><<<tgrid, 256, 0, s>>>((const float*)x, ldx, N, D, workspace + WS_RX * n64,
-                                                            (uint16_t*)gb.xt, (uint16_t*)gb.xt_lo, L.ldt);
-      }));
+      using TS = TransSide<float, uint16_t>;
+      const TS ty{(const float*)y, ldy, workspace + WS_RY * n64, (uint16_t*)gb.yt, (uint16_t*)gb.yt_lo};
+      const TS tx{(const float*)x, ldx, workspace + WS_RX * n64, (uint16_t*)gb.xt, (uint16_t*)gb.xt_lo};
+      DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(x3, LO,
+          k_transpose_split<NORM, LO><<<tgrid, 256, 0, s>>>(acc_x ? ty : tx, tx, N, D, L.ldt)));
     } else {
       DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, {
-        if (acc_x)
-          k_transpose<T, NORM><<<tgrid, 256, 0, s>>>((const T*)y, ldy, N, D, workspace + WS_RY * n64, (T*)gb.yt,
-                                                     L.ldt);
-        if (acc_y)
-          k_transpose<T, NORM><<<tgrid, 256, 0, s>>>((const T*)x, ldx, N, D, workspace + WS_RX * n64, (T*)gb.xt,
-                                                     L.ldt);
+        using TS = TransSide<T>;
+        const TS ty{(const T*)y, ldy, workspace + WS_RY * n64, (T*)gb.yt, nullptr};
+        const TS tx{(const T*)x, ldx, workspace + WS_RX * n64, (T*)gb.xt, nullptr};
+        k_transpose<T, NORM><<<tgrid, 256, 0, s>>>(acc_x ? ty : tx, tx, N, D, L.ldt);
       }));
     }
     rc = check_launch("transpose");
@@ -714,6 +731,12 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
               k_grad_step<T, LIT, NORM, VEC, true><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
                   (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp_g, acc_x, acc_y))));
         }
+      } else if (small) {
+        if constexpr (std::is_same<T, float>::value)
+          DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM,
+              k_grad_step<T, LIT, NORM, true, true, false, true><<<(unsigned)grid, GemmTile<T, true, true>::NT, 0,
+                                                                   s>>>(
+                  (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y)));
       } else {
         DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, DISPATCH_BOOL(cdma, CDMA,
             k_grad_step<T, LIT, NORM, VEC, CDMA><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
@@ -820,14 +843,13 @@ int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   const float* ry = workspace + WS_RY * n64;
   const float* kap = workspace + WS_KAPPA * n64;
   const float a = (float)((double)grad_scale / (lit ? (double)n : 2.0 * (double)n));
-  dim3 grid((unsigned)((n + 3) / 4));
+  // one launch for both sides (blockIdx.y)
+  const unsigned nsides = (acc_x ? 1u : 0u) + (acc_y ? 1u : 0u);
+  dim3 grid((unsigned)((n + 3) / 4), nsides);
   DISPATCH_DTYPE(data_dtype(dtype), T, DISPATCH_BOOL(normalize, NORM, {
-    if (acc_x)
-      k_postpass<T, NORM><<<grid, 256, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, rx, ry, kap, a,
-                                               grad_output, acc_x, (T*)dx);
-    if (acc_y)
-      k_postpass<T, NORM><<<grid, 256, 0, s>>>((const T*)y, ldy, (const T*)x, ldx, N, D, ry, rx, kap, a,
-                                               grad_output, acc_y, (T*)dy);
+    const PostSide<T> px{(const T*)x, ldx, (const T*)y, ldy, rx, ry, acc_x, (T*)dx};
+    const PostSide<T> py{(const T*)y, ldy, (const T*)x, ldx, ry, rx, acc_y, (T*)dy};
+    k_postpass<T, NORM><<<grid, 256, 0, s>>>(acc_x ? px : py, py, N, D, kap, a, grad_output);
   }));
   return check_launch("postpass");
 }

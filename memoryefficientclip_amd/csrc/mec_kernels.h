@@ -142,6 +142,12 @@ template <typename T> struct FwdTileSel<T, true, false> { using type = TileD<128
 template <typename T> struct FwdTileSel<T, true, true> { using type = TileD<256, 256, false, 4, 2, kind16<T>()>; };
 template <typename T> struct FwdTileSel<T, false, true> { using type = Tile16V<Is16<T>::f16>; };
 template <typename T, bool VEC> using FwdTile = typename FwdTileSel<T, VEC>::type;
+// fp32 at a small N (few 128 x 128 tiles for the CUs): 64 x 64 direct-to-LDS
+// tiles of 2 x 2 waves (32 x 32 each) for the forward, the gradient-matrix
+// tiles and the contractions
+template <typename T, bool VEC, bool SMALL> struct GemmTileSel { using type = FwdTile<T, VEC>; };
+template <> struct GemmTileSel<float, true, true> { using type = TileD<64, 64, false, 2, 2, gdma::K_F32>; };
+template <typename T, bool VEC, bool SMALL> using GemmTile = typename GemmTileSel<T, VEC, SMALL>::type;
 // Contractions.  fp32 stores the gradient-matrix blocks in both layouts (G'
 // for the x side, G'^T for the y side) and runs them inside k_grad_step, on
 // the direct-to-LDS core when its 32-bit offsets reach across a transposed
@@ -161,6 +167,14 @@ template <typename T, bool DMA> struct ConTileSel<T, DMA, true> {
 };
 template <typename T, bool DMA = true> using ConTileX = typename ConTileSel<T, DMA>::x;
 template <typename T, bool DMA = true> using ConTileY = typename ConTileSel<T, DMA>::y;
+template <typename T, bool DMA, bool SMALL> struct ConTileSmall {
+  using x = ConTileX<T, DMA>;
+  using y = ConTileY<T, DMA>;
+};
+template <> struct ConTileSmall<float, true, true> {
+  using x = TileD<64, 64, false, 2, 2, gdma::K_F32>;
+  using y = x;
+};
 // the 16-bit types keep one layout of the gradient-matrix blocks (G'^T)
 template <typename T> struct GtOnly { static constexpr bool value = Is16<T>::value; };
 // Scale of the stored gradient-matrix entries.  0 < G'_ij <= 2 (E_ij <= 1,
@@ -253,12 +267,24 @@ __device__ __forceinline__ void sumexp_tile(const f32x16 (&acc)[TL::FM][TL::FN],
     sumexp_epilogue<TL, NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
   else
     sumexp_epilogue<TL, NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
+  if constexpr (TL::FM == 1) {
+    // one 32-row block: its 16 row sums padded to the 32 of the reduction
+    float v[32];
 #pragma unroll
-  for (int h = 0; h < TL::FM / 2; ++h) {
-    const float rs = transpose_reduce32(*reinterpret_cast<float(*)[32]>(&rowv[32 * h]), lane);
+    for (int k = 0; k < 32; ++k) v[k] = k < 16 ? rowv[k] : 0.f;
+    const float rs = transpose_reduce32(v, lane);
     const int q = lane & 31;
-    const int ml = wm * TL::TM + h * 64 + (q >> 4) * 32 + acc_row(q & 15, lane);
-    __hip_atomic_fetch_add(&s_row[ml], rs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (q < 16)
+      __hip_atomic_fetch_add(&s_row[wm * TL::TM + acc_row(q, lane)], rs, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+  } else {
+#pragma unroll
+    for (int h = 0; h < TL::FM / 2; ++h) {
+      const float rs = transpose_reduce32(*reinterpret_cast<float(*)[32]>(&rowv[32 * h]), lane);
+      const int q = lane & 31;
+      const int ml = wm * TL::TM + h * 64 + (q >> 4) * 32 + acc_row(q & 15, lane);
+      __hip_atomic_fetch_add(&s_row[ml], rs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
   }
   if (!LIT) {
 #pragma unroll
@@ -298,12 +324,12 @@ template <typename T, bool VEC, bool NORM> struct FwdChain {
 // tile's k-loop loads chunk 0 of its next tile, which lands during the
 // epilogue; each tile's sums go to ws after the next tile's first barrier, so
 // that barrier does not wait for them.  Otherwise one tile per workgroup.
-template <typename T, bool LIT, bool NORM, bool VEC>
-__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_sumexp(
+template <typename T, bool LIT, bool NORM, bool VEC, bool SMALL = false>
+__global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::fwd)) void k_sumexp(
     const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
     float* __restrict__ ws, int tiles_m, int tiles_n) {
-  using TL = FwdTile<T, VEC>;
-  static_assert(TL::FM % 2 == 0, "the row reduction takes 64-row halves of the wave sub-tile");
+  using TL = GemmTile<T, VEC, SMALL>;
+  static_assert(TL::FM % 2 == 0 || TL::FM == 1, "the row reduction takes 64-row halves of the wave sub-tile");
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
   __shared__ float s_rx[TL::BM], s_ry[TL::BN], s_row[TL::BM], s_col[TL::BN];
   const int64_t n64 = N;
@@ -923,15 +949,15 @@ __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int
 // contractions of diagonal diag_c (the 16-bit types run those in k_grad_contract); CDMA
 // selects the fp32 contraction core.  X3: bf16 split operands (K = 3 dp),
 // G'^T written as hi and lo planes.
-template <typename T, bool LIT, bool NORM, bool VEC, bool CDMA, bool X3 = false>
-__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::bwd)) void k_grad_step(
+template <typename T, bool LIT, bool NORM, bool VEC, bool CDMA, bool X3 = false, bool SMALL = false>
+__global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) void k_grad_step(
     const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
     const float* __restrict__ ws, GradBufs gb, BlockGrid bg, StepPlan sp, float* __restrict__ acc_x,
     float* __restrict__ acc_y) {
-  using TF = FwdTile<T, VEC>;
+  using TF = GemmTile<T, VEC, SMALL>;
   constexpr bool FUSED = !GtOnly<T>::value;  // contractions in this kernel
-  using TCX = typename std::conditional<FUSED, ConTileX<T, CDMA>, TF>::type;
-  using TCY = typename std::conditional<FUSED, ConTileY<T, CDMA>, TF>::type;
+  using TCX = typename std::conditional<FUSED, typename ConTileSmall<T, CDMA, SMALL>::x, TF>::type;
+  using TCY = typename std::conditional<FUSED, typename ConTileSmall<T, CDMA, SMALL>::y, TF>::type;
   static_assert(TCX::NT == TF::NT && TCY::NT == TF::NT, "one workgroup size per launch");
   constexpr int GT_LDS = GtOnly<T>::value ? TF::BN * gt_pitch(TF::BM) : 0;
   __shared__ __attribute__((aligned(1024)))

@@ -73,32 +73,46 @@ __device__ __forceinline__ double softplus_log_ratio(double off, double t) {
   return u > 0.0 ? u + log1p(exp(-u)) : log1p(exp(u));
 }
 
+// The loss term of row i (a CLIP row and column, or a LiT row), and 1/R_i,
+// 1/C_i and kappa_i into the workspace.
+template <bool LIT>
+__device__ __forceinline__ double finalize_row(int i, int64_t n, double inv_t, float* __restrict__ ws) {
+  const double s = (double)ws[WS_DIAG * n + i] * (double)ws[WS_RX * n + i] * (double)ws[WS_RY * n + i];
+  const double t = (s - 1.0) * inv_t;
+  const double e = exp(t);
+  const double ro = ws[WS_ROW_OFF * n + i];
+  const double R = ro + e;
+  double acc = softplus_log_ratio(ro, t);
+  ws[WS_INV_ROW * n + i] = (float)(1.0 / R);
+  double kap = -(ro / R);
+  if (!LIT) {
+    const double co = ws[WS_COL_OFF * n + i];
+    const double C = co + e;
+    acc += softplus_log_ratio(co, t);
+    ws[WS_INV_COL * n + i] = (float)(1.0 / C);
+    kap -= co / C;
+  }
+  ws[WS_KAPPA * n + i] = (float)kap;
+  return acc;
+}
+
 // Pass 1: one thread per row (rows beyond N contribute nothing); each
 // workgroup writes the fp64 sum of its rows' loss terms to partial[blockIdx.x].
-template <bool LIT>
+// SINGLE (N <= FIN_SINGLE * FIN_ROWS, one workgroup): thread t takes rows
+// t, t + FIN_ROWS, ... in that order, and the workgroup writes the loss
+// itself (no second pass, one launch fewer for a small N).
+constexpr int FIN_SINGLE = 4;
+template <bool LIT, bool SINGLE>
 __global__ __launch_bounds__(FIN_ROWS) void k_finalize_rows(int N, double inv_t, float* __restrict__ ws,
-                                                            double* __restrict__ partial) {
+                                                            double* __restrict__ partial, float* __restrict__ loss) {
   __shared__ double red[FIN_ROWS / 64];
   const int64_t n = N;
-  const int i = blockIdx.x * FIN_ROWS + threadIdx.x;
   double acc = 0.0;
-  if (i < N) {
-    const double s = (double)ws[WS_DIAG * n + i] * (double)ws[WS_RX * n + i] * (double)ws[WS_RY * n + i];
-    const double t = (s - 1.0) * inv_t;
-    const double e = exp(t);
-    const double ro = ws[WS_ROW_OFF * n + i];
-    const double R = ro + e;
-    acc += softplus_log_ratio(ro, t);
-    ws[WS_INV_ROW * n + i] = (float)(1.0 / R);
-    double kap = -(ro / R);
-    if (!LIT) {
-      const double co = ws[WS_COL_OFF * n + i];
-      const double C = co + e;
-      acc += softplus_log_ratio(co, t);
-      ws[WS_INV_COL * n + i] = (float)(1.0 / C);
-      kap -= co / C;
-    }
-    ws[WS_KAPPA * n + i] = (float)kap;
+  if (SINGLE) {
+    for (int i = threadIdx.x; i < N; i += FIN_ROWS) acc += finalize_row<LIT>(i, n, inv_t, ws);
+  } else {
+    const int i = blockIdx.x * FIN_ROWS + threadIdx.x;
+    if (i < N) acc = finalize_row<LIT>(i, n, inv_t, ws);
   }
   acc = wave_sum_f64(acc);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -107,7 +121,10 @@ __global__ __launch_bounds__(FIN_ROWS) void k_finalize_rows(int N, double inv_t,
   if (threadIdx.x == 0) {
     double tot = 0.0;
     for (int k = 0; k < FIN_ROWS / 64; ++k) tot += red[k];
-    partial[blockIdx.x] = tot;
+    if (SINGLE)
+      *loss = (float)(tot / (LIT ? (double)N : 2.0 * (double)N));
+    else
+      partial[blockIdx.x] = tot;
   }
 }
 
@@ -140,13 +157,32 @@ __global__ __launch_bounds__(1024) void k_finalize_sum(int N, int nparts, const 
 // by the same lane.  One wave per row; rows of D <= 64 * POST_REG are read
 // once (held in registers across the reduction), longer rows twice.
 constexpr int POST_REG = 32;
+// One side of the post-pass (the x side: own = x, oth = y, acc_x -> dx); the
+// two sides share one launch: blockIdx.y picks the side.
+template <typename T>
+struct PostSide {
+  const T* own;
+  int64_t ld_own;
+  const T* oth;
+  int64_t ld_oth;
+  const float* r_own;
+  const float* r_oth;
+  const float* acc;
+  T* out;
+};
 template <typename T, bool NORM>
-__global__ __launch_bounds__(256) void k_postpass(const T* __restrict__ own, int64_t ld_own,
-                                                  const T* __restrict__ oth, int64_t ld_oth, int N, int D,
-                                                  const float* __restrict__ r_own, const float* __restrict__ r_oth,
+__global__ __launch_bounds__(256) void k_postpass(PostSide<T> s0, PostSide<T> s1, int N, int D,
                                                   const float* __restrict__ kappa, float a,
-                                                  const float* __restrict__ grad_output,
-                                                  const float* acc, T* out) {
+                                                  const float* __restrict__ grad_output) {
+  const PostSide<T>& sd = blockIdx.y ? s1 : s0;
+  const T* __restrict__ own = sd.own;
+  const int64_t ld_own = sd.ld_own;
+  const T* __restrict__ oth = sd.oth;
+  const int64_t ld_oth = sd.ld_oth;
+  const float* __restrict__ r_own = sd.r_own;
+  const float* __restrict__ r_oth = sd.r_oth;
+  const float* acc = sd.acc;
+  T* out = sd.out;
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= N) return;
@@ -200,14 +236,29 @@ __global__ __launch_bounds__(256) void k_postpass(const T* __restrict__ own, int
   }
 }
 
+// One feature matrix to transpose: X (row pitch ldx), its row scales and the
+// destination plane(s) (pitch ldt).  The transposes of the two sides share
+// one launch: blockIdx.z picks the side.
+template <typename T, typename TO = T>
+struct TransSide {
+  const T* X;
+  int64_t ldx;
+  const float* scale;
+  TO* XT;
+  TO* XTl;  // k_transpose_split with LO: the lo plane
+};
+
 // Transposed, normalised copy of one feature matrix for the backward's
 // contractions: XT[d, i] = scale_i * X[i, d] (scale = 1/max(||x_i||, 1e-12)
 // when NORM) for i < N and 0 for N <= i < ldt, rounded to T once.  64 x 64
 // tiles through LDS; both the loads and the stores are coalesced.
 template <typename T, bool NORM>
-__global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ X, int64_t ldx, int N, int D,
-                                                   const float* __restrict__ scale, T* __restrict__ XT,
-                                                   int64_t ldt) {
+__global__ __launch_bounds__(256) void k_transpose(TransSide<T> s0, TransSide<T> s1, int N, int D, int64_t ldt) {
+  const TransSide<T>& sd = blockIdx.z ? s1 : s0;
+  const T* __restrict__ X = sd.X;
+  const int64_t ldx = sd.ldx;
+  const float* __restrict__ scale = sd.scale;
+  T* __restrict__ XT = sd.XT;
   __shared__ float tile[64][65];
   const int i0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
@@ -296,9 +347,14 @@ __global__ __launch_bounds__(256) void k_split1(const float* __restrict__ X, int
 // LO, XT_lo[d][i] = lo(v), with v = scale_i x_i[d] (fp32), zero for
 // N <= i < ldt.
 template <bool NORM, bool LO>
-__global__ __launch_bounds__(256) void k_transpose_split(const float* __restrict__ X, int64_t ldx, int N, int D,
-                                                         const float* __restrict__ scale, uint16_t* __restrict__ XTh,
-                                                         uint16_t* __restrict__ XTl, int64_t ldt) {
+__global__ __launch_bounds__(256) void k_transpose_split(TransSide<float, uint16_t> s0,
+                                                         TransSide<float, uint16_t> s1, int N, int D, int64_t ldt) {
+  const TransSide<float, uint16_t>& sd = blockIdx.z ? s1 : s0;
+  const float* __restrict__ X = sd.X;
+  const int64_t ldx = sd.ldx;
+  const float* __restrict__ scale = sd.scale;
+  uint16_t* __restrict__ XTh = sd.XT;
+  uint16_t* __restrict__ XTl = sd.XTl;
   __shared__ float tile[64][65];
   const int i0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;

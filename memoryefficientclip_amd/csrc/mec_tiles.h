@@ -2,7 +2,9 @@
 //
 //   fp32                      128 x 128 tiles everywhere; direct global->LDS
 //                             loads (mec_gemm_dma.h) for 16-byte vectors,
-//                             else staged through registers (mec_gemm_f32.h)
+//                             else staged through registers (mec_gemm_f32.h);
+//                             64 x 64 direct-to-LDS tiles at a small n
+//                             (f32_small_n), so that the grid covers the CUs
 //   bf16 / fp16, 16-byte      forward sums and gradient-matrix tiles 256 x 256
 //   vectors                   (x rows x y rows, 8 waves), direct global->LDS
 //                             loads (mec_gemm_dma.h); contractions 256 x 256
@@ -32,15 +34,22 @@ constexpr int kDtypeF16 = 2;
 constexpr int kDtypeX3 = 3;   // fp32 data, products as three bf16 MFMA terms
 constexpr int kDtypeF32B = 4;  // fp32 data, bf16 products
 
+// fp32 direct-to-LDS problems whose 128 x 128 grid has fewer than two tiles
+// per CU of a 256-CU device (n <= 2816) run 64 x 64 tiles instead (`small`)
+inline bool f32_small_n(int64_t n) {
+  const int64_t t = (n + 127) / 128;
+  return t * t < 512;
+}
 // forward sums and gradient-matrix tiles (x rows x y rows)
-inline TileDims fwd_tile_dims(int dtype, bool vec) {
+inline TileDims fwd_tile_dims(int dtype, bool vec, bool small = false) {
   if (dtype == kDtypeX3 || dtype == kDtypeF32B) return {256, 256};
+  if (dtype == kDtypeF32 && vec && small) return {64, 64};
   if (dtype == kDtypeF32 || !vec) return {128, 128};
   return {256, 256};
 }
 // contraction tiles (output rows x feature columns)
-inline TileDims con_tile_dims(int dtype) {
-  if (dtype == kDtypeF32) return {128, 128};
+inline TileDims con_tile_dims(int dtype, bool small = false) {
+  if (dtype == kDtypeF32) return small ? TileDims{64, 64} : TileDims{128, 128};
   return {256, 256};
 }
 // contractions run in their own kernel (k_grad_contract) rather than inside k_grad_step

@@ -6,6 +6,10 @@ while a transposed input panel (128 rows of pitch ~N) fits its 32-bit
 offsets (N up to about 4.2M); otherwise on the register-staged core.  The
 second choice cannot be reached at test sizes, so MEC_F32_CONTRACT_DMA=0
 forces it here; a row stride past the 32-bit range exercises the first.
+
+Up to N = 2816 the direct-to-LDS kernels run 64 x 64 tiles (a 128 x 128
+grid would leave CUs idle); MEC_F32_SMALL_TILES=0 / 1 forces either tile
+size, so both are checked on both sides of that bound.
 """
 import os
 
@@ -83,3 +87,43 @@ def test_f32_row_stride_beyond_the_direct_core_range():
     say(f"  loss rel {rel_err(loss.detach().cpu(), rl):.2e} grads {ea:.2e} {eb:.2e}")
     assert rel_err(loss.detach().cpu(), rl) <= TOL_LOSS
     assert ea <= TOL_GRAD and eb <= TOL_GRAD
+
+
+def run_env(env, module, a, b, grad_b=True):
+    """run() with the environment variables `env` set for the call."""
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return run(module, a, b, grad_b)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("lit", [False, True], ids=["clip", "lit"])
+@pytest.mark.parametrize("n,d", [(1024, 512), (1000, 130), (2900, 72), (63, 8)])
+def test_f32_small_and_large_tiles(lit, n, d):
+    """64 x 64 and 128 x 128 direct-to-LDS tiles (forward sums,
+    gradient-matrix tiles, contractions) agree with the oracle and with each
+    other, below the 2816-row bound (where 64 x 64 is the default: config 1's
+    shape, a ragged N, a tiny N) and above it (n = 2900)."""
+    a, b = randn_pair(n, d, seed=41 + n)
+    mod = MemoryEfficientLiTLoss(0.07) if lit else MemoryEfficientCLIPLoss(0.07)
+    say(f"fp32 {'LiT' if lit else 'CLIP'} n={n} d={d}: 64 x 64 vs 128 x 128 tiles")
+    l_s, da_s, db_s = run_env({"MEC_F32_SMALL_TILES": "1"}, mod, a, b, grad_b=not lit)
+    l_l, da_l, db_l = run_env({"MEC_F32_SMALL_TILES": "0"}, mod, a, b, grad_b=not lit)
+    if lit:
+        rl, rda = oracle.lit_loss_and_grads(a, b, 0.07)
+        pairs = [(da_s, rda), (da_l, rda)]
+    else:
+        rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+        pairs = [(da_s, rda), (db_s, rdb), (da_l, rda), (db_l, rdb)]
+    errs = [max_rel(g, r) for g, r in pairs]
+    say(f"  loss rel {rel_err(l_s, rl):.2e} / {rel_err(l_l, rl):.2e}; grads {['%.2e' % e for e in errs]}")
+    assert rel_err(l_s, rl) <= TOL_LOSS and rel_err(l_l, rl) <= TOL_LOSS
+    assert all(e <= TOL_GRAD for e in errs)
+    # the same products summed in a different order
+    assert rel_err(l_s, l_l) < 1e-5 and max_rel(da_s, da_l) < 1e-5
