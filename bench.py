@@ -257,10 +257,13 @@ def cpu_baseline(mode, d, dt, normalized, temperature, gen, n_cpu, runs=3):
     }
 
 
-def measure(cfg, dt, steps, warmup, with_events=True):
+def measure(cfg, dt, steps, warmup, with_events=True, calling_thread=False):
     """Times `steps` fwd+bwd steps of configuration `cfg` (input dtype dt)
     through the drop-in module, after `warmup` steps.  Returns (row, a, b)
-    with the device inputs a, b."""
+    with the device inputs a, b.  calling_thread: the timed loop runs under
+    torch.autograd.set_multithreading_enabled(False), so that loss.backward()
+    runs the backward on the calling thread instead of handing it to the
+    autograd engine's device thread (a diagnostic of host overhead)."""
     import torch
     from memoryefficientclip_amd import MemoryEfficientCLIPLoss, MemoryEfficientLiTLoss
     mode, n, d, _, normalized, temperature, gen, _ = CONFIGS[cfg]
@@ -295,12 +298,15 @@ def measure(cfg, dt, steps, warmup, with_events=True):
     peak_extra = torch.cuda.max_memory_allocated(dev) - base
     loss_val = float(loss.detach())
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(steps):
-        step(evs[k] if with_events else None)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with torch.autograd.set_multithreading_enabled(not calling_thread):
+        for _ in range(warmup if calling_thread else 0):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(steps):
+            step(evs[k] if with_events else None)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     ms = wall * 1e3 / steps
     row = {"config": cfg, "workload": f"{mode}_loss_fwd_bwd", "n": n, "d": d, "dtype": dt,
            "normalized_inputs": normalized, "temperature": temperature, "steps": steps,
@@ -469,10 +475,20 @@ def main():
                 del ta, tb
                 torch.cuda.empty_cache()
             row["frac_of_peak"] = round(row["tflops"] / PEAK_TFLOPS[row["dtype"]], 4)
+            if CONFIGS[cfg][1] <= 4096:
+                # small N: the host, not the GPU, sets the step; the same loop with
+                # the backward on the calling thread shows how much of it is the
+                # autograd engine's hand-off to its device thread
+                ct, ta, tb = measure(cfg, CONFIGS[cfg][3], *TABLE_STEPS[cfg], calling_thread=True)
+                del ta, tb
+                row["ms_per_step_backward_on_calling_thread"] = ct["ms_per_step"]
             table.append(row)
             log(f"bench: table config {cfg}: {row['ms_per_step']:.3f} ms/step (fwd {row['fwd_ms']:.3f}, "
                 f"bwd {row['bwd_ms']:.3f}), {row['tflops']:.1f} TFLOP/s, {100 * row['frac_of_peak']:.1f}% of "
                 f"{row['dtype']} peak, extra HBM {row['peak_extra_hbm_bytes'] / 1e9:.2f} GB")
+            if "ms_per_step_backward_on_calling_thread" in row:
+                log(f"bench: table config {cfg}, backward on the calling thread: "
+                    f"{row['ms_per_step_backward_on_calling_thread']:.3f} ms/step")
 
     cpu = None
     if not args.no_cpu:
