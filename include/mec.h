@@ -95,8 +95,9 @@ extern "C" {
 /* OR into `mode`: the forward sums are formed without atomics across
  * workgroups, in a fixed order, so the loss and (through the sums) the
  * gradients are bitwise reproducible for the same inputs on the same device.
- * The backward is deterministic in either mode.  Costs one extra pass over
- * the similarity tiles for CLIP (the column sums). */
+ * The backward is deterministic in either mode.  The similarity tiles are
+ * still visited once (in P x Q blocks, unchained), with the partial sums
+ * combined in a fixed order by a second, O(n) launch. */
 #define MEC_FLAG_DETERMINISTIC 0x100
 
 /* Thread-local message for the last error on this thread ("" if none). */
@@ -108,7 +109,7 @@ const char* mec_version(void);
 /* Number of floats of the per-call workspace: 8 vectors of length n
  * (inverse norms rx, ry; raw diagonal x_i.y_i; off-diagonal row/column sums
  * of E = exp((S-1)/T); 1/R; 1/C; diagonal gradient coefficient), then
- * ceil(n/1024) doubles of loss partials (mec_finalize), then 8 x n floats
+ * ceil(n/1024) doubles of loss partials (mec_finalize), then 48 x n floats
  * of partial sums (the deterministic forward, MEC_FLAG_DETERMINISTIC).  The
  * workspace must be 8-byte aligned.  The same workspace must be passed to
  * mec_forward and the matching mec_backward (it replaces

@@ -138,15 +138,24 @@ def backward(ctx, grad_output: torch.Tensor, need_x: bool, need_y: bool):
         else:
             dx = torch.empty((n, d), dtype=x.dtype, device=dev) if need_x else None
             dy = torch.empty((n, d), dtype=y.dtype, device=dev) if need_y else None
+        # The gradient scratch comes straight from PyTorch's caching allocator
+        # (stream-ordered, like a tensor): the kernels write every byte of it
+        # before reading it, so the NaN fill that torch.empty performs under
+        # torch.use_deterministic_algorithms(True) (gigabytes at large N) would
+        # be wasted work.
         nbytes = lib.mec_grad_scratch_bytes(n, d, dt)
-        scratch = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        stream = torch.cuda.current_stream(dev)
+        scratch = torch.cuda.caching_allocator_alloc(nbytes, dev, stream)
 
         def ptr(t):
             return None if t is None else t.data_ptr()
 
-        _lib.call("mec_backward", x.data_ptr(), ldx, y.data_ptr(), ldy, n, d, dt, mode, int(normalize),
-                  temperature, grad_scale, ws.data_ptr(), go.data_ptr(), scratch.data_ptr(), nbytes,
-                  ptr(acc_x), ptr(acc_y), ptr(dx), ptr(dy), _stream(dev))
+        try:
+            _lib.call("mec_backward", x.data_ptr(), ldx, y.data_ptr(), ldy, n, d, dt, mode, int(normalize),
+                      temperature, grad_scale, ws.data_ptr(), go.data_ptr(), scratch, nbytes,
+                      ptr(acc_x), ptr(acc_y), ptr(dx), ptr(dy), stream.cuda_stream)
+        finally:
+            torch.cuda.caching_allocator_delete(scratch)
     return dx, dy
 
 

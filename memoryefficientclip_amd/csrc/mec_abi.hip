@@ -139,10 +139,10 @@ int check_temperature(float t) {
 bool is_lit(int mode) { return (mode & MEC_MODE_MASK) == MEC_MODE_LIT; }
 
 // workspace: WS_NSLOTS vectors of n floats, the fp64 loss partials, then the
-// DET_SPLITS x n partial sums of the deterministic forward
+// (DET_Q + DET_P) x n partial sums of the deterministic forward
 int64_t loss_partials_floats(int64_t n) { return 2 * ((n + FIN_ROWS - 1) / FIN_ROWS); }
 int64_t det_partials_offset(int64_t n) { return (int64_t)WS_NSLOTS * n + loss_partials_floats(n); }
-int64_t base_workspace_floats(int64_t n) { return det_partials_offset(n) + (int64_t)DET_SPLITS * n; }
+int64_t base_workspace_floats(int64_t n) { return det_partials_offset(n) + (int64_t)(DET_Q + DET_P) * n; }
 
 // Split modes: the bf16 operands of the similarity GEMMs follow, 16-byte
 // aligned: A (x rows) and B (y rows), n rows of ld = terms * dp bf16 each,
@@ -460,24 +460,19 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   dim3 grid((unsigned)nwg);
   const bool lit = is_lit(mode);
   if (mode & MEC_FLAG_DETERMINISTIC) {
-    // row sums, then (CLIP) the column sums as the row sums of the swapped problem
+    // one pass over the tile grid in P x Q blocks, then the partials in order
     const int64_t n64 = n;
-    float* part = workspace + det_partials_offset(n);
-    const int64_t nwg_det = (int64_t)tiles_m * DET_SPLITS;
-    if (nwg_det > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "forward grid too large");
+    float* rowpart = workspace + det_partials_offset(n);
+    float* colpart = rowpart + (int64_t)DET_Q * n64;
+    const int P = tiles_m < DET_P ? tiles_m : DET_P, Q = tiles_n < DET_Q ? tiles_n : DET_Q;
     const unsigned sum_grid = (unsigned)((n + 255) / 256);
-    DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, {
-      k_sumexp_rows_det<T, NORM, VEC><<<(unsigned)nwg_det, FwdTile<T, VEC>::NT, 0, s>>>(
-          (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace + WS_RX * n64, workspace + WS_RY * n64, part,
-          tiles_m, tiles_n);
-      k_det_sum<<<sum_grid, 256, 0, s>>>(part, N, workspace + WS_ROW_OFF * n64);
-      if (!lit) {
-        k_sumexp_rows_det<T, NORM, VEC><<<(unsigned)nwg_det, FwdTile<T, VEC>::NT, 0, s>>>(
-            (const T*)y, ldy, (const T*)x, ldx, N, D, D, c, workspace + WS_RY * n64, workspace + WS_RX * n64,
-            part, tiles_m, tiles_n);
-        k_det_sum<<<sum_grid, 256, 0, s>>>(part, N, workspace + WS_COL_OFF * n64);
-      }
-    })));
+    DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, {
+      k_sumexp_det<T, LIT, NORM, VEC><<<(unsigned)(P * Q), FwdTile<T, VEC>::NT, 0, s>>>(
+          (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace + WS_RX * n64, workspace + WS_RY * n64, rowpart,
+          colpart, tiles_m, tiles_n, P, Q);
+      k_det_reduce<LIT><<<sum_grid, 256, 0, s>>>(rowpart, Q, colpart, P, N, workspace + WS_ROW_OFF * n64,
+                                                 workspace + WS_COL_OFF * n64);
+    }))));
     return check_launch("sumexp (deterministic)");
   }
   int cus = 0;

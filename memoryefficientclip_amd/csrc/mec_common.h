@@ -46,9 +46,11 @@ enum WsSlot {
   WS_INV_ROW = 5, WS_INV_COL = 6, WS_KAPPA = 7, WS_NSLOTS = 8
 };
 constexpr int FIN_ROWS = 1024;  // rows per workgroup of the loss finalize
-// deterministic forward: column splits per row tile, whose DET_SPLITS x n
-// partial row sums follow the loss partials in the workspace
-constexpr int DET_SPLITS = 8;
+// deterministic forward: at most DET_P row blocks x DET_Q column blocks of
+// tiles, whose (DET_Q + DET_P) x n partial sums follow the loss partials in
+// the workspace (DET_Q row partials per row, then DET_P column partials per
+// column)
+constexpr int DET_P = 32, DET_Q = 16;
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 

@@ -18,9 +18,9 @@
 //                       runs both kinds of tile in this launch.
 //   k_grad_contract the 16-bit types' contractions of one pipeline step, in
 //                       a launch of their own with larger tiles.
-//   k_sumexp_rows_det, k_det_sum
+//   k_sumexp_det, k_det_reduce
 //                   the forward sums without atomics across workgroups
-//                       (deterministic mode).
+//                       (deterministic mode), in one pass.
 #pragma once
 #include <type_traits>
 
@@ -388,97 +388,101 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::fwd)) 
 }
 
 // ------------------------------------------------- deterministic forward
-// The sums without atomics across workgroups.  Workgroup (s, tm) walks the
-// column tiles of split s (of DET_SPLITS equal ranges) against row tile tm in
-// order.  After each tile every lane adds its rows' sums over the tile into
-// its own LDS slot (wave column wn, row i): one writer per slot, in tile
-// order.  The workgroup then writes slot 0 + slot 1 of each row to
-// part[s * N + i], and k_det_sum adds the DET_SPLITS partials of each row in
-// split order.  The column sums of CLIP are the row sums of the swapped
-// problem (Y against X), a second launch.  Every sum is therefore a fixed
-// function of the inputs.
-
-// E of this wave's accumulators added to rowv (row sums only); ry is read per
-// column from global memory (the column tile changes along the walk).
-template <class TL, bool NORM, bool MASK>
-__device__ __forceinline__ void rowsum_accumulate(const f32x16 (&acc)[TL::FM][TL::FN], float c, int m0, int n0,
-                                                  int N, const float* s_rx, const float* __restrict__ ry,
-                                                  float (&rowv)[TL::FM * 16]) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
-#pragma unroll
-  for (int bn = 0; bn < TL::FN; ++bn) {
-    const int j = n0 + wn * TL::TN + bn * 32 + (lane & 31);
-    const float cy = NORM ? c * (j < N ? ry[j] : 1.f) : c;
-#pragma unroll
-    for (int bm = 0; bm < TL::FM; ++bm) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ml = wm * TL::TM + bm * 32 + acc_row(r, lane);
-        const int i = m0 + ml;
-        const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
-        float e = fast_exp2(fmaf(sc, cy, -c));
-        if (MASK) e = (i < N && j < N && i != j) ? e : 0.f;
-        rowv[bm * 16 + r] += e;
-      }
-    }
-  }
-}
-
-template <typename T, bool NORM, bool VEC>
-__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_sumexp_rows_det(
+// The sums without atomics across workgroups, in one pass over the tiles.
+// The tile grid is cut into P x Q blocks (P <= DET_P row blocks, Q <= DET_Q
+// column blocks, both clamped to the tile counts); workgroup (p, q) walks its
+// block, row tiles outer and column tiles inner, in order.  Within a tile:
+//   rows: each lane's row sums over its columns (registers, fixed order),
+//     transpose_reduce32 across the half-wave, one LDS slot per (wave column,
+//     row) with one writer; thread t adds the slots in wave order to its
+//     running sum of row m0 + t over the block's column tiles, and writes it
+//     to rowpart[q * N + row] after the last one;
+//   columns (CLIP): each lane's column sums over its rows, plus the other
+//     lane half, one LDS slot per (wave row, column); thread t adds the slots
+//     in wave order and adds that to colpart[p * N + column] (written at the
+//     block's first row tile; only this workgroup touches these entries).
+// k_det_reduce then sums the Q row partials and the P column partials of each
+// index in order.  Every sum is a fixed function of the inputs and of the
+// tile shape, E is computed once, and the partials take (DET_P + DET_Q) * N
+// floats of the workspace.
+template <typename T, bool LIT, bool NORM, bool VEC>
+__global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_sumexp_det(
     const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
-    const float* __restrict__ rx, const float* __restrict__ ry, float* __restrict__ part, int tiles_m,
-    int tiles_n) {
+    const float* __restrict__ rx, const float* __restrict__ ry, float* __restrict__ rowpart,
+    float* __restrict__ colpart, int tiles_m, int tiles_n, int P, int Q) {
   using TL = FwdTile<T, VEC>;
   static_assert(TL::FM == 2, "row reduction assumes 64-row wave sub-tiles");
   static_assert(TL::WN == 2, "two row-sum slots per row");
+  static_assert(TL::NT >= TL::BM && TL::NT >= TL::BN, "one row and one column per thread");
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
-  __shared__ float s_rx[TL::BM], s_row[TL::WN][TL::BM];
+  __shared__ float s_rx[TL::BM], s_ry[TL::BN], s_row[TL::WN][TL::BM], s_col[TL::WM][TL::BN];
   const int pid = xcd_remap(blockIdx.x, gridDim.x);
-  const int s = pid / tiles_m, tm = pid - s * tiles_m;  // neighbouring ids share the split's column tiles
-  const int m0 = tm * TL::BM;
-  const int tn0 = (int)((int64_t)s * tiles_n / DET_SPLITS), tn1 = (int)((int64_t)(s + 1) * tiles_n / DET_SPLITS);
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / TL::WN, wn = w % TL::WN;
-  for (int u = t; u < TL::BM; u += TL::NT) {
-    s_rx[u] = (NORM && m0 + u < N) ? rx[m0 + u] : 1.f;
-    s_row[0][u] = 0.f;
-    s_row[1][u] = 0.f;
-  }
-  // the row (within the tile) whose slot this lane owns after transpose_reduce32
-  const int q = lane & 31;
-  const int my_row = wm * TL::TM + (q >> 4) * 32 + acc_row(q & 15, lane);
-  const auto A = tile_op<TL>(X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax);
-  for (int tn = tn0; tn < tn1; ++tn) {
-    const int n0 = tn * TL::BN;
-    const auto B = tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax);
-    f32x16 acc[TL::FM][TL::FN];
-    __syncthreads();  // every wave is done with the previous tile's LDS stages; s_rx, s_row are visible
-    TL::template run<VEC, VEC>(A, B, D, lds, acc);
-    float rowv[TL::FM * 16];
-#pragma unroll
-    for (int k = 0; k < TL::FM * 16; ++k) rowv[k] = 0.f;
-    const bool diag = m0 < n0 + TL::BN && n0 < m0 + TL::BM;
-    if (!diag && m0 + TL::BM <= N && n0 + TL::BN <= N)
-      rowsum_accumulate<TL, NORM, false>(acc, c, m0, n0, N, s_rx, ry, rowv);
-    else
-      rowsum_accumulate<TL, NORM, true>(acc, c, m0, n0, N, s_rx, ry, rowv);
-    s_row[wn][my_row] += transpose_reduce32(rowv, lane);  // this lane is the slot's only writer
-  }
-  __syncthreads();
+  const int p = pid / Q, q = pid - p * Q;  // neighbouring ids share the row block's x panels
+  const int tm0 = (int)((int64_t)p * tiles_m / P), tm1 = (int)((int64_t)(p + 1) * tiles_m / P);
+  const int tn0 = (int)((int64_t)q * tiles_n / Q), tn1 = (int)((int64_t)(q + 1) * tiles_n / Q);
   const int64_t n64 = N;
-  for (int u = t; u < TL::BM; u += TL::NT)
-    if (m0 + u < N) part[(int64_t)s * n64 + m0 + u] = s_row[0][u] + s_row[1][u];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / TL::WN, wn = w % TL::WN;
+  // the row (within the tile) whose slot this lane owns after transpose_reduce32
+  const int qr = lane & 31;
+  const int my_row = wm * TL::TM + (qr >> 4) * 32 + acc_row(qr & 15, lane);
+  for (int tm = tm0; tm < tm1; ++tm) {
+    const int m0 = tm * TL::BM;
+    const auto A = tile_op<TL>(X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax);
+    float rs = 0.f;  // thread t: row m0 + t over this block's column tiles
+    for (int tn = tn0; tn < tn1; ++tn) {
+      const int n0 = tn * TL::BN;
+      const auto B = tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax);
+      __syncthreads();  // the previous tile's epilogue is done with the LDS stages and slots
+      if (t < TL::BM) s_rx[t] = (NORM && m0 + t < N) ? rx[m0 + t] : 1.f;
+      if (t < TL::BN) s_ry[t] = (NORM && n0 + t < N) ? ry[n0 + t] : 1.f;
+      f32x16 acc[TL::FM][TL::FN];
+      TL::template run<VEC, VEC>(A, B, D, lds, acc);  // its first barrier publishes s_rx, s_ry
+      float rowv[TL::FM * 16];
+      float colv[TL::FN];
+      const bool diag = m0 < n0 + TL::BN && n0 < m0 + TL::BM;
+      if (!diag && m0 + TL::BM <= N && n0 + TL::BN <= N)
+        sumexp_epilogue<TL, NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
+      else
+        sumexp_epilogue<TL, NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
+      s_row[wn][my_row] = transpose_reduce32(rowv, lane);
+      if (!LIT) {
+#pragma unroll
+        for (int bn = 0; bn < TL::FN; ++bn) {
+          const float v = colv[bn] + __shfl_xor(colv[bn], 32, 64);
+          if (lane < 32) s_col[wm][wn * TL::TN + bn * 32 + lane] = v;
+        }
+      }
+      lds_barrier();
+      if (t < TL::BM) rs += s_row[0][t] + s_row[1][t];
+      if (!LIT && t < TL::BN && n0 + t < N) {
+        float v = s_col[0][t];
+#pragma unroll
+        for (int k = 1; k < TL::WM; ++k) v += s_col[k][t];
+        float* cp = colpart + (int64_t)p * n64 + n0 + t;
+        *cp = tm == tm0 ? v : *cp + v;
+      }
+    }
+    if (t < TL::BM && m0 + t < N && tn1 > tn0) rowpart[(int64_t)q * n64 + m0 + t] = rs;
+  }
 }
 
-// out[i] = sum over s = 0 .. DET_SPLITS-1 of part[s * N + i], in that order
-__global__ __launch_bounds__(256) void k_det_sum(const float* __restrict__ part, int N, float* __restrict__ out) {
+// out_row[i] = sum over q < Q of rowpart[q * N + i] and (CLIP) out_col[i] =
+// sum over p < P of colpart[p * N + i], each in that order
+template <bool LIT>
+__global__ __launch_bounds__(256) void k_det_reduce(const float* __restrict__ rowpart, int Q,
+                                                    const float* __restrict__ colpart, int P, int N,
+                                                    float* __restrict__ out_row, float* __restrict__ out_col) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= N) return;
   const int64_t n64 = N;
   float v = 0.f;
-#pragma unroll
-  for (int s = 0; s < DET_SPLITS; ++s) v += part[s * n64 + i];
-  out[i] = v;
+  for (int k = 0; k < Q; ++k) v += rowpart[k * n64 + i];
+  out_row[i] = v;
+  if (!LIT) {
+    float u = 0.f;
+    for (int k = 0; k < P; ++k) u += colpart[k * n64 + i];
+    out_col[i] = u;
+  }
 }
 
 // ---------------------------------------------------------------- backward

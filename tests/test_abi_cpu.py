@@ -35,8 +35,9 @@ def test_library_exports_every_declared_symbol():
 def test_sizes():
     lib = _lib.load()
     # 8 vectors, ceil(n / 1024) fp64 loss partials, 8 vectors of deterministic partial sums
-    assert lib.mec_workspace_floats(1000) == 8000 + 2 + 8000
-    assert lib.mec_workspace_floats(1025) == 8 * 1025 + 4 + 8 * 1025
+    # 8 vectors, the fp64 loss partials (2 floats per 1024 rows), 48 x n deterministic partials
+    assert lib.mec_workspace_floats(1000) == 8000 + 2 + 48000
+    assert lib.mec_workspace_floats(1025) == 8 * 1025 + 4 + 48 * 1025
     assert lib.mec_workspace_floats(0) < 0
     # scratch is O(n*d): two block diagonals of the N x N gradient matrix (fp32:
     # in both layouts; bf16 and fp16: transposed only), plus transposed copies of

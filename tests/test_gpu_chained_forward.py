@@ -7,7 +7,7 @@ also the last) and of several.
 
 * The row and column sums (workspace slots 3 and 4 after mec_sumexp) are
   compared with those of the deterministic forward, which walks its tiles
-  without chaining (k_sumexp_rows_det + k_det_sum).  A tile visited twice or
+  without chaining (k_sumexp_det + k_det_reduce).  A tile visited twice or
   missed would move the sums of its 256 rows by about 256 / N of their value,
   far above the 1e-5 allowed for the different order of the additions.
 * Loss and gradients through the module against the fp64 oracle at the

@@ -4,14 +4,17 @@ Python by torch.use_deterministic_algorithms(True)).
 The default forward adds each tile's row and column sums into the workspace
 with relaxed fp32 atomics (as the reference does, clip_loss.py:63-64), so the
 loss may differ in its last bits between runs.  The deterministic forward
-walks each row tile's column splits in order and adds the split partials in
-a fixed order.  Checked here:
+walks the tile grid in P x Q blocks (one workgroup each, tiles in order),
+keeps one row partial per column block and one column partial per row block,
+and adds those partials in a fixed order.  Checked here:
 
 * the sums and the loss agree with the fp64 oracle, and with the atomic path;
 * repeated runs are bitwise identical (sums, loss, and through the module the
   gradients);
-* shapes with fewer column tiles than splits (empty splits), ragged N, all
-  three dtypes, both modes, fused normalisation on and off.
+* shapes with fewer tiles than blocks (the block counts clamp to the tile
+  counts), blocks of uneven tile counts (6000 rows: 47 fp32 tiles over 32 row
+  blocks), ragged N, all three dtypes, both modes, fused normalisation on and
+  off.
 """
 import pytest
 import torch
