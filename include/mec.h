@@ -96,8 +96,10 @@ extern "C" {
  * workgroups, in a fixed order, so the loss and (through the sums) the
  * gradients are bitwise reproducible for the same inputs on the same device.
  * The backward is deterministic in either mode.  The similarity tiles are
- * still visited once (in P x Q blocks, unchained), with the partial sums
- * combined in a fixed order by a second, O(n) launch. */
+ * still visited once (in P x Q blocks), with the partial sums combined in a
+ * fixed order by a second, O(n) launch.  The 16-bit forward with 16-byte rows
+ * and normalize = 0 always runs this way (chained tiles; it is faster than
+ * the atomic forward there), with or without the flag. */
 #define MEC_FLAG_DETERMINISTIC 0x100
 
 /* Thread-local message for the last error on this thread ("" if none). */

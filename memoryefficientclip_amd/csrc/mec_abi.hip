@@ -451,15 +451,21 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   x = g.x, ldx = g.ldx, y = g.y, ldy = g.ldy, d = g.d, dtype = g.dtype;
   const int N = (int)n, D = (int)d;
   const bool vec = vec_ok(x, ldx, y, ldy, d, dtype);
-  // (the deterministic sums keep the 128 x 128 tiles)
-  const bool small = dtype == MEC_DTYPE_F32 && vec && !(mode & MEC_FLAG_DETERMINISTIC) && f32_small_tiles(n);
+  // Deterministic sums on request, and always for the 16-bit direct-to-LDS
+  // tiles without the norm scaling (FwdChain), whose chained block walk is
+  // faster than the atomic forward.  They keep the default tile size.
+  bool chain = false;
+  DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, {
+    chain = FwdChain<T, VEC, NORM>::value;
+  })));
+  const bool det = (mode & MEC_FLAG_DETERMINISTIC) || chain;
+  const bool small = dtype == MEC_DTYPE_F32 && vec && !det && f32_small_tiles(n);
   const TileDims td = fwd_tile_dims(dtype, vec, small);
   const int tiles_m = (int)((n + td.bm - 1) / td.bm), tiles_n = (int)((n + td.bn - 1) / td.bn);
   const int64_t nwg = (int64_t)tiles_m * tiles_n;
   if (nwg > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "forward grid too large");
-  dim3 grid((unsigned)nwg);
   const bool lit = is_lit(mode);
-  if (mode & MEC_FLAG_DETERMINISTIC) {
+  if (det) {
     // one pass over the tile grid in P x Q blocks, then the partials in order
     const int64_t n64 = n;
     float* rowpart = workspace + det_partials_offset(n);
@@ -475,22 +481,17 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
     }))));
     return check_launch("sumexp (deterministic)");
   }
-  int cus = 0;
-  if (vec) {
-    rc = compute_units(&cus);
-    if (rc) return rc;
-  }
+  dim3 grid((unsigned)nwg);
   DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, {
-    // the chained (direct-to-LDS) tiles: one resident workgroup per slot
-    const int64_t slots = (int64_t)cus * Occ<T, VEC>::fwd;
-    if (FwdChain<T, VEC, NORM>::value && nwg > slots) grid.x = (unsigned)slots;
-    if (small) {
-      if constexpr (std::is_same<T, float>::value && VEC)
-        k_sumexp<T, LIT, NORM, VEC, true><<<grid, GemmTile<T, VEC, true>::NT, 0, s>>>(
+    if constexpr (!FwdChain<T, VEC, NORM>::value) {
+      if (small) {
+        if constexpr (std::is_same<T, float>::value && VEC)
+          k_sumexp<T, LIT, NORM, VEC, true><<<grid, GemmTile<T, VEC, true>::NT, 0, s>>>(
+              (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, tiles_m, tiles_n);
+      } else {
+        k_sumexp<T, LIT, NORM, VEC><<<grid, FwdTile<T, VEC>::NT, 0, s>>>(
             (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, tiles_m, tiles_n);
-    } else {
-      k_sumexp<T, LIT, NORM, VEC><<<grid, FwdTile<T, VEC>::NT, 0, s>>>((const T*)x, ldx, (const T*)y, ldy, N, D, D,
-                                                                      c, workspace, tiles_m, tiles_n);
+      }
     }
   }))));
   return check_launch("sumexp");

@@ -310,20 +310,22 @@ __device__ __forceinline__ void sums_flush(float* __restrict__ ws, int m0, int n
 }
 
 // Forward tiles that chain (FwdChain): the 16-bit direct-to-LDS tiles
-// without the norm scaling.  Measured: the 16-bit forward (one workgroup per
-// CU, nothing else to overlap its epilogue) is 7% faster chained; fp32 (two
-// workgroups per CU, one's epilogue already overlaps the other's k-loop) was
-// 4% slower; the normalized 16-bit epilogue spills registers in the loop.
+// without the norm scaling, which always take the deterministic forward's
+// block walk (k_sumexp_det) with chained tiles.  Measured: the 16-bit forward
+// (one workgroup per CU, nothing else to overlap its epilogue) is 7% faster
+// chained, and the block walk with its fixed-order sums another 2-7% faster
+// than chained tiles with atomic sums; fp32 (two workgroups per CU, one's
+// epilogue already overlaps the other's k-loop) was 4% slower chained; the
+// normalizing 16-bit epilogue spills registers in the chained loop, or is
+// slower when kept from spilling.
 template <typename T, bool VEC, bool NORM> struct FwdChain {
   static constexpr bool value = FwdTile<T, VEC>::CHAIN && Is16<T>::value && !NORM;
 };
 
-// Forward sums.  Tiles t = blockIdx.x + i * gridDim.x of the tiles_m x
-// tiles_n grid (XCD-grouped order).  Chained tiles: a workgroup stays
-// resident (the launch covers the CUs once) and the last chunk of each
-// tile's k-loop loads chunk 0 of its next tile, which lands during the
-// epilogue; each tile's sums go to ws after the next tile's first barrier, so
-// that barrier does not wait for them.  Otherwise one tile per workgroup.
+// Forward sums with relaxed atomics into ws (as the reference,
+// clip_loss.py:63-64): one tile per workgroup of the tiles_m x tiles_n grid
+// (XCD-grouped order).  The chain-eligible 16-bit tiles (FwdChain) run
+// k_sumexp_det instead.
 template <typename T, bool LIT, bool NORM, bool VEC, bool SMALL = false>
 __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::fwd)) void k_sumexp(
     const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
@@ -333,58 +335,18 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::fwd)) 
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
   __shared__ float s_rx[TL::BM], s_ry[TL::BN], s_row[TL::BM], s_col[TL::BN];
   const int64_t n64 = N;
-  const int ntiles = tiles_m * tiles_n;
   const int t = threadIdx.x;
-  auto coords = [&](int tile, int& m0, int& n0) {
-    int tm, tn;
-    tile_swizzle(tile, ntiles, tiles_m, tiles_n, 8, tm, tn);
-    m0 = tm * TL::BM;
-    n0 = tn * TL::BN;
-  };
-  auto op_a = [&](int m0) { return tile_op<TL>(X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax); };
-  auto op_b = [&](int n0) { return tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax); };
-  auto rx_of = [&](int m0) { return (NORM && t < TL::BM && m0 + t < N) ? ws[WS_RX * n64 + m0 + t] : 1.f; };
-  auto ry_of = [&](int n0) { return (NORM && t < TL::BN && n0 + t < N) ? ws[WS_RY * n64 + n0 + t] : 1.f; };
+  int tm, tn;
+  tile_swizzle(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, 8, tm, tn);
+  const int m0 = tm * TL::BM, n0 = tn * TL::BN;
+  const float rxv = (NORM && t < TL::BM && m0 + t < N) ? ws[WS_RX * n64 + m0 + t] : 1.f;
+  const float ryv = (NORM && t < TL::BN && n0 + t < N) ? ws[WS_RY * n64 + n0 + t] : 1.f;
   f32x16 acc[TL::FM][TL::FN];
-  int tile = blockIdx.x, m0, n0;
-  coords(tile, m0, n0);
-  if constexpr (FwdChain<T, VEC, NORM>::value) {
-    typename TL::Plan lp;
-    float rxv = rx_of(m0), ryv = ry_of(n0);
-    TL::start(op_a(m0), op_b(n0), lds, lp);
-    int p0 = 0;
-    bool pending = false;  // sums of the previous tile (pm0, pn0) not yet in ws
-    int pm0 = 0, pn0 = 0;
-    float prs = 0.f, pcs = 0.f;
-    for (;;) {
-      const int next = tile + (int)gridDim.x;
-      const bool has_next = next < ntiles;
-      int m1 = m0, n1 = n0;
-      if (has_next) coords(next, m1, n1);
-      TL::chain(lp, op_a(m1), op_b(n1), has_next, D, lds, p0, acc, [&] {
-        if (pending) sums_flush<TL, LIT>(ws, pm0, pn0, N, prs, pcs);
-      });
-      // the next tile's norms, needed after its k-loop
-      const float rxn = has_next ? rx_of(m1) : 1.f, ryn = has_next ? ry_of(n1) : 1.f;
-      sumexp_tile<TL, LIT, NORM>(acc, c, m0, n0, N, rxv, ryv, s_rx, s_ry, s_row, s_col, prs, pcs);
-      pending = true;
-      pm0 = m0;
-      pn0 = n0;
-      if (!has_next) break;
-      tile = next;
-      m0 = m1;
-      n0 = n1;
-      rxv = rxn;
-      ryv = ryn;
-    }
-    sums_flush<TL, LIT>(ws, pm0, pn0, N, prs, pcs);
-    gdma::drain_loads();
-  } else {
-    TL::template run<VEC, VEC>(op_a(m0), op_b(n0), D, lds, acc);
-    float rs, cs;
-    sumexp_tile<TL, LIT, NORM>(acc, c, m0, n0, N, rx_of(m0), ry_of(n0), s_rx, s_ry, s_row, s_col, rs, cs);
-    sums_flush<TL, LIT>(ws, m0, n0, N, rs, cs);
-  }
+  TL::template run<VEC, VEC>(tile_op<TL>(X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax),
+                             tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax), D, lds, acc);
+  float rs, cs;
+  sumexp_tile<TL, LIT, NORM>(acc, c, m0, n0, N, rxv, ryv, s_rx, s_ry, s_row, s_col, rs, cs);
+  sums_flush<TL, LIT>(ws, m0, n0, N, rs, cs);
 }
 
 // ------------------------------------------------- deterministic forward
@@ -425,44 +387,83 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_s
   // the row (within the tile) whose slot this lane owns after transpose_reduce32
   const int qr = lane & 31;
   const int my_row = wm * TL::TM + (qr >> 4) * 32 + acc_row(qr & 15, lane);
-  for (int tm = tm0; tm < tm1; ++tm) {
+  auto op_a = [&](int tm) {
     const int m0 = tm * TL::BM;
-    const auto A = tile_op<TL>(X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax);
-    float rs = 0.f;  // thread t: row m0 + t over this block's column tiles
-    for (int tn = tn0; tn < tn1; ++tn) {
-      const int n0 = tn * TL::BN;
-      const auto B = tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax);
-      __syncthreads();  // the previous tile's epilogue is done with the LDS stages and slots
-      if (t < TL::BM) s_rx[t] = (NORM && m0 + t < N) ? rx[m0 + t] : 1.f;
-      if (t < TL::BN) s_ry[t] = (NORM && n0 + t < N) ? ry[n0 + t] : 1.f;
-      f32x16 acc[TL::FM][TL::FN];
-      TL::template run<VEC, VEC>(A, B, D, lds, acc);  // its first barrier publishes s_rx, s_ry
-      float rowv[TL::FM * 16];
-      float colv[TL::FN];
-      const bool diag = m0 < n0 + TL::BN && n0 < m0 + TL::BM;
-      if (!diag && m0 + TL::BM <= N && n0 + TL::BN <= N)
-        sumexp_epilogue<TL, NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
-      else
-        sumexp_epilogue<TL, NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
-      s_row[wn][my_row] = transpose_reduce32(rowv, lane);
-      if (!LIT) {
+    return tile_op<TL>(X + (int64_t)m0 * ldx, ldx, min(N - m0, TL::BM), kmax);
+  };
+  auto op_b = [&](int tn) {
+    const int n0 = tn * TL::BN;
+    return tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax);
+  };
+  // tile (tm, tn) of the block: its sums into the slots, then thread t's row
+  // sum into rs and its column partial into colpart
+  auto tile_sums = [&](const f32x16 (&acc)[TL::FM][TL::FN], int tm, int tn, float& rs) {
+    const int m0 = tm * TL::BM, n0 = tn * TL::BN;
+    float rowv[TL::FM * 16];
+    float colv[TL::FN];
+    const bool diag = m0 < n0 + TL::BN && n0 < m0 + TL::BM;
+    if (!diag && m0 + TL::BM <= N && n0 + TL::BN <= N)
+      sumexp_epilogue<TL, NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
+    else
+      sumexp_epilogue<TL, NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
+    s_row[wn][my_row] = transpose_reduce32(rowv, lane);
+    if (!LIT) {
 #pragma unroll
-        for (int bn = 0; bn < TL::FN; ++bn) {
-          const float v = colv[bn] + __shfl_xor(colv[bn], 32, 64);
-          if (lane < 32) s_col[wm][wn * TL::TN + bn * 32 + lane] = v;
-        }
-      }
-      lds_barrier();
-      if (t < TL::BM) rs += s_row[0][t] + s_row[1][t];
-      if (!LIT && t < TL::BN && n0 + t < N) {
-        float v = s_col[0][t];
-#pragma unroll
-        for (int k = 1; k < TL::WM; ++k) v += s_col[k][t];
-        float* cp = colpart + (int64_t)p * n64 + n0 + t;
-        *cp = tm == tm0 ? v : *cp + v;
+      for (int bn = 0; bn < TL::FN; ++bn) {
+        const float v = colv[bn] + __shfl_xor(colv[bn], 32, 64);
+        if (lane < 32) s_col[wm][wn * TL::TN + bn * 32 + lane] = v;
       }
     }
-    if (t < TL::BM && m0 + t < N && tn1 > tn0) rowpart[(int64_t)q * n64 + m0 + t] = rs;
+    lds_barrier();
+    if (t < TL::BM) rs += s_row[0][t] + s_row[1][t];
+    if (!LIT && t < TL::BN && n0 + t < N) {
+      float v = s_col[0][t];
+#pragma unroll
+      for (int k = 1; k < TL::WM; ++k) v += s_col[k][t];
+      float* cp = colpart + (int64_t)p * n64 + n0 + t;
+      *cp = tm == tm0 ? v : *cp + v;
+    }
+  };
+  if constexpr (FwdChain<T, VEC, NORM>::value) {
+    // chained tiles (no norm scaling: s_rx, s_ry unused): the last chunk of
+    // each tile's k-loop loads chunk 0 of the next, which lands during the
+    // epilogue.  The k-loop's barriers order one tile's slot reads before the
+    // next tile's slot writes.
+    const int ntn = tn1 - tn0, K = (tm1 - tm0) * ntn;
+    if (K <= 0) return;
+    typename TL::Plan lp;
+    TL::start(op_a(tm0), op_b(tn0), lds, lp);
+    int p0 = 0;
+    float rs = 0.f;  // thread t: row tm * BM + t over this block's column tiles
+    for (int k = 0; k < K; ++k) {
+      const int tm = tm0 + k / ntn, tn = tn0 + k % ntn;
+      const bool has_next = k + 1 < K;
+      const int tmn = has_next ? tm0 + (k + 1) / ntn : tm, tnn = has_next ? tn0 + (k + 1) % ntn : tn;
+      f32x16 acc[TL::FM][TL::FN];
+      TL::chain(lp, op_a(tmn), op_b(tnn), has_next, D, lds, p0, acc, gdma::NoHook());
+      tile_sums(acc, tm, tn, rs);
+      if (tn == tn1 - 1) {
+        if (t < TL::BM && tm * TL::BM + t < N) rowpart[(int64_t)q * n64 + tm * TL::BM + t] = rs;
+        rs = 0.f;
+      }
+    }
+    gdma::drain_loads();
+  } else {
+    for (int tm = tm0; tm < tm1; ++tm) {
+      const int m0 = tm * TL::BM;
+      const auto A = op_a(tm);
+      float rs = 0.f;  // thread t: row m0 + t over this block's column tiles
+      for (int tn = tn0; tn < tn1; ++tn) {
+        const int n0 = tn * TL::BN;
+        __syncthreads();  // the previous tile's epilogue is done with the LDS stages and slots
+        if (t < TL::BM) s_rx[t] = (NORM && m0 + t < N) ? rx[m0 + t] : 1.f;
+        if (t < TL::BN) s_ry[t] = (NORM && n0 + t < N) ? ry[n0 + t] : 1.f;
+        f32x16 acc[TL::FM][TL::FN];
+        TL::template run<VEC, VEC>(A, op_b(tn), D, lds, acc);  // its first barrier publishes s_rx, s_ry
+        tile_sums(acc, tm, tn, rs);
+      }
+      if (t < TL::BM && m0 + t < N && tn1 > tn0) rowpart[(int64_t)q * n64 + m0 + t] = rs;
+    }
   }
 }
 
