@@ -378,6 +378,7 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_s
   static_assert(TL::NT >= TL::BM && TL::NT >= TL::BN, "one row and one column per thread");
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
   __shared__ float s_rx[TL::BM], s_ry[TL::BN], s_row[TL::WN][TL::BM], s_col[TL::WM][TL::BN];
+  __shared__ __attribute__((aligned(16))) float s_cold[TL::BN];
   const int pid = xcd_remap(blockIdx.x, gridDim.x);
   const int p = pid / Q, q = pid - p * Q;  // neighbouring ids share the row block's x panels
   const int tm0 = (int)((int64_t)p * tiles_m / P), tm1 = (int)((int64_t)(p + 1) * tiles_m / P);
@@ -396,8 +397,9 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_s
     return tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, TL::BN), kmax);
   };
   // tile (tm, tn) of the block: its sums into the slots, then thread t's row
-  // sum into rs and its column partial into colpart
-  auto tile_sums = [&](const f32x16 (&acc)[TL::FM][TL::FN], int tm, int tn, float& rs) {
+  // sum into rs and its column partial into colpart (cold: the partial so far
+  // was prefetched into s_cold)
+  auto tile_sums = [&](const f32x16 (&acc)[TL::FM][TL::FN], int tm, int tn, float& rs, bool cold = false) {
     const int m0 = tm * TL::BM, n0 = tn * TL::BN;
     float rowv[TL::FM * 16];
     float colv[TL::FN];
@@ -421,7 +423,7 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_s
 #pragma unroll
       for (int k = 1; k < TL::WM; ++k) v += s_col[k][t];
       float* cp = colpart + (int64_t)p * n64 + n0 + t;
-      *cp = tm == tm0 ? v : *cp + v;
+      *cp = tm == tm0 ? v : (cold ? s_cold[t] : *cp) + v;
     }
   };
   if constexpr (FwdChain<T, VEC, NORM>::value) {
@@ -431,6 +433,12 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_s
     // next tile's slot writes.
     const int ntn = tn1 - tn0, K = (tm1 - tm0) * ntn;
     if (K <= 0) return;
+    // The column partials a tile adds to (written at an earlier row tile) reach
+    // s_cold by direct loads issued after the tile's first barrier; the next
+    // chunk's barrier awaits every load, so they have landed by the epilogue.
+    // With a single k-chunk there is no such barrier: the partials are read
+    // from global memory in the epilogue instead.
+    const bool pf = !LIT && D > TL::G::BK;
     typename TL::Plan lp;
     TL::start(op_a(tm0), op_b(tn0), lds, lp);
     int p0 = 0;
@@ -439,9 +447,18 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_s
       const int tm = tm0 + k / ntn, tn = tn0 + k % ntn;
       const bool has_next = k + 1 < K;
       const int tmn = has_next ? tm0 + (k + 1) / ntn : tm, tnn = has_next ? tn0 + (k + 1) % ntn : tn;
+      auto hook = [&] {
+        if (pf && tm > tm0 && w < TL::BN / 64) {
+          const int n0 = tn * TL::BN;
+          const __amdgpu_buffer_rsrc_t r =
+              __builtin_amdgcn_make_buffer_rsrc((void*)(colpart + (int64_t)p * n64 + n0), 0, (N - n0) * 4, 0x00020000);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)&s_cold[w * 64], 4,
+                                                   (uint32_t)(w * 64 + lane) * 4, 0, 0, 0);
+        }
+      };
       f32x16 acc[TL::FM][TL::FN];
-      TL::chain(lp, op_a(tmn), op_b(tnn), has_next, D, lds, p0, acc, gdma::NoHook());
-      tile_sums(acc, tm, tn, rs);
+      TL::chain(lp, op_a(tmn), op_b(tnn), has_next, D, lds, p0, acc, hook);
+      tile_sums(acc, tm, tn, rs, pf);
       if (tn == tn1 - 1) {
         if (t < TL::BM && tm * TL::BM + t < N) rowpart[(int64_t)q * n64 + tm * TL::BM + t] = rs;
         rs = 0.f;
