@@ -1010,8 +1010,10 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) 
 }
 
 // 16-bit gradient-matrix tiles of diagonal sp.diag_g on the direct-to-LDS
-// 256 x 256 tiles, chained like the forward: persistent workgroups walk the
-// tiles t = blockIdx.x + i * gridDim.x (XCD-grouped order), and the last
+// 256 x 256 tiles, chained as in the forward's block walk: persistent
+// workgroups walk the tiles t = blockIdx.x + i * gridDim.x (XCD-grouped
+// order; contiguous row-major runs of tiles or 2D blocks per workgroup were
+// slower here, unlike in the forward), and the last
 // chunk of each tile's k-loop loads chunk 0 of the next, which lands while
 // the tile's G'^T is staged (in the other ring stage) and stored
 // (grad_gt_store_chain).  The next tile's first barrier waits only for those
