@@ -383,8 +383,12 @@ __global__ __launch_bounds__((FwdTile<T, VEC>::NT), (Occ<T, VEC>::fwd)) void k_s
   __shared__ __attribute__((aligned(16))) float s_cold[TL::BN];
   const int pid = xcd_remap(blockIdx.x, gridDim.x);
   const int p = pid / Q, q = pid - p * Q;  // neighbouring ids share the row block's x panels
-  const int tm0 = (int)((int64_t)p * tiles_m / P), tm1 = (int)((int64_t)(p + 1) * tiles_m / P);
-  const int tn0 = (int)((int64_t)q * tiles_n / Q), tn1 = (int)((int64_t)(q + 1) * tiles_n / Q);
+  // the first tiles_m % P row blocks and tiles_n % Q column blocks take one
+  // tile more; they are the first dispatched, so the longer workgroups start
+  // early and the shorter ones fill in behind them
+  const int nbm = tiles_m / P, rbm = tiles_m % P, nbn = tiles_n / Q, rbn = tiles_n % Q;
+  const int tm0 = p * nbm + min(p, rbm), tm1 = tm0 + nbm + (p < rbm ? 1 : 0);
+  const int tn0 = q * nbn + min(q, rbn), tn1 = tn0 + nbn + (q < rbn ? 1 : 0);
   const int64_t n64 = N;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / TL::WN, wn = w % TL::WN;
   // the row (within the tile) whose slot this lane owns after transpose_reduce32
