@@ -455,7 +455,10 @@ def main():
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                 "launch_ms": round(t_k, 4), "flop_per_launch": mfma_per_flop * f_k, "launches_per_step": nl_k}
     t_f, _, f_f = stages["sumexp"]
-    roofline_fwd = {"kernel": "k_sumexp", "achieved": round(mfma_per_flop * f_f / (t_f * 1e-3) / 1e12, 3),
+    # (bf16/fp16 products on inputs already normalized: the forward runs the
+    # chained block walk, k_sumexp_det, with its O(N) reduction)
+    fkern = "k_sumexp_det+k_det_reduce" if (arith != "f32" and normalized) else "k_sumexp"
+    roofline_fwd = {"kernel": fkern, "achieved": round(mfma_per_flop * f_f / (t_f * 1e-3) / 1e12, 3),
                     "frac": round(mfma_per_flop * f_f / (t_f * 1e-3) / 1e12 / peak, 4), "launch_ms": round(t_f, 4),
                     "flop_per_launch": mfma_per_flop * f_f}
 
