@@ -340,6 +340,26 @@ bool f32_small_tiles(int64_t n) {
   return f32_small_n(n);
 }
 
+// 16-bit narrow contraction tiles (narrow_contract_shape) for blocks of bs
+// rows whose contraction launch has `wide` workgroups of 256 x 256 tiles,
+// `narrow` with them.  Used where they measured faster: a 512-row panel of the
+// gradient-matrix block (512 x bs x 2 bytes) within one XCD's 4 MB L2, i.e.
+// bs <= 4096 (7-13% less contraction time at D = 128-640; with larger blocks
+// the narrow tiles fall out of step with the wide tiles that share their panel
+// and read it from HBM: 2-11% more), and fewer rounds of workgroups over the
+// CUs than the wide tiles alone.  MEC_NARROW_CONTRACT=0 / 1 turns them off /
+// on wherever the shape allows (tests).
+bool narrow_contract_use(int bs, int64_t wide, int64_t narrow) {
+  if (const char* env = std::getenv("MEC_NARROW_CONTRACT")) {
+    if (env[0] == '0') return false;
+    if (env[0] == '1') return true;
+  }
+  if (bs > 4096) return false;
+  int cus = 0;
+  if (compute_units(&cus) != MEC_OK || cus <= 0) return false;
+  return (narrow + cus - 1) / cus < (wide + cus - 1) / cus;
+}
+
 bool f32_contract_dma(int64_t ldt, int64_t bs) {
   if (const char* env = std::getenv("MEC_F32_CONTRACT_DMA"))
     if (env[0] == '0') return false;
@@ -606,20 +626,31 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   const bool cdma = f32_contract_dma(L.ldt, bs);
   const bool small = dtype == MEC_DTYPE_F32 && vec && cdma && f32_small_tiles(n);
   const TileDims tf = fwd_tile_dims(dtype, vec, small), tc = con_tile_dims(dtype, small);
-  BlockGrid bg{bs, nb, bs / tf.bm, bs / tf.bn, bs / tc.bm, (D + tc.bn - 1) / tc.bn};
+  const bool sep = separate_contractions(dtype);
+  BlockGrid bg{bs, nb, bs / tf.bm, bs / tf.bn, bs / tc.bm, (D + tc.bn - 1) / tc.bn, 0};
+  if (sep && narrow_contract_shape(D, bg.ctm)) {
+    const int64_t sides = (acc_x ? 1 : 0) + (acc_y ? 1 : 0);
+    const int64_t wide = sides * nb * bg.ctm * bg.ctd;
+    const int64_t narrow = sides * nb * (bg.ctm / 2) * (2 * (D / tc.bn) + 1);
+    if (narrow_contract_use(bs, wide, narrow)) {
+      bg.ctd = D / tc.bn;
+      bg.cnw = 1;
+    }
+  }
+  // contraction tiles per block and side
+  const int ct_blk = bg.cnw ? (bg.ctm / 2) * (2 * bg.ctd + 1) : bg.ctm * bg.ctd;
   StepPlan sp{};
   sp.diag_g = step < nb ? (int)step : -1;
   sp.diag_c = step > 0 ? (int)step - 1 : -1;
   sp.accumulate = step > 1;
   sp.g_n = sp.diag_g >= 0 ? nb * bg.gtm * bg.gtn : 0;
-  sp.cx_n = (sp.diag_c >= 0 && acc_x) ? nb * bg.ctm * bg.ctd : 0;
-  sp.cy_n = (sp.diag_c >= 0 && acc_y) ? nb * bg.ctm * bg.ctd : 0;
+  sp.cx_n = (sp.diag_c >= 0 && acc_x) ? nb * ct_blk : 0;
+  sp.cy_n = (sp.diag_c >= 0 && acc_y) ? nb * ct_blk : 0;
   sp.g_pad = round8(sp.g_n);
   sp.cx_pad = round8(sp.cx_n);
   sp.cy_pad = round8(sp.cy_n);
   // bf16: the contractions of diagonal t-1 run in k_grad_contract, before the
   // G' tiles of diagonal t (different scratch buffers, so either order works)
-  const bool sep = separate_contractions(dtype);
   StepPlan sp_g = sp, sp_c = sp;
   if (sep) {
     sp_g.cx_n = sp_g.cy_n = sp_g.cx_pad = sp_g.cy_pad = 0;

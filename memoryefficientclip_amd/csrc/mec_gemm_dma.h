@@ -38,8 +38,9 @@
 //
 // Transposed A (TA = true): A is stored k-row-major (element (m, k) at
 // base[k * ld + m], m contiguous), e.g. a transposed gradient-matrix block.
-// Its stage region is [BK k-rows][BM m] (2 k-rows per 1 KB load block, the
-// 16-byte slot of m-vector v in k-row r at v ^ 4 (r & 3)), and each MFMA
+// Its stage region is [BK k-rows][BM m] (BM = 256: 2 k-rows per 1 KB load
+// block; BM = 512: one; the 16-byte slot of m-vector v in k-row r at
+// v ^ 4 (r & 3)), and each MFMA
 // fragment (8 consecutive k at one m) is assembled from two
 // ds_read_b64_tr_b16: within each group of 16 lanes, source lane j points at
 // 4 consecutive m of k-row k0 + j / 4, and result lane i receives k-rows
@@ -77,7 +78,8 @@ struct Geo {
   static __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
   static constexpr int MPB = KIND == K_F32 ? 4 : 1;    // MFMAs per block and k-step
   static constexpr bool TA = TA_;                      // A stored k-row-major
-  static_assert(!TA || (BM == 256 && ESZ == 2), "transposed A: 16-bit, 512-byte k-rows (BM = 256)");
+  static_assert(!TA || ((BM == 256 || BM == 512) && ESZ == 2), "transposed A: 16-bit, 512- or 1024-byte k-rows");
+  static constexpr int TKPB = TA ? 512 / BM : 1;       // transposed A: k-rows per 1 KB load block
   static constexpr int WM = WM_, WN = WN_, NW = WM * WN, NT = 64 * NW;
   static constexpr int TM = BM / WM, TN = BN / WN;     // wave sub-tile
   static constexpr int FM = TM / 32, FN = TN / 32;     // 32x32 MFMA blocks per wave
@@ -161,9 +163,10 @@ struct LoadPlan {
     for (int i = 0; i < G::IPW; ++i) {
       const int b = i * G::NW + w;
       if (G::TA && i < A_LOADS) {
-        // block b holds k-rows 2b, 2b+1 (within the chunk); lane l fills slot l % 32 of k-row 2b + l / 32
-        const int krow = 2 * b + kr;
-        const int slot = (lane & 31) ^ (4 * (krow & 3));
+        // BM = 256: block b holds k-rows 2b, 2b+1 (within the chunk), lane l fills slot l % 32 of k-row
+        // 2b + l / 32; BM = 512: block b is k-row b, lane l fills its slot l
+        const int krow = G::TKPB * b + (G::TKPB == 2 ? kr : 0);
+        const int slot = (G::TKPB == 2 ? (lane & 31) : lane) ^ (4 * (krow & 3));
         voff[i] = (uint32_t)((int64_t)krow * A.ld + slot * 8) * 2;
       } else {
         const int r = b * G::RPB + rib;
@@ -179,7 +182,7 @@ struct LoadPlan {
     constexpr bool isa = I < A_LOADS;
     uint32_t off, soff;
     if (G::TA && isa) {
-      off = (k0 + 2 * (I * G::NW + w) + kr < kmax_a) ? voff[I] : OOB;
+      off = (k0 + G::TKPB * (I * G::NW + w) + (G::TKPB == 2 ? kr : 0) < kmax_a) ? voff[I] : OOB;
       soff = (uint32_t)(k0 * lda);
     } else {
       off = (k0 + kv < (isa ? kmax_a : kmax_b)) ? voff[I] : OOB;

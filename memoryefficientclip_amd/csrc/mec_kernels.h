@@ -156,17 +156,26 @@ template <typename T, bool VEC, bool SMALL> using GemmTile = typename GemmTileSe
 // side reads transposed through LDS, in a kernel of their own
 // (k_grad_contract) with 256 x 256 tiles of 8 waves.
 template <typename T, bool DMA = true, bool IS16 = Is16<T>::value> struct ConTileSel;
+// (the gradient-matrix operand streams from HBM: three A stages, 160 KB of LDS)
+// nx, ny: the narrow tiles of a last feature column of at most 128 features
+// (D % 256 in [1, 128]): 512 rows x 128 features, the same 128 x 64 per-wave
+// sub-tile shape (operand reads per MFMA) as the wide tiles, two stages (160 KB)
 template <typename T, bool DMA> struct ConTileSel<T, DMA, false> {
   using x = typename std::conditional<DMA, TileD<128, 128, false, 2, 2, gdma::K_F32>, TileF32>::type;
   using y = x;
+  using nx = x;  // (no narrow tiles)
+  using ny = x;
 };
-// (the gradient-matrix operand streams from HBM: three A stages, 160 KB of LDS)
 template <typename T, bool DMA> struct ConTileSel<T, DMA, true> {
   using x = TileD<256, 256, true, 4, 2, kind16<T>(), 3>;
   using y = TileD<256, 256, false, 4, 2, kind16<T>(), 3>;
+  using nx = TileD<512, 128, true, 4, 2, kind16<T>(), 2>;
+  using ny = TileD<512, 128, false, 4, 2, kind16<T>(), 2>;
 };
 template <typename T, bool DMA = true> using ConTileX = typename ConTileSel<T, DMA>::x;
 template <typename T, bool DMA = true> using ConTileY = typename ConTileSel<T, DMA>::y;
+template <typename T> using ConTileNX = typename ConTileSel<T, true>::nx;
+template <typename T> using ConTileNY = typename ConTileSel<T, true>::ny;
 template <typename T, bool DMA, bool SMALL> struct ConTileSmall {
   using x = ConTileX<T, DMA>;
   using y = ConTileY<T, DMA>;
@@ -536,7 +545,9 @@ struct BlockGrid {
   int gtm;   // gradient-matrix tiles per block, row direction (bs / BM)
   int gtn;   // gradient-matrix tiles per block, column direction (bs / BN)
   int ctm;   // contraction tiles per block, row direction (bs / BM of the contraction)
-  int ctd;   // contraction tiles over the features (ceil(D / BN of the contraction))
+  int ctd;   // contraction tiles over the features (ceil(D / BN of the contraction); with cnw, floor(D / BN))
+  int cnw;   // 16-bit, D % 256 in [1, 128], ctm even: the features past ctd * 256 are contracted by narrow
+             // tiles of 512 rows (ConTileNX / ConTileNY), one per pair of row tiles
 };
 
 // Scratch of the backward (all in the input dtype T, row-major):
@@ -941,7 +952,8 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
 }
 
 // Contraction workgroup `sub` (in [0, cx_pad + cy_pad)) of one pipeline step.
-template <class TCX, class TCY, typename T, bool X3 = false>
+// TNX / TNY: the narrow tiles (bg.cnw).
+template <class TCX, class TCY, class TNX, class TNY, typename T, bool X3 = false>
 __device__ __forceinline__ void grad_contract_dispatch(int sub, int N, int D, const GradBufs& gb, const BlockGrid& bg,
                                                        const StepPlan& sp, float* __restrict__ acc_x,
                                                        float* __restrict__ acc_y, char* lds) {
@@ -950,29 +962,55 @@ __device__ __forceinline__ void grad_contract_dispatch(int sub, int N, int D, co
   if (!is_x) sub -= sp.cx_pad;
   const int pid = xcd_remap(sub, is_x ? sp.cx_pad : sp.cy_pad);
   if (pid >= (is_x ? sp.cx_n : sp.cy_n)) return;
-  int tmg, td;
+  int tmg, td, rows = bg.ctm;  // rows: row tiles per block of this tile's height
+  bool narrow = false;
   if constexpr (GtOnly<T>::value) {
     // 16-bit: feature tiles fastest, so the tiles sharing one gradient-matrix
     // panel run side by side on one XCD and the panel is fetched from HBM
     // about once (its contractions are bound by that traffic)
-    tmg = pid / bg.ctd;
-    td = pid - tmg * bg.ctd;
+    if (bg.cnw) {
+      // per pair of row tiles: the wide tiles of both, then the narrow tile
+      // of their 512 rows (feature tile 2 ctd of 128 features)
+      const int per = 2 * bg.ctd + 1;
+      const int grp = pid / per, u = pid - grp * per;
+      if (u == 2 * bg.ctd) {
+        narrow = true;
+        tmg = grp;
+        td = 2 * bg.ctd;
+        rows = bg.ctm / 2;
+      } else {
+        tmg = 2 * grp + u / bg.ctd;
+        td = u - (u / bg.ctd) * bg.ctd;
+      }
+    } else {
+      tmg = pid / bg.ctd;
+      td = pid - tmg * bg.ctd;
+    }
   } else {
     group_tile(pid, bg.nb * bg.ctm, bg.ctd, 8, tmg, td);
   }
-  const int P = tmg / bg.ctm, tm = tmg - P * bg.ctm;  // P: block owning the output rows
+  const int P = tmg / rows, tm = tmg - P * rows;  // P: block owning the output rows
   const int buf = sp.diag_c & 1;
   if (is_x) {
     const int Q = (P + sp.diag_c) % bg.nb;
     const T* gx = (const T*)(GtOnly<T>::value ? gb.gt[buf] : gb.g[buf]) + P * blk;
     const T* gxl = X3 ? (const T*)gb.gt_lo[buf] + P * blk : nullptr;
-    grad_contract_tile<TCX, T, X3>(N, D, gx, gxl, (const T*)gb.yt, (const T*)gb.yt_lo, gb.ldt, bg, P, Q, tm, td,
-                                   sp.accumulate != 0, acc_x, lds);
+    if (narrow)
+      grad_contract_tile<TNX, T, X3>(N, D, gx, gxl, (const T*)gb.yt, (const T*)gb.yt_lo, gb.ldt, bg, P, Q, tm, td,
+                                     sp.accumulate != 0, acc_x, lds);
+    else
+      grad_contract_tile<TCX, T, X3>(N, D, gx, gxl, (const T*)gb.yt, (const T*)gb.yt_lo, gb.ldt, bg, P, Q, tm, td,
+                                     sp.accumulate != 0, acc_x, lds);
   } else {
     const int Q = (P - sp.diag_c + bg.nb) % bg.nb;
+    const T* gy = (const T*)gb.gt[buf] + Q * blk;
     const T* gyl = X3 ? (const T*)gb.gt_lo[buf] + Q * blk : nullptr;
-    grad_contract_tile<TCY, T, X3>(N, D, (const T*)gb.gt[buf] + Q * blk, gyl, (const T*)gb.xt, (const T*)gb.xt_lo,
-                                   gb.ldt, bg, P, Q, tm, td, sp.accumulate != 0, acc_y, lds);
+    if (narrow)
+      grad_contract_tile<TNY, T, X3>(N, D, gy, gyl, (const T*)gb.xt, (const T*)gb.xt_lo, gb.ldt, bg, P, Q, tm, td,
+                                     sp.accumulate != 0, acc_y, lds);
+    else
+      grad_contract_tile<TCY, T, X3>(N, D, gy, gyl, (const T*)gb.xt, (const T*)gb.xt_lo, gb.ldt, bg, P, Q, tm, td,
+                                     sp.accumulate != 0, acc_y, lds);
   }
 }
 
@@ -984,9 +1022,14 @@ __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int
                                                                      float* __restrict__ acc_y) {
   using TCX = ConTileX<T>;
   using TCY = ConTileY<T>;
+  using TNX = ConTileNX<T>;
+  using TNY = ConTileNY<T>;
   static_assert(TCX::BM == TCY::BM && TCX::BN == TCY::BN && TCX::NT == TCY::NT, "one contraction tile shape");
-  __shared__ __attribute__((aligned(1024))) char lds[CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value];
-  grad_contract_dispatch<TCX, TCY, T, X3>(blockIdx.x, N, D, gb, bg, sp, acc_x, acc_y, lds);
+  static_assert(TNX::NT == TCX::NT && TNY::NT == TCX::NT && TNX::BM == 2 * TCX::BM && 2 * TNX::BN == TCX::BN,
+                "narrow tiles: two row tiles high, half a feature tile wide");
+  __shared__ __attribute__((aligned(1024)))
+  char lds[CMax<CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value, CMax<TNX::LDS_BYTES, TNY::LDS_BYTES>::value>::value];
+  grad_contract_dispatch<TCX, TCY, TNX, TNY, T, X3>(blockIdx.x, N, D, gb, bg, sp, acc_x, acc_y, lds);
 }
 
 // One pipeline step: G' tiles of diagonal diag_g and, for fp32, the
@@ -1010,7 +1053,7 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) 
   const int64_t blk = (int64_t)bg.bs * bg.bs;  // elements per G' block
   int sub = blockIdx.x;
   if (sub < sp.cx_pad + sp.cy_pad) {
-    if constexpr (FUSED) grad_contract_dispatch<TCX, TCY, T>(sub, N, D, gb, bg, sp, acc_x, acc_y, lds);
+    if constexpr (FUSED) grad_contract_dispatch<TCX, TCY, TCX, TCY, T>(sub, N, D, gb, bg, sp, acc_x, acc_y, lds);
     return;
   }
   sub -= sp.cx_pad + sp.cy_pad;

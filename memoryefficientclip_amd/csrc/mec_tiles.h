@@ -9,7 +9,8 @@
 //   vectors                   (x rows x y rows, 8 waves), direct global->LDS
 //                             loads (mec_gemm_dma.h); contractions 256 x 256
 //                             (output rows x feature columns, 8 waves) in a
-//                             kernel of their own
+//                             kernel of their own, a last column of at most
+//                             128 features in 512 x 128 tiles where faster
 //   bf16 / fp16, other        forward sums and gradient-matrix tiles 128 x 128
 //   layouts                   staged through registers (mec_gemm_16.h); the
 //                             contractions read internal buffers, which are
@@ -54,6 +55,13 @@ inline TileDims con_tile_dims(int dtype, bool small = false) {
 }
 // contractions run in their own kernel (k_grad_contract) rather than inside k_grad_step
 inline bool separate_contractions(int dtype) { return dtype != kDtypeF32; }
+// k_grad_contract: a last feature column of at most 128 of the 256 features
+// of a tile is contracted by 512 x 128 tiles (one per pair of row tiles, so
+// the block's row tiles must pair up) instead of half-empty 256 x 256 tiles
+inline bool narrow_contract_shape(int d, int ctm) {
+  const int rem = d % 256;
+  return rem != 0 && rem <= 128 && ctm % 2 == 0;
+}
 inline int block_quantum(int dtype) { return dtype == kDtypeF32 ? 128 : 256; }
 
 }  // namespace mec
