@@ -21,7 +21,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import TOL, max_rel, randn_pair, rel_err
+from helpers import TOL, matmul_precision, max_rel, randn_pair, rel_err
 from memoryefficientclip_amd.clip_loss import MemoryEfficientCLIPLoss
 from memoryefficientclip_amd.lit_loss import MemoryEfficientLiTLoss
 
@@ -81,6 +81,36 @@ def test_narrow_contraction_tiles(dt, lit, n, d, normed):
         pairs = [(da_n, rda), (db_n, rdb)]
     errs = [max_rel(g.float(), r) for g, r in pairs]
     tol = TOL[dt]
+    say(f"  loss rel {rel_err(l_n, rl):.2e}; grads {['%.2e' % e for e in errs]}")
+    assert rel_err(l_n, rl) <= tol["loss"]
+    assert all(e <= tol["grad"] for e in errs)
+
+
+@pytest.mark.parametrize("prec,tol", [("high", TOL[torch.float32]), ("medium", TOL[torch.bfloat16])],
+                         ids=["bf16x3", "bf16-products"])
+@pytest.mark.parametrize("lit", [False, True], ids=["clip", "lit"])
+@pytest.mark.parametrize("n,d", [(1024, 300), (2048, 100)])
+def test_narrow_contraction_tiles_fp32_split(prec, tol, lit, n, d):
+    """fp32 inputs under matmul precision "high" (bf16x3: three passes over
+    hi / lo planes) and "medium" (bf16 products) run the same contraction
+    kernel on their bf16 copies."""
+    a, b = randn_pair(n, d, seed=11 * n + d)
+    kind = "LiT" if lit else "CLIP"
+    mod = (MemoryEfficientLiTLoss if lit else MemoryEfficientCLIPLoss)(0.1)
+    say(f"fp32 ({prec}) {kind} n={n} d={d}: narrow vs wide contraction tiles")
+    with matmul_precision(prec):
+        l_n, da_n, db_n = run(mod, a, b, not lit, {"MEC_NARROW_CONTRACT": "1"})
+        l_w, da_w, db_w = run(mod, a, b, not lit, {"MEC_NARROW_CONTRACT": "0"})
+    assert torch.equal(l_n, l_w) and torch.equal(da_n, da_w)
+    if not lit:
+        assert torch.equal(db_n, db_w)
+    if lit:
+        rl, rda = oracle.lit_loss_and_grads(a, b, 0.1)
+        pairs = [(da_n, rda)]
+    else:
+        rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.1)
+        pairs = [(da_n, rda), (db_n, rdb)]
+    errs = [max_rel(g, r) for g, r in pairs]
     say(f"  loss rel {rel_err(l_n, rl):.2e}; grads {['%.2e' % e for e in errs]}")
     assert rel_err(l_n, rl) <= tol["loss"]
     assert all(e <= tol["grad"] for e in errs)
