@@ -16,11 +16,15 @@
 //                       contractions without contending atomics
 //                       (clip_loss.py:127-156, lit_loss.py:123-148); fp32
 //                       runs both kinds of tile in this launch.
+//   k_grad_g_chain  the 16-bit gradient-matrix tiles of inputs already
+//                       normalized, chained in persistent workgroups.
 //   k_grad_contract the 16-bit types' contractions of one pipeline step, in
-//                       a launch of their own with larger tiles.
+//                       a launch of their own with larger tiles (and narrow
+//                       ones for a last column of at most 128 features).
 //   k_sumexp_det, k_det_reduce
-//                   the forward sums without atomics across workgroups
-//                       (deterministic mode), in one pass.
+//                   the forward sums without atomics across workgroups, in
+//                       one pass (deterministic mode, and always for the
+//                       16-bit tiles that chain).
 #pragma once
 #include <type_traits>
 
@@ -583,7 +587,7 @@ struct StepPlan {
   int diag_c;        // diagonal this launch contracts (-1: none)
   int accumulate;    // contraction adds to the accumulators (else overwrites)
   int g_n, g_pad;    // G' tiles (nb * gtm * gtn or 0), padded to a multiple of 8
-  int cx_n, cx_pad;  // x-side contraction tiles (nb * ctm * ctd or 0), padded
+  int cx_n, cx_pad;  // x-side contraction tiles (nb * ctm * ctd; cnw: nb * ctm / 2 * (2 ctd + 1); or 0), padded
   int cy_n, cy_pad;  // y-side contraction tiles, padded
 };
 
