@@ -58,7 +58,21 @@ constexpr uint32_t OOB = 0x80000000u;  // buffer offset that reads as zero
 // and block) and fp32 (v_mfma_f32_32x32x2_f32, four per k-step and block)
 enum Kind { K_BF16 = 0, K_F16 = 1, K_F32 = 2 };
 
-template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16, int SA_ = 2>
+// Blocked gradient-matrix layout (GB): a bs x bs 16-bit block of G'^T
+// (rows j, columns i) stored as 1 KB blocks of 32 rows x 16 columns, block
+// (jb, ib) at element ((jb * bs / 16) + ib) * 512; within it, the 8 values
+// i = 16 ib + 8 ih .. + 7 of row j = 32 jb + jj form the 16-byte slot
+// gb_slot(jj, ih, ib & 1).  A wave's accumulators (after a lane-half swap)
+// fill one whole block per 16-byte store, and the contractions copy whole
+// blocks into LDS.  The XOR keeps their transposed fragment reads (4 rows j x
+// 32 columns i per pass) on distinct banks.
+__host__ __device__ constexpr int gb_slot(int jj, int ih, int ibp) { return (jj ^ (8 * ih + 4 * ibp)) + 32 * ih; }
+__host__ __device__ constexpr int64_t gb_offset(int j, int i, int bs) {
+  return ((int64_t)(j >> 5) * (bs >> 4) + (i >> 4)) * 512 + gb_slot(j & 31, (i >> 3) & 1, (i >> 4) & 1) * 8 + (i & 7);
+}
+
+template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16, int SA_ = 2,
+          bool GB_ = false>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_;
   static constexpr int KIND = KIND_;
@@ -80,6 +94,24 @@ struct Geo {
   static constexpr bool TA = TA_;                      // A stored k-row-major
   static_assert(!TA || ((BM == 256 || BM == 512) && ESZ == 2), "transposed A: 16-bit, 512- or 1024-byte k-rows");
   static constexpr int TKPB = TA ? 512 / BM : 1;       // transposed A: k-rows per 1 KB load block
+  // A in the blocked gradient-matrix layout (gb_offset; bs = ld): TA, the x
+  // side's operand (m = i, k = j: a chunk is 2 x BM/16 blocks), else the y
+  // side's (m = j, k = i: BM/32 x 4 blocks).  Stage block b holds block
+  // (jb, ib) of the chunk: b = jb * BM/16 + ib (TA), b = jb * 4 + ib (else).
+  // k-step s, lane half h take the k-vector kvec(s, h): one i-block per
+  // k-step (blocked) or vector h * NS + s (row-major operands).
+  static constexpr bool GB = GB_;
+  static_assert(!GB || (ESZ == 2 && BK == 64), "blocked A: 16-bit, 64 k per chunk");
+  static __device__ __forceinline__ int kvec(int s, int h) { return GB ? 2 * s + h : h * NS + s; }
+  static __device__ __forceinline__ void gb_block(int b, int& jb, int& ib) {
+    if (TA) {
+      jb = b / (BM / 16);
+      ib = b - jb * (BM / 16);
+    } else {
+      jb = b >> 2;
+      ib = b & 3;
+    }
+  }
   static constexpr int WM = WM_, WN = WN_, NW = WM * WN, NT = 64 * NW;
   static constexpr int TM = BM / WM, TN = BN / WN;     // wave sub-tile
   static constexpr int FM = TM / 32, FN = TN / 32;     // 32x32 MFMA blocks per wave
@@ -143,7 +175,15 @@ struct LoadPlan {
   int kmax_a, kmax_b;
   int64_t lda;     // transposed A: bytes per k-row
   static __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_a(const Operand& A) {
-    return G::TA ? make_rsrc_t<G::BM>(A) : make_rsrc<G::ESZ>(A);
+    if constexpr (G::GB) {
+      // the tile's blocks: TA, i-blocks [0, BM/16) of the j-block rows up to
+      // kmax; else its BM/32 j-block rows (every i-block)
+      const int64_t rows32 = ((int64_t)A.kmax + 31) / 32;
+      const int64_t elems = G::TA ? (rows32 > 0 ? (rows32 - 1) * 32 * A.ld + G::BM * 32 : 0) : (int64_t)G::BM * A.ld;
+      return __builtin_amdgcn_make_buffer_rsrc((void*)A.base, 0, (int)(elems * 2), 0x00020000);
+    } else {
+      return G::TA ? make_rsrc_t<G::BM>(A) : make_rsrc<G::ESZ>(A);
+    }
   }
   static __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_b(const Operand& B) { return make_rsrc<G::ESZ>(B); }
   __device__ __forceinline__ void init(const Operand& A, const Operand& B) {
@@ -162,7 +202,12 @@ struct LoadPlan {
 #pragma unroll
     for (int i = 0; i < G::IPW; ++i) {
       const int b = i * G::NW + w;
-      if (G::TA && i < A_LOADS) {
+      if (G::GB && i < A_LOADS) {
+        // blocked A: load i copies block (jb, ib) of the chunk, lane l its slot l
+        int jb, ib;
+        G::gb_block(b, jb, ib);
+        voff[i] = (uint32_t)(((int64_t)jb * 32 * A.ld + ib * 512 + lane * 8) * 2);
+      } else if (G::TA && i < A_LOADS) {
         // BM = 256: block b holds k-rows 2b, 2b+1 (within the chunk), lane l fills slot l % 32 of k-row
         // 2b + l / 32; BM = 512: block b is k-row b, lane l fills its slot l
         const int krow = G::TKPB * b + (G::TKPB == 2 ? kr : 0);
@@ -181,7 +226,21 @@ struct LoadPlan {
   __device__ __forceinline__ void issue(int k0, char* ad, char* bd) const {
     constexpr bool isa = I < A_LOADS;
     uint32_t off, soff;
-    if (G::TA && isa) {
+    if (G::GB && isa) {
+      int jb, ib;
+      G::gb_block(I * G::NW + w, jb, ib);
+      const int lane = threadIdx.x & 63;
+      if (G::TA) {
+        // k = j: this lane's row of the block; a chunk is k0 / 32 j-block rows down
+        const int jj = (lane & 31) ^ (8 * kr + 4 * (ib & 1));
+        off = (k0 + 32 * jb + jj < kmax_a) ? voff[I] : OOB;
+        soff = (uint32_t)(k0 * lda);
+      } else {
+        // k = i: this lane's 8 columns; a chunk is k0 / 16 blocks along
+        off = (k0 + 16 * ib + 8 * kr < kmax_a) ? voff[I] : OOB;
+        soff = (uint32_t)k0 * 64;
+      }
+    } else if (G::TA && isa) {
       off = (k0 + G::TKPB * (I * G::NW + w) + (G::TKPB == 2 ? kr : 0) < kmax_a) ? voff[I] : OOB;
       soff = (uint32_t)(k0 * lda);
     } else {
@@ -228,36 +287,64 @@ __device__ __forceinline__ i16x4_t read_tr4(const char* p) {
   return v;
 }
 
+// Operand addresses of k-step s for this lane.  a_ptr: its A vector of
+// fragment 0 (fragment i is 4 KB further: 32 rows of 128 bytes, or 4 blocks
+// of the blocked layout), for A that is not transposed.  ta_ptr: the source
+// address of transposed-A read `half` of fragment i: lane group g = lane / 16
+// covers m0 + 16 (g & 1) .. + 15 and k-vector kvec(s, g >> 1); source lane j
+// reads k-row kb + 4 half + j / 4, m-quad j % 4.  b_ptr: its B vector of
+// fragment 0.
+template <class G>
+__device__ __forceinline__ const char* a_ptr(const char* stage, int s) {
+  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) / G::WN;
+  const int q = lane & 31, h = lane >> 5;
+  if constexpr (G::GB) {
+    // m = j: block (wm * TM / 32, s), row q, i-half h
+    return stage + ((wm * G::TM / 32) * 4 + s) * 1024 + gb_slot(q, h, s & 1) * 16;
+  } else {
+    return stage + (wm * G::TM + q) * G::ROWB + ((G::kvec(s, h) ^ G::swz(q)) << 4);
+  }
+}
+template <class G>
+__device__ __forceinline__ const char* ta_ptr(const char* stage, int s, int i, int half) {
+  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) / G::WN;
+  const int g = lane >> 4, j = lane & 15;
+  const int kb = G::kvec(s, g >> 1) * 8;
+  const int m = wm * G::TM + i * 32 + 16 * (g & 1) + 4 * (j & 3);
+  const int krow = kb + 4 * half + (j >> 2);
+  if constexpr (G::GB) {
+    // krow = 32 (s >> 1) + 16 (s & 1) + r with r < 16, and the slot's XOR
+    // touches bits 2-3 only: the k-step adds a constant to a per-lane offset
+    const int ib = m >> 4, ih = (m >> 3) & 1, r = krow & 15;
+    const int lane_off = ib * 1024 + ((r ^ (8 * ih + 4 * (ib & 1))) + 32 * ih) * 16 + (m & 7) * 2;
+    return stage + lane_off + (s >> 1) * (G::BM / 16) * 1024 + (s & 1) * 256;
+  } else {
+    const int slot = (m >> 3) ^ (4 * (krow & 3));
+    return stage + krow * (G::BM * 2) + slot * 16 + (m & 7) * 2;
+  }
+}
+template <class G>
+__device__ __forceinline__ const char* b_ptr(const char* bstage, int s) {
+  const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) % G::WN;
+  const int q = lane & 31, h = lane >> 5;
+  return bstage + (wn * G::TN + q) * G::ROWB + ((G::kvec(s, h) ^ G::swz(q)) << 4);
+}
+
 template <class G>
 __device__ __forceinline__ void read_frags(const char* stage, const char* bstage, int s, Frags<G>& f) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wm = w / G::WN, wn = w % G::WN;
-  const int q = lane & 31, h = lane >> 5;
-  const int off = (((h * G::NS + s) ^ G::swz(q)) << 4);
-  if (G::TA) {
-    // fragment of 32 m x 16 k: lane group g = lane / 16 covers m0 + 16 (g & 1) .. + 15 and
-    // logical k-vector (g >> 1) * NS + s; source lane j reads k-row kb + j / 4, m-quad j % 4
-    const int g = lane >> 4, j = lane & 15;
-    const int kb = ((g >> 1) * G::NS + s) * 8;
+  if constexpr (G::TA) {
+    // fragment of 32 m x 16 k: the low and the high four k-values of each lane
 #pragma unroll
     for (int i = 0; i < G::FM; ++i) {
-      const int m = wm * G::TM + i * 32 + 16 * (g & 1) + 4 * (j & 3);
-      i16x4_t lo, hi;
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int krow = kb + 4 * half + (j >> 2);
-        const int slot = (m >> 3) ^ (4 * (krow & 3));
-        const i16x4_t v = read_tr4(stage + krow * (G::BM * 2) + slot * 16 + (m & 7) * 2);
-        if (half == 0) lo = v;
-        else hi = v;
-      }
+      const i16x4_t lo = read_tr4(ta_ptr<G>(stage, s, i, 0));
+      const i16x4_t hi = read_tr4(ta_ptr<G>(stage, s, i, 1));
       f.a[i] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   } else {
-    const uint32_t abase = lds_off(stage + (wm * G::TM + q) * G::ROWB + off);
+    const uint32_t abase = lds_off(a_ptr<G>(stage, s));
     static_for<G::FM>([&](auto i) { f.a[i] = lds_read_b128<i * 32 * G::ROWB>(abase); });
   }
-  const uint32_t bbase = lds_off(bstage + (wn * G::TN + q) * G::ROWB + off);
+  const uint32_t bbase = lds_off(b_ptr<G>(bstage, s));
   static_for<G::FN>([&](auto j) { f.b[j] = lds_read_b128<j * 32 * G::ROWB>(bbase); });
 }
 
@@ -275,26 +362,15 @@ struct FragReader {
   uint32_t abase, bbase;
   uint32_t ta[G::TA ? G::FM : 1][2];  // transposed A: per fragment and half
   __device__ __forceinline__ FragReader(const char* stage, const char* bstage, int s) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int wm = w / G::WN, wn = w % G::WN;
-    const int q = lane & 31, h = lane >> 5;
-    const int off = (((h * G::NS + s) ^ G::swz(q)) << 4);
-    abase = lds_off(stage + (wm * G::TM + q) * G::ROWB + off);
-    bbase = lds_off(bstage + (wn * G::TN + q) * G::ROWB + off);
+    bbase = lds_off(b_ptr<G>(bstage, s));
     if constexpr (G::TA) {
-      // the addresses of read_frags' transposed-A branch
-      const int g = lane >> 4, j = lane & 15;
-      const int kb = ((g >> 1) * G::NS + s) * 8;
+      abase = 0;
 #pragma unroll
-      for (int i = 0; i < G::FM; ++i) {
-        const int m = wm * G::TM + i * 32 + 16 * (g & 1) + 4 * (j & 3);
+      for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int krow = kb + 4 * half + (j >> 2);
-          const int slot = (m >> 3) ^ (4 * (krow & 3));
-          ta[i][half] = lds_off(stage + krow * (G::BM * 2) + slot * 16 + (m & 7) * 2);
-        }
-      }
+        for (int half = 0; half < 2; ++half) ta[i][half] = lds_off(ta_ptr<G>(stage, s, i, half));
+    } else {
+      abase = lds_off(a_ptr<G>(stage, s));
     }
   }
   template <int R>

@@ -47,7 +47,7 @@ namespace mec {
 struct TileF32 {
   using Elem = float;
   using Op = g32::Operand;
-  static constexpr bool TA = false;
+  static constexpr bool TA = false, GB = false;
   static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2, WM = 2, WN = 2, NT = 256;
   static constexpr int LDS_BYTES = g32::LDS_FLOATS * 4;
   static constexpr bool CHAIN = false;
@@ -65,6 +65,7 @@ struct TileF32 {
 template <bool F16>
 struct Pack16 {
   static __device__ __forceinline__ uint16_t pack(float v) { return F16 ? f32_to_f16(v) : f32_to_bf16(v); }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) { return F16 ? pack2_f16(a, b) : pack2_bf16(a, b); }
   static __device__ __forceinline__ void store4(uint16_t* p, float a, float b, float c, float d) {
     if constexpr (F16)
       *(uint2*)p = uint2{pack2_f16(a, b), pack2_f16(c, d)};
@@ -78,7 +79,7 @@ template <bool F16>
 struct Tile16V : Pack16<F16> {
   using Elem = uint16_t;
   using Op = g16::Operand;
-  static constexpr bool TA = false;
+  static constexpr bool TA = false, GB = false;
   static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2, WM = 2, WN = 2, NT = 256;
   static constexpr int LDS_BYTES = g16::Cfg<MEC_16BIT_BK>::LDS_ELEMS * 2;
   static constexpr bool CHAIN = false;
@@ -100,13 +101,14 @@ template <> struct PackOf<gdma::K_F32> { using type = PackF32; };
 // BM_ x BN_, direct global->LDS loads (16-byte aligned rows, ld and kmax
 // multiples of the elements per 16-byte vector), element kind KIND (bf16,
 // fp16 or fp32); TA_: A stored k-row-major (a transposed 16-bit
-// gradient-matrix block)
-template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND, int SA_ = 2>
+// gradient-matrix block); GB_: A a 16-bit gradient-matrix block in the
+// blocked layout (gdma::gb_offset; TA_ then selects the x side's reading)
+template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND, int SA_ = 2, bool GB_ = false>
 struct TileD : PackOf<KIND>::type {
   using Elem = typename std::conditional<KIND == gdma::K_F32, float, uint16_t>::type;
   using Op = gdma::Operand;
-  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, SA_>;
-  static constexpr bool TA = TA_;
+  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, SA_, GB_>;
+  static constexpr bool TA = TA_, GB = GB_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
   static constexpr int LDS_BYTES = G::LDS_BYTES;
@@ -171,10 +173,10 @@ template <typename T, bool DMA> struct ConTileSel<T, DMA, false> {
   using ny = x;
 };
 template <typename T, bool DMA> struct ConTileSel<T, DMA, true> {
-  using x = TileD<256, 256, true, 4, 2, kind16<T>(), 3>;
-  using y = TileD<256, 256, false, 4, 2, kind16<T>(), 3>;
-  using nx = TileD<512, 128, true, 4, 2, kind16<T>(), 2>;
-  using ny = TileD<512, 128, false, 4, 2, kind16<T>(), 2>;
+  using x = TileD<256, 256, true, 4, 2, kind16<T>(), 3, true>;
+  using y = TileD<256, 256, false, 4, 2, kind16<T>(), 3, true>;
+  using nx = TileD<512, 128, true, 4, 2, kind16<T>(), 2, true>;
+  using ny = TileD<512, 128, false, 4, 2, kind16<T>(), 2, true>;
 };
 template <typename T, bool DMA = true> using ConTileX = typename ConTileSel<T, DMA>::x;
 template <typename T, bool DMA = true> using ConTileY = typename ConTileSel<T, DMA>::y;
@@ -557,8 +559,8 @@ struct BlockGrid {
 // Scratch of the backward (all in the input dtype T, row-major):
 //   G[2]   two buffers of nb blocks of bs x bs: block I of buffer s&1 holds
 //          G'(I, (I+s) mod nb) of diagonal s (fp32 only);
-//   GT[2]  the same blocks transposed (fp32: CLIP only; 16-bit: always, the
-//          only copy);
+//   GT[2]  the same blocks transposed (fp32: CLIP only, row-major; 16-bit:
+//          always, the only copy, in the blocked layout gdma::gb_offset);
 //   XT, YT the normalised inputs transposed, [D][ldt] with ldt = N rounded
 //          up to 128 and zero columns [N, ldt): element (d, i) = rx_i x_i[d].
 // Every contraction operand is then K-major (k contiguous).  The bf16x3 mode
@@ -633,11 +635,11 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN]
 
 // 16-bit: G'_ij of this wave's TM x TN accumulators, staged through LDS as
 // [j][i] (row pitch gt_pitch(BM) = 2 BM + 16 bytes; 4 consecutive i per 8-byte write), then
-// written to GTb (row pitch bs) as whole tile rows of 2 BM bytes, 16 bytes
-// per lane.  MASK zeroes the diagonal and entries outside [0, N).  Every row of
-// the tile is written (zeros for j >= N), so the contractions may read a
-// tile's rows and columns past N as zeros.  lds must hold BN * gt_pitch(BM) bytes
-// and be free (no wave still reading it).
+// written to the tile's blocks at GTb (blocked layout, gt_write_plane).
+// MASK zeroes the diagonal and entries outside [0, N).  Every row of the tile
+// is written (zeros for j >= N), so the contractions may read a tile's rows
+// and columns past N as zeros.  lds must hold BN * gt_pitch(BM) bytes and be
+// free (no wave still reading it).
 // The 8-byte chunk c of row j sits at chunk c ^ ((j >> 4) & 1): the 32 lanes
 // of a half-wave write one chunk of 32 consecutive rows, which then fall on
 // 32 distinct bank pairs (rows j and j + 16 would share them at this pitch).
@@ -651,20 +653,25 @@ __device__ __forceinline__ void gt_stage4(char* lds, int ml, int row, float a, f
   TL::store4((uint16_t*)(lds + row * gt_pitch(TL::BM) + chunk * 8), a, b, c, d);
 }
 
-// the staged tile to GTb (row pitch bs) as whole tile rows, 16 bytes per lane.
-// Non-temporal stores: the block is read back from HBM by the next launch's
-// contractions and would only evict their operand panels from L2 (measured:
-// config 4 backward 22.6 -> 21.9 ms).
+// The staged tile to GTb, the tile's first block in the blocked layout
+// (gdma::gb_offset): each wave instruction writes one whole 1 KB block
+// (32 tile columns j x 16 rows i), reading its 64 16-byte slots from the
+// staging.  Non-temporal stores: the block is read back from HBM by the next
+// launch's contractions and would only evict their operand panels from L2
+// (measured: config 4 backward 22.6 -> 21.9 ms).
 template <class TL>
 __device__ __forceinline__ void gt_write_plane(const char* lds, uint16_t* __restrict__ GTb, int bs) {
   constexpr int PITCH = gt_pitch(TL::BM);
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  constexpr int VPR = TL::BM * 2 / 16;  // 16-byte vectors per tile row
-  for (int v = threadIdx.x; v < TL::BN * VPR; v += TL::NT) {
-    const int row = v / VPR, cv = v - row * VPR;
-    u32x4 u = *(const u32x4*)(lds + row * PITCH + cv * 16);
+  constexpr int IBT = TL::BM / 16;  // i-blocks per tile
+  const int64_t rowb = (int64_t)(bs >> 4) * 512;
+  for (int v = threadIdx.x; v < TL::BN * TL::BM / 8; v += TL::NT) {
+    const int blk = v >> 6, slot = v & 63;
+    const int jb = blk / IBT, ib = blk - jb * IBT;
+    const int ih = slot >> 5, row = jb * 32 + ((slot & 31) ^ (8 * ih + 4 * (ib & 1)));
+    u32x4 u = *(const u32x4*)(lds + row * PITCH + (2 * ib + ih) * 16);
     if ((row >> 4) & 1) u = u32x4{u.z, u.w, u.x, u.y};  // undo the chunk swizzle
-    __builtin_nontemporal_store(u, (u32x4*)(GTb + (int64_t)row * bs + cv * 8));
+    __builtin_nontemporal_store(u, (u32x4*)(GTb + jb * rowb + ib * 512 + slot * 8));
   }
 }
 
@@ -707,11 +714,13 @@ __device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL
 }
 
 // bf16x3: G'^T as a bf16 hi plane bf16(G') at GTh and a lo plane
-// bf16(G' - hi) at GTl.  Both planes of half the tile's columns fit the
-// staging area of one full plane, so the tile goes out in two halves: each
-// wave's column blocks bn < FN/2, then the rest.  Staging row s (of BN/2)
-// holds tile column nl(s) as in grad_gt_store_lds (same swizzle), the hi
-// plane in rows [0, BN/2), the lo plane after it.
+// bf16(G' - hi) at GTl (both tile pointers in the blocked layout).  Both
+// planes of half the tile's columns fit the staging area of one full plane,
+// so the tile goes out in two halves: each wave's column blocks bn < FN/2,
+// then the rest.  Staging row s (of BN/2) holds tile column nl(s) as in
+// grad_gt_store_lds (same swizzle), the hi plane in rows [0, BN/2), the lo
+// plane after it; every 32 consecutive staged rows are 32 consecutive tile
+// columns, one row of blocks.
 template <class TL>
 __device__ __forceinline__ int x3_stage_col(int srow, int half) {
   constexpr int HT = TL::TN / 2;  // staged columns per wave and half
@@ -730,6 +739,7 @@ __device__ __forceinline__ void grad_gt_store_lds_x3(const f32x16 (&acc)[TL::FM]
   constexpr int VPR = TL::BM * 2 / 16;  // 16-byte vectors per tile row
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
+  const int64_t rowb = (int64_t)(bs >> 4) * 512;
   char* lds_lo = lds + HROWS * PITCH;
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
@@ -765,56 +775,60 @@ __device__ __forceinline__ void grad_gt_store_lds_x3(const f32x16 (&acc)[TL::FM]
       }
     }
     __syncthreads();
+    // one whole block per wave instruction (see gt_write_plane)
+    constexpr int IBT = TL::BM / 16;
+    static_assert(HT % 32 == 0 && HROWS * VPR % 64 == 0, "staged rows in whole rows of blocks");
     for (int v = threadIdx.x; v < 2 * HROWS * VPR; v += TL::NT) {
-      const int prow = v / VPR, cv = v - prow * VPR;  // staged row over both planes
-      const int lo = prow >= HROWS, srow = prow - lo * HROWS;
-      u32x4 u = *(const u32x4*)(lds + prow * PITCH + cv * 16);
+      const int lo = v >= HROWS * VPR, u0 = v - lo * HROWS * VPR;
+      const int blk = u0 >> 6, slot = u0 & 63;
+      const int jg = blk / IBT, ib = blk - jg * IBT;
+      const int ih = slot >> 5, srow = jg * 32 + ((slot & 31) ^ (8 * ih + 4 * (ib & 1)));
+      u32x4 u = *(const u32x4*)(lds + (lo * HROWS + srow) * PITCH + (2 * ib + ih) * 16);
       if ((srow >> 4) & 1) u = u32x4{u.z, u.w, u.x, u.y};  // undo the chunk swizzle
-      const int nl = x3_stage_col<TL>(srow, half);
-      __builtin_nontemporal_store(u, (u32x4*)((lo ? GTl : GTh) + (int64_t)nl * bs + cv * 8));
+      const int jb = x3_stage_col<TL>(jg * 32, half) >> 5;
+      __builtin_nontemporal_store(u, (u32x4*)((lo ? GTl : GTh) + jb * rowb + ib * 512 + slot * 8));
     }
     if (half == 0) __syncthreads();  // every wave is done reading the first half
   }
 }
 
-// Chained 16-bit gradient-matrix tiles (k_grad_g_chain): G'^T staged half a
-// tile at a time in the ring stage the next tile's loads leave free (64 KB).
-// Half h holds tile columns j of blocks bn = 2h, 2h + 1 of each wave column:
-// staging row s = wn * 64 + (bn - 2h) * 32 + l % 32 (512 bytes, no padding),
-// with the 8-byte chunk c (4 consecutive i) of row s at c ^ (s % 32), so that
-// the 32 lanes writing one chunk of 32 rows hit 32 distinct bank pairs and a
-// half-wave reading one row covers it once.  Each staged row is one 512-byte
-// row of G'^T, written as 32 16-byte stores; 16 per lane per tile.
+// Chained 16-bit gradient-matrix tiles (k_grad_g_chain): G'^T straight from
+// the accumulators into the tile's blocks at GTb (blocked layout,
+// gdma::gb_offset), no staging.  For a 32 x 32 accumulator block, register
+// group g4 of lane l holds rows i = 8 g4 + 4 (l / 32) .. + 3 of column
+// j = l % 32; swapping groups 2p + 1 of the low lane half with groups 2p of
+// the high half (v_permlane32_swap) leaves lane l with the 8 rows
+// 16 p + 8 (l / 32) .. + 7, i.e. slot (l % 32, l / 32) of i-block p: every
+// 16-byte store of the wave writes one whole 1 KB block, 16 per lane and tile.
 template <class TL>
 constexpr int gt_chain_stores() {
-  return 2 * (TL::BN / 2) * (TL::BM * 2 / 16) / TL::NT;
+  return TL::FM * TL::FN * 2;
 }
 template <class TL, bool LIT, bool NORM, bool MASK, int GSC>
 __device__ __forceinline__ void grad_gt_store_chain(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0,
                                                     int N, uint16_t* __restrict__ GTb, int bs, const float* s_rx,
-                                                    const float* s_ry, const float* s_ir, const float* s_ic,
-                                                    char* stage) {
-  static_assert(TL::BM == 256 && TL::WN == 2 && TL::FN == 4 && TL::TN == 128, "256 x 256 tiles, 2 wave columns");
+                                                    const float* s_ry, const float* s_ir, const float* s_ic) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
+  const int64_t rowb = (int64_t)(bs >> 4) * 512;  // elements per row of blocks
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  for (int bn = 0; bn < TL::FN; ++bn) {
+    const int nl = wn * TL::TN + bn * 32 + (lane & 31);
+    const int j = j0 + nl;
+    const float cy = NORM ? c * s_ry[nl] : c;
+    const float icj = s_ic[nl];
+    uint16_t* gjb = GTb + ((wn * TL::TN + bn * 32) >> 5) * rowb;
 #pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-      const int bn = 2 * half + bb;
-      const int nl = wn * TL::TN + bn * 32 + (lane & 31);
-      const int j = j0 + nl;
-      const int srow = wn * 64 + bb * 32 + (lane & 31);
-      const float cy = NORM ? c * s_ry[nl] : c;
-      const float icj = s_ic[nl];
+    for (int bm = 0; bm < TL::FM; ++bm) {
 #pragma unroll
-      for (int bm = 0; bm < TL::FM; ++bm) {
+      for (int p = 0; p < 2; ++p) {
+        uint32_t pk[2][2];
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
+        for (int q = 0; q < 2; ++q) {
           float gv[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int r = 4 * g4 + e;
+            const int r = 4 * (2 * p + q) + e;
             const int ml = wm * TL::TM + bm * 32 + acc_row(r, lane);
             const int i = i0 + ml;
             const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
@@ -824,22 +838,20 @@ __device__ __forceinline__ void grad_gt_store_chain(const f32x16 (&acc)[TL::FM][
             if (MASK) g = (i < N && j < N && i != j) ? g : 0.f;
             gv[e] = g;
           }
-          const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g4, lane);
-          const int pos = (ml >> 2) ^ (srow & 31);
-          TL::store4((uint16_t*)(stage + srow * 512 + pos * 8), gv[0], gv[1], gv[2], gv[3]);
+          pk[q][0] = TL::pack2(gv[0], gv[1]);
+          pk[q][1] = TL::pack2(gv[2], gv[3]);
         }
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(pk[0][d], pk[1][d], false, false);
+          pk[0][d] = sw[0];
+          pk[1][d] = sw[1];
+        }
+        const int ib = (wm * TL::TM + bm * 32) / 16 + p;
+        const u32x4 u = u32x4{pk[0][0], pk[0][1], pk[1][0], pk[1][1]};
+        __builtin_nontemporal_store(u, (u32x4*)(gjb + ib * 512 + gdma::gb_slot(lane & 31, lane >> 5, p) * 8));
       }
     }
-    lds_barrier();
-    // the staged half: row s is tile column wn * TN + half * 64 + s % 64
-    for (int v = threadIdx.x; v < (TL::BN / 2) * 32; v += TL::NT) {
-      const int srow = v >> 5, cv = v & 31, k = srow & 31;
-      u32x4 u = *(const u32x4*)(stage + srow * 512 + ((cv ^ (k >> 1)) << 4));
-      if (k & 1) u = u32x4{u.z, u.w, u.x, u.y};
-      const int nl = (srow >> 6) * TL::TN + half * 64 + (srow & 63);
-      __builtin_nontemporal_store(u, (u32x4*)(GTb + (int64_t)nl * bs + cv * 8));
-    }
-    if (half == 0) lds_barrier();  // every wave done reading before the second half is staged
   }
 }
 
@@ -917,8 +929,9 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
   const int qn = min(bg.bs, N - q0);
   // entries of G' and XT/YT at k in [qn, round8(qn)) are stored zeros
   const int kq = (qn + 7) & ~7;
-  // A: rows tm*BM.. of the block (K-major), or columns tm*BM.. of a transposed block
-  const int64_t a_off = TC::TA ? (int64_t)(tm * TC::BM) : (int64_t)(tm * TC::BM) * bg.bs;
+  // A: rows tm*BM.. of the block (K-major), or columns tm*BM.. of a transposed
+  // block (blocked layout: i-block tm*BM/16 of the first j-block row)
+  const int64_t a_off = TC::TA ? (int64_t)(tm * TC::BM) * (TC::GB ? 32 : 1) : (int64_t)(tm * TC::BM) * bg.bs;
   const auto A = tile_op<TC>(Gblk + a_off, bg.bs, TC::BM, kq);
   const int64_t b_off = (int64_t)d0 * ldt + q0;
   const auto B = tile_op<TC>(OT + b_off, ldt, min(D - d0, TC::BN), kq);
@@ -1071,7 +1084,9 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) 
   if (i0 >= N || j0 >= N) return;  // never read by the contraction
   const int buf = sp.diag_g & 1;
   T* Gb = GtOnly<T>::value ? nullptr : (T*)gb.g[buf] + I * blk + (int64_t)(tm * TF::BM) * bg.bs + tn * TF::BN;
-  const int64_t gt_off = I * blk + (int64_t)(tn * TF::BN) * bg.bs + tm * TF::BM;
+  // G'^T: row-major (fp32) or the tile's first block in the blocked layout (16-bit)
+  const int64_t gt_off = I * blk + (GtOnly<T>::value ? gdma::gb_offset(tn * TF::BN, tm * TF::BM, bg.bs)
+                                                     : (int64_t)(tn * TF::BN) * bg.bs + tm * TF::BM);
   T* GTb = (LIT && !GtOnly<T>::value) ? nullptr : (T*)gb.gt[buf] + gt_off;
   T* GTl = X3 ? (T*)gb.gt_lo[buf] + gt_off : nullptr;
   grad_g_tile<TF, T, LIT, NORM, VEC, X3>(X, ldx, Y, ldy, N, D, kmax, c, ws, Gb, GTb, GTl, bg.bs, i0, j0, lds, s_rx,
@@ -1084,7 +1099,7 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) 
 // order; contiguous row-major runs of tiles or 2D blocks per workgroup were
 // slower here, unlike in the forward), and the last
 // chunk of each tile's k-loop loads chunk 0 of the next, which lands while
-// the tile's G'^T is staged (in the other ring stage) and stored
+// the tile's G'^T is stored straight from the accumulators
 // (grad_gt_store_chain).  The next tile's first barrier waits only for those
 // loads, not for the stores.  The per-row and per-column vectors of a tile
 // (rx, ry, 1/R, 1/C) reach LDS by direct loads into one of two buffers,
@@ -1097,7 +1112,6 @@ __global__ __launch_bounds__((FwdTile<T, true>::NT), 1) void k_grad_g_chain(
   using TL = FwdTile<T, true>;
   static_assert(TL::CHAIN && GtOnly<T>::value, "chained 16-bit direct-to-LDS tiles");
   static_assert(TL::BM == 256 && TL::BN == 256 && TL::NT == 512, "one 64-float quarter per vector load, 8 waves");
-  static_assert(TL::STAGE_BYTES >= (TL::BN / 2) * 512, "a staged half fits one ring stage");
   enum { V_RX = 0, V_RY = 1, V_IR = 2, V_IC = 3 };
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
   __shared__ __attribute__((aligned(16))) float s_vec[2][4][TL::BM];
@@ -1116,7 +1130,7 @@ __global__ __launch_bounds__((FwdTile<T, true>::NT), 1) void k_grad_g_chain(
     const int J = (I + sp.diag_g) % bg.nb;
     i0 = I * bg.bs + tm * TL::BM;
     j0 = J * bg.bs + tn * TL::BN;
-    gt = (uint16_t*)gb.gt[buf] + I * blk + (int64_t)(tn * TL::BN) * bg.bs + tm * TL::BM;
+    gt = (uint16_t*)gb.gt[buf] + I * blk + gdma::gb_offset(tn * TL::BN, tm * TL::BM, bg.bs);
     return i0 < N && j0 < N;
   };
   auto next_valid = [&](int tile, int& i0, int& j0, uint16_t*& gt) {
@@ -1167,20 +1181,16 @@ __global__ __launch_bounds__((FwdTile<T, true>::NT), 1) void k_grad_g_chain(
     };
     TL::template chain<decltype(hook), NST>(lp, op_a(i1), op_b(j1), has_next, D, lds, p0, acc, hook, !first);
     first = false;
-    // every wave is past its last read of the stage the staging reuses (the
-    // one the next tile's chunk 0 does not go to)
-    lds_barrier();
-    char* stage = lds + (p0 ^ 1) * TL::STAGE_BYTES;
     const float* sv = &s_vec[vb][0][0];
     const bool diag = i0 < j0 + TL::BN && j0 < i0 + TL::BM;
     if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
       grad_gt_store_chain<TL, LIT, NORM, false, (int)GScale<T>::value>(
           acc, c, i0, j0, N, gt, bg.bs, sv + V_RX * TL::BM, sv + V_RY * TL::BM, sv + V_IR * TL::BM,
-          sv + V_IC * TL::BM, stage);
+          sv + V_IC * TL::BM);
     else
       grad_gt_store_chain<TL, LIT, NORM, true, (int)GScale<T>::value>(
           acc, c, i0, j0, N, gt, bg.bs, sv + V_RX * TL::BM, sv + V_RY * TL::BM, sv + V_IR * TL::BM,
-          sv + V_IC * TL::BM, stage);
+          sv + V_IC * TL::BM);
     if (!has_next) break;
     tile = next;
     i0 = i1;
