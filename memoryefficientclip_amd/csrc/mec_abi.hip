@@ -291,8 +291,9 @@ void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
 //   bf16x3:                [GT0 | GT1 | GTlo0 | GTlo1 | XT | YT | XTlo | YTlo]
 // G0/G1 (and their transposes GT0/GT1) double-buffer one block diagonal of
 // G' (nb blocks of bs x bs; the 16-bit types keep only the transposed copy,
-// bf16x3 its hi and lo planes); XT/YT are the normalised inputs transposed,
-// [d][ldt] with ldt = n rounded up to 128 (bf16x3: hi and lo planes).
+// in the blocked layout gdma::gb_offset, bf16x3 its hi and lo planes); XT/YT
+// are the normalised inputs transposed, [d][ldt] with ldt = n rounded up to
+// 128 (bf16x3: hi and lo planes).
 struct ScratchLayout {
   int bs, nb;
   int ncopies;                     // gradient-matrix buffers: 4 or 2
