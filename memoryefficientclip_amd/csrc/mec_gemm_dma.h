@@ -138,7 +138,8 @@ struct Geo {
 };
 
 struct Operand {
-  const void* base;  // element (row, k) at base[row * ld + k] (transposed A: base[k * ld + row])
+  const void* base;  // element (row, k) at base[row * ld + k] (transposed A: base[k * ld + row];
+                     // blocked A: the tile's first block, ld = the block's bs)
   int64_t ld;
   int rows;          // valid rows from base (rows beyond read as 0; transposed A: all BM rows readable)
   int kmax;          // valid k range [0, kmax), a multiple of the elements per 16-byte vector
