@@ -633,16 +633,12 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN]
   }
 }
 
-// 16-bit: G'_ij of this wave's TM x TN accumulators, staged through LDS as
-// [j][i] (row pitch gt_pitch(BM) = 2 BM + 16 bytes; 4 consecutive i per 8-byte write), then
-// written to the tile's blocks at GTb (blocked layout, gt_write_plane).
-// MASK zeroes the diagonal and entries outside [0, N).  Every row of the tile
-// is written (zeros for j >= N), so the contractions may read a tile's rows
-// and columns past N as zeros.  lds must hold BN * gt_pitch(BM) bytes and be
-// free (no wave still reading it).
-// The 8-byte chunk c of row j sits at chunk c ^ ((j >> 4) & 1): the 32 lanes
-// of a half-wave write one chunk of 32 consecutive rows, which then fall on
-// 32 distinct bank pairs (rows j and j + 16 would share them at this pitch).
+// bf16x3 staging (grad_gt_store_lds_x3): G'_ij staged through LDS as [j][i]
+// (row pitch gt_pitch(BM) = 2 BM + 16 bytes; 4 consecutive i per 8-byte
+// write).  The 8-byte chunk c of row j sits at chunk c ^ ((j >> 4) & 1): the
+// 32 lanes of a half-wave write one chunk of 32 consecutive rows, which then
+// fall on 32 distinct bank pairs (rows j and j + 16 would share them at this
+// pitch).
 constexpr int gt_pitch(int bm) { return 2 * bm + 16; }
 
 // 4 consecutive i (tile rows ml .. ml+3) into staging row `row` (a tile
@@ -653,74 +649,14 @@ __device__ __forceinline__ void gt_stage4(char* lds, int ml, int row, float a, f
   TL::store4((uint16_t*)(lds + row * gt_pitch(TL::BM) + chunk * 8), a, b, c, d);
 }
 
-// The staged tile to GTb, the tile's first block in the blocked layout
-// (gdma::gb_offset): each wave instruction writes one whole 1 KB block
-// (32 tile columns j x 16 rows i), reading its 64 16-byte slots from the
-// staging.  Non-temporal stores: the block is read back from HBM by the next
-// launch's contractions and would only evict their operand panels from L2
-// (measured: config 4 backward 22.6 -> 21.9 ms).
-template <class TL>
-__device__ __forceinline__ void gt_write_plane(const char* lds, uint16_t* __restrict__ GTb, int bs) {
-  constexpr int PITCH = gt_pitch(TL::BM);
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  constexpr int IBT = TL::BM / 16;  // i-blocks per tile
-  const int64_t rowb = (int64_t)(bs >> 4) * 512;
-  for (int v = threadIdx.x; v < TL::BN * TL::BM / 8; v += TL::NT) {
-    const int blk = v >> 6, slot = v & 63;
-    const int jb = blk / IBT, ib = blk - jb * IBT;
-    const int ih = slot >> 5, row = jb * 32 + ((slot & 31) ^ (8 * ih + 4 * (ib & 1)));
-    u32x4 u = *(const u32x4*)(lds + row * PITCH + (2 * ib + ih) * 16);
-    if ((row >> 4) & 1) u = u32x4{u.z, u.w, u.x, u.y};  // undo the chunk swizzle
-    __builtin_nontemporal_store(u, (u32x4*)(GTb + jb * rowb + ib * 512 + slot * 8));
-  }
-}
-
-template <class TL, bool LIT, bool NORM, bool MASK>
-__device__ __forceinline__ void grad_gt_store_lds(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0, int N,
-                                                  uint16_t* __restrict__ GTb, int bs, const float* s_rx,
-                                                  const float* s_ry, const float* s_ir, const float* s_ic,
-                                                  char* lds) {
-  static_assert(gt_pitch(TL::BM) % 256 == 16, "rows j and j + 16 share banks only as the swizzle assumes");
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
-#pragma unroll
-  for (int bm = 0; bm < TL::FM; ++bm) {
-#pragma unroll
-    for (int bn = 0; bn < TL::FN; ++bn) {
-      const int nl = wn * TL::TN + bn * 32 + (lane & 31);
-      const int j = j0 + nl;
-      const float cy = NORM ? c * s_ry[nl] : c;
-      const float icj = s_ic[nl];
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        float gv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * g4 + e;
-          const int ml = wm * TL::TM + bm * 32 + acc_row(r, lane);
-          const int i = i0 + ml;
-          const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
-          const float ex = fast_exp2(fmaf(sc, cy, -c));
-          float g = LIT ? ex * s_ir[ml] : ex * (s_ir[ml] + icj);
-          if (MASK) g = (i < N && j < N && i != j) ? g : 0.f;
-          gv[e] = g;
-        }
-        const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g4, lane);
-        gt_stage4<TL>(lds, ml, nl, gv[0], gv[1], gv[2], gv[3]);
-      }
-    }
-  }
-  __syncthreads();
-  gt_write_plane<TL>(lds, GTb, bs);
-}
-
 // bf16x3: G'^T as a bf16 hi plane bf16(G') at GTh and a lo plane
 // bf16(G' - hi) at GTl (both tile pointers in the blocked layout).  Both
 // planes of half the tile's columns fit the staging area of one full plane,
 // so the tile goes out in two halves: each wave's column blocks bn < FN/2,
-// then the rest.  Staging row s (of BN/2) holds tile column nl(s) as in
-// grad_gt_store_lds (same swizzle), the hi plane in rows [0, BN/2), the lo
-// plane after it; every 32 consecutive staged rows are 32 consecutive tile
-// columns, one row of blocks.
+// then the rest.  Staging row s (of BN/2) holds tile column nl(s) (chunk
+// swizzle of gt_stage4), the hi plane in rows [0, BN/2), the lo plane after
+// it; every 32 consecutive staged rows are 32 consecutive tile columns, one
+// row of blocks, written one whole 1 KB block per wave instruction.
 template <class TL>
 __device__ __forceinline__ int x3_stage_col(int srow, int half) {
   constexpr int HT = TL::TN / 2;  // staged columns per wave and half
@@ -775,7 +711,7 @@ __device__ __forceinline__ void grad_gt_store_lds_x3(const f32x16 (&acc)[TL::FM]
       }
     }
     __syncthreads();
-    // one whole block per wave instruction (see gt_write_plane)
+    // one whole block per wave instruction: thread v takes slot v % 64 of block v / 64
     constexpr int IBT = TL::BM / 16;
     static_assert(HT % 32 == 0 && HROWS * VPR % 64 == 0, "staged rows in whole rows of blocks");
     for (int v = threadIdx.x; v < 2 * HROWS * VPR; v += TL::NT) {
@@ -792,9 +728,10 @@ __device__ __forceinline__ void grad_gt_store_lds_x3(const f32x16 (&acc)[TL::FM]
   }
 }
 
-// Chained 16-bit gradient-matrix tiles (k_grad_g_chain): G'^T straight from
-// the accumulators into the tile's blocks at GTb (blocked layout,
-// gdma::gb_offset), no staging.  For a 32 x 32 accumulator block, register
+// 16-bit gradient-matrix tiles (k_grad_g_chain, and k_grad_step's 16-bit
+// tiles other than bf16x3): G'^T straight from the accumulators into the
+// tile's blocks at GTb (blocked layout, gdma::gb_offset), no staging.  GSC:
+// the storage scale, when s_ir / s_ic do not already carry it.  For a 32 x 32 accumulator block, register
 // group g4 of lane l holds rows i = 8 g4 + 4 (l / 32) .. + 3 of column
 // j = l % 32; swapping groups 2p + 1 of the low lane half with groups 2p of
 // the high half (v_permlane32_swap) leaves lane l with the 8 rows
@@ -805,7 +742,7 @@ constexpr int gt_chain_stores() {
   return TL::FM * TL::FN * 2;
 }
 template <class TL, bool LIT, bool NORM, bool MASK, int GSC>
-__device__ __forceinline__ void grad_gt_store_chain(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0,
+__device__ __forceinline__ void grad_gt_store_direct(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0,
                                                     int N, uint16_t* __restrict__ GTb, int bs, const float* s_rx,
                                                     const float* s_ry, const float* s_ir, const float* s_ic) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -893,10 +830,11 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
     else
       grad_gt_store_lds_x3<TL, LIT, NORM, true>(acc, c, i0, j0, N, GTb, GTl, bs, s_rx, s_ry, s_ir, s_ic, lds);
   } else if constexpr (GtOnly<T>::value) {
+    // (s_ir, s_ic carry the storage scale)
     if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
-      grad_gt_store_lds<TL, LIT, NORM, false>(acc, c, i0, j0, N, (uint16_t*)GTb, bs, s_rx, s_ry, s_ir, s_ic, lds);
+      grad_gt_store_direct<TL, LIT, NORM, false, 1>(acc, c, i0, j0, N, (uint16_t*)GTb, bs, s_rx, s_ry, s_ir, s_ic);
     else
-      grad_gt_store_lds<TL, LIT, NORM, true>(acc, c, i0, j0, N, (uint16_t*)GTb, bs, s_rx, s_ry, s_ir, s_ic, lds);
+      grad_gt_store_direct<TL, LIT, NORM, true, 1>(acc, c, i0, j0, N, (uint16_t*)GTb, bs, s_rx, s_ry, s_ir, s_ic);
   } else {
     if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
       grad_g_store<TL, LIT, NORM, false>(acc, c, i0, j0, N, Gb, GTb, bs, s_rx, s_ry, s_ir, s_ic);
@@ -1063,7 +1001,7 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) 
   using TCX = typename std::conditional<FUSED, typename ConTileSmall<T, CDMA, SMALL>::x, TF>::type;
   using TCY = typename std::conditional<FUSED, typename ConTileSmall<T, CDMA, SMALL>::y, TF>::type;
   static_assert(TCX::NT == TF::NT && TCY::NT == TF::NT, "one workgroup size per launch");
-  constexpr int GT_LDS = GtOnly<T>::value ? TF::BN * gt_pitch(TF::BM) : 0;
+  constexpr int GT_LDS = X3 ? TF::BN * gt_pitch(TF::BM) : 0;  // the bf16x3 staging
   __shared__ __attribute__((aligned(1024)))
   char lds[CMax<CMax<TF::LDS_BYTES, GT_LDS>::value, CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value>::value];
   __shared__ float s_rx[TF::BM], s_ry[TF::BN], s_ir[TF::BM], s_ic[TF::BN];
@@ -1100,7 +1038,7 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) 
 // slower here, unlike in the forward), and the last
 // chunk of each tile's k-loop loads chunk 0 of the next, which lands while
 // the tile's G'^T is stored straight from the accumulators
-// (grad_gt_store_chain).  The next tile's first barrier waits only for those
+// (grad_gt_store_direct).  The next tile's first barrier waits only for those
 // loads, not for the stores.  The per-row and per-column vectors of a tile
 // (rx, ry, 1/R, 1/C) reach LDS by direct loads into one of two buffers,
 // issued right after the previous tile's first barrier (when every wave is
@@ -1184,11 +1122,11 @@ __global__ __launch_bounds__((FwdTile<T, true>::NT), 1) void k_grad_g_chain(
     const float* sv = &s_vec[vb][0][0];
     const bool diag = i0 < j0 + TL::BN && j0 < i0 + TL::BM;
     if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
-      grad_gt_store_chain<TL, LIT, NORM, false, (int)GScale<T>::value>(
+      grad_gt_store_direct<TL, LIT, NORM, false, (int)GScale<T>::value>(
           acc, c, i0, j0, N, gt, bg.bs, sv + V_RX * TL::BM, sv + V_RY * TL::BM, sv + V_IR * TL::BM,
           sv + V_IC * TL::BM);
     else
-      grad_gt_store_chain<TL, LIT, NORM, true, (int)GScale<T>::value>(
+      grad_gt_store_direct<TL, LIT, NORM, true, (int)GScale<T>::value>(
           acc, c, i0, j0, N, gt, bg.bs, sv + V_RX * TL::BM, sv + V_RY * TL::BM, sv + V_IR * TL::BM,
           sv + V_IC * TL::BM);
     if (!has_next) break;
