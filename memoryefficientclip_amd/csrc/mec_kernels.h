@@ -633,103 +633,8 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN]
   }
 }
 
-// bf16x3 staging (grad_gt_store_lds_x3): G'_ij staged through LDS as [j][i]
-// (row pitch gt_pitch(BM) = 2 BM + 16 bytes; 4 consecutive i per 8-byte
-// write).  The 8-byte chunk c of row j sits at chunk c ^ ((j >> 4) & 1): the
-// 32 lanes of a half-wave write one chunk of 32 consecutive rows, which then
-// fall on 32 distinct bank pairs (rows j and j + 16 would share them at this
-// pitch).
-constexpr int gt_pitch(int bm) { return 2 * bm + 16; }
-
-// 4 consecutive i (tile rows ml .. ml+3) into staging row `row` (a tile
-// column j) of the [j][i] staging
-template <class TL>
-__device__ __forceinline__ void gt_stage4(char* lds, int ml, int row, float a, float b, float c, float d) {
-  const int chunk = (ml >> 2) ^ ((row >> 4) & 1);
-  TL::store4((uint16_t*)(lds + row * gt_pitch(TL::BM) + chunk * 8), a, b, c, d);
-}
-
-// bf16x3: G'^T as a bf16 hi plane bf16(G') at GTh and a lo plane
-// bf16(G' - hi) at GTl (both tile pointers in the blocked layout).  Both
-// planes of half the tile's columns fit the staging area of one full plane,
-// so the tile goes out in two halves: each wave's column blocks bn < FN/2,
-// then the rest.  Staging row s (of BN/2) holds tile column nl(s) (chunk
-// swizzle of gt_stage4), the hi plane in rows [0, BN/2), the lo plane after
-// it; every 32 consecutive staged rows are 32 consecutive tile columns, one
-// row of blocks, written one whole 1 KB block per wave instruction.
-template <class TL>
-__device__ __forceinline__ int x3_stage_col(int srow, int half) {
-  constexpr int HT = TL::TN / 2;  // staged columns per wave and half
-  const int wn = srow / HT, rem = srow - wn * HT;
-  return wn * TL::TN + half * HT + rem;
-}
-template <class TL, bool LIT, bool NORM, bool MASK>
-__device__ __forceinline__ void grad_gt_store_lds_x3(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0,
-                                                     int N, uint16_t* __restrict__ GTh, uint16_t* __restrict__ GTl,
-                                                     int bs, const float* s_rx, const float* s_ry, const float* s_ir,
-                                                     const float* s_ic, char* lds) {
-  constexpr int PITCH = gt_pitch(TL::BM);
-  static_assert(PITCH % 256 == 16, "rows j and j + 16 share banks only as the swizzle assumes");
-  static_assert(TL::FN % 2 == 0, "two halves of whole column blocks");
-  constexpr int HB = TL::FN / 2, HT = TL::TN / 2, HROWS = TL::BN / 2;
-  constexpr int VPR = TL::BM * 2 / 16;  // 16-byte vectors per tile row
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
-  const int64_t rowb = (int64_t)(bs >> 4) * 512;
-  char* lds_lo = lds + HROWS * PITCH;
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-#pragma unroll
-    for (int bm = 0; bm < TL::FM; ++bm) {
-#pragma unroll
-      for (int bb = 0; bb < HB; ++bb) {
-        const int bn = half * HB + bb;
-        const int nl = wn * TL::TN + bn * 32 + (lane & 31);
-        const int srow = wn * HT + bb * 32 + (lane & 31);
-        const int j = j0 + nl;
-        const float cy = NORM ? c * s_ry[nl] : c;
-        const float icj = s_ic[nl];
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          float gv[4], lv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * g4 + e;
-            const int ml = wm * TL::TM + bm * 32 + acc_row(r, lane);
-            const int i = i0 + ml;
-            const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
-            const float ex = fast_exp2(fmaf(sc, cy, -c));
-            float g = LIT ? ex * s_ir[ml] : ex * (s_ir[ml] + icj);
-            if (MASK) g = (i < N && j < N && i != j) ? g : 0.f;
-            gv[e] = g;
-            lv[e] = g - bf16_to_f32(f32_to_bf16(g));
-          }
-          const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g4, lane);
-          gt_stage4<TL>(lds, ml, srow, gv[0], gv[1], gv[2], gv[3]);
-          gt_stage4<TL>(lds_lo, ml, srow, lv[0], lv[1], lv[2], lv[3]);
-        }
-      }
-    }
-    __syncthreads();
-    // one whole block per wave instruction: thread v takes slot v % 64 of block v / 64
-    constexpr int IBT = TL::BM / 16;
-    static_assert(HT % 32 == 0 && HROWS * VPR % 64 == 0, "staged rows in whole rows of blocks");
-    for (int v = threadIdx.x; v < 2 * HROWS * VPR; v += TL::NT) {
-      const int lo = v >= HROWS * VPR, u0 = v - lo * HROWS * VPR;
-      const int blk = u0 >> 6, slot = u0 & 63;
-      const int jg = blk / IBT, ib = blk - jg * IBT;
-      const int ih = slot >> 5, srow = jg * 32 + ((slot & 31) ^ (8 * ih + 4 * (ib & 1)));
-      u32x4 u = *(const u32x4*)(lds + (lo * HROWS + srow) * PITCH + (2 * ib + ih) * 16);
-      if ((srow >> 4) & 1) u = u32x4{u.z, u.w, u.x, u.y};  // undo the chunk swizzle
-      const int jb = x3_stage_col<TL>(jg * 32, half) >> 5;
-      __builtin_nontemporal_store(u, (u32x4*)((lo ? GTl : GTh) + jb * rowb + ib * 512 + slot * 8));
-    }
-    if (half == 0) __syncthreads();  // every wave is done reading the first half
-  }
-}
-
-// 16-bit gradient-matrix tiles (k_grad_g_chain, and k_grad_step's 16-bit
-// tiles other than bf16x3): G'^T straight from the accumulators into the
+// 16-bit gradient-matrix tiles (k_grad_g_chain and k_grad_step): G'^T
+// straight from the accumulators into the
 // tile's blocks at GTb (blocked layout, gdma::gb_offset), no staging.  GSC:
 // the storage scale, when s_ir / s_ic do not already carry it.  For a 32 x 32 accumulator block, register
 // group g4 of lane l holds rows i = 8 g4 + 4 (l / 32) .. + 3 of column
@@ -741,11 +646,14 @@ template <class TL>
 constexpr int gt_chain_stores() {
   return TL::FM * TL::FN * 2;
 }
-template <class TL, bool LIT, bool NORM, bool MASK, int GSC>
+// X3 (bf16x3): a second plane bf16(G' - bf16(G')) at GTl, the same way.
+template <class TL, bool LIT, bool NORM, bool MASK, int GSC, bool X3 = false>
 __device__ __forceinline__ void grad_gt_store_direct(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0,
-                                                    int N, uint16_t* __restrict__ GTb, int bs, const float* s_rx,
-                                                    const float* s_ry, const float* s_ir, const float* s_ic) {
+                                                     int N, uint16_t* __restrict__ GTb, int bs, const float* s_rx,
+                                                     const float* s_ry, const float* s_ir, const float* s_ic,
+                                                     uint16_t* __restrict__ GTl = nullptr) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int NP = X3 ? 2 : 1;  // planes
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
   const int64_t rowb = (int64_t)(bs >> 4) * 512;  // elements per row of blocks
 #pragma unroll
@@ -754,12 +662,12 @@ __device__ __forceinline__ void grad_gt_store_direct(const f32x16 (&acc)[TL::FM]
     const int j = j0 + nl;
     const float cy = NORM ? c * s_ry[nl] : c;
     const float icj = s_ic[nl];
-    uint16_t* gjb = GTb + ((wn * TL::TN + bn * 32) >> 5) * rowb;
+    const int64_t jrow = ((wn * TL::TN + bn * 32) >> 5) * rowb;
 #pragma unroll
     for (int bm = 0; bm < TL::FM; ++bm) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        uint32_t pk[2][2];
+        uint32_t pk[NP][2][2];
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           float gv[4];
@@ -775,18 +683,28 @@ __device__ __forceinline__ void grad_gt_store_direct(const f32x16 (&acc)[TL::FM]
             if (MASK) g = (i < N && j < N && i != j) ? g : 0.f;
             gv[e] = g;
           }
-          pk[q][0] = TL::pack2(gv[0], gv[1]);
-          pk[q][1] = TL::pack2(gv[2], gv[3]);
-        }
+          pk[0][q][0] = TL::pack2(gv[0], gv[1]);
+          pk[0][q][1] = TL::pack2(gv[2], gv[3]);
+          if constexpr (X3) {
 #pragma unroll
-        for (int d = 0; d < 2; ++d) {
-          const auto sw = __builtin_amdgcn_permlane32_swap(pk[0][d], pk[1][d], false, false);
-          pk[0][d] = sw[0];
-          pk[1][d] = sw[1];
+            for (int e = 0; e < 4; ++e) gv[e] -= bf16_to_f32(f32_to_bf16(gv[e]));
+            pk[NP - 1][q][0] = TL::pack2(gv[0], gv[1]);
+            pk[NP - 1][q][1] = TL::pack2(gv[2], gv[3]);
+          }
         }
         const int ib = (wm * TL::TM + bm * 32) / 16 + p;
-        const u32x4 u = u32x4{pk[0][0], pk[0][1], pk[1][0], pk[1][1]};
-        __builtin_nontemporal_store(u, (u32x4*)(gjb + ib * 512 + gdma::gb_slot(lane & 31, lane >> 5, p) * 8));
+        const int64_t off = jrow + ib * 512 + gdma::gb_slot(lane & 31, lane >> 5, p) * 8;
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) {
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(pk[pl][0][d], pk[pl][1][d], false, false);
+            pk[pl][0][d] = sw[0];
+            pk[pl][1][d] = sw[1];
+          }
+          const u32x4 u = u32x4{pk[pl][0][0], pk[pl][0][1], pk[pl][1][0], pk[pl][1][1]};
+          __builtin_nontemporal_store(u, (u32x4*)((pl ? GTl : GTb) + off));
+        }
       }
     }
   }
@@ -826,9 +744,9 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
   if constexpr (X3) {
     static_assert(std::is_same<T, uint16_t>::value, "bf16x3 runs on bf16 split operands");
     if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
-      grad_gt_store_lds_x3<TL, LIT, NORM, false>(acc, c, i0, j0, N, GTb, GTl, bs, s_rx, s_ry, s_ir, s_ic, lds);
+      grad_gt_store_direct<TL, LIT, NORM, false, 1, true>(acc, c, i0, j0, N, GTb, bs, s_rx, s_ry, s_ir, s_ic, GTl);
     else
-      grad_gt_store_lds_x3<TL, LIT, NORM, true>(acc, c, i0, j0, N, GTb, GTl, bs, s_rx, s_ry, s_ir, s_ic, lds);
+      grad_gt_store_direct<TL, LIT, NORM, true, 1, true>(acc, c, i0, j0, N, GTb, bs, s_rx, s_ry, s_ir, s_ic, GTl);
   } else if constexpr (GtOnly<T>::value) {
     // (s_ir, s_ic carry the storage scale)
     if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
@@ -1001,9 +919,7 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) 
   using TCX = typename std::conditional<FUSED, typename ConTileSmall<T, CDMA, SMALL>::x, TF>::type;
   using TCY = typename std::conditional<FUSED, typename ConTileSmall<T, CDMA, SMALL>::y, TF>::type;
   static_assert(TCX::NT == TF::NT && TCY::NT == TF::NT, "one workgroup size per launch");
-  constexpr int GT_LDS = X3 ? TF::BN * gt_pitch(TF::BM) : 0;  // the bf16x3 staging
-  __shared__ __attribute__((aligned(1024)))
-  char lds[CMax<CMax<TF::LDS_BYTES, GT_LDS>::value, CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value>::value];
+  __shared__ __attribute__((aligned(1024))) char lds[CMax<TF::LDS_BYTES, CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value>::value];
   __shared__ float s_rx[TF::BM], s_ry[TF::BN], s_ir[TF::BM], s_ic[TF::BN];
   const int64_t blk = (int64_t)bg.bs * bg.bs;  // elements per G' block
   int sub = blockIdx.x;
