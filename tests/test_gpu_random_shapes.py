@@ -35,7 +35,8 @@ def draw_cases(seed=20261201, count=20, dtypes=("f32", "bf16", "f16")):
     return cases
 
 
-CASES = draw_cases() + [(20 + c[0],) + c[1:] for c in draw_cases(seed=777, count=8, dtypes=("f32x3",))]
+CASES = (draw_cases() + [(20 + c[0],) + c[1:] for c in draw_cases(seed=777, count=8, dtypes=("f32x3",))]
+         + [(100 + c[0],) + c[1:] for c in draw_cases(seed=101, count=30)])
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "-".join(str(v) for v in c[:6]))
