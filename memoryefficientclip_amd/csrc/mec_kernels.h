@@ -61,17 +61,10 @@ struct TileF32 {
   }
 };
 
-// fp32 -> 16-bit packing of the gradient-matrix tiles
+// fp32 -> 16-bit packing of the gradient-matrix tiles (two values per 32-bit word)
 template <bool F16>
 struct Pack16 {
-  static __device__ __forceinline__ uint16_t pack(float v) { return F16 ? f32_to_f16(v) : f32_to_bf16(v); }
   static __device__ __forceinline__ uint32_t pack2(float a, float b) { return F16 ? pack2_f16(a, b) : pack2_bf16(a, b); }
-  static __device__ __forceinline__ void store4(uint16_t* p, float a, float b, float c, float d) {
-    if constexpr (F16)
-      *(uint2*)p = uint2{pack2_f16(a, b), pack2_f16(c, d)};
-    else
-      *(uint2*)p = uint2{pack2_bf16(a, b), pack2_bf16(c, d)};
-  }
 };
 
 // bf16 / fp16, 128 x 128, operands staged through registers (any alignment / D)
