@@ -361,6 +361,26 @@ bool narrow_contract_use(int bs, int64_t wide, int64_t narrow) {
   return (narrow + cus - 1) / cus < (wide + cus - 1) / cus;
 }
 
+// 16-bit contraction tiles 384 features wide (ConTileSel::wx / wy; 1.5 times
+// the work of a 256 x 256 tile) for a launch of t384 such tiles instead of
+// t256 tiles of 256 x 256 (or the narrow ones): where they take fewer
+// tile-rounds of work over the compute units.  At D = 1152 (config 5) the
+// 256-wide tiles spend a tenth of the launch on a half-empty fifth feature
+// column (8.99 -> 8.09 ms per launch); at equal cost (D = 768: 2.68-2.69 ms
+// both) the 256-wide tiles stay; at D = 300 with few tiles per CU the
+// 384-wide ones were 17% slower.  MEC_WIDE_CONTRACT=0 / 1 turns them off /
+// on for every D (tests).
+bool wide_contract_use(int64_t t384, int64_t t256) {
+  if (const char* env = std::getenv("MEC_WIDE_CONTRACT")) {
+    if (env[0] == '0') return false;
+    if (env[0] == '1') return true;
+  }
+  int cus = 0;
+  if (compute_units(&cus) != MEC_OK || cus <= 0) return false;
+  const int64_t r384 = (t384 + cus - 1) / cus, r256 = (t256 + cus - 1) / cus;
+  return 3 * r384 < 2 * r256;
+}
+
 bool f32_contract_dma(int64_t ldt, int64_t bs) {
   if (const char* env = std::getenv("MEC_F32_CONTRACT_DMA"))
     if (env[0] == '0') return false;
@@ -629,13 +649,24 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   const TileDims tf = fwd_tile_dims(dtype, vec, small), tc = con_tile_dims(dtype, small);
   const bool sep = separate_contractions(dtype);
   BlockGrid bg{bs, nb, bs / tf.bm, bs / tf.bn, bs / tc.bm, (D + tc.bn - 1) / tc.bn, 0};
-  if (sep && narrow_contract_shape(D, bg.ctm)) {
+  bool w384 = false;  // 16-bit contractions in 256 x 384 tiles
+  if (sep) {
     const int64_t sides = (acc_x ? 1 : 0) + (acc_y ? 1 : 0);
     const int64_t wide = sides * nb * bg.ctm * bg.ctd;
-    const int64_t narrow = sides * nb * (bg.ctm / 2) * (2 * (D / tc.bn) + 1);
-    if (narrow_contract_use(bs, wide, narrow)) {
-      bg.ctd = D / tc.bn;
-      bg.cnw = 1;
+    int64_t tiles = wide;
+    if (narrow_contract_shape(D, bg.ctm)) {
+      const int64_t narrow = sides * nb * (bg.ctm / 2) * (2 * (D / tc.bn) + 1);
+      if (narrow_contract_use(bs, wide, narrow)) {
+        bg.ctd = D / tc.bn;
+        bg.cnw = 1;
+        tiles = narrow;
+      }
+    }
+    const int ctd384 = (D + 383) / 384;
+    if (wide_contract_use(sides * nb * bg.ctm * ctd384, tiles)) {
+      w384 = true;
+      bg.ctd = ctd384;
+      bg.cnw = 0;
     }
   }
   // contraction tiles per block and side
@@ -715,7 +746,8 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
     const int DK = (int)go.d;
     DISPATCH_BOOL(x3, X3, {
       if (grid_c > 0) {
-        k_grad_contract<T, X3><<<(unsigned)grid_c, ConTileX<T>::NT, 0, s>>>(N, D, gb, bg, sp_c, acc_x, acc_y);
+        DISPATCH_BOOL(w384, W, k_grad_contract<T, X3, W><<<(unsigned)grid_c, ConTileX<T>::NT, 0, s>>>(
+                                   N, D, gb, bg, sp_c, acc_x, acc_y));
         rc = check_launch("grad_contract");
       }
       if (!rc && grid > 0) {
@@ -740,7 +772,8 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   DISPATCH_DTYPE(dtype, T, {
     if (grid_c > 0) {
       if constexpr (Is16<T>::value) {
-        k_grad_contract<T><<<(unsigned)grid_c, ConTileX<T>::NT, 0, s>>>(N, D, gb, bg, sp_c, acc_x, acc_y);
+        DISPATCH_BOOL(w384, W, k_grad_contract<T, false, W><<<(unsigned)grid_c, ConTileX<T>::NT, 0, s>>>(
+                                   N, D, gb, bg, sp_c, acc_x, acc_y));
         rc = check_launch("grad_contract");
       }
     }

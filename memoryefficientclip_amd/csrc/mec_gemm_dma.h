@@ -6,8 +6,10 @@
 // v_mfma_f32_32x32x16_{bf16,f16} (one per block and k-step) or
 // v_mfma_f32_32x32x2_f32 (four per block and k-step).  The 16-bit tiles
 // (forward, gradient matrix, contractions) are 256 x 256 with 4 x 2 waves,
-// one workgroup per CU (96 KB of ring); fp32 tiles are 128 x 128 with 2 x 2
-// waves (48 KB), two (forward) or three (backward) workgroups per CU.
+// one workgroup per CU (96 KB of ring; contractions 256 x 384 with 2 x 4
+// waves where that takes fewer rounds, on the rolling operand schedule at the
+// end of this file); fp32 tiles are 128 x 128 with 2 x 2 waves (48 KB), two
+// (forward) or three (backward) workgroups per CU.
 //
 // Operands are K-major (element (row, k) at base[row * ld + k]).  K is staged
 // in chunks of ROWB bytes per row through a ring of LDS stages ([row][ROWB]):
@@ -622,6 +624,208 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
   prologue<G>(A, B, lds, lp);
   int p0 = 0;
   mainloop_core<G, ZERO, false>(lp, lp.ra, lp.rb, false, K, lds, p0, acc);
+  drain_loads();
+}
+
+// ------------------------------------------------- rolling operand schedule
+// For per-wave sub-tiles whose accumulators leave no room for two fragment
+// sets (the 256 x 384 contraction tiles: 192 accumulator registers per wave):
+// one fragment set.  A k-step's MFMAs run over the outer operand's fragments
+// (the one with fewer fragments per wave), each against every inner fragment;
+// the next k-step's read of a fragment is issued right after the MFMA that
+// last uses it, into the same registers:
+//   outer fragment o < NO - 1  after MFMA o NI + NI - 1,
+//   inner fragment l           after MFMA (NO - 1) NI + l,
+//   the last outer fragment    after the last MFMA,
+// so every read is issued at least NI - 1 MFMAs before its first use, and
+// each MFMA waits (lgkmcnt) only for the reads it needs.  The workgroup
+// barrier of chunk kt + 1 sits in k-step 3 of chunk kt after its first NI
+// MFMAs (SPLIT), before the first read from the next stage, and the loads of
+// chunk kt + 2 follow it.
+template <class G>
+struct RollSched {
+  static constexpr int FM = G::FM, FN = G::FN, NMF = G::NMF;
+  static constexpr int NA = G::TA ? 2 : 1;     // LDS reads per A fragment (transposed: low and high k)
+  static constexpr bool AOUT = FM <= FN;       // A the outer operand (MFMA m = i FN + j), else B (m = j FM + i)
+  static constexpr int NO = AOUT ? FM : FN, NI = AOUT ? FN : FM;
+  static constexpr int RO = AOUT ? NA : 1, RI = AOUT ? 1 : NA;  // reads per outer / inner fragment
+  static constexpr int NR = NO * RO + NI * RI;  // reads per k-step
+  static constexpr int SPLIT = NI;              // MFMAs of k-step 3 before the barrier
+  static_assert(NR <= 15, "lgkmcnt range");
+  static_assert(G::KIND != K_F32 && NMF == FM * FN && NO >= 2, "16-bit MFMAs, one per 32 x 32 block");
+  // MFMA m: blocks (i, j)
+  static constexpr int mi(int m) { return AOUT ? m / FN : m % FM; }
+  static constexpr int mj(int m) { return AOUT ? m % FN : m / FM; }
+  // read r in issue order: outer fragments 0 .. NO - 2, the inner ones, the
+  // last outer one; per fragment its reads (transposed A: half 0, 1)
+  static constexpr int R1 = (NO - 1) * RO, R2 = R1 + NI * RI;
+  static constexpr bool outer(int r) { return r < R1 || r >= R2; }
+  static constexpr int frag(int r) { return r < R1 ? r / RO : (r < R2 ? (r - R1) / RI : NO - 1); }
+  static constexpr int half(int r) { return r < R1 ? r % RO : (r < R2 ? (r - R1) % RI : (r - R2) % RO); }
+  static constexpr bool is_a(int r) { return outer(r) == AOUT; }
+  static constexpr int pos(int r) {
+    return r < R1 ? frag(r) * NI + NI - 1 : (r < R2 ? (NO - 1) * NI + frag(r) : NMF - 1);
+  }
+  // index of the last read of outer fragment o / inner fragment l
+  static constexpr int last_o(int o) { return o < NO - 1 ? (o + 1) * RO - 1 : NR - 1; }
+  static constexpr int last_i(int l) { return R1 + (l + 1) * RI - 1; }
+  static constexpr int last_a(int i) { return AOUT ? last_o(i) : last_i(i); }
+  static constexpr int last_b(int j) { return AOUT ? last_i(j) : last_o(j); }
+  // index of the last read that MFMAs 0..m need
+  static constexpr int need(int m) {
+    int l = -1;
+    for (int u = 0; u <= m; ++u) {
+      const int a = last_a(mi(u)), b = last_b(mj(u));
+      l = a > l ? a : l;
+      l = b > l ? b : l;
+    }
+    return l;
+  }
+  static constexpr int issued_before(int m) {
+    int c = 0;
+    for (int r = 0; r < NR; ++r) c += pos(r) < m ? 1 : 0;
+    return c;
+  }
+};
+
+// Per-lane LDS addresses of the rolling reads, for stage 0 (stage p adds
+// p * STAGE); the k-step and the fragment are instruction offsets.
+template <class G>
+struct RollReader {
+  static_assert(G::GB && G::ESZ == 2 && G::SA == 2 && G::NS == 4, "blocked 16-bit A, two stages, four k-steps");
+  uint32_t a[2];  // A: transposed, read half 0 / 1; else the slot of even / odd k-steps
+  uint32_t b[4];  // B: k-step 0..3
+  __device__ __forceinline__ explicit RollReader(char* lds) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if constexpr (G::TA) {
+        a[h] = lds_off(ta_ptr<G>(G::a_stage(lds, 0), 0, 0, h));
+      } else {
+        // a_ptr of k-step h (0 or 1): k-steps 2 and 3 are 2 KB further
+        a[h] = lds_off(a_ptr<G>(G::a_stage(lds, 0), h)) - h * 1024;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) b[s] = lds_off(b_ptr<G>(G::b_stage(lds, 0), s));
+  }
+  template <int S, int R>
+  __device__ __forceinline__ void read(Frags<G>& f, uint32_t soff) const {
+    using RS = RollSched<G>;
+    constexpr int fr = RS::frag(R);
+    if constexpr (RS::is_a(R)) {
+      if constexpr (G::TA) {
+        // fragment i is 2 KB further, k-steps as in ta_ptr
+        constexpr int off = fr * 2048 + (S >> 1) * (G::BM / 16) * 1024 + (S & 1) * 256;
+        static_assert(off < 65536, "ds offset");
+        i16x4_t v;
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(a[RS::half(R)] + soff), "n"(off) : "memory");
+        if constexpr (RS::half(R) == 0)
+          f.a[fr].lo = v;
+        else
+          f.a[fr].hi = v;
+      } else {
+        f.a[fr] = lds_read_b128<S * 1024 + fr * 32 * G::ROWB>(a[S & 1] + soff);
+      }
+    } else {
+      f.b[fr] = lds_read_b128<fr * 32 * G::ROWB>(b[S] + soff);
+    }
+  }
+};
+
+// MFMAs [M0, M1) of k-step `S` (fragments f), each after the wait for the
+// reads it needs.  READ: the reads of k-step SN (stage offset sn) are issued
+// at their positions (and those at position M0 - 1 first).  Loads [L0, L1) of
+// the chunk at k1 into (ad, bd), one after each of the range's first MFMAs.
+template <class G, int S, bool READ, int SN, int M0, int M1, int L0, int L1>
+__device__ __forceinline__ void roll_range(Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const RollReader<G>& rd,
+                                           uint32_t sn, const LoadPlan<G>& lp, int k1, char* ad, char* bd) {
+  using RS = RollSched<G>;
+  static_assert(L1 - L0 <= M1 - M0, "one load per MFMA");
+  if constexpr (READ && M0 > 0) {
+    static_for<RS::NR>([&](auto rc) {
+      if constexpr (RS::pos(rc) == M0 - 1) rd.template read<SN, rc>(f, sn);
+    });
+  }
+  static_for<M1 - M0>([&](auto mc) {
+    constexpr int m = M0 + mc;
+    constexpr int i = RS::mi(m), j = RS::mj(m);
+    if constexpr (m == M0 || RS::need(m) > RS::need(m - 1)) {
+      // reads of k-step S still allowed in flight, plus those of SN issued so far
+      constexpr int n = RS::NR - 1 - RS::need(m) + (READ ? RS::issued_before(m) : 0);
+      sched_fence();
+      asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(n) : "memory");
+      // every fragment tied to the wait: no MFMA is scheduled above it
+#pragma unroll
+      for (int u = 0; u < G::FM; ++u) asm volatile("" : "+v"(f.a[u]));
+#pragma unroll
+      for (int u = 0; u < G::FN; ++u) asm volatile("" : "+v"(f.b[u]));
+      sched_fence();
+    }
+    acc[i][j] = mfma16_32x32x16<G::F16>(f.a[i], f.b[j], acc[i][j]);
+    if constexpr (READ || (mc < L1 - L0)) {
+      sched_fence();
+      if constexpr (READ)
+        static_for<RS::NR>([&](auto rc) {
+          if constexpr (RS::pos(rc) == m) rd.template read<SN, rc>(f, sn);
+        });
+      if constexpr (mc < L1 - L0) lp.template issue<L0 + mc>(k1, ad, bd);
+      sched_fence();
+    }
+  });
+}
+
+// One tile on the rolling schedule (not chained): chunk 0 into stage 0, the
+// k-loop, the zero loads past the last chunk awaited (ZERO = false: added to
+// acc).
+template <class G, bool ZERO = true>
+__device__ __forceinline__ void mainloop_roll(const Operand& A, const Operand& B, int K, char* lds,
+                                              f32x16 (&acc)[G::FM][G::FN]) {
+  using RS = RollSched<G>;
+  constexpr int SPL = RS::SPLIT, NMF = G::NMF, BK = G::BK;
+  constexpr int LH = G::IPW / 2;  // loads after the barrier in k-step 3, the rest in k-step 0
+  static_assert(LH <= NMF - SPL && G::IPW - LH <= NMF, "load slots");
+  if constexpr (ZERO) {
+#pragma unroll
+    for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < G::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  }
+  LoadPlan<G> lp;
+  prologue<G>(A, B, lds, lp);
+  const RollReader<G> rd(lds);
+  Frags<G> f;
+  const int nk = (K + BK - 1) / BK;
+  // k-steps 0..2 and the first half of k-step 3 of chunk kt (stage offset
+  // sc), the first half of chunk kt + 1's loads already issued
+  auto chunk = [&](int kt, uint32_t sc, char* na, char* nb) {
+    const int k1 = (kt + 1) * BK;
+    roll_range<G, 0, true, 1, 0, NMF, LH, G::IPW>(f, acc, rd, sc, lp, k1, na, nb);
+    roll_range<G, 1, true, 2, 0, NMF, 0, 0>(f, acc, rd, sc, lp, 0, na, nb);
+    roll_range<G, 2, true, 3, 0, NMF, 0, 0>(f, acc, rd, sc, lp, 0, na, nb);
+    roll_range<G, 3, false, 0, 0, SPL, 0, 0>(f, acc, rd, sc, lp, 0, na, nb);
+  };
+  // chunk 0 landed: its k-step 0 reads, then chunk 1's first loads
+  wait_barrier<0>();
+  sched_fence();
+  static_for<RS::NR>([&](auto rc) { rd.template read<0, rc>(f, 0); });
+  static_for<LH>([&](auto l) { lp.template issue<l>(BK, G::a_stage(lds, 1), G::b_stage(lds, 1)); });
+  sched_fence();
+  chunk(0, 0, G::a_stage(lds, 1), G::b_stage(lds, 1));
+  for (int kt = 1; kt < nk; ++kt) {
+    const int c = kt & 1;
+    const uint32_t sc = c ? G::STAGE : 0;  // stage of chunk kt
+    char* na = G::a_stage(lds, c ^ 1);
+    char* nb = G::b_stage(lds, c ^ 1);
+    // chunk kt landed; every wave is done with chunk kt - 1's stage.  Then
+    // k-step 3 of chunk kt - 1, second half, reading k-step 0 of chunk kt
+    wait_barrier<0>();
+    sched_fence();
+    roll_range<G, 3, true, 0, SPL, NMF, 0, LH>(f, acc, rd, sc, lp, (kt + 1) * BK, na, nb);
+    chunk(kt, sc, na, nb);
+  }
+  roll_range<G, 3, false, 0, SPL, NMF, 0, 0>(f, acc, rd, 0, lp, 0, lds, lds);
   drain_loads();
 }
 

@@ -19,8 +19,10 @@
 //   k_grad_g_chain  the 16-bit gradient-matrix tiles of inputs already
 //                       normalized, chained in persistent workgroups.
 //   k_grad_contract the 16-bit types' contractions of one pipeline step, in
-//                       a launch of their own with larger tiles (and narrow
-//                       ones for a last column of at most 128 features).
+//                       a launch of their own with larger tiles (256 x 256,
+//                       or 256 x 384 where that takes fewer rounds, and
+//                       narrow ones for a last column of at most 128
+//                       features).
 //   k_sumexp_det, k_det_reduce
 //                   the forward sums without atomics across workgroups, in
 //                       one pass (deterministic mode, and always for the
@@ -96,19 +98,23 @@ template <> struct PackOf<gdma::K_F32> { using type = PackF32; };
 // fp16 or fp32); TA_: A stored k-row-major (a transposed 16-bit
 // gradient-matrix block); GB_: A a 16-bit gradient-matrix block in the
 // blocked layout (gdma::gb_offset; TA_ then selects the x side's reading)
-template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND, int SA_ = 2, bool GB_ = false>
+template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND, int SA_ = 2, bool GB_ = false, bool ROLL_ = false>
 struct TileD : PackOf<KIND>::type {
   using Elem = typename std::conditional<KIND == gdma::K_F32, float, uint16_t>::type;
   using Op = gdma::Operand;
   using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, SA_, GB_>;
-  static constexpr bool TA = TA_, GB = GB_;
+  static constexpr bool TA = TA_, GB = GB_, ROLL = ROLL_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
   static constexpr int LDS_BYTES = G::LDS_BYTES;
   static constexpr bool CHAIN = true;
   template <bool VECA, bool VECB, bool ZERO = true>
   static __device__ __forceinline__ void run(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN]) {
-    gdma::mainloop<G, ZERO>(a, b, K, (char*)lds, acc);
+    if constexpr (ROLL) {
+      gdma::mainloop_roll<G, ZERO>(a, b, K, (char*)lds, acc);
+    } else {
+      gdma::mainloop<G, ZERO>(a, b, K, (char*)lds, acc);
+    }
   }
   // Tiles in a chain (a persistent workgroup): start() issues the first
   // tile's chunk 0; chain() runs one tile and, with has_next, leaves chunk 0
@@ -159,17 +165,25 @@ template <typename T, bool DMA = true, bool IS16 = Is16<T>::value> struct ConTil
 // nx, ny: the narrow tiles of a last feature column of at most 128 features
 // (D % 256 in [1, 128]): 512 rows x 128 features, the same 128 x 64 per-wave
 // sub-tile shape (operand reads per MFMA) as the wide tiles, two stages (160 KB)
+// wx, wy: 256 rows x 384 features where those take fewer rounds of work
+// (D = 1152: three feature tiles instead of four and a half-empty fifth), 2 x
+// 4 waves of 128 x 96: 192 accumulator registers, one fragment set on the
+// rolling operand schedule (gdma::mainloop_roll), two stages (160 KB)
 template <typename T, bool DMA> struct ConTileSel<T, DMA, false> {
   using x = typename std::conditional<DMA, TileD<128, 128, false, 2, 2, gdma::K_F32>, TileF32>::type;
   using y = x;
   using nx = x;  // (no narrow tiles)
   using ny = x;
+  using wx = x;
+  using wy = x;
 };
 template <typename T, bool DMA> struct ConTileSel<T, DMA, true> {
   using x = TileD<256, 256, true, 4, 2, kind16<T>(), 3, true>;
   using y = TileD<256, 256, false, 4, 2, kind16<T>(), 3, true>;
   using nx = TileD<512, 128, true, 4, 2, kind16<T>(), 2, true>;
   using ny = TileD<512, 128, false, 4, 2, kind16<T>(), 2, true>;
+  using wx = TileD<256, 384, true, 2, 4, kind16<T>(), 2, true, true>;
+  using wy = TileD<256, 384, false, 2, 4, kind16<T>(), 2, true, true>;
 };
 template <typename T, bool DMA = true> using ConTileX = typename ConTileSel<T, DMA>::x;
 template <typename T, bool DMA = true> using ConTileY = typename ConTileSel<T, DMA>::y;
@@ -544,7 +558,8 @@ struct BlockGrid {
   int gtm;   // gradient-matrix tiles per block, row direction (bs / BM)
   int gtn;   // gradient-matrix tiles per block, column direction (bs / BN)
   int ctm;   // contraction tiles per block, row direction (bs / BM of the contraction)
-  int ctd;   // contraction tiles over the features (ceil(D / BN of the contraction); with cnw, floor(D / BN))
+  int ctd;   // contraction tiles over the features (ceil(D / BN of the contraction, 256 or 384); with cnw,
+             // floor(D / 256))
   int cnw;   // 16-bit, D % 256 in [1, 128], ctm even: the features past ctd * 256 are contracted by narrow
              // tiles of 512 rows (ConTileNX / ConTileNY), one per pair of row tiles
 };
@@ -882,16 +897,19 @@ __device__ __forceinline__ void grad_contract_dispatch(int sub, int N, int D, co
 
 // 16-bit (and bf16x3) contractions of one pipeline step (the x side of
 // diagonal diag_c, then the y side).
-template <typename T, bool X3 = false>
+// W: the 256 x 384 tiles (ConTileSel::wx / wy; no narrow tiles)
+template <typename T, bool X3 = false, bool W = false>
 __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int D, GradBufs gb, BlockGrid bg,
                                                                      StepPlan sp, float* __restrict__ acc_x,
                                                                      float* __restrict__ acc_y) {
-  using TCX = ConTileX<T>;
-  using TCY = ConTileY<T>;
-  using TNX = ConTileNX<T>;
-  using TNY = ConTileNY<T>;
-  static_assert(TCX::BM == TCY::BM && TCX::BN == TCY::BN && TCX::NT == TCY::NT, "one contraction tile shape");
-  static_assert(TNX::NT == TCX::NT && TNY::NT == TCX::NT && TNX::BM == 2 * TCX::BM && 2 * TNX::BN == TCX::BN,
+  using Sel = ConTileSel<T, true>;
+  using TCX = typename std::conditional<W, typename Sel::wx, typename Sel::x>::type;
+  using TCY = typename std::conditional<W, typename Sel::wy, typename Sel::y>::type;
+  using TNX = typename std::conditional<W, TCX, typename Sel::nx>::type;
+  using TNY = typename std::conditional<W, TCY, typename Sel::ny>::type;
+  static_assert(TCX::BM == TCY::BM && TCX::BN == TCY::BN && TCX::NT == TCY::NT && TCX::NT == ConTileX<T>::NT,
+                "one contraction tile shape and workgroup size");
+  static_assert(W || (TNX::NT == TCX::NT && TNY::NT == TCX::NT && TNX::BM == 2 * TCX::BM && 2 * TNX::BN == TCX::BN),
                 "narrow tiles: two row tiles high, half a feature tile wide");
   __shared__ __attribute__((aligned(1024)))
   char lds[CMax<CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value, CMax<TNX::LDS_BYTES, TNY::LDS_BYTES>::value>::value];

@@ -10,7 +10,8 @@
 //                             loads (mec_gemm_dma.h); contractions 256 x 256
 //                             (output rows x feature columns, 8 waves) in a
 //                             kernel of their own, a last column of at most
-//                             128 features in 512 x 128 tiles where faster
+//                             128 features in 512 x 128 tiles where faster;
+//                             256 x 384 where those take fewer rounds of work
 //   bf16 / fp16, other        forward sums and gradient-matrix tiles 128 x 128
 //   layouts                   staged through registers (mec_gemm_16.h); the
 //                             contractions read internal buffers, which are
