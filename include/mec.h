@@ -155,7 +155,9 @@ int mec_grad_blocking(int64_t n, int64_t d, int dtype, int64_t* block_rows, int6
 
 /* rx, ry (1 if !normalize), diag; clears the sum accumulators.
  * MEC_DTYPE_F32_BF16X3, MEC_DTYPE_F32_BF16: also writes the bf16 (split)
- * copies of x and y into the workspace. */
+ * copies of x and y into the workspace, normalized (x_i rx_i, y_j ry_j) when
+ * normalize is set; mec_sumexp and the backward then run their GEMMs on
+ * those copies, so every stage of one step takes the same normalize. */
 int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                 int dtype, int normalize, float* workspace, void* stream);
 

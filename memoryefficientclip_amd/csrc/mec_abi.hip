@@ -461,13 +461,19 @@ int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
     const unsigned sgrid = (unsigned)((nthr + 255) / 256);
     uint16_t* sa = (uint16_t*)split_a(workspace, n);
     uint16_t* sb = (uint16_t*)split_b(workspace, n, d, dtype);
-    if (is_x3(dtype)) {
-      k_split3<0><<<sgrid, 256, 0, s>>>((const float*)x, ldx, N, D, (int)dp, sa, ld);
-      k_split3<1><<<sgrid, 256, 0, s>>>((const float*)y, ldy, N, D, (int)dp, sb, ld);
-    } else {
-      k_split1<<<sgrid, 256, 0, s>>>((const float*)x, ldx, N, D, (int)dp, sa, ld);
-      k_split1<<<sgrid, 256, 0, s>>>((const float*)y, ldy, N, D, (int)dp, sb, ld);
-    }
+    // (normalize: of x^ and y^, scaled by the norms just computed, so that the
+    // GEMM kernels run without the norm scaling)
+    const float* rx = workspace + WS_RX * n;
+    const float* ry = workspace + WS_RY * n;
+    DISPATCH_BOOL(normalize, NORM, {
+      if (is_x3(dtype)) {
+        k_split3<0, NORM><<<sgrid, 256, 0, s>>>((const float*)x, ldx, N, D, (int)dp, sa, ld, rx);
+        k_split3<1, NORM><<<sgrid, 256, 0, s>>>((const float*)y, ldy, N, D, (int)dp, sb, ld, ry);
+      } else {
+        k_split1<NORM><<<sgrid, 256, 0, s>>>((const float*)x, ldx, N, D, (int)dp, sa, ld, rx);
+        k_split1<NORM><<<sgrid, 256, 0, s>>>((const float*)y, ldy, N, D, (int)dp, sb, ld, ry);
+      }
+    });
   }
   return check_launch("prepass");
 }
@@ -482,12 +488,14 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   if (!workspace) return fail(MEC_ERR_INVALID, "workspace must be non-null");
   hipStream_t s = (hipStream_t)stream;
   const float c = (float)(1.4426950408889634 / (double)temperature);
-  // split modes: the bf16 sums over the copies (K = terms * dp) that mec_prepass wrote
+  // split modes: the bf16 sums over the copies (K = terms * dp) that mec_prepass
+  // wrote, already normalized when normalize is set
   GemmOperands g{x, ldx, y, ldy, d, dtype};
   if (is_split(dtype)) {
     if (!aligned16(workspace))
       return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for the bf16-product modes");
     g = split_operands(workspace, n, d, dtype);
+    normalize = 0;
   }
   x = g.x, ldx = g.ldx, y = g.y, ldy = g.ldy, d = g.d, dtype = g.dtype;
   const int N = (int)n, D = (int)d;
@@ -751,18 +759,19 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
         rc = check_launch("grad_contract");
       }
       if (!rc && grid > 0) {
-        if (!X3 && !normalize) {
-          // chained tiles (the normalising epilogue would spill registers in the tile loop)
+        // (the copies are already normalized: no norm scaling in the tiles)
+        if (!X3) {
+          // chained tiles
           rc = compute_units(&cus);
           if (!rc)
             DISPATCH_BOOL(lit, LIT,
                 k_grad_g_chain<T, LIT, false><<<(unsigned)(grid < cus ? grid : cus), FwdTile<T, true>::NT, 0, s>>>(
                     (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g));
         } else {
-          DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM,
-              k_grad_step<T, LIT, NORM, true, true, X3><<<(unsigned)grid, FwdTile<T, true>::NT, 0, s>>>(
+          DISPATCH_BOOL(lit, LIT,
+              k_grad_step<T, LIT, false, true, true, X3><<<(unsigned)grid, FwdTile<T, true>::NT, 0, s>>>(
                   (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g, acc_x,
-                  acc_y)));
+                  acc_y));
         }
       }
     });

@@ -296,22 +296,25 @@ __device__ __forceinline__ void split2_bf16(float a, float b, uint32_t& hi, uint
 // to 8 elements: ORDER 0 (x side) hi, lo, hi; ORDER 1 (y side) hi, hi, lo.
 // The dot product of an x row with a y row over the 3 dp elements is then
 // hi.hi + lo.hi + hi.lo, one bf16 GEMM with K = 3 dp.  Columns D .. dp-1 of
-// each segment are zero.  One thread per 8 columns; out and ld3 16-byte
-// aligned.
-template <int ORDER>
+// each segment are zero.  NORM: the rows are normalized first (x_i rx_i in
+// fp32, rx from the pre-pass), so that the GEMM kernels need no norm scaling.
+// One thread per 8 columns; out and ld3 16-byte aligned.
+template <int ORDER, bool NORM>
 __global__ __launch_bounds__(256) void k_split3(const float* __restrict__ X, int64_t ldx, int N, int D, int dp,
-                                                uint16_t* __restrict__ out, int64_t ld3) {
+                                                uint16_t* __restrict__ out, int64_t ld3,
+                                                const float* __restrict__ rxv) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const int vpr = dp / 8;
   const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (v >= (int64_t)N * vpr) return;
   const int i = (int)(v / vpr), d0 = (int)(v - (int64_t)i * vpr) * 8;
   const float* x = X + (int64_t)i * ldx;
+  const float r = NORM ? rxv[i] : 1.f;
   u32x4 hi, lo;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int d = d0 + 2 * e;
-    const float a = d < D ? x[d] : 0.f, b = d + 1 < D ? x[d + 1] : 0.f;
+    const float a = d < D ? x[d] * r : 0.f, b = d + 1 < D ? x[d + 1] * r : 0.f;
     uint32_t h, l;
     split2_bf16(a, b, h, l);
     hi[e] = h;
@@ -324,21 +327,25 @@ __global__ __launch_bounds__(256) void k_split3(const float* __restrict__ X, int
 }
 
 // bf16 copies of the inputs for the fp32-data / bf16-product mode: row i of
-// out (pitch ldo) is bf16(x_i) (round to nearest even), zero-padded to dp
-// columns.  One thread per 8 columns; out and ldo 16-byte aligned.
+// out (pitch ldo) is bf16(x_i) (NORM: bf16(x_i rx_i)), round to nearest
+// even, zero-padded to dp columns.  One thread per 8 columns; out and ldo
+// 16-byte aligned.
+template <bool NORM>
 __global__ __launch_bounds__(256) void k_split1(const float* __restrict__ X, int64_t ldx, int N, int D, int dp,
-                                                uint16_t* __restrict__ out, int64_t ldo) {
+                                                uint16_t* __restrict__ out, int64_t ldo,
+                                                const float* __restrict__ rxv) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const int vpr = dp / 8;
   const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (v >= (int64_t)N * vpr) return;
   const int i = (int)(v / vpr), d0 = (int)(v - (int64_t)i * vpr) * 8;
   const float* x = X + (int64_t)i * ldx;
+  const float r = NORM ? rxv[i] : 1.f;
   u32x4 hi;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int d = d0 + 2 * e;
-    hi[e] = pack2_bf16(d < D ? x[d] : 0.f, d + 1 < D ? x[d + 1] : 0.f);
+    hi[e] = pack2_bf16(d < D ? x[d] * r : 0.f, d + 1 < D ? x[d + 1] * r : 0.f);
   }
   *(u32x4*)(out + (int64_t)i * ldo + d0) = hi;
 }

@@ -4,7 +4,8 @@ as hi*hi + lo*hi + hi*lo from bf16 terms on the bf16 MFMA.
 
 * The split copies of x and y that mec_prepass writes into the workspace are
   checked bit for bit against a numpy restatement of the split (round to
-  nearest even, lo = bf16(v - hi)).
+  nearest even, lo = bf16(v - hi)) of the rows, normalized first (x_i rx_i
+  in fp32, rx as the pre-pass wrote it) when normalize is set.
 * Loss and gradients are held to the fp32 tolerances (loss rel 1e-4,
   gradient max-rel 1e-3) against the fp64 CPU oracle at small sizes and
   against the dense fp64 definition on the GPU (PyTorch fp64 GEMMs, none of
@@ -41,8 +42,9 @@ def run(module, a, b, grad_b=True):
     return loss.detach().cpu(), ga.grad.cpu(), (gb.grad.cpu() if grad_b else None)
 
 
+@pytest.mark.parametrize("norm", [1, 0], ids=["normalize", "raw"])
 @pytest.mark.parametrize("n,d,ld", [(300, 96, 96), (77, 3, 5), (1000, 130, 136)])
-def test_split_copies_are_exact(n, d, ld):
+def test_split_copies_are_exact(n, d, ld, norm):
     """k_split3 output read back from the workspace, bit for bit."""
     g = torch.Generator().manual_seed(n + d)
     xw = torch.randn(n, ld, generator=g) * torch.exp(torch.randn(n, ld, generator=g))  # wide dynamic range
@@ -52,8 +54,8 @@ def test_split_copies_are_exact(n, d, ld):
     lib = _lib.load()
     nf = lib.mec_workspace_floats_for(n, d, dt)
     ws = torch.zeros(nf, dtype=torch.float32, device=DEV)
-    say(f"split n={n} d={d} ld={ld}")
-    _lib.call("mec_prepass", x.data_ptr(), ld, y.data_ptr(), ld, n, d, dt, 1, ws.data_ptr(),
+    say(f"split n={n} d={d} ld={ld} normalize={norm}")
+    _lib.call("mec_prepass", x.data_ptr(), ld, y.data_ptr(), ld, n, d, dt, norm, ws.data_ptr(),
               torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     off = (lib.mec_workspace_floats(n) + 3) // 4 * 4
@@ -62,11 +64,15 @@ def test_split_copies_are_exact(n, d, ld):
     assert raw.size == 2 * n * 3 * dp
     a3 = raw[: n * 3 * dp].reshape(n, 3 * dp)
     b3 = raw[n * 3 * dp:].reshape(n, 3 * dp)
-    np.testing.assert_array_equal(a3, split_rows(xw[:, :d].numpy(), 0))
-    np.testing.assert_array_equal(b3, split_rows(yw[:, :d].numpy(), 1))
+    rx = ws[:n].cpu().numpy()[:, None]
+    ry = ws[n:2 * n].cpu().numpy()[:, None]
+    if not norm:
+        assert np.all(rx == 1) and np.all(ry == 1)
+    np.testing.assert_array_equal(a3, split_rows(xw[:, :d].numpy() * rx, 0))
+    np.testing.assert_array_equal(b3, split_rows(yw[:, :d].numpy() * ry, 1))
     # the norms and the diagonal come from the fp32 inputs, as in the fp32 mode
     ws32 = torch.zeros(lib.mec_workspace_floats(n), dtype=torch.float32, device=DEV)
-    _lib.call("mec_prepass", x.data_ptr(), ld, y.data_ptr(), ld, n, d, _lib.DTYPE_F32, 1, ws32.data_ptr(),
+    _lib.call("mec_prepass", x.data_ptr(), ld, y.data_ptr(), ld, n, d, _lib.DTYPE_F32, norm, ws32.data_ptr(),
               torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert torch.equal(ws[: 3 * n].cpu(), ws32[: 3 * n].cpu())

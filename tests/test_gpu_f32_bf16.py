@@ -4,7 +4,8 @@ accumulate), PyTorch's meaning of "medium"; the norms, the diagonal and the
 post-pass stay fp32.
 
 * The bf16 copies that mec_prepass writes are checked bit for bit against a
-  numpy round-to-nearest-even restatement.
+  numpy round-to-nearest-even restatement (of x_i rx_i when normalize is
+  set).
 * Loss and gradients are held to the bf16 tolerances (1e-2) against the fp64
   CPU oracle, and at the benchmark's fp32 shape against the dense fp64
   definition on the GPU.
@@ -38,8 +39,9 @@ def run(module, a, b, grad_b=True):
     return loss.detach().cpu(), ga.grad.cpu(), (gb.grad.cpu() if grad_b else None)
 
 
+@pytest.mark.parametrize("norm", [1, 0], ids=["normalize", "raw"])
 @pytest.mark.parametrize("n,d,ld", [(300, 96, 96), (77, 3, 5)])
-def test_bf16_copies_are_exact(n, d, ld):
+def test_bf16_copies_are_exact(n, d, ld, norm):
     g = torch.Generator().manual_seed(n + d)
     xw = torch.randn(n, ld, generator=g) * torch.exp(torch.randn(n, ld, generator=g))
     yw = torch.randn(n, ld, generator=g)
@@ -47,16 +49,21 @@ def test_bf16_copies_are_exact(n, d, ld):
     dt = _lib.DTYPE_F32_BF16
     lib = _lib.load()
     ws = torch.zeros(lib.mec_workspace_floats_for(n, d, dt), dtype=torch.float32, device=DEV)
-    say(f"bf16 copies n={n} d={d} ld={ld}")
-    _lib.call("mec_prepass", x.data_ptr(), ld, y.data_ptr(), ld, n, d, dt, 1, ws.data_ptr(),
+    say(f"bf16 copies n={n} d={d} ld={ld} normalize={norm}")
+    _lib.call("mec_prepass", x.data_ptr(), ld, y.data_ptr(), ld, n, d, dt, norm, ws.data_ptr(),
               torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     off = (lib.mec_workspace_floats(n) + 3) // 4 * 4
     dp = (d + 7) // 8 * 8
     raw = ws[off:].cpu().numpy().view(np.uint16)
     assert raw.size == 2 * n * dp
-    np.testing.assert_array_equal(raw[: n * dp].reshape(n, dp), split_rows(xw[:, :d].numpy(), 2))
-    np.testing.assert_array_equal(raw[n * dp:].reshape(n, dp), split_rows(yw[:, :d].numpy(), 2))
+    # normalize: the copies are of x_i rx_i (fp32 product, rx as the pre-pass wrote it)
+    rx = ws[:n].cpu().numpy()[:, None]
+    ry = ws[n:2 * n].cpu().numpy()[:, None]
+    if not norm:
+        assert np.all(rx == 1) and np.all(ry == 1)
+    np.testing.assert_array_equal(raw[: n * dp].reshape(n, dp), split_rows(xw[:, :d].numpy() * rx, 2))
+    np.testing.assert_array_equal(raw[n * dp:].reshape(n, dp), split_rows(yw[:, :d].numpy() * ry, 2))
 
 
 CASES = [
