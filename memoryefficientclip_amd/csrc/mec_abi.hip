@@ -759,20 +759,12 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
         rc = check_launch("grad_contract");
       }
       if (!rc && grid > 0) {
-        // (the copies are already normalized: no norm scaling in the tiles)
-        if (!X3) {
-          // chained tiles
-          rc = compute_units(&cus);
-          if (!rc)
-            DISPATCH_BOOL(lit, LIT,
-                k_grad_g_chain<T, LIT, false><<<(unsigned)(grid < cus ? grid : cus), FwdTile<T, true>::NT, 0, s>>>(
-                    (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g));
-        } else {
+        // (the copies are already normalized: no norm scaling in the tiles; chained tiles)
+        rc = compute_units(&cus);
+        if (!rc)
           DISPATCH_BOOL(lit, LIT,
-              k_grad_step<T, LIT, false, true, true, X3><<<(unsigned)grid, FwdTile<T, true>::NT, 0, s>>>(
-                  (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g, acc_x,
-                  acc_y));
-        }
+              k_grad_g_chain<T, LIT, false, X3><<<(unsigned)(grid < cus ? grid : cus), FwdTile<T, true>::NT, 0, s>>>(
+                  (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g));
       }
     });
     if (rc) return rc;

@@ -970,7 +970,7 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) 
 // (rx, ry, 1/R, 1/C) reach LDS by direct loads into one of two buffers,
 // issued right after the previous tile's first barrier (when every wave is
 // done with that buffer).
-template <typename T, bool LIT, bool NORM>
+template <typename T, bool LIT, bool NORM, bool X3 = false>
 __global__ __launch_bounds__((FwdTile<T, true>::NT), 1) void k_grad_g_chain(
     const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
     const float* __restrict__ ws, GradBufs gb, BlockGrid bg, StepPlan sp) {
@@ -1048,14 +1048,16 @@ __global__ __launch_bounds__((FwdTile<T, true>::NT), 1) void k_grad_g_chain(
     first = false;
     const float* sv = &s_vec[vb][0][0];
     const bool diag = i0 < j0 + TL::BN && j0 < i0 + TL::BM;
+    // (X3: the lo plane at the same offset in gt_lo)
+    uint16_t* gtl = X3 ? (uint16_t*)gb.gt_lo[buf] + (gt - (uint16_t*)gb.gt[buf]) : nullptr;
     if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
-      grad_gt_store_direct<TL, LIT, NORM, false, (int)GScale<T>::value>(
+      grad_gt_store_direct<TL, LIT, NORM, false, (int)GScale<T>::value, X3>(
           acc, c, i0, j0, N, gt, bg.bs, sv + V_RX * TL::BM, sv + V_RY * TL::BM, sv + V_IR * TL::BM,
-          sv + V_IC * TL::BM);
+          sv + V_IC * TL::BM, gtl);
     else
-      grad_gt_store_direct<TL, LIT, NORM, true, (int)GScale<T>::value>(
+      grad_gt_store_direct<TL, LIT, NORM, true, (int)GScale<T>::value, X3>(
           acc, c, i0, j0, N, gt, bg.bs, sv + V_RX * TL::BM, sv + V_RY * TL::BM, sv + V_IR * TL::BM,
-          sv + V_IC * TL::BM);
+          sv + V_IC * TL::BM, gtl);
     if (!has_next) break;
     tile = next;
     i0 = i1;
