@@ -980,7 +980,7 @@ __global__ __launch_bounds__((FwdTile<T, true>::NT), 1) void k_grad_g_chain(
   enum { V_RX = 0, V_RY = 1, V_IR = 2, V_IC = 3 };
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
   __shared__ __attribute__((aligned(16))) float s_vec[2][4][TL::BM];
-  constexpr int NST = gt_chain_stores<TL>();
+  constexpr int NST = gt_chain_stores<TL>() * (X3 ? 2 : 1);  // G'^T stores per lane and tile (X3: two planes)
   const int64_t n64 = N;
   const int64_t blk = (int64_t)bg.bs * bg.bs;
   const int buf = sp.diag_g & 1;
