@@ -664,6 +664,14 @@ __device__ __forceinline__ void grad_gt_store_direct(const f32x16 (&acc)[TL::FM]
   constexpr int NP = X3 ? 2 : 1;  // planes
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
   const int64_t rowb = (int64_t)(bs >> 4) * 512;  // elements per row of blocks
+  // Non-temporal stores through buffer descriptors at the tile's planes (the
+  // write-once G'^T should not displace the operand panels from the caches).
+  // __builtin_nontemporal_store lost its hint in this function for the
+  // one-plane case (no nt bit in the stores); the buffer store's cache-policy
+  // operand (2: nt) keeps it.  A tile's offsets stay below 8 * bs * 64 bytes.
+  const __amdgpu_buffer_rsrc_t rs_hi = __builtin_amdgcn_make_buffer_rsrc((void*)GTb, 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_lo =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(X3 ? GTl : GTb), 0, 0x7fffffff, 0x00020000);
 #pragma unroll
   for (int bn = 0; bn < TL::FN; ++bn) {
     const int nl = wn * TL::TN + bn * 32 + (lane & 31);
@@ -711,7 +719,7 @@ __device__ __forceinline__ void grad_gt_store_direct(const f32x16 (&acc)[TL::FM]
             pk[pl][1][d] = sw[1];
           }
           const u32x4 u = u32x4{pk[pl][0][0], pk[pl][0][1], pk[pl][1][0], pk[pl][1][1]};
-          __builtin_nontemporal_store(u, (u32x4*)((pl ? GTl : GTb) + off));
+          __builtin_amdgcn_raw_buffer_store_b128(u, pl ? rs_lo : rs_hi, (uint32_t)(off * 2), 0, 2);
         }
       }
     }
