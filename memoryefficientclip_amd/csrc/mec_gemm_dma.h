@@ -251,8 +251,14 @@ struct LoadPlan {
       soff = (uint32_t)k0 * G::ESZ;
     }
     char* dst = isa ? ad + (I * G::NW + w) * 1024 : bd + (I * G::NW + w - A_BLOCKS) * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(isa ? ra : rb, (__attribute__((address_space(3))) void*)dst, 16, off,
-                                             soff, 0, 0);
+    // the gradient-matrix operand (blocked A) streams from HBM once per side:
+    // non-temporal (cache policy 2), so that it does not displace the
+    // transposed-input panels the other tiles re-read
+    if constexpr (G::GB && isa)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)dst, 16, off, soff, 0, 2);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(isa ? ra : rb, (__attribute__((address_space(3))) void*)dst, 16, off,
+                                               soff, 0, 0);
   }
 };
 
