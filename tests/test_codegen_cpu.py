@@ -1,0 +1,82 @@
+"""Code generation of the built library (CPU: disassembles this build's own
+gfx950 code object with the ROCm LLVM tools, no GPU needed).
+
+The cache policies below are performance properties that the compiler can
+drop without any change in results, so no parity test would notice:
+
+* the gradient-matrix kernels (`k_grad_g_chain`, and the 16-bit
+  `k_grad_step`) store G'^T non-temporally: every 16-byte store is a
+  `buffer_store_dwordx4 ... nt`.  (`__builtin_nontemporal_store` once lost
+  its hint in the one-plane case, which cost 3% of a config-4 step.)
+* the contractions (`k_grad_contract`) load their gradient-matrix operand
+  with direct-to-LDS loads carrying `nt`, and their other operand without.
+"""
+import os
+import re
+import shutil
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "memoryefficientclip_amd", "lib", "libmec.so")
+LLVM = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "llvm", "bin")
+TOOLS = {t: os.path.join(LLVM, t) for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump")}
+
+
+def _disassembly():
+    if not os.path.exists(LIB):
+        pytest.skip("library not built")
+    missing = [t for t, p in TOOLS.items() if not os.path.exists(p)]
+    if missing:
+        pytest.skip(f"ROCm LLVM tools missing: {missing}")
+    with tempfile.TemporaryDirectory() as tmp:
+        fat = os.path.join(tmp, "fatbin.bin")
+        co = os.path.join(tmp, "gfx950.o")
+        subprocess.run([TOOLS["llvm-objcopy"], f"--dump-section=.hip_fatbin={fat}", LIB, os.devnull], check=True)
+        subprocess.run([TOOLS["clang-offload-bundler"], "--unbundle", "--type=o", f"--input={fat}",
+                        "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--output={co}"], check=True)
+        out = subprocess.run([TOOLS["llvm-objdump"], "-d", "--mcpu=gfx950", co], check=True,
+                             capture_output=True, text=True).stdout
+    # function symbol -> its instructions
+    funcs, cur = {}, None
+    for line in out.splitlines():
+        m = re.match(r"^[0-9a-f]+ <(\S+)>:$", line)
+        if m:
+            cur = m.group(1)
+            funcs[cur] = []
+        elif cur is not None and line.strip():
+            funcs[cur].append(line.strip())
+    return funcs
+
+
+@pytest.fixture(scope="module")
+def funcs():
+    return _disassembly()
+
+
+def _select(funcs, prefix, exclude=()):
+    sel = {k: v for k, v in funcs.items() if k.startswith(prefix) and not any(e in k for e in exclude)}
+    assert sel, f"no kernels {prefix}*"
+    return sel
+
+
+def test_gradient_matrix_stores_are_non_temporal(funcs):
+    # k_grad_g_chain<T, ...> and the 16-bit k_grad_step<T, ...> (T = bf16 bits `t`, fp16 `DF16_`)
+    chain = _select(funcs, "_ZN3mec14k_grad_g_chain")
+    step16 = {k: v for k, v in funcs.items()
+              if k.startswith("_ZN3mec11k_grad_stepIt") or k.startswith("_ZN3mec11k_grad_stepIDF16_")}
+    assert step16
+    for name, body in {**chain, **step16}.items():
+        stores = [l for l in body if "buffer_store_dwordx4" in l]
+        assert stores, name
+        assert all(re.search(r"\bnt\b", l) for l in stores), (name, [l for l in stores if " nt" not in l][:3])
+        assert not any("global_store_dwordx4" in l for l in body), name
+
+
+def test_contraction_streams_its_gradient_matrix_operand(funcs):
+    for name, body in _select(funcs, "_ZN3mec15k_grad_contract").items():
+        loads = [l for l in body if re.match(r"buffer_load_dwordx4 .* lds", l)]
+        nt = [l for l in loads if re.search(r"\bnt\b", l)]
+        assert nt and len(nt) < len(loads), (name, len(nt), len(loads))
