@@ -98,8 +98,9 @@ extern "C" {
  * The backward is deterministic in either mode.  The similarity tiles are
  * still visited once (in P x Q blocks), with the partial sums combined in a
  * fixed order by a second, O(n) launch.  The 16-bit forward with 16-byte rows
- * and normalize = 0 always runs this way (chained tiles; it is faster than
- * the atomic forward there), with or without the flag. */
+ * and normalize = 0, and the forward of MEC_DTYPE_F32_BF16X3 /
+ * MEC_DTYPE_F32_BF16 (on normalized copies), always run this way (chained
+ * tiles; faster than the atomic forward there), with or without the flag. */
 #define MEC_FLAG_DETERMINISTIC 0x100
 
 /* Thread-local message for the last error on this thread ("" if none). */
