@@ -109,6 +109,12 @@ struct Geo {
     if (TA) {
       jb = b / (BM / 16);
       ib = b - jb * (BM / 16);
+    } else if (SA == 4) {
+      // half-chunk slots: blocks [0, A_BLOCKS / 2) are k-steps 0-1 (i-blocks
+      // 0, 1), the rest k-steps 2-3; within a half, block b' = 2 jb + (ib & 1)
+      const int hh = b / (BM / 16), bh = b - hh * (BM / 16);
+      jb = bh >> 1;
+      ib = 2 * hh + (bh & 1);
     } else {
       jb = b >> 2;
       ib = b & 3;
@@ -121,16 +127,19 @@ struct Geo {
   static constexpr int STAGE = ROWS * ROWB;
   // A stages: 2 (the ring's stages hold A and B of one chunk each), or 3 (A
   // gets a ring of its own, one chunk deeper than B's, for an A streamed from
-  // HBM; not chained): then A stages s = 0..2 come first, B's two after them
+  // HBM; not chained): then A stages s = 0..2 come first, B's two after them.
+  // 4: A in four half-chunk slots (blocked A on the rolling schedule: the
+  // k-steps 0-1 and 2-3 of a chunk are whole 1 KB blocks), B in two stages
+  // after them; a_stage(s) is half-slot s.  Same LDS as two stages.
   static constexpr int SA = SA_;
-  static_assert(SA == 2 || SA == 3, "two or three A stages");
+  static_assert(SA == 2 || SA == 3 || SA == 4, "two or three A stages, or four A half-stages");
   static constexpr int A_STAGE = BM * ROWB, B_STAGE = BN * ROWB;
-  static constexpr int LDS_BYTES = SA == 2 ? S * STAGE : 3 * A_STAGE + 2 * B_STAGE;
+  static constexpr int LDS_BYTES = SA == 2 ? S * STAGE : (SA == 3 ? 3 : 2) * A_STAGE + 2 * B_STAGE;
   static __device__ __forceinline__ char* a_stage(char* lds, int s) {
-    return SA == 2 ? lds + s * STAGE : lds + s * A_STAGE;
+    return SA == 2 ? lds + s * STAGE : lds + s * (SA == 4 ? A_STAGE / 2 : A_STAGE);
   }
   static __device__ __forceinline__ char* b_stage(char* lds, int s) {
-    return SA == 2 ? lds + s * STAGE + A_STAGE : lds + 3 * A_STAGE + s * B_STAGE;
+    return SA == 2 ? lds + s * STAGE + A_STAGE : lds + (SA == 3 ? 3 : 2) * A_STAGE + s * B_STAGE;
   }
   static constexpr int IPW = ROWS / RPB / NW;          // load instructions per wave per chunk
   static constexpr int NMF = FM * FN * MPB;            // MFMAs per k-step
@@ -250,7 +259,9 @@ struct LoadPlan {
       off = (k0 + kv < (isa ? kmax_a : kmax_b)) ? voff[I] : OOB;
       soff = (uint32_t)k0 * G::ESZ;
     }
-    char* dst = isa ? ad + (I * G::NW + w) * 1024 : bd + (I * G::NW + w - A_BLOCKS) * 1024;
+    // (four A half-stages: ad is the half-slot of load I's half, I / (A_LOADS / 2))
+    char* dst = isa ? ad + ((G::SA == 4 ? I % (A_LOADS / 2) : I) * G::NW + w) * 1024
+                    : bd + (I * G::NW + w - A_BLOCKS) * 1024;
     // the gradient-matrix operand (blocked A) streams from HBM once per side:
     // non-temporal (cache policy 2), so that it does not displace the
     // transposed-input panels the other tiles re-read
@@ -307,7 +318,11 @@ template <class G>
 __device__ __forceinline__ const char* a_ptr(const char* stage, int s) {
   const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) / G::WN;
   const int q = lane & 31, h = lane >> 5;
-  if constexpr (G::GB) {
+  if constexpr (G::GB && G::SA == 4) {
+    // four A half-stages: block (wm * TM / 32, s) of the half-slot of k-step s
+    // at 2 KB per j-block and 1 KB per odd k-step
+    return stage + ((wm * G::TM / 32) * 2 + (s & 1)) * 1024 + gb_slot(q, h, s & 1) * 16;
+  } else if constexpr (G::GB) {
     // m = j: block (wm * TM / 32, s), row q, i-half h
     return stage + ((wm * G::TM / 32) * 4 + s) * 1024 + gb_slot(q, h, s & 1) * 16;
   } else {
@@ -508,6 +523,16 @@ __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G:
 template <class G>
 __device__ __forceinline__ void prologue(const Operand& A, const Operand& B, char* lds, LoadPlan<G>& lp) {
   lp.init(A, B);
+  if constexpr (G::SA == 4) {
+    // four A half-stages: A half 0, B of chunk 0, A halves 1 and 2 (the first
+    // barrier waits for the first two, the k-step 1 one for half 1)
+    constexpr int AH = LoadPlan<G>::A_LOADS / 2;
+    static_for<AH>([&](auto i) { lp.template issue<i>(0, G::a_stage(lds, 0), nullptr); });
+    static_for<G::IPW - 2 * AH>([&](auto i) { lp.template issue<2 * AH + i>(0, nullptr, G::b_stage(lds, 0)); });
+    static_for<AH>([&](auto i) { lp.template issue<AH + i>(0, G::a_stage(lds, 1), nullptr); });
+    static_for<AH>([&](auto i) { lp.template issue<i>(G::BK, G::a_stage(lds, 2), nullptr); });
+    return;
+  }
   static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, G::a_stage(lds, 0), G::b_stage(lds, 0)); });
   // three A stages: A's chunk 1 as well, issued last (the first barrier waits for all but it)
   if constexpr (G::SA == 3)
@@ -539,6 +564,7 @@ __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_r
                                               bool vmf_first = false) {
   static_assert(G::S == 2 && G::NS == 4, "two stages, four k-steps per chunk");
   static_assert(G::SA == 2 || !CHAIN, "three A stages: one tile per call");
+  static_assert(G::SA != 4, "four A half-stages: the rolling schedule only");
   if constexpr (ZERO) {
 #pragma unroll
     for (int i = 0; i < G::FM; ++i)
@@ -645,9 +671,8 @@ __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int
 //   the last outer fragment    after the last MFMA,
 // so every read is issued at least NI - 1 MFMAs before its first use, and
 // each MFMA waits (lgkmcnt) only for the reads it needs.  The workgroup
-// barrier of chunk kt + 1 sits in k-step 3 of chunk kt after its first NI
-// MFMAs (SPLIT), before the first read from the next stage, and the loads of
-// chunk kt + 2 follow it.
+// barriers sit in k-steps 1 and 3 after their first NI MFMAs (SPLIT), before
+// the first read from the next A half-stage, and loads follow them.
 template <class G>
 struct RollSched {
   static constexpr int FM = G::FM, FN = G::FN, NMF = G::NMF;
@@ -694,11 +719,12 @@ struct RollSched {
   }
 };
 
-// Per-lane LDS addresses of the rolling reads, for stage 0 (stage p adds
-// p * STAGE); the k-step and the fragment are instruction offsets.
+// Per-lane LDS addresses of the rolling reads, for A's half-slot 0 and B's
+// stage 0 (the reads add half-slot h's h * A_STAGE / 2 and stage p's p *
+// B_STAGE); the k-step and the fragment are instruction offsets.
 template <class G>
 struct RollReader {
-  static_assert(G::GB && G::ESZ == 2 && G::SA == 2 && G::NS == 4, "blocked 16-bit A, two stages, four k-steps");
+  static_assert(G::GB && G::ESZ == 2 && G::SA == 4 && G::NS == 4, "blocked 16-bit A, four A half-stages, four k-steps");
   uint32_t a[2];  // A: transposed, read half 0 / 1; else the slot of even / odd k-steps
   uint32_t b[4];  // B: k-step 0..3
   __device__ __forceinline__ explicit RollReader(char* lds) {
@@ -707,7 +733,7 @@ struct RollReader {
       if constexpr (G::TA) {
         a[h] = lds_off(ta_ptr<G>(G::a_stage(lds, 0), 0, 0, h));
       } else {
-        // a_ptr of k-step h (0 or 1): k-steps 2 and 3 are 2 KB further
+        // a_ptr of k-step h (0 or 1); k-steps 2 and 3 are in the next half-slot
         a[h] = lds_off(a_ptr<G>(G::a_stage(lds, 0), h)) - h * 1024;
       }
     }
@@ -715,41 +741,41 @@ struct RollReader {
     for (int s = 0; s < 4; ++s) b[s] = lds_off(b_ptr<G>(G::b_stage(lds, 0), s));
   }
   template <int S, int R>
-  __device__ __forceinline__ void read(Frags<G>& f, uint32_t soff) const {
+  __device__ __forceinline__ void read(Frags<G>& f, uint32_t sa, uint32_t sb) const {
     using RS = RollSched<G>;
     constexpr int fr = RS::frag(R);
     if constexpr (RS::is_a(R)) {
       if constexpr (G::TA) {
         // fragment i is 2 KB further, k-steps as in ta_ptr
-        constexpr int off = fr * 2048 + (S >> 1) * (G::BM / 16) * 1024 + (S & 1) * 256;
+        constexpr int off = fr * 2048 + (S & 1) * 256;
         static_assert(off < 65536, "ds offset");
         i16x4_t v;
-        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(a[RS::half(R)] + soff), "n"(off) : "memory");
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(a[RS::half(R)] + sa), "n"(off) : "memory");
         if constexpr (RS::half(R) == 0)
           f.a[fr].lo = v;
         else
           f.a[fr].hi = v;
       } else {
-        f.a[fr] = lds_read_b128<S * 1024 + fr * 32 * G::ROWB>(a[S & 1] + soff);
+        f.a[fr] = lds_read_b128<(S & 1) * 1024 + fr * 2048>(a[S & 1] + sa);
       }
     } else {
-      f.b[fr] = lds_read_b128<fr * 32 * G::ROWB>(b[S] + soff);
+      f.b[fr] = lds_read_b128<fr * 32 * G::ROWB>(b[S] + sb);
     }
   }
 };
 
 // MFMAs [M0, M1) of k-step `S` (fragments f), each after the wait for the
-// reads it needs.  READ: the reads of k-step SN (stage offset sn) are issued
-// at their positions (and those at position M0 - 1 first).  Loads [L0, L1) of
-// the chunk at k1 into (ad, bd), one after each of the range's first MFMAs.
-template <class G, int S, bool READ, int SN, int M0, int M1, int L0, int L1>
+// reads it needs.  READ: the reads of k-step SN (A's and B's stage offsets
+// sna, snb) are issued at their positions (and those at position M0 - 1
+// first).  ld(q), q < NL: the range's loads, one after each of its first MFMAs.
+template <class G, int S, bool READ, int SN, int M0, int M1, int NL, class LD>
 __device__ __forceinline__ void roll_range(Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const RollReader<G>& rd,
-                                           uint32_t sn, const LoadPlan<G>& lp, int k1, char* ad, char* bd) {
+                                           uint32_t sna, uint32_t snb, const LD& ld) {
   using RS = RollSched<G>;
-  static_assert(L1 - L0 <= M1 - M0, "one load per MFMA");
+  static_assert(NL <= M1 - M0, "one load per MFMA");
   if constexpr (READ && M0 > 0) {
     static_for<RS::NR>([&](auto rc) {
-      if constexpr (RS::pos(rc) == M0 - 1) rd.template read<SN, rc>(f, sn);
+      if constexpr (RS::pos(rc) == M0 - 1) rd.template read<SN, rc>(f, sna, snb);
     });
   }
   static_for<M1 - M0>([&](auto mc) {
@@ -768,28 +794,39 @@ __device__ __forceinline__ void roll_range(Frags<G>& f, f32x16 (&acc)[G::FM][G::
       sched_fence();
     }
     acc[i][j] = mfma16_32x32x16<G::F16>(f.a[i], f.b[j], acc[i][j]);
-    if constexpr (READ || (mc < L1 - L0)) {
+    if constexpr (READ || (mc < NL)) {
       sched_fence();
       if constexpr (READ)
         static_for<RS::NR>([&](auto rc) {
-          if constexpr (RS::pos(rc) == m) rd.template read<SN, rc>(f, sn);
+          if constexpr (RS::pos(rc) == m) rd.template read<SN, rc>(f, sna, snb);
         });
-      if constexpr (mc < L1 - L0) lp.template issue<L0 + mc>(k1, ad, bd);
+      if constexpr (mc < NL) ld(mc);
       sched_fence();
     }
   });
 }
 
-// One tile on the rolling schedule (not chained): chunk 0 into stage 0, the
-// k-loop, the zero loads past the last chunk awaited (ZERO = false: added to
-// acc).
+// One tile on the rolling schedule (not chained): the first chunk and a
+// half, the k-loop, the zero loads past the last chunk awaited (ZERO = false:
+// added to acc).
+//
+// A (streamed from HBM) in four half-stages, B in two stages: half h of A
+// (k-steps 2 (h % 2) and + 1 of chunk h / 2) lives in half-slot h % 4.  A
+// second barrier, in k-step 1 of chunk kt, frees the half-slot of chunk kt's
+// k-steps 0-1 for half 2 kt + 4; the barrier in k-step 3 also frees the other
+// half-slot, for half 2 kt + 5, beside B's stage for chunk kt + 2.  Every A
+// half then has a chunk and a half of lead.  Per wave the loads go out as
+// groups [B(kt + 2), A(2 kt + 5)] (k-step 3 barrier) and A(2 kt + 4) (k-step
+// 1 barrier); vector-memory loads complete in issue order, so the k-step 3
+// barrier of chunk kt + 1, which needs B(kt + 1) and A(2 kt + 2), waits until
+// at most A(2 kt + 3) and A(2 kt + 4) (2 A_LOADS / 2 loads) are outstanding,
+// and the k-step 1 barrier of chunk kt + 1, which needs A(2 kt + 3), until at
+// most A(2 kt + 4) and the group [B(kt + 2), A(2 kt + 5)] are.
 template <class G, bool ZERO = true>
 __device__ __forceinline__ void mainloop_roll(const Operand& A, const Operand& B, int K, char* lds,
                                               f32x16 (&acc)[G::FM][G::FN]) {
   using RS = RollSched<G>;
   constexpr int SPL = RS::SPLIT, NMF = G::NMF, BK = G::BK;
-  constexpr int LH = G::IPW / 2;  // loads after the barrier in k-step 3, the rest in k-step 0
-  static_assert(LH <= NMF - SPL && G::IPW - LH <= NMF, "load slots");
   if constexpr (ZERO) {
 #pragma unroll
     for (int i = 0; i < G::FM; ++i)
@@ -803,35 +840,64 @@ __device__ __forceinline__ void mainloop_roll(const Operand& A, const Operand& B
   const RollReader<G> rd(lds);
   Frags<G> f;
   const int nk = (K + BK - 1) / BK;
-  // k-steps 0..2 and the first half of k-step 3 of chunk kt (stage offset
-  // sc), the first half of chunk kt + 1's loads already issued
-  auto chunk = [&](int kt, uint32_t sc, char* na, char* nb) {
-    const int k1 = (kt + 1) * BK;
-    roll_range<G, 0, true, 1, 0, NMF, LH, G::IPW>(f, acc, rd, sc, lp, k1, na, nb);
-    roll_range<G, 1, true, 2, 0, NMF, 0, 0>(f, acc, rd, sc, lp, 0, na, nb);
-    roll_range<G, 2, true, 3, 0, NMF, 0, 0>(f, acc, rd, sc, lp, 0, na, nb);
-    roll_range<G, 3, false, 0, 0, SPL, 0, 0>(f, acc, rd, sc, lp, 0, na, nb);
-  };
-  // chunk 0 landed: its k-step 0 reads, then chunk 1's first loads
-  wait_barrier<0>();
-  sched_fence();
-  static_for<RS::NR>([&](auto rc) { rd.template read<0, rc>(f, 0); });
-  static_for<LH>([&](auto l) { lp.template issue<l>(BK, G::a_stage(lds, 1), G::b_stage(lds, 1)); });
-  sched_fence();
-  chunk(0, 0, G::a_stage(lds, 1), G::b_stage(lds, 1));
-  for (int kt = 1; kt < nk; ++kt) {
-    const int c = kt & 1;
-    const uint32_t sc = c ? G::STAGE : 0;  // stage of chunk kt
-    char* na = G::a_stage(lds, c ^ 1);
-    char* nb = G::b_stage(lds, c ^ 1);
-    // chunk kt landed; every wave is done with chunk kt - 1's stage.  Then
-    // k-step 3 of chunk kt - 1, second half, reading k-step 0 of chunk kt
-    wait_barrier<0>();
+  const auto none = [](auto) {};
+  static_assert(G::SA == 4, "four A half-stages");
+  {  // (scope of the schedule's constants)
+    constexpr int AH = LoadPlan<G>::A_LOADS / 2, NB = G::IPW - 2 * AH;
+    constexpr int NX = NB + AH;        // the k-step 3 barrier's group
+    constexpr int XH = NX / 2;         // its loads after the barrier, the rest in k-step 0
+    constexpr int WX = 2 * AH, WY = AH + NX;  // vmcnt of the two barriers
+    static_assert(XH <= NMF - SPL && NX - XH <= NMF && AH <= NMF - SPL, "load slots");
+    constexpr uint32_t HALF = G::A_STAGE / 2;
+    // group load q of chunk kc (B first, then A's second half), half-slot / stage parity c
+    const auto xload = [&](auto q, int kc, int c) {
+      constexpr int I = q < NB ? 2 * AH + q : AH + (q - NB);
+      lp.template issue<I>(kc * BK, G::a_stage(lds, 2 * c + 1), G::b_stage(lds, c));
+    };
+    // k-steps 0..2 and the first half of k-step 3 of chunk kt (parity c), the
+    // first XH loads of chunk kt + 1's group already issued; then its barrier
+    // and the second half of k-step 3, reading chunk kt + 1
+    auto chunk = [&](int kt, int c) {
+      const uint32_t a0 = 2 * c * HALF, a1 = a0 + HALF, sb = c * G::B_STAGE;
+      roll_range<G, 0, true, 1, 0, NMF, NX - XH>(f, acc, rd, a0, sb,
+                                                  [&](auto q) { xload(std::integral_constant<int, XH + q>{}, kt + 1, c ^ 1); });
+      roll_range<G, 1, false, 2, 0, SPL, 0>(f, acc, rd, 0, 0, none);
+      // every wave is done with half 2 kt; half 2 kt + 1 landed
+      wait_barrier<WY>();
+      sched_fence();
+      roll_range<G, 1, true, 2, SPL, NMF, AH>(f, acc, rd, a1, sb, [&](auto q) {
+        lp.template issue<q>((kt + 2) * BK, G::a_stage(lds, 2 * c), nullptr);
+      });
+      roll_range<G, 2, true, 3, 0, NMF, 0>(f, acc, rd, a1, sb, none);
+      roll_range<G, 3, false, 0, 0, SPL, 0>(f, acc, rd, 0, 0, none);
+      // chunk kt + 1's B and first A half landed; every wave is done with
+      // chunk kt's B and A half 2 kt + 1
+      wait_barrier<WX>();
+      sched_fence();
+      roll_range<G, 3, true, 0, SPL, NMF, XH>(f, acc, rd, a0 ^ (2 * HALF), sb ^ G::B_STAGE,
+                                              [&](auto q) { xload(q, kt + 2, c); });
+    };
+    // chunk 0's B and first A half landed: its k-step 0 reads, then chunk 1's group
+    wait_barrier<WX>();
     sched_fence();
-    roll_range<G, 3, true, 0, SPL, NMF, 0, LH>(f, acc, rd, sc, lp, (kt + 1) * BK, na, nb);
-    chunk(kt, sc, na, nb);
+    static_for<RS::NR>([&](auto rc) { rd.template read<0, rc>(f, 0, 0); });
+    static_for<XH>([&](auto q) { xload(q, 1, 1); });
+    sched_fence();
+    for (int kt = 0; kt < nk - 1; ++kt) chunk(kt, kt & 1);
+    {
+      // the last chunk: no further barrier in k-step 3 (nothing else is read)
+      const int kt = nk - 1, c = kt & 1;
+      const uint32_t a0 = 2 * c * HALF, a1 = a0 + HALF, sb = c * G::B_STAGE;
+      roll_range<G, 0, true, 1, 0, NMF, NX - XH>(f, acc, rd, a0, sb,
+                                                  [&](auto q) { xload(std::integral_constant<int, XH + q>{}, kt + 1, c ^ 1); });
+      roll_range<G, 1, false, 2, 0, SPL, 0>(f, acc, rd, 0, 0, none);
+      wait_barrier<WY>();
+      sched_fence();
+      roll_range<G, 1, true, 2, SPL, NMF, 0>(f, acc, rd, a1, sb, none);
+      roll_range<G, 2, true, 3, 0, NMF, 0>(f, acc, rd, a1, sb, none);
+      roll_range<G, 3, false, 0, 0, NMF, 0>(f, acc, rd, 0, 0, none);
+    }
   }
-  roll_range<G, 3, false, 0, SPL, NMF, 0, 0>(f, acc, rd, 0, lp, 0, lds, lds);
   drain_loads();
 }
 

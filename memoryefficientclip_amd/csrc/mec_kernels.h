@@ -168,7 +168,8 @@ template <typename T, bool DMA = true, bool IS16 = Is16<T>::value> struct ConTil
 // wx, wy: 256 rows x 384 features where those take fewer rounds of work
 // (D = 1152: three feature tiles instead of four and a half-empty fifth), 2 x
 // 4 waves of 128 x 96: 192 accumulator registers, one fragment set on the
-// rolling operand schedule (gdma::mainloop_roll), two stages (160 KB)
+// rolling operand schedule (gdma::mainloop_roll), the gradient-matrix operand
+// in four half-chunk stages and the other in two (160 KB)
 template <typename T, bool DMA> struct ConTileSel<T, DMA, false> {
   using x = typename std::conditional<DMA, TileD<128, 128, false, 2, 2, gdma::K_F32>, TileF32>::type;
   using y = x;
@@ -182,8 +183,8 @@ template <typename T, bool DMA> struct ConTileSel<T, DMA, true> {
   using y = TileD<256, 256, false, 4, 2, kind16<T>(), 3, true>;
   using nx = TileD<512, 128, true, 4, 2, kind16<T>(), 2, true>;
   using ny = TileD<512, 128, false, 4, 2, kind16<T>(), 2, true>;
-  using wx = TileD<256, 384, true, 2, 4, kind16<T>(), 2, true, true>;
-  using wy = TileD<256, 384, false, 2, 4, kind16<T>(), 2, true, true>;
+  using wx = TileD<256, 384, true, 2, 4, kind16<T>(), 4, true, true>;
+  using wy = TileD<256, 384, false, 2, 4, kind16<T>(), 4, true, true>;
 };
 template <typename T, bool DMA = true> using ConTileX = typename ConTileSel<T, DMA>::x;
 template <typename T, bool DMA = true> using ConTileY = typename ConTileSel<T, DMA>::y;
