@@ -364,12 +364,13 @@ bool narrow_contract_use(int bs, int64_t wide, int64_t narrow) {
 // 16-bit contraction tiles 384 features wide (ConTileSel::wx / wy; 1.5 times
 // the work of a 256 x 256 tile) for a launch of t384 such tiles instead of
 // t256 tiles of 256 x 256 (or the narrow ones): where they take fewer
-// tile-rounds of work over the compute units.  At D = 1152 (config 5) the
-// 256-wide tiles spend a tenth of the launch on a half-empty fifth feature
-// column (8.99 -> 8.09 ms per launch); at equal cost (D = 768: 2.68-2.69 ms
-// both) the 256-wide tiles stay; at D = 300 with few tiles per CU the
-// 384-wide ones were 17% slower.  MEC_WIDE_CONTRACT=0 / 1 turns them off /
-// on for every D (tests).
+// tile-rounds of work over the compute units, or as many.  At D = 1152
+// (config 5) the 256-wide tiles spend a tenth of the launch on a half-empty
+// fifth feature column (8.92 -> 7.80 ms per launch); at equal rounds the
+// 384-wide tiles' lower share of loads per MFMA wins (N = 65536, D = 768: 2.68
+// -> 2.49 ms; D = 1536: 5.28 -> 4.98 ms); with more rounds they lose (D = 512
+// and D = 300: 16-23% slower).  MEC_WIDE_CONTRACT=0 / 1 turns them off / on
+// for every D (tests).
 bool wide_contract_use(int64_t t384, int64_t t256) {
   if (const char* env = std::getenv("MEC_WIDE_CONTRACT")) {
     if (env[0] == '0') return false;
@@ -378,7 +379,7 @@ bool wide_contract_use(int64_t t384, int64_t t256) {
   int cus = 0;
   if (compute_units(&cus) != MEC_OK || cus <= 0) return false;
   const int64_t r384 = (t384 + cus - 1) / cus, r256 = (t256 + cus - 1) / cus;
-  return 3 * r384 < 2 * r256;
+  return 3 * r384 <= 2 * r256;
 }
 
 bool f32_contract_dma(int64_t ldt, int64_t bs) {
