@@ -1,5 +1,6 @@
 """GPU parity of the 16-bit contraction tiles 384 features wide (256 x 384
-tiles, 8 waves of 64 x 192 on the rolling operand schedule).
+tiles, 8 waves of 128 x 96 on the rolling operand schedule, the
+gradient-matrix operand in four half-chunk LDS stages).
 
 MEC_WIDE_CONTRACT=1 forces them for every 16-bit contraction, =0 the 256 x
 256 tiles (with the narrow tiles where those apply).  Every output element
@@ -9,7 +10,11 @@ gradients are bitwise equal; both agree with the fp64 CPU oracle within the
 the forward sums (atomic for unnormalized 16-bit inputs otherwise) are
 bitwise reproducible too.  The shapes cover D below, at and between
 multiples of 384 (the last feature tile partly empty), ragged N with a
-short last block, and several k-chunks per tile.
+short last block, and several k-chunks per tile.  The contraction's k runs
+over a block's rows in chunks of 64 of two half-chunks each: the shapes end
+k within the first half of the last chunk (N = 513, 1300, 20, 150), within
+the second (N = 1000, 700, 40, 100), on a chunk boundary (N = 1024), and
+cover one, two and three chunks in all (N = 20 and 40, 100, 150).
 """
 import os
 
@@ -51,7 +56,8 @@ def run(module, a, b, grad_b, env):
 
 
 SHAPES = [(1024, 300, False), (1000, 384, True), (2048, 100, False), (1300, 1152, True), (700, 768, False),
-          (1024, 385, False), (513, 1000, True), (3000, 64, False)]
+          (1024, 385, False), (513, 1000, True), (3000, 64, False), (20, 768, True), (40, 300, False),
+          (100, 1152, False), (150, 384, True)]
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
