@@ -816,10 +816,11 @@ __device__ __forceinline__ void roll_range(Frags<G>& f, f32x16 (&acc)[G::FM][G::
 // k-steps 0-1 for half 2 kt + 4; the barrier in k-step 3 also frees the other
 // half-slot, for half 2 kt + 5, beside B's stage for chunk kt + 2.  Every A
 // half then has a chunk and a half of lead.  Per wave the loads go out as
-// groups [B(kt + 2), A(2 kt + 5)] (k-step 3 barrier) and A(2 kt + 4) (k-step
-// 1 barrier); vector-memory loads complete in issue order, so the k-step 3
+// groups [B(kt + 2), A(2 kt + 5)] (from the k-step 3 barrier of chunk kt on,
+// the rest in k-step 0 of chunk kt + 1) and A(2 kt + 4) (after the k-step 1
+// barrier); vector-memory loads complete in issue order, so the k-step 3
 // barrier of chunk kt + 1, which needs B(kt + 1) and A(2 kt + 2), waits until
-// at most A(2 kt + 3) and A(2 kt + 4) (2 A_LOADS / 2 loads) are outstanding,
+// at most A(2 kt + 3) and A(2 kt + 4) (A_LOADS loads) are outstanding,
 // and the k-step 1 barrier of chunk kt + 1, which needs A(2 kt + 3), until at
 // most A(2 kt + 4) and the group [B(kt + 2), A(2 kt + 5)] are.
 template <class G, bool ZERO = true>
