@@ -37,9 +37,10 @@
  *     (MEC_ERR_UNSUPPORTED beyond, returned before any launch).  Memory
  *     bounds n further: the caller holds the inputs, the workspace, two fp32
  *     n x d accumulators and the gradient scratch (mec_grad_scratch_bytes;
- *     about 54 GB at n = 2^21, d = 1152, fp32).  16-bit rows that are 16-byte aligned (x, y
- *     16-byte aligned, d, ldx, ldy multiples of 8) use the direct-to-LDS
- *     tiles; other layouts are supported at lower speed.
+ *     16 GiB at n = 2^21, d = 1152, fp32).  Rows that are 16-byte aligned
+ *     (x, y 16-byte aligned, d, ldx, ldy multiples of 8 elements for the
+ *     16-bit types, 4 for fp32) use the direct-to-LDS tiles; other layouts
+ *     are supported at lower speed.
  *   - mode: MEC_MODE_CLIP or MEC_MODE_LIT, optionally OR
  *     MEC_FLAG_DETERMINISTIC.  Every function accepts the flag; only the
  *     forward sums (mec_sumexp, mec_forward) depend on it.
@@ -48,8 +49,20 @@
  *     the data; the forward sizes its persistent launches by that device's
  *     compute units).  No function synchronises the host and none allocates
  *     device memory: the workspace and the gradient scratch are caller-owned.
+ *   - HIP graph capture is not supported: a function called on a stream that
+ *     is being captured (hipStreamIsCapturing, including a legacy default
+ *     stream joined to another stream's capture) returns
+ *     MEC_ERR_UNSUPPORTED before any launch.  A captured step of this loss
+ *     ended in a host segmentation fault during graph instantiation on
+ *     MI355X, with no cause found in these launches.
  *   - Argument validation is pure host code; invalid arguments are reported
  *     before anything touches the GPU.
+ *   - Resident device memory: the library's code object holds the
+ *     MEC_NOALLOC_SCRATCH_BYTES (256 MiB) array of mec_backward_noalloc, so
+ *     every GPU on which any function of this library runs carries those
+ *     256 MiB for the life of the process, whether or not
+ *     mec_backward_noalloc is ever called.  PyTorch's allocator statistics do
+ *     not include it.
  */
 #ifndef MEC_H_
 #define MEC_H_
@@ -103,6 +116,12 @@ extern "C" {
  * tiles; faster than the atomic forward there), with or without the flag. */
 #define MEC_FLAG_DETERMINISTIC 0x100
 
+/* Sides of the backward, for the size queries: the x side (acc_x, dx) and
+ * the y side (acc_y, dy; CLIP only).  mec_grad and friends compute the sides
+ * whose accumulators are non-NULL. */
+#define MEC_SIDE_X 1
+#define MEC_SIDE_Y 2
+
 /* Thread-local message for the last error on this thread ("" if none). */
 const char* mec_last_error(void);
 
@@ -130,22 +149,48 @@ int64_t mec_workspace_floats(int64_t n);
  * in the reference. */
 int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype);
 
-/* Bytes of gradient scratch needed by mec_grad / mec_grad_step /
- * mec_backward for (n, d, dtype), all in the input dtype:
- *   - the gradient-matrix buffers: two buffers holding one block diagonal of
- *     the off-diagonal gradient matrix each (nb blocks of bs x bs), for fp32
- *     the same blocks transposed as well (4 copies; bf16x3: hi and lo planes,
- *     4 copies; the other dtypes 2 copies);
- *   - transposed normalised copies of x and y ([d][n rounded up to 128];
- *     bf16x3: hi and lo planes of each).
+/* Bytes of gradient scratch that mec_grad / mec_grad_step / mec_backward
+ * need for (n, d, dtype, mode, sides), sides a mask of MEC_SIDE_X and
+ * MEC_SIDE_Y (LiT: the x side only).  The layout, in the scratch element type
+ * (fp32 for MEC_DTYPE_F32, 16 bits for every other dtype):
+ *   - the gradient-matrix buffers: one block diagonal of the off-diagonal
+ *     gradient matrix (nb blocks of bs x bs), double-buffered (one buffer
+ *     when a single block covers n).  fp32 keeps H = diag(rx) G' diag(ry)
+ *     once, row-major; the 16-bit types keep G'^T in a blocked layout
+ *     (bf16x3: hi and lo planes);
+ *   - the 16-bit types (and the bf16-product modes) only: transposed
+ *     normalised copies of the inputs, [d][n rounded up to 128], one for each
+ *     side computed (bf16x3: hi and lo planes).  fp32 reads its raw inputs.
  * bs targets ~4d rows for fp32 and ~8d for the other dtypes (~16d when
- * n >= 8192 and 8d would give fewer than 16 blocks; at most 32512 rows), and
- * is shortened until the gradient-matrix buffers fit the smaller of 16 GiB
- * and the bytes of a dense fp32 n x n logit matrix (n^2 x 4), but not below
- * 1024 rows.  The total is therefore about copies x n x bs x elem +
- * 2 x d x n x elem: O(n*d).  The fp32-data modes keep these in bf16.
+ * n >= 8192 and 8d would give fewer than 16 blocks; at most 16384 rows for
+ * fp32 and 32512 for the 16-bit kernels), and is shortened, never below 128
+ * (fp32) or 256 rows, until the gradient-matrix buffers fit
+ * min(16 GiB, max(64 n d elem, 256 MiB)): O(n*d).  Examples: n = 32768,
+ * d = 1152 fp32 CLIP 1.07 GB; LiT the same; n = 1024, d = 512 fp32 4.2 MB.
  * Returns < 0 on bad args or n outside [1, 2^22]. */
+int64_t mec_grad_scratch_bytes_for(int64_t n, int64_t d, int dtype, int mode, int sides);
+
+/* mec_grad_scratch_bytes_for(n, d, dtype, MEC_MODE_CLIP, MEC_SIDE_X | MEC_SIDE_Y):
+ * enough for every mode and side. */
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype);
+
+/* The backward's plan for (n, d, dtype, mode, sides) on a device of
+ * `compute_units` CUs (<= 0: the current device's), for 16-byte aligned rows.
+ * No counterpart in the reference; for callers sizing buffers and for tests
+ * of the selection rules without a GPU. */
+typedef struct mec_backward_plan_t {
+  int64_t block_rows;            /* rows per block of the gradient matrix */
+  int64_t num_blocks;            /* blocks (mec_grad runs num_blocks + 1 steps) */
+  int64_t scratch_bytes;         /* mec_grad_scratch_bytes_for */
+  int64_t noalloc_block_rows;    /* mec_backward_noalloc's block rows, -1 if it refuses the problem */
+  int64_t noalloc_scratch_bytes; /* bytes of its array that it uses, -1 if it refuses the problem */
+  int32_t contract_tile_rows;    /* contraction tile: output rows ... */
+  int32_t contract_tile_features;/* ... and features (16-bit: 256 or 384) */
+  int32_t narrow_tiles;          /* 16-bit: 512 x 128 tiles for a last column of <= 128 features */
+  int32_t reserved;
+} mec_backward_plan_t;
+int mec_backward_plan(int64_t n, int64_t d, int dtype, int mode, int sides, int compute_units,
+                      mec_backward_plan_t* plan);
 
 /* Block decomposition of the backward for (n, d, dtype): the n x n gradient
  * matrix is cut into num_blocks^2 blocks of block_rows rows (the last block
@@ -184,7 +229,12 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
  * Replaces clip_grad_kernel (clip_loss.py:67-156) and lit_grad_kernel
  * (lit_loss.py:65-148).  A NULL accumulator skips that side (e.g. a frozen
  * tower); at least one is required.  scratch must hold
- * mec_grad_scratch_bytes(n, d, dtype) bytes, 16-byte aligned.
+ * mec_grad_scratch_bytes_for(n, d, dtype, mode, sides) bytes for the sides
+ * requested, 16-byte aligned.  MEC_DTYPE_F32: the accumulators hold the
+ * contractions of H = diag(rx) G' diag(ry) with the raw inputs, i.e. row i of
+ * acc_x is rx_i sum_j G'_ij y^_j (and acc_y's row j ry_j sum_i G'_ij x^_i;
+ * rx = ry = 1 when normalize = 0), which mec_postpass expects for that dtype;
+ * row strides up to 2^24 elements (MEC_ERR_UNSUPPORTED beyond).
  * Equivalent to mec_grad_step for step = 0 .. num_blocks in order. */
 int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
              int dtype, int mode, int normalize, float temperature, const float* workspace,
@@ -201,7 +251,8 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
                   int64_t step, void* scratch, int64_t scratch_bytes, float* acc_x, float* acc_y,
                   void* stream);
 
-/* Final gradients from the accumulators: scale a = grad_scale/(2n) (LiT:
+/* Final gradients from the accumulators (as mec_grad leaves them for the same
+ * dtype and normalize): scale a = grad_scale/(2n) (LiT:
  * grad_scale/n), exact diagonal term, F.normalize backward when normalize,
  * times *grad_output (device fp32 scalar, NULL = 1), cast to dtype.
  * grad_scale is 1/T for the standard loss and sqrt(n/T) for the Stable
@@ -229,16 +280,19 @@ int mec_backward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
 
 /* mec_backward without caller scratch and without any allocation.  No
  * counterpart in the reference: it is for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc).  The gradient scratch is a file-scope device array of
- * MEC_NOALLOC_SCRATCH_BYTES on each GPU the library runs on, held until the
- * process ends; its address is resolved once per device on the first call.
- * The blocking is mec_backward's when its scratch fits the array, else
- * shorter blocks (down to 1024 rows); problems whose scratch does not fit even
- * then (e.g. more than about 2^15 rows at d = 1152) return
- * MEC_ERR_UNSUPPORTED before any launch.  Nothing in the array needs to start
- * at zero.  Every call on one GPU uses the same array: calls that overlap on
- * one GPU (other streams, other threads) race and must be serialised by the
+ * memory (tight serving loops, harnesses that forbid hipMalloc; not HIP graph
+ * capture, which every function here refuses).  The gradient scratch is a
+ * file-scope device array of MEC_NOALLOC_SCRATCH_BYTES on each GPU the
+ * library runs on, held until the process ends (resident from the library's
+ * first use on that GPU, see above); its address is resolved once per device
+ * on the first call.  The blocking is mec_backward's when its scratch fits
+ * the array, else shorter blocks (down to 128 rows for fp32, 256 for the
+ * other dtypes); problems whose scratch does not fit even then return
+ * MEC_ERR_UNSUPPORTED before any launch.  mec_backward_plan reports, for any
+ * shape, whether it fits and with which blocks (the largest n at d = 1152,
+ * CLIP: see the integration notes).  Nothing in the array needs to start at
+ * zero.  Every call on one GPU uses the same array: calls that overlap on one
+ * GPU (other streams, other threads) race and must be serialised by the
  * caller.  Arguments and results otherwise as mec_backward. */
 int mec_backward_noalloc(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
                          int mode, int normalize, float temperature, float grad_scale, const float* workspace,

@@ -143,7 +143,8 @@ def backward(ctx, grad_output: torch.Tensor, need_x: bool, need_y: bool):
         # before reading it, so the NaN fill that torch.empty performs under
         # torch.use_deterministic_algorithms(True) (gigabytes at large N) would
         # be wasted work.
-        nbytes = lib.mec_grad_scratch_bytes(n, d, dt)
+        sides = (_lib.SIDE_X if need_x else 0) | (_lib.SIDE_Y if need_y else 0)
+        nbytes = lib.mec_grad_scratch_bytes_for(n, d, dt, mode, sides)
         stream = torch.cuda.current_stream(dev)
         scratch = torch.cuda.caching_allocator_alloc(nbytes, dev, stream)
 

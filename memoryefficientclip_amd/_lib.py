@@ -26,6 +26,8 @@ DTYPE_F32_BF16 = 4  # fp32 data, bf16 products
 MODE_CLIP = 0
 MODE_LIT = 1
 FLAG_DETERMINISTIC = 0x100  # OR into the mode of mec_sumexp / mec_forward
+SIDE_X = 1  # MEC_SIDE_X: the x side of the backward (acc_x, dx)
+SIDE_Y = 2  # MEC_SIDE_Y: the y side (CLIP only)
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -39,6 +41,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mec_workspace_floats": (_i64, [_i64]),
     "mec_workspace_floats_for": (_i64, [_i64, _i64, _int]),
     "mec_grad_scratch_bytes": (_i64, [_i64, _i64, _int]),
+    "mec_grad_scratch_bytes_for": (_i64, [_i64, _i64, _int, _int, _int]),
+    "mec_backward_plan": (_int, [_i64, _i64, _int, _int, _int, _int, _vp]),
     "mec_grad_blocking": (_int, [_i64, _i64, _int, _vp, _vp]),
     "mec_prepass": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp]),
     "mec_sumexp": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _int, _int, _f32, _vp, _vp]),
@@ -56,6 +60,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                     _vp, _vp, _vp, _vp, _vp]),
 }
 NOALLOC_SCRATCH_BYTES = 256 << 20  # MEC_NOALLOC_SCRATCH_BYTES
+
+
+class BackwardPlan(ctypes.Structure):
+    """mec_backward_plan_t (include/mec.h)."""
+    _fields_ = [("block_rows", ctypes.c_int64), ("num_blocks", ctypes.c_int64), ("scratch_bytes", ctypes.c_int64),
+                ("noalloc_block_rows", ctypes.c_int64), ("noalloc_scratch_bytes", ctypes.c_int64),
+                ("contract_tile_rows", ctypes.c_int32), ("contract_tile_features", ctypes.c_int32),
+                ("narrow_tiles", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -97,6 +109,16 @@ def grad_blocking(n: int, d: int, dtype: int) -> tuple[int, int]:
     bs, nb = ctypes.c_int64(), ctypes.c_int64()
     call("mec_grad_blocking", n, d, dtype, ctypes.byref(bs), ctypes.byref(nb))
     return bs.value, nb.value
+
+
+def backward_plan(n: int, d: int, dtype: int, mode: int = MODE_CLIP, sides: int = SIDE_X | SIDE_Y,
+                  compute_units: int = 0) -> BackwardPlan:
+    """The backward's plan (blocking, scratch, contraction tiles, what
+    mec_backward_noalloc would use) for (n, d, dtype, mode, sides) on a device
+    of `compute_units` CUs (0: the current device)."""
+    plan = BackwardPlan()
+    call("mec_backward_plan", n, d, dtype, mode, sides, compute_units, ctypes.byref(plan))
+    return plan
 
 
 def last_error() -> str:

@@ -89,6 +89,30 @@ int check_launch(const char* what) {
   return MEC_OK;
 }
 
+// Launches into a stream that is being captured into a HIP graph are
+// refused (MEC_ERR_UNSUPPORTED, before any launch): capturing a step of the
+// loss ended in a host segmentation fault during graph instantiation on the
+// MI355X box, with no cause found in these launches.  A legacy default
+// stream implicitly joined to another stream's capture counts as capturing.
+// MEC_TEST_ASSUME_CAPTURING=1 makes the check report a capture without
+// asking HIP (tests of this refusal on machines without a GPU).
+int check_not_capturing(void* stream) {
+  const char* env = std::getenv("MEC_TEST_ASSUME_CAPTURING");
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  const hipError_t e = (env && env[0] == '1') ? hipSuccess : hipStreamIsCapturing((hipStream_t)stream, &st);
+  if ((env && env[0] == '1') || e == hipErrorStreamCaptureImplicit ||
+      (e == hipSuccess && st != hipStreamCaptureStatusNone)) {
+    if (e != hipSuccess) (void)hipGetLastError();
+    return fail(MEC_ERR_UNSUPPORTED,
+                "the stream is being captured into a HIP graph; graph capture of these kernels is not supported");
+  }
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MEC_ERR_HIP, "hipStreamIsCapturing: %s", hipGetErrorString(e));
+  }
+  return MEC_OK;
+}
+
 // Largest supported n, every dtype.  The 16-bit contractions address a
 // 256-row panel of the transposed inputs ([d][ldt], ldt ~ n) with 32-bit
 // buffer offsets, and the forward's grid of 128 x 128 fp32 tiles,
@@ -199,8 +223,8 @@ bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, i
 // blocks of tb quanta of q rows (q = block_quantum: 128 for fp32, 256 for
 // the bf16 kernels, so every tile kind divides a block).  Longer blocks mean
 // fewer pipeline launches and fewer fp32 accumulator updates through HBM
-// (one per launch); the scratch grows as n * bs.  Targets (at least 1024
-// rows), measured on the 128-byte ring:
+// (one per launch); the scratch grows as n * bs.  Targets, measured on the
+// 128-byte ring:
 //   fp32: bs ~ 4d (headline shape: backward 53.2 ms with 2048-row blocks,
 //         52.4 ms with 4096);
 //   bf16 kernels: bs ~ 8d, or ~16d when n >= 8192 and 8d would give fewer
@@ -211,48 +235,59 @@ bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, i
 // target is preferred (no short last block, whose contractions would have a
 // short K); otherwise the quanta are balanced over the blocks.
 //
-// Memory bound: the gradient-matrix buffers (copies x nb x bs^2 elements,
-// about copies x n x bs) are kept within `gbudget` bytes by shortening the
-// blocks, down to a floor of 1024 rows, which wins over the budget (below
-// it the pipeline's launches and accumulator updates dominate).
-constexpr int64_t kFloorRows = 1024;
-int g_copies(int dtype) { return (dtype == MEC_DTYPE_F32 || is_x3(dtype)) ? 4 : 2; }
+// The target is at least 1024 rows (fewer launches for a small d).
+//
+// Memory bound: the gradient-matrix buffers (nbuf x planes x nb x bs^2
+// elements, about nbuf x planes x n x bs; nbuf = 2 double-buffered
+// diagonals, or 1 when a single block covers n) are kept within `gbudget`
+// bytes by shortening the blocks, never below one quantum.  The default
+// budget is O(n d): 64 n d scratch elements (32 times the two inputs in the
+// scratch element type), at least 256 MiB (so that small problems keep long
+// blocks and few launches) and at most 16 GiB; it wins over the 1024-row
+// target.
+int g_planes(int dtype) { return is_x3(dtype) ? 2 : 1; }
 int64_t g_elem(int dtype) { return dtype == MEC_DTYPE_F32 ? 4 : 2; }
 // bytes of the gradient-matrix buffers for blocks of tb quanta
 int64_t g_bytes(int64_t tiles, int64_t q, int64_t tb, int dtype) {
   const int64_t nb = (tiles + tb - 1) / tb, bs = tb * q;
-  return (int64_t)g_copies(dtype) * nb * bs * bs * g_elem(dtype);
+  return (nb > 1 ? 2 : 1) * g_planes(dtype) * nb * bs * bs * g_elem(dtype);
 }
-// Default budget of the gradient-matrix buffers: the bytes of a dense fp32
-// n x n logit matrix (what the memory-efficient path exists to avoid), and
-// at most 16 GiB.  Neither binds at the benchmark shapes.
 constexpr int64_t kGradBudgetCap = int64_t(16) << 30;
-int64_t default_gbudget(int64_t n) {
-  const int64_t dense = n * n * 4;
-  return dense < kGradBudgetCap ? dense : kGradBudgetCap;
+constexpr int64_t kGradBudgetMin = int64_t(256) << 20;
+constexpr int64_t kGradBudgetRatio = 64;
+constexpr int64_t kTargetMinRows = 1024;
+int64_t default_gbudget(int64_t n, int64_t d, int dtype) {
+  int64_t b = kGradBudgetRatio * n * d * g_elem(dtype);
+  if (b < kGradBudgetMin) b = kGradBudgetMin;
+  return b < kGradBudgetCap ? b : kGradBudgetCap;
 }
 void grad_blocks_budget(int64_t n, int64_t d, int dtype, int64_t gbudget, int* bs, int* nb) {
   const int64_t q = block_quantum(dtype);
   const int64_t tiles = (n + q - 1) / q;
-  const int64_t floor_tb = (kFloorRows + q - 1) / q;
-  // 16-bit: a transposed gradient-matrix block is a direct-to-LDS operand
-  // ((bs - 1) * bs + 256 elements within dma_max_elems): bs <= 127 * 256
-  int64_t cap = dtype == MEC_DTYPE_F32 ? tiles : 127;
-  // the largest block within the budget (never below the floor)
+  // The y side of fp32 reads a gradient-matrix block transposed with 32-bit
+  // offsets ((bs - 1) * bs + 128 floats within 2^31 bytes: bs <= 16384); the
+  // 16-bit contractions read a transposed block as a direct-to-LDS operand
+  // ((bs - 1) * bs + 256 elements within 2^31 bytes: bs <= 127 * 256).
+  int64_t cap = dtype == MEC_DTYPE_F32 ? 128 : 127;
+  if (cap > tiles) cap = tiles;
+  // the longest blocks within the budget (at least one quantum): an
+  // estimate from the double-buffered size, then a short walk down
   {
-    // g_bytes(tb) >= copies * tiles * tb * q^2 * elem bounds tb from above; the
-    // rounding of the last block is then settled by a short walk down
-    const int64_t per_tb = (int64_t)g_copies(dtype) * tiles * q * q * g_elem(dtype);
-    int64_t tb = cap < tiles ? cap : tiles;
-    if (gbudget / per_tb < tb) tb = gbudget / per_tb;
-    if (tb < floor_tb) tb = floor_tb;
-    while (tb > floor_tb && g_bytes(tiles, q, tb, dtype) > gbudget) --tb;
+    int64_t tb = cap;
+    if (g_bytes(tiles, q, tb, dtype) > gbudget) {
+      const int64_t per_tb = 2 * (int64_t)g_planes(dtype) * tiles * q * q * g_elem(dtype);
+      if (gbudget / per_tb < tb) tb = gbudget / per_tb;
+      if (tb < 1) tb = 1;
+      while (tb > 1 && g_bytes(tiles, q, tb, dtype) > gbudget) --tb;
+    }
     cap = tb;
   }
   int64_t mult = dtype == MEC_DTYPE_F32 ? 4 : 8;
   if (dtype != MEC_DTYPE_F32 && n >= 8192 && n < 16 * 8 * d) mult = 16;
-  int64_t target = (mult * d + q - 1) / q;
-  if (target < floor_tb) target = floor_tb;
+  // at least 1024 rows (below that the pipeline's launches and accumulator
+  // updates dominate), where the budget allows
+  const int64_t target_rows = mult * d > kTargetMinRows ? mult * d : kTargetMinRows;
+  int64_t target = (target_rows + q - 1) / q;
   if (const char* env = std::getenv("MEC_GRAD_BLOCK_TILES")) {
     long v = std::strtol(env, nullptr, 10);
     if (v >= 1 && v <= 4096) target = v;
@@ -276,62 +311,91 @@ void grad_blocks_budget(int64_t n, int64_t d, int dtype, int64_t gbudget, int* b
       tb = (tiles + nbv - 1) / nbv;
     }
   }
-  // balanced blocks may round past the budget: shorten them (not below the floor)
-  while (tb > 1 && tb > floor_tb && g_bytes(tiles, q, tb, dtype) > gbudget) --tb;
+  // balanced blocks may round past the budget: shorten them (not below a quantum)
+  while (tb > 1 && g_bytes(tiles, q, tb, dtype) > gbudget) --tb;
   *bs = (int)(tb * q);
   *nb = (int)((tiles + tb - 1) / tb);
 }
 void grad_blocks(int64_t n, int64_t d, int dtype, int* bs, int* nb) {
-  grad_blocks_budget(n, d, dtype, default_gbudget(n), bs, nb);
+  grad_blocks_budget(n, d, dtype, default_gbudget(n, d, dtype), bs, nb);
 }
 
-// Scratch layout of the backward (element type = input dtype; split modes: bf16):
-//   fp32:                  [G0 | G1 | GT0 | GT1 | XT | YT]
+// Sides of the backward: the x side (acc_x, dx) and the y side (CLIP only)
+constexpr int kSideX = MEC_SIDE_X, kSideY = MEC_SIDE_Y;
+
+// Scratch layout of the backward (elements: fp32 for MEC_DTYPE_F32, else
+// 16-bit), for the sides that are computed:
+//   fp32:                  [H0 | H1]
 //   bf16, fp16, fp32/bf16: [GT0 | GT1 | XT | YT]
-//   bf16x3:                [GT0 | GT1 | GTlo0 | GTlo1 | XT | YT | XTlo | YTlo]
-// G0/G1 (and their transposes GT0/GT1) double-buffer one block diagonal of
-// G' (nb blocks of bs x bs; the 16-bit types keep only the transposed copy,
-// in the blocked layout gdma::gb_offset, bf16x3 its hi and lo planes); XT/YT
-// are the normalised inputs transposed, [d][ldt] with ldt = n rounded up to
-// 128 (bf16x3: hi and lo planes).
+//   bf16x3:                [GT0 | GT1 | GTlo0 | GTlo1 | XT | XTlo | YT | YTlo]
+// H0/H1 double-buffer one block diagonal of H = diag(rx) G' diag(ry) (nb
+// blocks of bs x bs, row-major); GT0/GT1 the 16-bit types' transposed blocks
+// of G' in the blocked layout gdma::gb_offset (bf16x3: hi and lo planes).
+// With a single block (nb = 1) only buffer 0 exists.  XT/YT are the
+// normalised inputs transposed, [d][ldt] with ldt = n rounded up to 128
+// (bf16x3: hi and lo planes), only for the sides computed: YT for the x
+// side, XT for the y side.  fp32 reads its raw inputs instead.
 struct ScratchLayout {
   int bs, nb;
-  int ncopies;                     // gradient-matrix buffers: 4 or 2
-  int ntrans;                      // transposed-input buffers: 2 or 4
-  int64_t ldt, gbuf, tbuf, total;  // bytes except ldt (elements)
+  int nbuf;            // gradient-matrix diagonals held: 2, or 1 with one block
+  int planes;          // planes per diagonal (bf16x3: hi and lo)
+  int ntp;             // transposed planes per side (0 for fp32; bf16x3: 2)
+  int64_t ldt;         // elements
+  int64_t gbuf, tbuf;  // bytes of one diagonal plane / one transposed plane
+  int64_t xt, yt;      // byte offsets of XT and YT (-1: not held)
+  int64_t total;
 };
-
-// transposed-input bytes of the scratch
-int64_t trans_bytes(int64_t n, int64_t d, int dtype) {
-  return (is_x3(dtype) ? 4 : 2) * d * ((n + 127) / 128 * 128) * g_elem(dtype);
-}
-ScratchLayout scratch_layout_blocks(int64_t n, int64_t d, int dtype, int bs, int nb) {
+ScratchLayout scratch_layout_blocks(int64_t n, int64_t d, int dtype, int sides, int bs, int nb) {
   ScratchLayout L;
   L.bs = bs;
   L.nb = nb;
   const int64_t elem = g_elem(dtype);
+  L.nbuf = nb > 1 ? 2 : 1;
+  L.planes = g_planes(dtype);
+  L.ntp = dtype == MEC_DTYPE_F32 ? 0 : (is_x3(dtype) ? 2 : 1);
   L.ldt = (n + 127) / 128 * 128;
   L.gbuf = (int64_t)L.nb * L.bs * L.bs * elem;
   L.tbuf = d * L.ldt * elem;
-  L.ncopies = g_copies(dtype);
-  L.ntrans = is_x3(dtype) ? 4 : 2;
-  L.total = L.ncopies * L.gbuf + L.ntrans * L.tbuf;
+  int64_t off = (int64_t)L.nbuf * L.planes * L.gbuf;
+  L.xt = L.yt = -1;
+  if (L.ntp > 0 && (sides & kSideY)) {
+    L.xt = off;
+    off += L.ntp * L.tbuf;
+  }
+  if (L.ntp > 0 && (sides & kSideX)) {
+    L.yt = off;
+    off += L.ntp * L.tbuf;
+  }
+  L.total = off;
   return L;
 }
-ScratchLayout scratch_layout(int64_t n, int64_t d, int dtype) {
+ScratchLayout scratch_layout(int64_t n, int64_t d, int dtype, int sides) {
   int bs, nb;
   grad_blocks(n, d, dtype, &bs, &nb);
-  return scratch_layout_blocks(n, d, dtype, bs, nb);
+  return scratch_layout_blocks(n, d, dtype, sides, bs, nb);
+}
+// transposed-input bytes of the scratch for these sides
+int64_t trans_bytes(int64_t n, int64_t d, int dtype, int sides) {
+  return scratch_layout_blocks(n, d, dtype, sides, 0, 1).total;
 }
 
-int64_t scratch_bytes_for(int64_t n, int64_t d, int dtype) { return scratch_layout(n, d, dtype).total; }
+// The blocking and layout of mec_backward_noalloc: the default blocking when
+// its scratch fits the array, else shorter blocks within what the transposed
+// inputs leave of it (not below one quantum); ok = false when even that does
+// not fit.
+ScratchLayout noalloc_layout(int64_t n, int64_t d, int dtype, int sides, bool* ok) {
+  const int64_t trans = trans_bytes(n, d, dtype, sides);
+  int64_t gbudget = kNoAllocScratch - trans;
+  if (gbudget > default_gbudget(n, d, dtype)) gbudget = default_gbudget(n, d, dtype);
+  int bs = block_quantum(dtype), nb = 1;
+  if (gbudget > 0) grad_blocks_budget(n, d, dtype, gbudget, &bs, &nb);
+  const ScratchLayout L = scratch_layout_blocks(n, d, dtype, sides, bs, nb);
+  *ok = gbudget > 0 && L.total <= kNoAllocScratch;
+  return L;
+}
 
 int round8(int v) { return (v + 7) & ~7; }
 
-// fp32 contractions run on the direct-to-LDS core when a transposed input
-// panel (128 rows of pitch ldt) and a gradient-matrix block panel (128 rows of
-// pitch bs) fit its 32-bit offsets, i.e. up to n of about 4.2M; beyond that on
-// the register-staged core.  MEC_F32_CONTRACT_DMA=0 forces the latter (tests).
 // 64 x 64 fp32 tiles (f32_small_n; MEC_F32_SMALL_TILES=0 or 1 overrides, for tests)
 bool f32_small_tiles(int64_t n) {
   if (const char* env = std::getenv("MEC_F32_SMALL_TILES")) {
@@ -343,21 +407,20 @@ bool f32_small_tiles(int64_t n) {
 
 // 16-bit narrow contraction tiles (narrow_contract_shape) for blocks of bs
 // rows whose contraction launch has `wide` workgroups of 256 x 256 tiles,
-// `narrow` with them.  Used where they measured faster: a 512-row panel of the
-// gradient-matrix block (512 x bs x 2 bytes) within one XCD's 4 MB L2, i.e.
-// bs <= 4096 (7-13% less contraction time at D = 128-640; with larger blocks
-// the narrow tiles fall out of step with the wide tiles that share their panel
-// and read it from HBM: 2-11% more), and fewer rounds of workgroups over the
-// CUs than the wide tiles alone.  MEC_NARROW_CONTRACT=0 / 1 turns them off /
-// on wherever the shape allows (tests).
-bool narrow_contract_use(int bs, int64_t wide, int64_t narrow) {
+// `narrow` with them, on `cus` compute units.  Used where they measured
+// faster: a 512-row panel of the gradient-matrix block (512 x bs x 2 bytes)
+// within one XCD's 4 MB L2, i.e. bs <= 4096 (7-13% less contraction time at
+// D = 128-640; with larger blocks the narrow tiles fall out of step with the
+// wide tiles that share their panel and read it from HBM: 2-11% more), and
+// fewer rounds of workgroups over the CUs than the wide tiles alone.
+// MEC_NARROW_CONTRACT=0 / 1 turns them off / on wherever the shape allows
+// (tests).
+bool narrow_contract_use(int bs, int64_t wide, int64_t narrow, int cus) {
   if (const char* env = std::getenv("MEC_NARROW_CONTRACT")) {
     if (env[0] == '0') return false;
     if (env[0] == '1') return true;
   }
-  if (bs > 4096) return false;
-  int cus = 0;
-  if (compute_units(&cus) != MEC_OK || cus <= 0) return false;
+  if (bs > 4096 || cus <= 0) return false;
   return (narrow + cus - 1) / cus < (wide + cus - 1) / cus;
 }
 
@@ -369,24 +432,51 @@ bool narrow_contract_use(int bs, int64_t wide, int64_t narrow) {
 // fifth feature column (8.92 -> 7.80 ms per launch); at equal rounds the
 // 384-wide tiles' lower share of loads per MFMA wins (N = 65536, D = 768: 2.68
 // -> 2.49 ms; D = 1536: 5.28 -> 4.98 ms); with more rounds they lose (D = 512
-// and D = 300: 16-23% slower).  MEC_WIDE_CONTRACT=0 / 1 turns them off / on
-// for every D (tests).
-bool wide_contract_use(int64_t t384, int64_t t256) {
+// and D = 300: 16-23% slower).  A 384-wide tile reads a 384-row panel of a
+// transposed input with 32-bit offsets ((383 ldt + bs) x 2 bytes below 2^31,
+// ldt up to about 2.8M): beyond that only the 256-wide tiles (whose 256-row
+// panels fit up to n = 2^22) are used.  MEC_WIDE_CONTRACT=0 / 1 turns them
+// off / on for every D where the panel fits (tests).
+bool wide_contract_fits(int64_t ldt, int64_t bs) { return (383 * ldt + bs) * 2 < (int64_t(1) << 31); }
+bool wide_contract_use(int64_t t384, int64_t t256, int64_t ldt, int64_t bs, int cus) {
+  if (!wide_contract_fits(ldt, bs)) return false;
   if (const char* env = std::getenv("MEC_WIDE_CONTRACT")) {
     if (env[0] == '0') return false;
     if (env[0] == '1') return true;
   }
-  int cus = 0;
-  if (compute_units(&cus) != MEC_OK || cus <= 0) return false;
+  if (cus <= 0) return false;
   const int64_t r384 = (t384 + cus - 1) / cus, r256 = (t256 + cus - 1) / cus;
   return 3 * r384 <= 2 * r256;
 }
 
-bool f32_contract_dma(int64_t ldt, int64_t bs) {
-  if (const char* env = std::getenv("MEC_F32_CONTRACT_DMA"))
-    if (env[0] == '0') return false;
-  const int64_t pitch = ldt > bs ? ldt : bs;
-  return (dma_rows(MEC_DTYPE_F32) - 1) * pitch + bs <= dma_max_elems(MEC_DTYPE_F32);
+// Tile grid of a backward launch: gradient-matrix tiles of tf, contraction
+// tiles of tc; the 16-bit types choose narrow or 384-wide contraction tiles
+// for the launch's `sides` (on `cus` compute units).
+BlockGrid block_grid(int64_t d, int dtype, int sides, int bs, int nb, int64_t ldt, int cus, TileDims tf, TileDims tc,
+                     bool* w384) {
+  const int D = (int)d;
+  BlockGrid bg{bs, nb, bs / tf.bm, bs / tf.bn, bs / tc.bm, (D + tc.bn - 1) / tc.bn, 0};
+  *w384 = false;
+  if (separate_contractions(dtype)) {
+    const int64_t nsides = ((sides & kSideX) ? 1 : 0) + ((sides & kSideY) ? 1 : 0);
+    const int64_t wide = nsides * nb * bg.ctm * bg.ctd;
+    int64_t tiles = wide;
+    if (narrow_contract_shape(D, bg.ctm)) {
+      const int64_t narrow = nsides * nb * (bg.ctm / 2) * (2 * (D / tc.bn) + 1);
+      if (narrow_contract_use(bs, wide, narrow, cus)) {
+        bg.ctd = D / tc.bn;
+        bg.cnw = 1;
+        tiles = narrow;
+      }
+    }
+    const int ctd384 = (D + 383) / 384;
+    if (wide_contract_use(nsides * nb * bg.ctm * ctd384, tiles, ldt, bs, cus)) {
+      *w384 = true;
+      bg.ctd = ctd384;
+      bg.cnw = 0;
+    }
+  }
+  return bg;
 }
 
 // T = element type of dtype: float, bf16 bits (uint16_t) or fp16 (_Float16);
@@ -437,7 +527,49 @@ int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype) {
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype) {
   if (n < 1 || n > kMaxN || d < 1 || d > kMaxD) return -1;
   if (!known_dtype(dtype)) return -1;
-  return scratch_bytes_for(n, d, dtype);
+  return scratch_layout(n, d, dtype, kSideX | kSideY).total;
+}
+
+int64_t mec_grad_scratch_bytes_for(int64_t n, int64_t d, int dtype, int mode, int sides) {
+  if (n < 1 || n > kMaxN || d < 1 || d > kMaxD || !known_dtype(dtype)) return -1;
+  if (check_mode(mode) != MEC_OK) return -1;
+  if (is_lit(mode)) sides &= kSideX;
+  if (sides < 1 || sides > (kSideX | kSideY)) return -1;
+  return scratch_layout(n, d, dtype, sides).total;
+}
+
+int mec_backward_plan(int64_t n, int64_t d, int dtype, int mode, int sides, int cus, mec_backward_plan_t* plan) {
+  g_err.clear();
+  if (n < 1 || d < 1 || d > kMaxD) return fail(MEC_ERR_INVALID, "n or d out of range");
+  if (n > kMaxN) return fail(MEC_ERR_UNSUPPORTED, "n=%lld exceeds the supported maximum 2^22", (long long)n);
+  if (!known_dtype(dtype)) return fail(MEC_ERR_INVALID, "unknown dtype %d", dtype);
+  int rc = check_mode(mode);
+  if (rc) return rc;
+  if (is_lit(mode)) sides &= kSideX;
+  if (sides < 1 || sides > (kSideX | kSideY)) return fail(MEC_ERR_INVALID, "sides must name the x or y side");
+  if (!plan) return fail(MEC_ERR_INVALID, "plan must be non-null");
+  if (cus <= 0) {
+    rc = compute_units(&cus);
+    if (rc) return rc;
+  }
+  const ScratchLayout L = scratch_layout(n, d, dtype, sides);
+  plan->block_rows = L.bs;
+  plan->num_blocks = L.nb;
+  plan->scratch_bytes = L.total;
+  // the tiles of a launch with contractions (16-byte rows assumed)
+  const int gdt = is_split(dtype) ? MEC_DTYPE_BF16 : dtype;
+  const bool small = gdt == MEC_DTYPE_F32 && f32_small_tiles(n);
+  bool w384 = false;
+  const BlockGrid bg = block_grid(d, gdt, sides, L.bs, L.nb, L.ldt, cus, fwd_tile_dims(gdt, true, small),
+                                  con_tile_dims(gdt, small), &w384);
+  plan->contract_tile_rows = con_tile_dims(gdt, small).bm;
+  plan->contract_tile_features = w384 ? 384 : con_tile_dims(gdt, small).bn;
+  plan->narrow_tiles = bg.cnw;
+  bool ok = false;
+  const ScratchLayout Ln = noalloc_layout(n, d, dtype, sides, &ok);
+  plan->noalloc_block_rows = ok ? Ln.bs : -1;
+  plan->noalloc_scratch_bytes = ok ? Ln.total : -1;
+  return MEC_OK;
 }
 
 int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
@@ -448,6 +580,8 @@ int mec_prepass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
   if (!workspace) return fail(MEC_ERR_INVALID, "workspace must be non-null");
   if (is_split(dtype) && !aligned16(workspace))
     return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for the bf16-product modes");
+  rc = check_not_capturing(stream);
+  if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
   const int N = (int)n, D = (int)d;
   dim3 grid((unsigned)((n + 3) / 4));
@@ -487,14 +621,16 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   if (!rc) rc = check_temperature(temperature);
   if (rc) return rc;
   if (!workspace) return fail(MEC_ERR_INVALID, "workspace must be non-null");
+  if (is_split(dtype) && !aligned16(workspace))
+    return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for the bf16-product modes");
+  rc = check_not_capturing(stream);
+  if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
   const float c = (float)(1.4426950408889634 / (double)temperature);
   // split modes: the bf16 sums over the copies (K = terms * dp) that mec_prepass
   // wrote, already normalized when normalize is set
   GemmOperands g{x, ldx, y, ldy, d, dtype};
   if (is_split(dtype)) {
-    if (!aligned16(workspace))
-      return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for the bf16-product modes");
     g = split_operands(workspace, n, d, dtype);
     normalize = 0;
   }
@@ -556,6 +692,8 @@ int mec_finalize(int64_t n, int mode, float temperature, float* workspace, float
   if (rc) return rc;
   if (!workspace || !loss) return fail(MEC_ERR_INVALID, "workspace and loss must be non-null");
   if (reinterpret_cast<uintptr_t>(workspace) & 7u) return fail(MEC_ERR_INVALID, "workspace must be 8-byte aligned");
+  rc = check_not_capturing(stream);
+  if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
   const double inv_t = 1.0 / (double)temperature;
   const int nparts = (int)((n + FIN_ROWS - 1) / FIN_ROWS);
@@ -611,7 +749,12 @@ struct StepArgs {
   const float* workspace;
   float* acc_x;  // null: side skipped (LiT: acc_y always null)
   float* acc_y;
+  int sides() const { return (acc_x ? kSideX : 0) | (acc_y ? kSideY : 0); }
 };
+
+// fp32 reads its raw input rows as the contractions' feature operand, with
+// 32-bit offsets within a 32-row chunk: row strides up to 2^24 elements
+constexpr int64_t kMaxLdF32 = int64_t(1) << 24;
 
 // Validation shared by mec_grad_step, mec_grad and mec_backward_noalloc:
 // problem, mode, temperature, workspace and at least one accumulator (LiT
@@ -628,11 +771,14 @@ static int check_step_args(StepArgs& a) {
     return fail(MEC_ERR_INVALID, "no gradient requested (acc_x%s null)", lit ? "" : " and acc_y");
   if (is_split(a.dtype) && !aligned16(a.workspace))
     return fail(MEC_ERR_INVALID, "workspace must be 16-byte aligned for the bf16-product modes");
+  if (a.dtype == MEC_DTYPE_F32 && (a.ldx > kMaxLdF32 || a.ldy > kMaxLdF32))
+    return fail(MEC_ERR_UNSUPPORTED, "row strides ldx=%lld ldy=%lld: the fp32 backward supports up to 2^24",
+                (long long)a.ldx, (long long)a.ldy);
   return MEC_OK;
 }
 
 // Pipeline step `step` of a checked problem on the scratch at `scratch`
-// (16-byte aligned, laid out as L: L.total bytes).
+// (16-byte aligned, laid out as L for the problem's sides: L.total bytes).
 static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L, void* scratch, void* stream) {
   const void *x = a.x, *y = a.y;
   const int64_t ldx = a.ldx, ldy = a.ldy, n = a.n, d = a.d;
@@ -641,11 +787,12 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   const float* workspace = a.workspace;
   float *acc_x = a.acc_x, *acc_y = a.acc_y;
   const bool lit = is_lit(mode);
-  int rc = MEC_OK;
-  int cus = 0;  // compute units, for the persistent gradient-matrix launch
   const int bs = L.bs, nb = L.nb;
   if (step < 0 || step > nb)
     return fail(MEC_ERR_INVALID, "step %lld out of range [0, %d]", (long long)step, nb);
+  int cus = 0;  // compute units: the persistent gradient-matrix launch, the contraction tile choice
+  int rc = compute_units(&cus);
+  if (rc) return rc;
   const int N = (int)n, D = (int)d;
   const float c = (float)(1.4426950408889634 / (double)temperature);
   const bool x3 = is_x3(dtype), split = is_split(dtype);
@@ -653,31 +800,11 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   const GemmOperands go = split ? split_operands(workspace, n, d, dtype) : GemmOperands{x, ldx, y, ldy, d, dtype};
   const bool vec = vec_ok(go.x, go.ldx, go.y, go.ldy, go.d, go.dtype);
   if (split && !vec) return fail(MEC_ERR_UNSUPPORTED, "split operands beyond the direct-load range");
-  const bool cdma = f32_contract_dma(L.ldt, bs);
-  const bool small = dtype == MEC_DTYPE_F32 && vec && cdma && f32_small_tiles(n);
-  const TileDims tf = fwd_tile_dims(dtype, vec, small), tc = con_tile_dims(dtype, small);
-  const bool sep = separate_contractions(dtype);
-  BlockGrid bg{bs, nb, bs / tf.bm, bs / tf.bn, bs / tc.bm, (D + tc.bn - 1) / tc.bn, 0};
+  const bool small = dtype == MEC_DTYPE_F32 && vec && f32_small_tiles(n);
   bool w384 = false;  // 16-bit contractions in 256 x 384 tiles
-  if (sep) {
-    const int64_t sides = (acc_x ? 1 : 0) + (acc_y ? 1 : 0);
-    const int64_t wide = sides * nb * bg.ctm * bg.ctd;
-    int64_t tiles = wide;
-    if (narrow_contract_shape(D, bg.ctm)) {
-      const int64_t narrow = sides * nb * (bg.ctm / 2) * (2 * (D / tc.bn) + 1);
-      if (narrow_contract_use(bs, wide, narrow)) {
-        bg.ctd = D / tc.bn;
-        bg.cnw = 1;
-        tiles = narrow;
-      }
-    }
-    const int ctd384 = (D + 383) / 384;
-    if (wide_contract_use(sides * nb * bg.ctm * ctd384, tiles)) {
-      w384 = true;
-      bg.ctd = ctd384;
-      bg.cnw = 0;
-    }
-  }
+  const BlockGrid bg = block_grid(d, dtype, a.sides(), bs, nb, L.ldt, cus, fwd_tile_dims(dtype, vec, small),
+                                  con_tile_dims(dtype, small), &w384);
+  const bool sep = separate_contractions(dtype);
   // contraction tiles per block and side
   const int ct_blk = bg.cnw ? (bg.ctm / 2) * (2 * bg.ctd + 1) : bg.ctm * bg.ctd;
   StepPlan sp{};
@@ -700,32 +827,31 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   const int64_t grid = sep ? (int64_t)sp.g_pad : (int64_t)sp.g_pad + sp.cx_pad + sp.cy_pad;
   const int64_t grid_c = sep ? (int64_t)sp.cx_pad + sp.cy_pad : 0;
   if (grid > 0x7fffffff || grid_c > 0x7fffffff) return fail(MEC_ERR_UNSUPPORTED, "backward grid too large");
+  // the layout's buffers: plane p of diagonal buffer s at (p nbuf + s) gbuf
   char* base = (char*)scratch;
   GradBufs gb{};
-  if (dtype == MEC_DTYPE_F32) {
-    gb.g[0] = base;
-    gb.g[1] = base + L.gbuf;
-    gb.gt[0] = base + 2 * L.gbuf;
-    gb.gt[1] = base + 3 * L.gbuf;
-  } else {
-    gb.gt[0] = base;
-    gb.gt[1] = base + L.gbuf;
-    if (x3) {
-      gb.gt_lo[0] = base + 2 * L.gbuf;
-      gb.gt_lo[1] = base + 3 * L.gbuf;
+  for (int sb = 0; sb < 2; ++sb) {
+    char* g0 = base + (int64_t)(sb < L.nbuf ? sb : 0) * L.gbuf;
+    if (dtype == MEC_DTYPE_F32) {
+      gb.g[sb] = g0;
+    } else {
+      gb.gt[sb] = g0;
+      if (x3) gb.gt_lo[sb] = g0 + (int64_t)L.nbuf * L.gbuf;
     }
   }
-  char* tb = base + L.ncopies * L.gbuf;
-  gb.xt = tb;
-  gb.yt = tb + L.tbuf;
-  if (x3) {
-    gb.xt_lo = tb + 2 * L.tbuf;
-    gb.yt_lo = tb + 3 * L.tbuf;
+  if (L.xt >= 0) {
+    gb.xt = base + L.xt;
+    if (x3) gb.xt_lo = base + L.xt + L.tbuf;
+  }
+  if (L.yt >= 0) {
+    gb.yt = base + L.yt;
+    if (x3) gb.yt_lo = base + L.yt + L.tbuf;
   }
   gb.ldt = L.ldt;
   hipStream_t s = (hipStream_t)stream;
-  if (step == 0) {
-    // transposed normalised operands of the contractions: YT for the x side, XT for the y side
+  if (step == 0 && dtype != MEC_DTYPE_F32) {
+    // transposed normalised operands of the 16-bit contractions: YT for the
+    // x side, XT for the y side (fp32 reads its raw inputs instead)
     const int64_t n64 = n;
     // one launch for both sides (blockIdx.z): YT when the x side is wanted,
     // XT when the y side is
@@ -739,10 +865,12 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
           k_transpose_split<NORM, LO><<<tgrid, 256, 0, s>>>(acc_x ? ty : tx, tx, N, D, L.ldt)));
     } else {
       DISPATCH_DTYPE(dtype, T, DISPATCH_BOOL(normalize, NORM, {
-        using TS = TransSide<T>;
-        const TS ty{(const T*)y, ldy, workspace + WS_RY * n64, (T*)gb.yt, nullptr};
-        const TS tx{(const T*)x, ldx, workspace + WS_RX * n64, (T*)gb.xt, nullptr};
-        k_transpose<T, NORM><<<tgrid, 256, 0, s>>>(acc_x ? ty : tx, tx, N, D, L.ldt);
+        if constexpr (Is16<T>::value) {
+          using TS = TransSide<T>;
+          const TS ty{(const T*)y, ldy, workspace + WS_RY * n64, (T*)gb.yt, nullptr};
+          const TS tx{(const T*)x, ldx, workspace + WS_RX * n64, (T*)gb.xt, nullptr};
+          k_transpose<T, NORM><<<tgrid, 256, 0, s>>>(acc_x ? ty : tx, tx, N, D, L.ldt);
+        }
       }));
     }
     rc = check_launch("transpose");
@@ -761,11 +889,9 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
       }
       if (!rc && grid > 0) {
         // (the copies are already normalized: no norm scaling in the tiles; chained tiles)
-        rc = compute_units(&cus);
-        if (!rc)
-          DISPATCH_BOOL(lit, LIT,
-              k_grad_g_chain<T, LIT, false, X3><<<(unsigned)(grid < cus ? grid : cus), FwdTile<T, true>::NT, 0, s>>>(
-                  (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g));
+        DISPATCH_BOOL(lit, LIT,
+            k_grad_g_chain<T, LIT, false, X3><<<(unsigned)(grid < cus ? grid : cus), FwdTile<T, true>::NT, 0, s>>>(
+                (const T*)go.x, go.ldx, (const T*)go.y, go.ldy, N, DK, DK, c, workspace, gb, bg, sp_g));
       }
     });
     if (rc) return rc;
@@ -784,26 +910,22 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
         if (vec && !normalize) {
           // direct-to-LDS tiles: persistent workgroups, one per CU, chained tiles
           // (the normalising epilogue would spill registers in the tile loop)
-          rc = compute_units(&cus);
-          if (!rc)
-            DISPATCH_BOOL(lit, LIT,
-                k_grad_g_chain<T, LIT, false><<<(unsigned)(grid < cus ? grid : cus), FwdTile<T, true>::NT, 0, s>>>(
-                    (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp_g));
+          DISPATCH_BOOL(lit, LIT,
+              k_grad_g_chain<T, LIT, false><<<(unsigned)(grid < cus ? grid : cus), FwdTile<T, true>::NT, 0, s>>>(
+                  (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp_g));
         } else {
           DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
-              k_grad_step<T, LIT, NORM, VEC, true><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
+              k_grad_step<T, LIT, NORM, VEC><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
                   (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp_g, acc_x, acc_y))));
         }
       } else if (small) {
-        if constexpr (std::is_same<T, float>::value)
-          DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM,
-              k_grad_step<T, LIT, NORM, true, true, false, true><<<(unsigned)grid, GemmTile<T, true, true>::NT, 0,
-                                                                   s>>>(
-                  (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y)));
+        DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM,
+            k_grad_step<T, LIT, NORM, true, false, true><<<(unsigned)grid, GemmTile<T, true, true>::NT, 0, s>>>(
+                (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y)));
       } else {
-        DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC, DISPATCH_BOOL(cdma, CDMA,
-            k_grad_step<T, LIT, NORM, VEC, CDMA><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
-                (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y)))));
+        DISPATCH_BOOL(lit, LIT, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(vec, VEC,
+            k_grad_step<T, LIT, NORM, VEC><<<(unsigned)grid, FwdTile<T, VEC>::NT, 0, s>>>(
+                (const T*)x, ldx, (const T*)y, ldy, N, D, D, c, workspace, gb, bg, sp, acc_x, acc_y))));
       }
     }
   });
@@ -811,11 +933,11 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   return check_launch("grad_step");
 }
 
-// the caller's scratch against the default layout
+// the caller's scratch against the default layout for the problem's sides
 static int check_scratch(const StepArgs& a, void* scratch, int64_t scratch_bytes, ScratchLayout* L) {
   if (!scratch) return fail(MEC_ERR_INVALID, "scratch must be non-null");
   if (!aligned16(scratch)) return fail(MEC_ERR_INVALID, "scratch must be 16-byte aligned");
-  *L = scratch_layout(a.n, a.d, a.dtype);
+  *L = scratch_layout(a.n, a.d, a.dtype, a.sides());
   if (scratch_bytes < L->total)
     return fail(MEC_ERR_INVALID, "scratch holds %lld bytes, %lld needed", (long long)scratch_bytes,
                 (long long)L->total);
@@ -830,6 +952,9 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
   int rc = check_step_args(a);
   ScratchLayout L;
   if (!rc) rc = check_scratch(a, scratch, scratch_bytes, &L);
+  if (!rc && (step < 0 || step > L.nb))
+    rc = fail(MEC_ERR_INVALID, "step %lld out of range [0, %d]", (long long)step, L.nb);
+  if (!rc) rc = check_not_capturing(stream);
   if (rc) return rc;
   return grad_step_run(a, step, L, scratch, stream);
 }
@@ -842,6 +967,7 @@ int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, 
   int rc = check_step_args(a);
   ScratchLayout L;
   if (!rc) rc = check_scratch(a, scratch, scratch_bytes, &L);
+  if (!rc) rc = check_not_capturing(stream);
   if (rc) return rc;
   for (int t = 0; t <= L.nb; ++t) {
     rc = grad_step_run(a, t, L, scratch, stream);
@@ -861,19 +987,15 @@ int mec_backward_noalloc(const void* x, int64_t ldx, const void* y, int64_t ldy,
   if (is_lit(mode)) dy = nullptr;
   if ((a.acc_x == nullptr) != (dx == nullptr) || (a.acc_y == nullptr) != (dy == nullptr))
     return fail(MEC_ERR_INVALID, "each side needs both its accumulator and its output (or neither)");
-  // the default blocking when it fits the array, else shorter blocks (not
-  // below 1024 rows) within what the transposed inputs leave of it
-  const int64_t trans = trans_bytes(n, d, dtype);
-  int64_t gbudget = kNoAllocScratch - trans;
-  if (gbudget > default_gbudget(n)) gbudget = default_gbudget(n);
-  int bs = 0, nb = 0;
-  if (gbudget > 0) grad_blocks_budget(n, d, dtype, gbudget, &bs, &nb);
-  const ScratchLayout L = scratch_layout_blocks(n, d, dtype, bs, nb);
-  if (gbudget <= 0 || L.total > kNoAllocScratch)
+  bool ok = false;
+  const ScratchLayout L = noalloc_layout(n, d, dtype, a.sides(), &ok);
+  if (!ok)
     return fail(MEC_ERR_UNSUPPORTED,
-                "the backward of n=%lld d=%lld needs %lld bytes of scratch; mec_backward_noalloc holds %lld "
+                "the backward of n=%lld d=%lld needs more than the %lld bytes mec_backward_noalloc holds "
                 "(use mec_backward with caller scratch)",
-                (long long)n, (long long)d, (long long)(gbudget > 0 ? L.total : trans), (long long)kNoAllocScratch);
+                (long long)n, (long long)d, (long long)kNoAllocScratch);
+  rc = check_not_capturing(stream);
+  if (rc) return rc;
   void* buf = nullptr;
   rc = noalloc_scratch(&buf);
   if (rc) return rc;
@@ -899,6 +1021,8 @@ int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   if ((acc_x == nullptr) != (dx == nullptr) || (acc_y == nullptr) != (dy == nullptr))
     return fail(MEC_ERR_INVALID, "each side needs both its accumulator and its output (or neither)");
   if (!acc_x && !acc_y) return fail(MEC_ERR_INVALID, "no gradient requested");
+  rc = check_not_capturing(stream);
+  if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
   const int N = (int)n, D = (int)d;
   const int64_t n64 = n;
@@ -909,11 +1033,15 @@ int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   // one launch for both sides (blockIdx.y)
   const unsigned nsides = (acc_x ? 1u : 0u) + (acc_y ? 1u : 0u);
   dim3 grid((unsigned)((n + 3) / 4), nsides);
-  DISPATCH_DTYPE(data_dtype(dtype), T, DISPATCH_BOOL(normalize, NORM, {
+  // fp32 (not the split modes): the accumulators carry the row's inverse norm
+  // (the contractions of H = diag(rx) G' diag(ry) with the raw inputs)
+  const bool accr = dtype == MEC_DTYPE_F32;
+  DISPATCH_DTYPE(data_dtype(dtype), T, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(accr, ACCR, {
     const PostSide<T> px{(const T*)x, ldx, (const T*)y, ldy, rx, ry, acc_x, (T*)dx};
     const PostSide<T> py{(const T*)y, ldy, (const T*)x, ldx, ry, rx, acc_y, (T*)dy};
-    k_postpass<T, NORM><<<grid, 256, 0, s>>>(acc_x ? px : py, py, N, D, kap, a, grad_output);
-  }));
+    if constexpr (!ACCR || std::is_same<T, float>::value)
+      k_postpass<T, NORM, ACCR><<<grid, 256, 0, s>>>(acc_x ? px : py, py, N, D, kap, a, grad_output);
+  })));
   return check_launch("postpass");
 }
 

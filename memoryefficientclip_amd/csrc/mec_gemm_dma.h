@@ -48,6 +48,20 @@
 // 4 consecutive m of k-row k0 + j / 4, and result lane i receives k-rows
 // k0 .. k0 + 3 of column m0 + i.  With the swizzle, the 32 lanes of a pass
 // (4 k-rows x 32 m x 2 bytes) cover all 64 banks once.
+//
+// Transposed fp32 operands (TA for A, TB for B; the backward's contractions:
+// the gradient-matrix block read across its rows, and the raw input rows as
+// the feature operand): the stage region is [BK k-rows][E] floats (E = BM or
+// BN, 256 or 512 bytes per k-row); the 16-byte slot of m-vector v in k-row r
+// sits at v ^ 8 ((r >> 4) & 1), so that the two lane halves of an MFMA
+// fragment read (k-rows 16 apart, 32 consecutive m each) land on different
+// banks.  A fragment (4 consecutive k at one m per lane, k = 16 h + 4 s + t
+// as for K-major operands) takes four ds_read_b32.  TB = 1 fills the stage
+// with 16-byte lanes (16-byte aligned rows, ld and the valid columns
+// multiples of 4); TB = 2 with 4-byte lanes (any layout), four loads per
+// 1 KB block.  The feature operand's buffer descriptor is rebased at every
+// chunk (64-bit base arithmetic), so its panel may span any number of rows;
+// per-lane offsets stay within a chunk (31 rows of pitch ld: ld < 2^24).
 #pragma once
 #include "mec_common.h"
 
@@ -74,7 +88,7 @@ __host__ __device__ constexpr int64_t gb_offset(int j, int i, int bs) {
 }
 
 template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16, int SA_ = 2,
-          bool GB_ = false>
+          bool GB_ = false, int TB_ = 0>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_;
   static constexpr int KIND = KIND_;
@@ -94,8 +108,17 @@ struct Geo {
   static __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
   static constexpr int MPB = KIND == K_F32 ? 4 : 1;    // MFMAs per block and k-step
   static constexpr bool TA = TA_;                      // A stored k-row-major
-  static_assert(!TA || ((BM == 256 || BM == 512) && ESZ == 2), "transposed A: 16-bit, 512- or 1024-byte k-rows");
-  static constexpr int TKPB = TA ? 512 / BM : 1;       // transposed A: k-rows per 1 KB load block
+  static_assert(!TA || (ESZ == 2 ? (BM == 256 || BM == 512) : (BM == 64 || BM == 128)),
+                "transposed A: 16-bit with 512- or 1024-byte k-rows, fp32 with 256- or 512-byte k-rows");
+  static constexpr int TKPB = TA ? 1024 / (BM * ESZ) : 1;  // transposed A: k-rows per 1 KB load block
+  // B stored k-row-major (fp32): 0 no, 1 with 16-byte lanes, 2 with 4-byte lanes
+  static constexpr int TB = TB_;
+  static_assert(TB == 0 || (KIND == K_F32 && (BN == 64 || BN == 128)), "transposed B: fp32, 256- or 512-byte k-rows");
+  static constexpr int TKPB_B = TB ? 1024 / (BN * ESZ) : 1;  // transposed B: k-rows per 1 KB block
+  static constexpr int BW = TB == 2 ? 4 : 1;                  // loads per 1 KB block of B
+  // fp32 transposed operands: slot XOR of k-row r (the two lane halves of a
+  // fragment read k-rows 16 apart)
+  static __host__ __device__ constexpr int swt32(int r) { return 8 * ((r >> 4) & 1); }
   // A in the blocked gradient-matrix layout (gb_offset; bs = ld): TA, the x
   // side's operand (m = i, k = j: a chunk is 2 x BM/16 blocks), else the y
   // side's (m = j, k = i: BM/32 x 4 blocks).  Stage block b holds block
@@ -141,9 +164,10 @@ struct Geo {
   static __device__ __forceinline__ char* b_stage(char* lds, int s) {
     return SA == 2 ? lds + s * STAGE + A_STAGE : lds + (SA == 3 ? 3 : 2) * A_STAGE + s * B_STAGE;
   }
-  static constexpr int IPW = ROWS / RPB / NW;          // load instructions per wave per chunk
+  static constexpr int A_BLK = BM / RPB, B_BLK = BN / RPB;  // 1 KB blocks of A / B per stage
+  static constexpr int IPW = A_BLK / NW + B_BLK / NW * BW;  // load instructions per wave per chunk
   static constexpr int NMF = FM * FN * MPB;            // MFMAs per k-step
-  static_assert(ROWS % (RPB * NW) == 0 && BM % RPB == 0, "load split");
+  static_assert(A_BLK % NW == 0 && B_BLK % NW == 0 && BM % RPB == 0, "load split");
   static_assert((NW * RPB) % 16 == 0, "the loads of one wave share the row swizzle");
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave sub-tile of 32x32 blocks");
 };
@@ -162,11 +186,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& op) {
   const int64_t elems = op.rows > 0 ? (int64_t)(op.rows - 1) * op.ld + op.kmax : 0;
   return __builtin_amdgcn_make_buffer_rsrc((void*)op.base, 0, (int)(elems * ESZ), 0x00020000);
 }
-// transposed A (16-bit): k-rows [0, kmax) of BM elements
-template <int BM>
+// transposed B: the descriptor of the chunk of BK k-rows starting at k-row
+// k0 of the panel at base (pitch ld elements): its valid rows (below kmax),
+// the last one up to ncols columns
+template <int ESZ, int BK>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_chunk(const char* base, int64_t ld, int kmax, int ncols,
+                                                                  int k0) {
+  const int rows = kmax - k0;
+  const int r = rows < BK ? rows : BK;
+  const int64_t bytes = r > 0 ? ((int64_t)(r - 1) * ld + ncols) * ESZ : 0;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)k0 * ld * ESZ), 0, (int)bytes, 0x00020000);
+}
+// transposed A: k-rows [0, kmax) of BM elements
+template <int BM, int ESZ>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_t(const Operand& op) {
   const int64_t elems = op.kmax > 0 ? (int64_t)(op.kmax - 1) * op.ld + BM : 0;
-  return __builtin_amdgcn_make_buffer_rsrc((void*)op.base, 0, (int)(elems * 2), 0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)op.base, 0, (int)(elems * ESZ), 0x00020000);
 }
 
 // This wave's IPW loads of every chunk: per-lane byte offset at k = 0, the
@@ -176,16 +211,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_t(const Operand& op)
 // compile time.
 template <class G>
 struct LoadPlan {
-  static constexpr int A_BLOCKS = G::BM / G::RPB;  // 1 KB blocks of A per stage (transposed A too)
-  static_assert(A_BLOCKS % G::NW == 0, "every wave loads whole rows of A blocks");
+  static constexpr int A_BLOCKS = G::A_BLK;  // 1 KB blocks of A per stage (transposed A too)
   static constexpr int A_LOADS = A_BLOCKS / G::NW;
+  // lanes per k-row of a 1 KB block of transposed A / B (16-byte lanes)
+  static constexpr int LPK_A = 64 / G::TKPB, LPK_B = 64 / G::TKPB_B;
+  static constexpr int KRB_B = G::BN * G::ESZ;  // transposed B: bytes per k-row
   __amdgpu_buffer_rsrc_t ra, rb;
   uint32_t voff[G::IPW];
   int kv;          // k of this lane's 16-byte vector within a chunk (K-major operands)
-  int kr;          // k-row of this lane within a 1 KB block (transposed A: 0 or 1)
+  int kr;          // this lane's half of the wave (lane / 32; blocked A)
+  int kt;          // transposed A: k-row of this lane within a 1 KB block
+  int kb;          // transposed B: this lane's k-row within the chunk for load A_LOADS (wide lanes)
   int w;           // wave index (uniform)
   int kmax_a, kmax_b;
   int64_t lda;     // transposed A: bytes per k-row
+  // transposed B: the panel (element (n, k) at b_base[k * ldb + n]) and its valid columns
+  const char* b_base;
+  int64_t ldb;
+  int ncols_b;
   static __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_a(const Operand& A) {
     if constexpr (G::GB) {
       // the tile's blocks: TA, i-blocks [0, BM/16) of the j-block rows up to
@@ -194,16 +237,20 @@ struct LoadPlan {
       const int64_t elems = G::TA ? (rows32 > 0 ? (rows32 - 1) * 32 * A.ld + G::BM * 32 : 0) : (int64_t)G::BM * A.ld;
       return __builtin_amdgcn_make_buffer_rsrc((void*)A.base, 0, (int)(elems * 2), 0x00020000);
     } else {
-      return G::TA ? make_rsrc_t<G::BM>(A) : make_rsrc<G::ESZ>(A);
+      return G::TA ? make_rsrc_t<G::BM, G::ESZ>(A) : make_rsrc<G::ESZ>(A);
     }
   }
   static __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_b(const Operand& B) { return make_rsrc<G::ESZ>(B); }
+  // transposed B, load q = I - A_LOADS: its k-row within the chunk, minus kb
+  // (a compile-time function of q; for wide lanes kb carries the lane's part)
+  static constexpr int tb_krow_off(int q) {
+    return G::BW == 1 ? G::TKPB_B * G::NW * q : G::TKPB_B * G::NW * (q / G::BW) + ((q % G::BW) * 256) / KRB_B;
+  }
   __device__ __forceinline__ void init(const Operand& A, const Operand& B) {
     ra = rsrc_a(A);
-    rb = rsrc_b(B);
     kmax_a = A.kmax;
     kmax_b = B.kmax;
-    lda = A.ld * 2;
+    lda = A.ld * G::ESZ;
     const int lane = threadIdx.x & 63;
     w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rib = lane / G::SLOTS, phys = lane % G::SLOTS;
@@ -211,6 +258,16 @@ struct LoadPlan {
     // whose swizzle does not depend on i
     kv = (phys ^ G::swz(w * G::RPB + rib)) * G::EPV;
     kr = lane >> 5;
+    kt = lane / LPK_A;
+    if constexpr (G::TB) {
+      b_base = (const char*)B.base;
+      ldb = B.ld;
+      ncols_b = B.rows < G::BN ? B.rows : G::BN;
+      kb = G::TKPB_B * w + (G::BW == 1 ? lane / LPK_B : 0);
+      rb = ra;  // (per chunk: rsrc_b_chunk)
+    } else {
+      rb = rsrc_b(B);
+    }
 #pragma unroll
     for (int i = 0; i < G::IPW; ++i) {
       const int b = i * G::NW + w;
@@ -220,11 +277,26 @@ struct LoadPlan {
         G::gb_block(b, jb, ib);
         voff[i] = (uint32_t)(((int64_t)jb * 32 * A.ld + ib * 512 + lane * 8) * 2);
       } else if (G::TA && i < A_LOADS) {
-        // BM = 256: block b holds k-rows 2b, 2b+1 (within the chunk), lane l fills slot l % 32 of k-row
-        // 2b + l / 32; BM = 512: block b is k-row b, lane l fills its slot l
-        const int krow = G::TKPB * b + (G::TKPB == 2 ? kr : 0);
-        const int slot = (G::TKPB == 2 ? (lane & 31) : lane) ^ (4 * (krow & 3));
-        voff[i] = (uint32_t)((int64_t)krow * A.ld + slot * 8) * 2;
+        // block b holds k-rows TKPB b .. + TKPB - 1 (within the chunk); lane l
+        // fills slot l % LPK_A of k-row TKPB b + l / LPK_A
+        const int krow = G::TKPB * b + kt;
+        const int sw = G::ESZ == 2 ? 4 * (krow & 3) : G::swt32(krow);
+        const int slot = (lane % LPK_A) ^ sw;
+        voff[i] = (uint32_t)(((int64_t)krow * A.ld + slot * G::EPV) * G::ESZ);
+      } else if (G::TB && i >= A_LOADS) {
+        // transposed B (offsets from the chunk's first k-row)
+        const int q = i - A_LOADS;
+        int krow, pos;  // k-row in the chunk, float within it
+        if (G::BW == 1) {
+          krow = G::TKPB_B * (q * G::NW + w) + lane / LPK_B;
+          pos = (lane % LPK_B) * 4;
+        } else {
+          const int byte = (q % G::BW) * 256 + 4 * lane;
+          krow = G::TKPB_B * ((q / G::BW) * G::NW + w) + byte / KRB_B;
+          pos = (byte % KRB_B) / 4;
+        }
+        const int lslot = (pos >> 2) ^ G::swt32(krow);
+        voff[i] = (uint32_t)(((int64_t)krow * ldb + lslot * 4 + (pos & 3)) * G::ESZ);
       } else {
         const int r = b * G::RPB + rib;
         voff[i] = (uint32_t)(((i < A_LOADS ? (int64_t)r * A.ld : (int64_t)(r - G::BM) * B.ld) + kv) * G::ESZ);
@@ -237,6 +309,20 @@ struct LoadPlan {
   template <int I>
   __device__ __forceinline__ void issue(int k0, char* ad, char* bd) const {
     constexpr bool isa = I < A_LOADS;
+    if constexpr (G::TB && !isa) {
+      // transposed B: 16- or 4-byte lanes into block (q / BW) * NW + w, part q % BW
+      constexpr int q = I - A_LOADS;
+      constexpr int koff = tb_krow_off(q);
+      const uint32_t off = (kb + koff < kmax_b - k0) ? voff[I] : OOB;
+      char* dst = bd + ((q / G::BW) * G::NW + w) * 1024 + (q % G::BW) * 256;
+      const __amdgpu_buffer_rsrc_t rc = make_rsrc_chunk<G::ESZ, G::BK>(b_base, ldb, kmax_b, ncols_b, k0);
+      // (the size operand must be a literal)
+      if constexpr (G::BW == 1)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)dst, 4, off, 0, 0, 0);
+      return;
+    }
     uint32_t off, soff;
     if (G::GB && isa) {
       int jb, ib;
@@ -253,7 +339,7 @@ struct LoadPlan {
         soff = (uint32_t)k0 * 64;
       }
     } else if (G::TA && isa) {
-      off = (k0 + G::TKPB * (I * G::NW + w) + (G::TKPB == 2 ? kr : 0) < kmax_a) ? voff[I] : OOB;
+      off = (k0 + G::TKPB * (I * G::NW + w) + kt < kmax_a) ? voff[I] : OOB;
       soff = (uint32_t)(k0 * lda);
     } else {
       off = (k0 + kv < (isa ? kmax_a : kmax_b)) ? voff[I] : OOB;
@@ -298,6 +384,13 @@ __device__ __forceinline__ i16x8 lds_read_b128(uint32_t addr) {
   static_assert(OFF >= 0 && OFF < 65536 && OFF % 16 == 0, "ds_read_b128 offset");
   i16x8 v;
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+  return v;
+}
+template <int OFF>
+__device__ __forceinline__ float lds_read_b32(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536 && OFF % 4 == 0, "ds_read_b32 offset");
+  float v;
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
   return v;
 }
 // 4 k-rows of one column per lane (see the transposed-A note above)
@@ -354,68 +447,102 @@ __device__ __forceinline__ const char* b_ptr(const char* bstage, int s) {
   return bstage + (wn * G::TN + q) * G::ROWB + ((G::kvec(s, h) ^ G::swz(q)) << 4);
 }
 
-template <class G>
-__device__ __forceinline__ void read_frags(const char* stage, const char* bstage, int s, Frags<G>& f) {
-  if constexpr (G::TA) {
-    // fragment of 32 m x 16 k: the low and the high four k-values of each lane
-#pragma unroll
-    for (int i = 0; i < G::FM; ++i) {
-      const i16x4_t lo = read_tr4(ta_ptr<G>(stage, s, i, 0));
-      const i16x4_t hi = read_tr4(ta_ptr<G>(stage, s, i, 1));
-      f.a[i] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
-  } else {
-    const uint32_t abase = lds_off(a_ptr<G>(stage, s));
-    static_for<G::FM>([&](auto i) { f.a[i] = lds_read_b128<i * 32 * G::ROWB>(abase); });
-  }
-  const uint32_t bbase = lds_off(b_ptr<G>(bstage, s));
-  static_for<G::FN>([&](auto j) { f.b[j] = lds_read_b128<j * 32 * G::ROWB>(bbase); });
+// fp32 transposed operand (stage region of E floats per k-row): this lane's
+// address of fragment i (32 m from m0 + 32 i), k-step s, k-value t = 0 (t
+// adds t * E * 4 bytes): m = m0 + 32 i + lane % 32, k-row 16 h + 4 s + t
+template <int E>
+__device__ __forceinline__ uint32_t t32_addr(const char* region, int m0, int i, int s) {
+  const int lane = threadIdx.x & 63, q = lane & 31, h = lane >> 5;
+  const int m = m0 + 32 * i + q;
+  const int krow = 16 * h + 4 * s;
+  return lds_off(region) + krow * (E * 4) + (((m >> 2) ^ (8 * h)) << 4) + (m & 3) * 4;
 }
 
-// LDS reads per read_frags call
+// LDS reads per fragment set: A, B, and both
+template <class G>
+constexpr int frag_reads_a() {
+  return G::TA ? (G::ESZ == 4 ? 4 : 2) * G::FM : G::FM;
+}
+template <class G>
+constexpr int frag_reads_b() {
+  return G::TB ? 4 * G::FN : G::FN;
+}
 template <class G>
 constexpr int frag_reads() {
-  return (G::TA ? 2 * G::FM : G::FM) + G::FN;
+  return frag_reads_a<G>() + frag_reads_b<G>();
 }
 
-// read_frags one read at a time: read R (of frag_reads) of a k-step's
-// fragments.  Transposed A takes two reads per fragment (its low and high
-// four k-values), written into the halves of f.a[i].
+// One k-step's fragment reads, one read at a time: read R (of frag_reads) of
+// k-step s.  16-bit transposed A takes two reads per fragment (its low and
+// high four k-values), written into the halves of f.a[i]; fp32 transposed
+// operands four (one k-value each).
 template <class G>
 struct FragReader {
+  static constexpr bool TA32 = G::TA && G::ESZ == 4, TA16 = G::TA && G::ESZ == 2;
   uint32_t abase, bbase;
-  uint32_t ta[G::TA ? G::FM : 1][2];  // transposed A: per fragment and half
+  uint32_t ta[TA16 ? G::FM : 1][2];  // 16-bit transposed A: per fragment and half
+  uint32_t a32[TA32 ? G::FM : 1];     // fp32 transposed A: per fragment
+  uint32_t b32[G::TB ? G::FN : 1];    // fp32 transposed B: per fragment
   __device__ __forceinline__ FragReader(const char* stage, const char* bstage, int s) {
-    bbase = lds_off(b_ptr<G>(bstage, s));
-    if constexpr (G::TA) {
+    const int w = threadIdx.x >> 6, wm = w / G::WN, wn = w % G::WN;
+    if constexpr (G::TB) {
+      bbase = 0;
+#pragma unroll
+      for (int j = 0; j < G::FN; ++j) b32[j] = t32_addr<G::BN>(bstage, wn * G::TN, j, s);
+    } else {
+      bbase = lds_off(b_ptr<G>(bstage, s));
+    }
+    if constexpr (TA16) {
       abase = 0;
 #pragma unroll
       for (int i = 0; i < G::FM; ++i)
 #pragma unroll
         for (int half = 0; half < 2; ++half) ta[i][half] = lds_off(ta_ptr<G>(stage, s, i, half));
+    } else if constexpr (TA32) {
+      abase = 0;
+#pragma unroll
+      for (int i = 0; i < G::FM; ++i) a32[i] = t32_addr<G::BM>(stage, wm * G::TM, i, s);
     } else {
       abase = lds_off(a_ptr<G>(stage, s));
     }
   }
   template <int R>
   __device__ __forceinline__ void read(Frags<G>& f) const {
-    constexpr int NA = G::TA ? 2 * G::FM : G::FM;
+    constexpr int NA = frag_reads_a<G>();
     if constexpr (R < NA) {
-      if constexpr (G::TA) {
+      if constexpr (TA16) {
         i16x4_t v;
         asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(ta[R / 2][R % 2]) : "memory");
         if constexpr (R % 2 == 0)
           f.a[R / 2].lo = v;
         else
           f.a[R / 2].hi = v;
+      } else if constexpr (TA32) {
+        f32x4 v = __builtin_bit_cast(f32x4, f.a[R / 4]);
+        v[R % 4] = lds_read_b32<(R % 4) * G::BM * 4>(a32[R / 4]);
+        f.a[R / 4] = __builtin_bit_cast(i16x8, v);
       } else {
         f.a[R] = lds_read_b128<R * 32 * G::ROWB>(abase);
       }
     } else {
-      f.b[R - NA] = lds_read_b128<(R - NA) * 32 * G::ROWB>(bbase);
+      constexpr int RB = R - NA;
+      if constexpr (G::TB) {
+        f32x4 v = __builtin_bit_cast(f32x4, f.b[RB / 4]);
+        v[RB % 4] = lds_read_b32<(RB % 4) * G::BN * 4>(b32[RB / 4]);
+        f.b[RB / 4] = __builtin_bit_cast(i16x8, v);
+      } else {
+        f.b[RB] = lds_read_b128<RB * 32 * G::ROWB>(bbase);
+      }
     }
   }
 };
+
+// every fragment of k-step s
+template <class G>
+__device__ __forceinline__ void read_frags(const char* stage, const char* bstage, int s, Frags<G>& f) {
+  const FragReader<G> rd(stage, bstage, s);
+  static_for<frag_reads<G>()>([&](auto r) { rd.template read<r>(f); });
+}
 
 // at most N LDS operations outstanding (the reads of `f` were issued before
 // the last N), then f's registers are tied to the wait so that no MFMA using
@@ -445,13 +572,38 @@ __device__ __forceinline__ void wait_barrier() {
 }
 
 // MFMAs of one k-step with loads [L0, L1) interleaved, in program order.
+// Loads [L0, L1) spread over the NMF MFMAs of a k-step: LPS loads after
+// every EVERY-th MFMA (one load per slot while there are at most NMF loads)
+// loads [I0, I1) in order
+template <class G, int I0, int I1>
+__device__ __forceinline__ void issue_loads(const LoadPlan<G>& lp, int k0, char* ad, char* bd) {
+  if constexpr (I0 < I1) {
+    lp.template issue<I0>(k0, ad, bd);
+    issue_loads<G, I0 + 1, I1>(lp, k0, ad, bd);
+  }
+}
+template <class G, int L0, int L1>
+struct LoadSlots {
+  static constexpr int NL = L1 - L0;
+  static constexpr int LPS = NL > G::NMF ? (NL + G::NMF - 1) / G::NMF : 1;
+  static constexpr int NSL = (NL + LPS - 1) / LPS;
+  static constexpr int EVERY = NSL > 0 ? G::NMF / NSL : G::NMF + 1;
+  // after MFMA m
+  template <int M>
+  static __device__ __forceinline__ void after(const LoadPlan<G>& lp, int k0, char* ad, char* bd) {
+    if constexpr (NL > 0 && (M % EVERY) == EVERY - 1 && M / EVERY < NSL) {
+      constexpr int I0 = L0 + (M / EVERY) * LPS;
+      constexpr int I1 = I0 + LPS < L1 ? I0 + LPS : L1;
+      sched_fence();
+      issue_loads<G, I0, I1>(lp, k0, ad, bd);
+      sched_fence();
+    }
+  }
+};
+
 template <class G, int L0, int L1>
 __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const LoadPlan<G>& lp,
                                           int k0, char* ad, char* bd) {
-  constexpr int NL = L1 - L0;
-  static_assert(NL <= G::NMF, "at most one load per MFMA");
-  // one load after every EVERY-th MFMA: floor(NMF / EVERY) >= NL slots
-  constexpr int EVERY = NL > 0 ? G::NMF / (NL > 0 ? NL : 1) : G::NMF + 1;
   static_for<G::NMF>([&](auto mc) {
     constexpr int m = mc;
     if constexpr (G::KIND == K_F32) {
@@ -463,11 +615,7 @@ __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM
       acc[m / G::FN][m % G::FN] =
           mfma16_32x32x16<G::F16>(f.a[m / G::FN], f.b[m % G::FN], acc[m / G::FN][m % G::FN]);
     }
-    if constexpr (NL > 0 && (m % EVERY) == EVERY - 1 && L0 + m / EVERY < L1) {
-      sched_fence();
-      lp.template issue<L0 + m / EVERY>(k0, ad, bd);
-      sched_fence();
-    }
+    LoadSlots<G, L0, L1>::template after<m>(lp, k0, ad, bd);
   });
 }
 
@@ -476,10 +624,8 @@ __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM
 template <class G, int L0, int L1>
 __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const LoadPlan<G>& lp,
                                              int k0, char* ad, char* bd, const FragReader<G>& rd, Frags<G>& nf) {
-  constexpr int NL = L1 - L0;
   constexpr int NR = frag_reads<G>();
-  static_assert(NL <= G::NMF && (NR + 1) / 2 <= G::NMF, "slots");
-  constexpr int EVERY = NL > 0 ? G::NMF / (NL > 0 ? NL : 1) : G::NMF + 1;
+  static_assert((NR + 1) / 2 <= G::NMF, "read slots");
   static_for<G::NMF>([&](auto mc) {
     constexpr int m = mc;
     if constexpr (G::KIND == K_F32) {
@@ -497,11 +643,7 @@ __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G:
       if constexpr (2 * m + 1 < NR) rd.template read<2 * m + 1>(nf);
       sched_fence();
     }
-    if constexpr (NL > 0 && (m % EVERY) == EVERY - 1 && L0 + m / EVERY < L1) {
-      sched_fence();
-      lp.template issue<L0 + m / EVERY>(k0, ad, bd);
-      sched_fence();
-    }
+    LoadSlots<G, L0, L1>::template after<m>(lp, k0, ad, bd);
   });
   sched_fence();  // the step's MFMAs stay above the caller's next wait
 }

@@ -50,6 +50,7 @@ struct TileF32 {
   using Elem = float;
   using Op = g32::Operand;
   static constexpr bool TA = false, GB = false;
+  static constexpr int TB = 0;
   static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2, WM = 2, WN = 2, NT = 256;
   static constexpr int LDS_BYTES = g32::LDS_FLOATS * 4;
   static constexpr bool CHAIN = false;
@@ -75,6 +76,7 @@ struct Tile16V : Pack16<F16> {
   using Elem = uint16_t;
   using Op = g16::Operand;
   static constexpr bool TA = false, GB = false;
+  static constexpr int TB = 0;
   static constexpr int BM = 128, BN = 128, TM = 64, TN = 64, FM = 2, FN = 2, WM = 2, WN = 2, NT = 256;
   static constexpr int LDS_BYTES = g16::Cfg<MEC_16BIT_BK>::LDS_ELEMS * 2;
   static constexpr bool CHAIN = false;
@@ -95,15 +97,18 @@ template <> struct PackOf<gdma::K_F32> { using type = PackF32; };
 
 // BM_ x BN_, direct global->LDS loads (16-byte aligned rows, ld and kmax
 // multiples of the elements per 16-byte vector), element kind KIND (bf16,
-// fp16 or fp32); TA_: A stored k-row-major (a transposed 16-bit
-// gradient-matrix block); GB_: A a 16-bit gradient-matrix block in the
-// blocked layout (gdma::gb_offset; TA_ then selects the x side's reading)
-template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND, int SA_ = 2, bool GB_ = false, bool ROLL_ = false>
+// fp16 or fp32); TA_: A stored k-row-major (a transposed gradient-matrix
+// block); GB_: A a 16-bit gradient-matrix block in the blocked layout
+// (gdma::gb_offset; TA_ then selects the x side's reading); TB_: B stored
+// k-row-major (fp32 raw input rows; 1: 16-byte lanes, 2: 4-byte lanes)
+template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND, int SA_ = 2, bool GB_ = false, bool ROLL_ = false,
+          int TB_ = 0>
 struct TileD : PackOf<KIND>::type {
   using Elem = typename std::conditional<KIND == gdma::K_F32, float, uint16_t>::type;
   using Op = gdma::Operand;
-  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, SA_, GB_>;
+  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, SA_, GB_, TB_>;
   static constexpr bool TA = TA_, GB = GB_, ROLL = ROLL_;
+  static constexpr int TB = TB_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
   static constexpr int WM = G::WM, WN = G::WN, NT = G::NT;
   static constexpr int LDS_BYTES = G::LDS_BYTES;
@@ -153,14 +158,16 @@ template <typename T, bool VEC> using FwdTile = typename FwdTileSel<T, VEC>::typ
 template <typename T, bool VEC, bool SMALL> struct GemmTileSel { using type = FwdTile<T, VEC>; };
 template <> struct GemmTileSel<float, true, true> { using type = TileD<64, 64, false, 2, 2, gdma::K_F32>; };
 template <typename T, bool VEC, bool SMALL> using GemmTile = typename GemmTileSel<T, VEC, SMALL>::type;
-// Contractions.  fp32 stores the gradient-matrix blocks in both layouts (G'
-// for the x side, G'^T for the y side) and runs them inside k_grad_step, on
-// the direct-to-LDS core when its 32-bit offsets reach across a transposed
-// input panel (DMA; 128 rows of pitch ~N), else on the register-staged one.
-// The 16-bit types store only G'^T, which the y side reads K-major and the x
-// side reads transposed through LDS, in a kernel of their own
-// (k_grad_contract) with 256 x 256 tiles of 8 waves.
-template <typename T, bool DMA = true, bool IS16 = Is16<T>::value> struct ConTileSel;
+// Contractions.  fp32 stores each gradient-matrix block once, row-major and
+// scaled by both norms (H = diag(rx) G' diag(ry)), and runs the contractions
+// inside k_grad_step on the direct-to-LDS core: the x side reads H K-major,
+// the y side reads it transposed (k = its row index), and both read the raw
+// input rows of the other side as a transposed feature operand (VEC: 16-byte
+// lanes, else 4-byte lanes), so no transposed copies exist.  The 16-bit types
+// store only G'^T, which the y side reads K-major and the x side reads
+// transposed through LDS, in a kernel of their own (k_grad_contract) with
+// 256 x 256 tiles of 8 waves, against transposed normalised input copies.
+template <typename T, bool VEC = true, bool IS16 = Is16<T>::value> struct ConTileSel;
 // (the gradient-matrix operand streams from HBM: three A stages, 160 KB of LDS)
 // nx, ny: the narrow tiles of a last feature column of at most 128 features
 // (D % 256 in [1, 128]): 512 rows x 128 features, the same 128 x 64 per-wave
@@ -170,15 +177,15 @@ template <typename T, bool DMA = true, bool IS16 = Is16<T>::value> struct ConTil
 // 4 waves of 128 x 96: 192 accumulator registers, one fragment set on the
 // rolling operand schedule (gdma::mainloop_roll), the gradient-matrix operand
 // in four half-chunk stages and the other in two (160 KB)
-template <typename T, bool DMA> struct ConTileSel<T, DMA, false> {
-  using x = typename std::conditional<DMA, TileD<128, 128, false, 2, 2, gdma::K_F32>, TileF32>::type;
-  using y = x;
+template <typename T, bool VEC> struct ConTileSel<T, VEC, false> {
+  using x = TileD<128, 128, false, 2, 2, gdma::K_F32, 2, false, false, VEC ? 1 : 2>;
+  using y = TileD<128, 128, true, 2, 2, gdma::K_F32, 2, false, false, VEC ? 1 : 2>;
   using nx = x;  // (no narrow tiles)
   using ny = x;
   using wx = x;
   using wy = x;
 };
-template <typename T, bool DMA> struct ConTileSel<T, DMA, true> {
+template <typename T, bool VEC> struct ConTileSel<T, VEC, true> {
   using x = TileD<256, 256, true, 4, 2, kind16<T>(), 3, true>;
   using y = TileD<256, 256, false, 4, 2, kind16<T>(), 3, true>;
   using nx = TileD<512, 128, true, 4, 2, kind16<T>(), 2, true>;
@@ -186,17 +193,17 @@ template <typename T, bool DMA> struct ConTileSel<T, DMA, true> {
   using wx = TileD<256, 384, true, 2, 4, kind16<T>(), 4, true, true>;
   using wy = TileD<256, 384, false, 2, 4, kind16<T>(), 4, true, true>;
 };
-template <typename T, bool DMA = true> using ConTileX = typename ConTileSel<T, DMA>::x;
-template <typename T, bool DMA = true> using ConTileY = typename ConTileSel<T, DMA>::y;
+template <typename T, bool VEC = true> using ConTileX = typename ConTileSel<T, VEC>::x;
+template <typename T, bool VEC = true> using ConTileY = typename ConTileSel<T, VEC>::y;
 template <typename T> using ConTileNX = typename ConTileSel<T, true>::nx;
 template <typename T> using ConTileNY = typename ConTileSel<T, true>::ny;
-template <typename T, bool DMA, bool SMALL> struct ConTileSmall {
-  using x = ConTileX<T, DMA>;
-  using y = ConTileY<T, DMA>;
+template <typename T, bool VEC, bool SMALL> struct ConTileSmall {
+  using x = ConTileX<T, VEC>;
+  using y = ConTileY<T, VEC>;
 };
-template <> struct ConTileSmall<float, true, true> {
-  using x = TileD<64, 64, false, 2, 2, gdma::K_F32>;
-  using y = x;
+template <bool VEC> struct ConTileSmall<float, VEC, true> {
+  using x = TileD<64, 64, false, 2, 2, gdma::K_F32, 2, false, false, VEC ? 1 : 2>;
+  using y = TileD<64, 64, true, 2, 2, gdma::K_F32, 2, false, false, VEC ? 1 : 2>;
 };
 // the 16-bit types keep one layout of the gradient-matrix blocks (G'^T)
 template <typename T> struct GtOnly { static constexpr bool value = Is16<T>::value; };
@@ -602,13 +609,16 @@ struct StepPlan {
   int cy_n, cy_pad;  // y-side contraction tiles, padded
 };
 
-// G'_ij of this wave's TM x TN accumulators into Gb (and GTb for CLIP), both
-// with row pitch bs.  MASK zeroes the diagonal and entries outside [0, N).
+// fp32 gradient-matrix tile: H_ij = rx_i G'_ij ry_j (G'_ij without the norm
+// scaling, NORM = false) of this wave's TM x TN accumulators, row-major at Gb
+// with row pitch bs (scalar stores, coalesced across lanes).  Stored once:
+// the x side's contraction reads its rows, the y side's reads it transposed,
+// and both multiply it with the raw inputs (the norms are in H).  MASK zeroes
+// the diagonal and entries outside [0, N).
 template <class TL, bool LIT, bool NORM, bool MASK>
 __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN], float c, int i0, int j0, int N,
-                                             typename TL::Elem* __restrict__ Gb, typename TL::Elem* __restrict__ GTb,
-                                             int bs, const float* s_rx, const float* s_ry, const float* s_ir,
-                                             const float* s_ic) {
+                                             float* __restrict__ Gb, int bs, const float* s_rx, const float* s_ry,
+                                             const float* s_ir, const float* s_ic) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
 #pragma unroll
   for (int bm = 0; bm < TL::FM; ++bm) {
@@ -616,27 +626,19 @@ __device__ __forceinline__ void grad_g_store(const f32x16 (&acc)[TL::FM][TL::FN]
     for (int bn = 0; bn < TL::FN; ++bn) {
       const int nl = wn * TL::TN + bn * 32 + (lane & 31);
       const int j = j0 + nl;
-      const float cy = NORM ? c * s_ry[nl] : c;
+      const float ryj = NORM ? s_ry[nl] : 1.f;
+      const float cy = c * ryj;
       const float icj = s_ic[nl];
-      float gv[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int ml = wm * TL::TM + bm * 32 + acc_row(r, lane);
         const int i = i0 + ml;
-        const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
-        const float e = fast_exp2(fmaf(sc, cy, -c));
+        const float rxi = NORM ? s_rx[ml] : 1.f;
+        const float e = fast_exp2(fmaf(acc[bm][bn][r] * rxi, cy, -c));
         float g = LIT ? e * s_ir[ml] : e * (s_ir[ml] + icj);
+        if (NORM) g *= rxi * ryj;
         if (MASK) g = (i < N && j < N && i != j) ? g : 0.f;
-        gv[r] = g;
-        Gb[(int64_t)ml * bs + nl] = TL::pack(g);
-      }
-      if (!LIT) {
-        // registers 4g..4g+3 hold 4 consecutive rows: one vector store per group
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int ml = wm * TL::TM + bm * 32 + acc_row(4 * g, lane);
-          TL::store4(GTb + (int64_t)nl * bs + ml, gv[4 * g], gv[4 * g + 1], gv[4 * g + 2], gv[4 * g + 3]);
-        }
+        Gb[(int64_t)ml * bs + nl] = g;
       }
     }
   }
@@ -728,9 +730,10 @@ __device__ __forceinline__ void grad_gt_store_direct(const f32x16 (&acc)[TL::FM]
 }
 
 // Recompute the similarity tile (i0, j0) and store G'_ij = E_ij (1/R_i + 1/C_j)
-// (LiT: E_ij / R_i) for i != j, 0 on the diagonal and outside [0, N), into
-// the G' block at Gb (row pitch bs) and, for CLIP, transposed at GTb (X3: its
-// bf16 hi plane at GTb and lo plane at GTl).
+// (LiT: E_ij / R_i) for i != j, 0 on the diagonal and outside [0, N): fp32
+// scaled by the norms (H, grad_g_store) into the block at Gb (row pitch bs);
+// the 16-bit types transposed at GTb in the blocked layout (X3: its bf16 hi
+// plane at GTb and lo plane at GTl).
 // Follows clip_loss.py:96-124 / lit_loss.py:94-120.
 template <class TL, typename T, bool LIT, bool NORM, bool VEC, bool X3>
 __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y,
@@ -772,9 +775,9 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
       grad_gt_store_direct<TL, LIT, NORM, true, 1>(acc, c, i0, j0, N, (uint16_t*)GTb, bs, s_rx, s_ry, s_ir, s_ic);
   } else {
     if (!diag && i0 + TL::BM <= N && j0 + TL::BN <= N)
-      grad_g_store<TL, LIT, NORM, false>(acc, c, i0, j0, N, Gb, GTb, bs, s_rx, s_ry, s_ir, s_ic);
+      grad_g_store<TL, LIT, NORM, false>(acc, c, i0, j0, N, (float*)Gb, bs, s_rx, s_ry, s_ir, s_ic);
     else
-      grad_g_store<TL, LIT, NORM, true>(acc, c, i0, j0, N, Gb, GTb, bs, s_rx, s_ry, s_ir, s_ic);
+      grad_g_store<TL, LIT, NORM, true>(acc, c, i0, j0, N, (float*)Gb, bs, s_rx, s_ry, s_ir, s_ic);
   }
 }
 
@@ -783,6 +786,11 @@ __device__ __forceinline__ void grad_g_tile(const T* __restrict__ X, int64_t ldx
 //   x side: acc_x[i, d] (+)= sum_{j in Q} G'(P,Q)[i, j]  * YT[d, j]   (Q = P + s)
 //           (16-bit: G'(P,Q)[i, j] read from the transposed block G'T(P,Q)[j, i])
 //   y side: acc_y[j, d] (+)= sum_{i in Q} G'T(Q,P)[j, i] * XT[d, i]   (Q = P - s)
+// fp32 (TC::TB): the blocks hold H = diag(rx) G' diag(ry) and OT is the raw
+// input of the other side, read by rows (element (k, d) at OT[k * ldt + d]):
+//   x side: acc_x[i, d] (+)= sum_j H(P,Q)[i, j] y[q0 + j, d] = rx_i (G' Y^)[i, d]
+//   y side: acc_y[j, d] (+)= sum_i H(Q,P)[i, j] x[q0 + i, d] = ry_j (G'^T X^)[j, d]
+// (the post-pass takes the row's norm factor out again).
 // Each output tile has one owner per launch: accumulation across launches
 // adds each element once per launch, in launch order (the reference instead
 // lets every (row-tile, column-tile) program add into dX/dY with contending
@@ -806,8 +814,10 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
   // block (blocked layout: i-block tm*BM/16 of the first j-block row)
   const int64_t a_off = TC::TA ? (int64_t)(tm * TC::BM) * (TC::GB ? 32 : 1) : (int64_t)(tm * TC::BM) * bg.bs;
   const auto A = tile_op<TC>(Gblk + a_off, bg.bs, TC::BM, kq);
-  const int64_t b_off = (int64_t)d0 * ldt + q0;
-  const auto B = tile_op<TC>(OT + b_off, ldt, min(D - d0, TC::BN), kq);
+  // the feature operand: transposed copy (rows d, k = q0 + j) or, fp32, the
+  // raw rows q0 + k (only the block's qn valid rows)
+  const int64_t b_off = TC::TB ? (int64_t)q0 * ldt + d0 : (int64_t)d0 * ldt + q0;
+  const auto B = tile_op<TC>(OT + b_off, ldt, min(D - d0, TC::BN), TC::TB ? qn : kq);
   f32x16 acc[TC::FM][TC::FN];
   TC::template run<true, true>(A, B, kq, lds, acc);
   if constexpr (X3) {
@@ -843,10 +853,12 @@ __device__ __forceinline__ void grad_contract_tile(int N, int D, const T* __rest
 
 // Contraction workgroup `sub` (in [0, cx_pad + cy_pad)) of one pipeline step.
 // TNX / TNY: the narrow tiles (bg.cnw).
+// X, Y: the raw inputs (fp32: the feature operands of the contractions).
 template <class TCX, class TCY, class TNX, class TNY, typename T, bool X3 = false>
 __device__ __forceinline__ void grad_contract_dispatch(int sub, int N, int D, const GradBufs& gb, const BlockGrid& bg,
                                                        const StepPlan& sp, float* __restrict__ acc_x,
-                                                       float* __restrict__ acc_y, char* lds) {
+                                                       float* __restrict__ acc_y, char* lds, const T* X = nullptr,
+                                                       int64_t ldx = 0, const T* Y = nullptr, int64_t ldy = 0) {
   const int64_t blk = (int64_t)bg.bs * bg.bs;  // elements per G' block
   const bool is_x = sub < sp.cx_pad;
   if (!is_x) sub -= sp.cx_pad;
@@ -888,16 +900,22 @@ __device__ __forceinline__ void grad_contract_dispatch(int sub, int N, int D, co
     if (narrow)
       grad_contract_tile<TNX, T, X3>(N, D, gx, gxl, (const T*)gb.yt, (const T*)gb.yt_lo, gb.ldt, bg, P, Q, tm, td,
                                      sp.accumulate != 0, acc_x, lds);
+    else if constexpr (TCX::TB)
+      grad_contract_tile<TCX, T, X3>(N, D, gx, gxl, Y, nullptr, ldy, bg, P, Q, tm, td, sp.accumulate != 0, acc_x,
+                                     lds);
     else
       grad_contract_tile<TCX, T, X3>(N, D, gx, gxl, (const T*)gb.yt, (const T*)gb.yt_lo, gb.ldt, bg, P, Q, tm, td,
                                      sp.accumulate != 0, acc_x, lds);
   } else {
     const int Q = (P - sp.diag_c + bg.nb) % bg.nb;
-    const T* gy = (const T*)gb.gt[buf] + Q * blk;
+    const T* gy = (const T*)(GtOnly<T>::value ? gb.gt[buf] : gb.g[buf]) + Q * blk;
     const T* gyl = X3 ? (const T*)gb.gt_lo[buf] + Q * blk : nullptr;
     if (narrow)
       grad_contract_tile<TNY, T, X3>(N, D, gy, gyl, (const T*)gb.xt, (const T*)gb.xt_lo, gb.ldt, bg, P, Q, tm, td,
                                      sp.accumulate != 0, acc_y, lds);
+    else if constexpr (TCY::TB)
+      grad_contract_tile<TCY, T, X3>(N, D, gy, gyl, X, nullptr, ldx, bg, P, Q, tm, td, sp.accumulate != 0, acc_y,
+                                     lds);
     else
       grad_contract_tile<TCY, T, X3>(N, D, gy, gyl, (const T*)gb.xt, (const T*)gb.xt_lo, gb.ldt, bg, P, Q, tm, td,
                                      sp.accumulate != 0, acc_y, lds);
@@ -926,25 +944,27 @@ __global__ __launch_bounds__(ConTileX<T>::NT, 1) void k_grad_contract(int N, int
 }
 
 // One pipeline step: G' tiles of diagonal diag_g and, for fp32, the
-// contractions of diagonal diag_c (the 16-bit types run those in k_grad_contract); CDMA
-// selects the fp32 contraction core.  X3: bf16 split operands (K = 3 dp),
-// G'^T written as hi and lo planes.
-template <typename T, bool LIT, bool NORM, bool VEC, bool CDMA, bool X3 = false, bool SMALL = false>
+// contractions of diagonal diag_c (the 16-bit types run those in
+// k_grad_contract; fp32 with the raw inputs as feature operands, VEC
+// selecting 16-byte or 4-byte load lanes for them).  X3: bf16 split operands
+// (K = 3 dp), G'^T written as hi and lo planes.
+template <typename T, bool LIT, bool NORM, bool VEC, bool X3 = false, bool SMALL = false>
 __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) void k_grad_step(
     const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ldy, int N, int D, int kmax, float c,
     const float* __restrict__ ws, GradBufs gb, BlockGrid bg, StepPlan sp, float* __restrict__ acc_x,
     float* __restrict__ acc_y) {
   using TF = GemmTile<T, VEC, SMALL>;
   constexpr bool FUSED = !GtOnly<T>::value;  // contractions in this kernel
-  using TCX = typename std::conditional<FUSED, typename ConTileSmall<T, CDMA, SMALL>::x, TF>::type;
-  using TCY = typename std::conditional<FUSED, typename ConTileSmall<T, CDMA, SMALL>::y, TF>::type;
+  using TCX = typename std::conditional<FUSED, typename ConTileSmall<T, VEC, SMALL>::x, TF>::type;
+  using TCY = typename std::conditional<FUSED, typename ConTileSmall<T, VEC, SMALL>::y, TF>::type;
   static_assert(TCX::NT == TF::NT && TCY::NT == TF::NT, "one workgroup size per launch");
   __shared__ __attribute__((aligned(1024))) char lds[CMax<TF::LDS_BYTES, CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value>::value];
   __shared__ float s_rx[TF::BM], s_ry[TF::BN], s_ir[TF::BM], s_ic[TF::BN];
   const int64_t blk = (int64_t)bg.bs * bg.bs;  // elements per G' block
   int sub = blockIdx.x;
   if (sub < sp.cx_pad + sp.cy_pad) {
-    if constexpr (FUSED) grad_contract_dispatch<TCX, TCY, TCX, TCY, T>(sub, N, D, gb, bg, sp, acc_x, acc_y, lds);
+    if constexpr (FUSED)
+      grad_contract_dispatch<TCX, TCY, TCX, TCY, T>(sub, N, D, gb, bg, sp, acc_x, acc_y, lds, X, ldx, Y, ldy);
     return;
   }
   sub -= sp.cx_pad + sp.cy_pad;
@@ -961,7 +981,7 @@ __global__ __launch_bounds__((GemmTile<T, VEC, SMALL>::NT), (Occ<T, VEC>::bwd)) 
   // G'^T: row-major (fp32) or the tile's first block in the blocked layout (16-bit)
   const int64_t gt_off = I * blk + (GtOnly<T>::value ? gdma::gb_offset(tn * TF::BN, tm * TF::BM, bg.bs)
                                                      : (int64_t)(tn * TF::BN) * bg.bs + tm * TF::BM);
-  T* GTb = (LIT && !GtOnly<T>::value) ? nullptr : (T*)gb.gt[buf] + gt_off;
+  T* GTb = GtOnly<T>::value ? (T*)gb.gt[buf] + gt_off : nullptr;
   T* GTl = X3 ? (T*)gb.gt_lo[buf] + gt_off : nullptr;
   grad_g_tile<TF, T, LIT, NORM, VEC, X3>(X, ldx, Y, ldy, N, D, kmax, c, ws, Gb, GTb, GTl, bg.bs, i0, j0, lds, s_rx,
                                          s_ry, s_ir, s_ic);

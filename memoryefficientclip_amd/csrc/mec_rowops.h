@@ -170,7 +170,12 @@ struct PostSide {
   const float* acc;
   T* out;
 };
-template <typename T, bool NORM>
+// ACCR (fp32 data on the fp32 kernels): the accumulator row carries the
+// row's own inverse norm, acc = r_i (sum_j G'_ij y^_j), since the
+// contractions multiply H = diag(rx) G' diag(ry) with the raw inputs.  Then
+// h = a (kappa_i r_i y^_i + acc) = r_i dx^_i, and the normalisation backward
+// r_i (dx^ - x^ <x^, dx^>) is h - x^ <x^, h>: no division by the norm.
+template <typename T, bool NORM, bool ACCR = false>
 __global__ __launch_bounds__(256) void k_postpass(PostSide<T> s0, PostSide<T> s1, int N, int D,
                                                   const float* __restrict__ kappa, float a,
                                                   const float* __restrict__ grad_output) {
@@ -191,7 +196,7 @@ __global__ __launch_bounds__(256) void k_postpass(PostSide<T> s0, PostSide<T> s1
   const float* ac = acc + (int64_t)row * D;
   T* o = out + (int64_t)row * D;
   const float ro = r_own[row];
-  const float kq = kappa[row] * r_oth[row];
+  const float kq = kappa[row] * r_oth[row] * (ACCR ? ro : 1.f);
   const float go = grad_output ? *grad_output : 1.f;
   if (NORM) {
     float dot = 0.f;
@@ -214,7 +219,10 @@ __global__ __launch_bounds__(256) void k_postpass(PostSide<T> s0, PostSide<T> s1
 #pragma unroll
       for (int k = 0; k < POST_REG; ++k) {
         const int d = lane + 64 * k;
-        if (d < D) Elem<T>::store(o, d, go * (clamped ? ro * g[k] : ro * (g[k] - xr[k] * dot)));
+        if (d < D) {
+          const float v = ACCR ? (clamped ? g[k] : g[k] - xr[k] * dot) : (clamped ? ro * g[k] : ro * (g[k] - xr[k] * dot));
+          Elem<T>::store(o, d, go * v);
+        }
       }
       return;
     }
@@ -225,7 +233,8 @@ __global__ __launch_bounds__(256) void k_postpass(PostSide<T> s0, PostSide<T> s1
     dot = wave_sum(dot);
     for (int d = lane; d < D; d += 64) {
       float g = a * fmaf(kq, Elem<T>::load(yo, d), ac[d]);
-      float v = clamped ? ro * g : ro * (g - Elem<T>::load(xo, d) * ro * dot);
+      const float xh = Elem<T>::load(xo, d) * ro;
+      float v = ACCR ? (clamped ? g : g - xh * dot) : (clamped ? ro * g : ro * (g - xh * dot));
       Elem<T>::store(o, d, go * v);
     }
   } else {

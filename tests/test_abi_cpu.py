@@ -32,27 +32,51 @@ def test_library_exports_every_declared_symbol():
         assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
 
 
+ELEM = {0: 4, 1: 2, 2: 2, 3: 2, 4: 2}   # scratch element bytes per dtype
+QUANTUM = {0: 128, 1: 256, 2: 256, 3: 256, 4: 256}
+
+
+def layout_bytes(n, d, dt, sides, bs, nb):
+    """Scratch of the backward for blocks (bs, nb): the gradient-matrix
+    diagonal (double-buffered unless one block covers n; bf16x3 hi and lo
+    planes) and, for the 16-bit kernels only, one transposed input per side
+    (bf16x3: two planes); fp32 reads its raw inputs."""
+    elem = ELEM[dt]
+    nbuf = 2 if nb > 1 else 1
+    planes = 2 if dt == 3 else 1
+    ldt = (n + 127) // 128 * 128
+    ntp = 0 if dt == 0 else planes
+    nsides = bin(sides).count("1")
+    return nbuf * planes * nb * bs * bs * elem + nsides * ntp * d * ldt * elem
+
+
+def budget(n, d, dt):
+    """Default bound of the gradient-matrix buffers: 64 n d elements, at
+    least 256 MiB, at most 16 GiB."""
+    return min(16 << 30, max(64 * n * d * ELEM[dt], 256 << 20))
+
+
 def test_sizes():
     lib = _lib.load()
-    # 8 vectors, ceil(n / 1024) fp64 loss partials, 8 vectors of deterministic partial sums
     # 8 vectors, the fp64 loss partials (2 floats per 1024 rows), 48 x n deterministic partials
     assert lib.mec_workspace_floats(1000) == 8000 + 2 + 48000
     assert lib.mec_workspace_floats(1025) == 8 * 1025 + 4 + 48 * 1025
     assert lib.mec_workspace_floats(0) < 0
-    # scratch is O(n*d): two block diagonals of the N x N gradient matrix (fp32:
-    # in both layouts; bf16 and fp16: transposed only), plus transposed copies of
-    # the two inputs; blocks are a multiple of 128 rows (fp32) or 256 rows (the
-    # 16-bit types: their tiles are 128 x 256 and 256 x 256)
     for n, d in [(1024, 512), (32768, 1152), (65536, 768), (262144, 1152), (1000, 3), (777, 1152)]:
-        for dt, elem, q, copies in [(0, 4, 128, 4), (1, 2, 256, 2), (2, 2, 256, 2)]:
-            b = lib.mec_grad_scratch_bytes(n, d, dt)
+        for dt in (0, 1, 2, 3, 4):
             bs, nb = _lib.grad_blocking(n, d, dt)
+            q = QUANTUM[dt]
             assert bs % q == 0 and nb * bs >= n > (nb - 1) * bs, (n, d, dt, bs, nb)
-            ldt = (n + 127) // 128 * 128
-            assert b == (copies * nb * bs * bs + 2 * d * ldt) * elem, (n, d, dt)
-            bs_max = 2 * max(1024, (4 if dt == 0 else 16) * d + q)
-            assert bs <= bs_max and b <= elem * (4 * (n + bs_max) * bs_max + 2 * d * (n + 128)), (n, d, dt, b)
+            assert lib.mec_grad_scratch_bytes(n, d, dt) == layout_bytes(n, d, dt, 3, bs, nb), (n, d, dt)
+            for mode, sides in ((0, 1), (0, 2), (0, 3), (1, 1), (1, 3)):
+                want = layout_bytes(n, d, dt, 1 if mode == 1 else sides, bs, nb)
+                assert lib.mec_grad_scratch_bytes_for(n, d, dt, mode, sides) == want, (n, d, dt, mode, sides)
     assert lib.mec_grad_scratch_bytes(10, 10, 7) < 0
+    # bad mode, no side, LiT without its x side
+    assert lib.mec_grad_scratch_bytes_for(10, 10, 0, 5, 3) < 0
+    assert lib.mec_grad_scratch_bytes_for(10, 10, 0, 0, 0) < 0
+    assert lib.mec_grad_scratch_bytes_for(10, 10, 0, 0, 4) < 0
+    assert lib.mec_grad_scratch_bytes_for(10, 10, 0, 1, 2) < 0
 
 
 def test_bf16_product_mode_sizes():
@@ -69,11 +93,13 @@ def test_bf16_product_mode_sizes():
         dp = (d + 7) // 8 * 8
         assert lib.mec_workspace_floats_for(n, d, x3) == (base + 3) // 4 * 4 + n * 3 * dp
         assert lib.mec_workspace_floats_for(n, d, x1) == (base + 3) // 4 * 4 + n * dp
-        ldt = (n + 127) // 128 * 128
-        for dt, planes in ((x3, 4), (x1, 2)):
-            assert _lib.grad_blocking(n, d, dt) == _lib.grad_blocking(n, d, 1)
+        for dt in (x3, x1):
+            # the same bf16 blocking unless the bf16x3 planes meet the budget first
             bs, nb = _lib.grad_blocking(n, d, dt)
-            assert lib.mec_grad_scratch_bytes(n, d, dt) == (planes * nb * bs * bs + planes * d * ldt) * 2
+            assert bs % 256 == 0 and nb * bs >= n > (nb - 1) * bs
+            if dt == x1:
+                assert (bs, nb) == _lib.grad_blocking(n, d, 1)
+            assert lib.mec_grad_scratch_bytes(n, d, dt) == layout_bytes(n, d, dt, 3, bs, nb)
     assert lib.mec_workspace_floats_for(10, 0, x3) < 0 and lib.mec_workspace_floats_for(10, 10, 7) < 0
     # the split copies need a 16-byte aligned workspace; rejected before any launch
     for dt in (x3, x1):
@@ -81,16 +107,18 @@ def test_bf16_product_mode_sizes():
         assert rc == _lib.MEC_ERR_INVALID and "16-byte" in _lib.last_error()
 
 
-def test_16bit_blocks_fit_the_32bit_operand_range():
+def test_blocks_fit_the_32bit_operand_range():
     # the direct-to-LDS core reads a transposed gradient-matrix block with 32-bit
-    # byte offsets masked at 2^31: (bs - 1) * bs + 256 elements of 2 bytes < 2^31
+    # byte offsets masked at 2^31: (bs - 1) * bs + 256 elements of 2 bytes
+    # (16-bit) or (bs - 1) * bs + 128 floats (fp32, the y side) below 2^31
     for n, d in [(65536, 8192), (65536, 4096), (33000, 4352), (2 ** 22, 1024), (40000, 100000)]:
         for dt in (1, 2):
             bs, nb = _lib.grad_blocking(n, d, dt)
             assert bs <= 32512 and ((bs - 1) * bs + 256) * 2 < 2 ** 31, (n, d, bs)
             assert nb * bs >= n > (nb - 1) * bs
-    # fp32 addresses with 64-bit pointers; its ~4d target (131072 rows here)
-    # gives way to the memory budget of the gradient-matrix buffers (16 GiB)
+        bs, nb = _lib.grad_blocking(n, d, 0)
+        assert bs <= 16384 and ((bs - 1) * bs + 128) * 4 < 2 ** 31, (n, d, bs)
+    # fp32's ~4d target (131072 rows here) gives way to that cap
     assert _lib.grad_blocking(65536, 32768, 0) == (16384, 4)
 
 
@@ -105,8 +133,10 @@ def test_blocking_prefers_exact_divisors():
     assert _lib.grad_blocking(65536, 768, 1) == (16384, 4)
     assert _lib.grad_blocking(262144, 1152, 1) == (8192, 32)
     assert _lib.grad_blocking(32768, 1152, _lib.DTYPE_F32_BF16X3) == (16384, 2)
+    # at least 1024 rows where the budget allows: one block for a small problem
     assert _lib.grad_blocking(1000, 64, 0) == (1024, 1)
     assert _lib.grad_blocking(1000, 64, 1) == (1024, 1)
+    assert _lib.grad_blocking(1024, 512, 0) == (1024, 1)
 
 
 VALID = dict(x=16, ldx=64, y=16, ldy=64, n=10, d=64, dtype=0, mode=0, normalize=1, temperature=0.07)
@@ -141,44 +171,122 @@ def test_mode_and_deterministic_flag(mode, ok):
     assert rc == _lib.MEC_ERR_INVALID and (("non-null" if ok else "mode") in _lib.last_error())
 
 
-def gbuf_bytes(n, d, dt):
-    """Bytes of the gradient-matrix buffers: 4 copies (fp32: both layouts,
-    double-buffered; bf16x3: hi and lo planes) or 2 copies of nb blocks of bs^2."""
-    bs, nb = _lib.grad_blocking(n, d, dt)
-    copies = 4 if dt in (0, 3) else 2
-    elem = 4 if dt == 0 else 2
-    return copies * nb * bs * bs * elem, bs
-
-
 @pytest.mark.parametrize("dt", [0, 1, 2, 3, 4])
 def test_scratch_stays_within_its_budget(dt):
-    """The gradient-matrix buffers stay within the bytes of a dense fp32 n x n
-    logit matrix and within 16 GiB, unless the 1024-row block floor alone
-    exceeds that; the transposed input copies add 2 (bf16x3: 4) n x d planes."""
-    lib = _lib.load()
+    """The gradient-matrix buffers stay within O(n d): 64 n d elements, at
+    least 256 MiB, at most 16 GiB; only blocks of a single quantum (128 or
+    256 rows, the smallest tile) may exceed that."""
     for n in (1024, 3000, 4096, 8192, 16384, 32768, 65536, 262144, 1 << 21, 1 << 22):
-        for d in (64, 512, 768, 1152, 2048, 4096, 8192):
-            g, bs = gbuf_bytes(n, d, dt)
-            budget = min(n * n * 4, 16 << 30)
-            q = 128 if dt == 0 else 256
-            floor_rows = max(1024, q)
-            elem = 4 if dt == 0 else 2
-            copies = 4 if dt in (0, 3) else 2
-            nb_floor = -(-n // floor_rows)
-            floor_bytes = copies * nb_floor * floor_rows * floor_rows * elem
-            assert g <= budget or (bs == floor_rows and g <= floor_bytes), (n, d, dt, bs, g, budget)
-            ldt = (n + 127) // 128 * 128
-            planes = 4 if dt == 3 else 2
-            assert lib.mec_grad_scratch_bytes(n, d, dt) == g + planes * d * ldt * elem
+        for d in (1, 16, 64, 512, 768, 1152, 2048, 4096, 8192):
+            bs, nb = _lib.grad_blocking(n, d, dt)
+            g = layout_bytes(n, d, dt, 0, bs, nb)
+            q = QUANTUM[dt]
+            assert g <= budget(n, d, dt) or bs == q, (n, d, dt, bs, g)
+            # the whole scratch for both sides: buffers plus the transposed inputs
+            assert _lib.load().mec_grad_scratch_bytes(n, d, dt) == layout_bytes(n, d, dt, 3, bs, nb)
 
 
 def test_scratch_at_two_million_rows():
-    # n = 2^21 pairs at the headline width: 1024-row blocks, about 54 GB of
-    # scratch (34 GB gradient-matrix buffers + 19 GB transposed inputs), within
-    # the 288 GB of one MI355X beside the inputs and gradients (4 x 9.7 GB)
+    # n = 2^21 pairs at the headline width: 1024-row blocks within the 16 GiB
+    # cap (fp32 keeps no transposed copies), beside the inputs and gradients
+    # (4 x 9.7 GB) on one MI355X
     lib = _lib.load()
     assert _lib.grad_blocking(1 << 21, 1152, 0) == (1024, 2048)
-    assert lib.mec_grad_scratch_bytes(2097152, 1152, 0) <= 60 * 10 ** 9
+    assert lib.mec_grad_scratch_bytes(2097152, 1152, 0) == 16 << 30
+
+
+def test_scratch_by_mode_and_side():
+    # LiT (x side only) and a frozen tower reserve only what their launches use
+    lib = _lib.load()
+    n, d = 32768, 1152
+    clip = lib.mec_grad_scratch_bytes_for(n, d, 0, 0, 3)
+    lit = lib.mec_grad_scratch_bytes_for(n, d, 0, 1, 1)
+    # config 3 (LiT fp32): one H diagonal, double-buffered (8 blocks of 4096 rows)
+    assert lit == 2 * 8 * 4096 * 4096 * 4 <= 1.4e9
+    assert clip == lit  # fp32 reads its raw inputs: no side-dependent buffers
+    # 16-bit: a transposed input per side computed
+    for dt in (1, 2, 3, 4):
+        both = lib.mec_grad_scratch_bytes_for(n, d, dt, 0, 3)
+        one = lib.mec_grad_scratch_bytes_for(n, d, dt, 0, 1)
+        planes = 2 if dt == 3 else 1
+        assert both - one == planes * d * n * 2
+        assert lib.mec_grad_scratch_bytes_for(n, d, dt, 0, 2) == one
+        assert lib.mec_grad_scratch_bytes_for(n, d, dt, 1, 3) == one
+
+
+def test_config1_extra_memory():
+    # benchmark configuration 1 (n = 1024, d = 512, fp32): one block, one H
+    # plane; the backward's scratch and the forward's workspace together stay
+    # within twice a dense fp32 logit matrix (the returned gradients are the
+    # outputs, as in the reference)
+    lib = _lib.load()
+    n, d = 1024, 512
+    dense = n * n * 4
+    scratch = lib.mec_grad_scratch_bytes_for(n, d, 0, 0, 3)
+    ws = lib.mec_workspace_floats_for(n, d, 0) * 4
+    assert scratch == dense
+    assert scratch + ws <= 2 * dense
+
+
+def test_backward_plan():
+    lib = _lib.load()
+    p = _lib.backward_plan(32768, 1152, 0, compute_units=256)
+    assert (p.block_rows, p.num_blocks, p.scratch_bytes) == (4096, 8, lib.mec_grad_scratch_bytes(32768, 1152, 0))
+    assert (p.contract_tile_rows, p.contract_tile_features) == (128, 128)
+    p = _lib.backward_plan(1024, 512, 0, compute_units=256)
+    assert (p.contract_tile_rows, p.contract_tile_features) == (64, 64)
+    # configs 4 and 5 take the 384-wide contraction tiles on 256 CUs
+    for n, d in [(65536, 768), (262144, 1152)]:
+        p = _lib.backward_plan(n, d, 1, compute_units=256)
+        assert (p.contract_tile_rows, p.contract_tile_features, p.narrow_tiles) == (256, 384, 0)
+    with pytest.raises(_lib.MecError, match="sides"):
+        _lib.backward_plan(1024, 512, 0, sides=0, compute_units=256)
+    with pytest.raises(_lib.MecError, match="2\\^22"):
+        _lib.backward_plan((1 << 22) + 1, 512, 0, compute_units=256)
+
+
+def test_wide_contraction_tiles_stay_within_32bit_offsets(monkeypatch):
+    # a 384-wide tile reads a 384-row panel of a transposed input ([d][ldt])
+    # with 32-bit byte offsets: (383 ldt + bs) x 2 < 2^31, ldt up to ~2.8M;
+    # past that the 256-wide tiles (fine up to n = 2^22) are used even where
+    # MEC_WIDE_CONTRACT=1 forces the wide ones
+    monkeypatch.setenv("MEC_WIDE_CONTRACT", "1")
+    for n, ok in [(2_700_000, True), (2_850_000, False), (1 << 22, False)]:
+        p = _lib.backward_plan(n, 1152, 1, compute_units=256)
+        ldt = (n + 127) // 128 * 128
+        assert ((383 * ldt + p.block_rows) * 2 < 2 ** 31) == ok
+        assert p.contract_tile_features == (384 if ok else 256), (n, p.contract_tile_features)
+
+
+def test_noalloc_fit_rule():
+    # mec_backward_noalloc's 256 MiB array at d = 1152, CLIP: the largest n it
+    # takes per dtype (fp32 holds only H; the 16-bit types also their
+    # transposed inputs, 2 d bytes per row and side; bf16x3 two planes)
+    d = 1152
+
+    def largest(dt):
+        lo, hi = 1, 1 << 22
+        while lo < hi:
+            mid = (lo + hi + 1) // 2
+            if _lib.backward_plan(mid, d, dt, compute_units=256).noalloc_block_rows > 0:
+                lo = mid
+            else:
+                hi = mid - 1
+        return lo
+
+    limits = {dt: largest(dt) for dt in (0, 1, 3)}
+    mib256 = _lib.NOALLOC_SCRATCH_BYTES
+    # fp32: two diagonals of 128-row blocks, 2 x 128 x 4 bytes per row
+    assert limits[0] == mib256 // (2 * 128 * 4) == 262144, limits
+    # bf16: two diagonals of 256-row blocks (1 KB per row) and the two
+    # transposed inputs (2 d x 2 bytes per row, n rounded up to 128)
+    assert limits[1] == 47616 and 47616 * (1024 + 4 * d) <= mib256 < 47744 * (1024 + 4 * d), limits
+    # bf16x3: hi and lo planes of both
+    assert limits[3] == 23808 and 23808 * 2 * (1024 + 4 * d) <= mib256, limits
+    # the headline shape fits (fp32, 1024-row blocks), config 5 does not
+    p = _lib.backward_plan(32768, 1152, 0, compute_units=256)
+    assert p.noalloc_block_rows == 1024 and p.noalloc_scratch_bytes <= _lib.NOALLOC_SCRATCH_BYTES
+    assert _lib.backward_plan(262144, 1152, 1, compute_units=256).noalloc_block_rows == -1
 
 
 @pytest.mark.parametrize("dtype", [0, 1, 2, 3, 4])
@@ -278,14 +386,14 @@ def test_missing_library_fails_loudly(tmp_path):
 
 def test_noalloc_rejects_problems_beyond_its_array():
     # mec_backward_noalloc holds its scratch in a 256 MiB device array: a
-    # problem whose scratch does not fit even with 1024-row blocks is refused
-    # in host code, before any HIP call (no device here)
+    # problem whose scratch does not fit even with single-quantum blocks is
+    # refused in host code, before any HIP call (no device here)
     lib = _lib.load()
-    n, d = 65536, 768  # config 4 (bf16): the transposed inputs alone are 201 MB
+    n, d = 131072, 768  # bf16: the transposed inputs alone are 403 MB
     rc = lib.mec_backward_noalloc(16, d, 16, d, n, d, _lib.DTYPE_BF16, 0, 0, 0.07, 1.0 / 0.07, 16, None, 16, 16,
                                   16, 16, None)
     assert rc == _lib.MEC_ERR_UNSUPPORTED and "mec_backward_noalloc holds" in _lib.last_error()
-    n, d = 1 << 20, 1024  # fp32: 8 GB of transposed inputs
+    n, d = 1 << 20, 1024  # fp32: H at 128-row blocks is 1.07 GB
     rc = lib.mec_backward_noalloc(16, d, 16, d, n, d, 0, 0, 1, 0.07, 1.0 / 0.07, 16, None, 16, 16, 16, 16, None)
     assert rc == _lib.MEC_ERR_UNSUPPORTED
     # argument errors as mec_backward
@@ -295,3 +403,31 @@ def test_noalloc_rejects_problems_beyond_its_array():
     rc = lib.mec_backward_noalloc(16, 64, 16, 64, 10, 64, 0, 0, 1, 0.07, float("nan"), 16, None, 16, 16, 16, 16,
                                   None)
     assert rc == _lib.MEC_ERR_INVALID and "grad_scale" in _lib.last_error()
+
+
+def test_graph_capture_is_refused_before_any_launch(monkeypatch):
+    # every entry point that launches checks the stream for an active HIP
+    # graph capture and returns MEC_ERR_UNSUPPORTED first; the check is
+    # stubbed here (no GPU) by MEC_TEST_ASSUME_CAPTURING=1
+    monkeypatch.setenv("MEC_TEST_ASSUME_CAPTURING", "1")
+    lib = _lib.load()
+    n, d = 10, 64
+    need = lib.mec_grad_scratch_bytes(n, d, 0)
+    calls = {
+        "mec_prepass": lambda: lib.mec_prepass(16, d, 16, d, n, d, 0, 1, 16, None),
+        "mec_sumexp": lambda: lib.mec_sumexp(16, d, 16, d, n, d, 0, 0, 1, 0.07, 16, None),
+        "mec_finalize": lambda: lib.mec_finalize(n, 0, 0.07, 16, 16, None),
+        "mec_forward": lambda: lib.mec_forward(16, d, 16, d, n, d, 0, 0, 1, 0.07, 16, 16, None),
+        "mec_grad_step": lambda: lib.mec_grad_step(16, d, 16, d, n, d, 0, 0, 1, 0.07, 16, 0, 16, need, 16, 16, None),
+        "mec_grad": lambda: lib.mec_grad(16, d, 16, d, n, d, 0, 0, 1, 0.07, 16, 16, need, 16, 16, None),
+        "mec_postpass": lambda: lib.mec_postpass(16, d, 16, d, n, d, 0, 0, 1, 1.0, 16, None, 16, 16, 16, 16, None),
+        "mec_backward": lambda: lib.mec_backward(16, d, 16, d, n, d, 0, 0, 1, 0.07, 1.0, 16, None, 16, need, 16, 16,
+                                                 16, 16, None),
+        "mec_backward_noalloc": lambda: lib.mec_backward_noalloc(16, d, 16, d, n, d, 0, 0, 1, 0.07, 1.0, 16, None,
+                                                                 16, 16, 16, 16, None),
+    }
+    for name, call in calls.items():
+        assert call() == _lib.MEC_ERR_UNSUPPORTED, name
+        assert "graph" in _lib.last_error(), (name, _lib.last_error())
+    # argument errors still come first
+    assert lib.mec_prepass(16, d, 16, d, 0, d, 0, 1, 16, None) == _lib.MEC_ERR_INVALID

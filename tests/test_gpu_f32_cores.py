@@ -1,11 +1,12 @@
 """GPU parity of the fp32 core choices, against the fp64 CPU oracle.
 
-fp32 inputs whose rows are 16-byte aligned run the forward and
-gradient-matrix tiles on the direct-to-LDS core, and the contractions too
-while a transposed input panel (128 rows of pitch ~N) fits its 32-bit
-offsets (N up to about 4.2M); otherwise on the register-staged core.  The
-second choice cannot be reached at test sizes, so MEC_F32_CONTRACT_DMA=0
-forces it here; a row stride past the 32-bit range exercises the first.
+fp32 inputs whose rows are 16-byte aligned (base, d and the row stride
+multiples of 4 floats) run the forward and gradient-matrix tiles on the
+direct-to-LDS core, and the contractions read the raw input rows with 16-byte
+load lanes; other layouts run the forward and gradient-matrix tiles on the
+register-staged core and the contractions with 4-byte load lanes.  Both are
+checked against the oracle and against each other, and a row stride past the
+direct core's 32-bit panel range takes the second path too.
 
 Up to N = 2816 the direct-to-LDS kernels run 64 x 64 tiles (a 128 x 128
 grid would leave CUs idle); MEC_F32_SMALL_TILES=0 / 1 forces either tile
@@ -39,30 +40,47 @@ def run(module, a, b, grad_b=True):
     return loss.detach().cpu(), ga.grad.cpu(), (gb.grad.cpu() if grad_b else None)
 
 
+def strided(t, ld):
+    """A GPU copy of t [n, d] with row stride ld (ld >= d)."""
+    n, d = t.shape
+    flat = torch.zeros(n * ld, device=DEV)
+    g = flat.as_strided((n, d), (ld, 1))
+    g.copy_(t.to(DEV))
+    return g
+
+
 @pytest.mark.parametrize("lit", [False, True], ids=["clip", "lit"])
-def test_f32_register_staged_contractions(lit):
-    n, d = 2300, 96  # two backward blocks of 2048 rows, the last one short
-    a, b = randn_pair(n, d, seed=31)
+@pytest.mark.parametrize("n,d,ld", [(2300, 96, 97), (700, 130, 130), (4500, 64, 66)])
+def test_f32_unaligned_rows(lit, n, d, ld):
+    """Rows that are not 16-byte vectors (an odd row stride, d % 4 != 0):
+    register-staged gradient-matrix tiles, 4-byte load lanes for the
+    contractions' raw-input operand; against the oracle, and against the
+    same values in aligned rows (16-byte lanes, direct-to-LDS tiles).  The
+    shapes cover two backward blocks with a short last one (2300 rows at
+    d = 96), one block, and the 128 x 128 tiles (4500 rows)."""
+    a, b = randn_pair(n, d, seed=31 + n)
     mod = MemoryEfficientLiTLoss(0.07) if lit else MemoryEfficientCLIPLoss(0.07)
-    say(f"fp32 {'LiT' if lit else 'CLIP'} n={n} d={d}: direct-to-LDS vs register-staged contractions")
-    l_dma, da_dma, db_dma = run(mod, a, b, grad_b=not lit)
-    os.environ["MEC_F32_CONTRACT_DMA"] = "0"
-    try:
-        l_reg, da_reg, db_reg = run(mod, a, b, grad_b=not lit)
-    finally:
-        del os.environ["MEC_F32_CONTRACT_DMA"]
+    say(f"fp32 {'LiT' if lit else 'CLIP'} n={n} d={d}: row stride {ld} vs aligned rows")
+    l_al, da_al, db_al = run(mod, a, b, grad_b=not lit)
+    ga = strided(a, ld).requires_grad_(True)
+    gb = strided(b, ld).requires_grad_(not lit)
+    loss = mod(ga, gb)
+    loss.backward()
+    torch.cuda.synchronize()
+    l_un, da_un = loss.detach().cpu(), ga.grad.cpu()
+    db_un = None if lit else gb.grad.cpu()
     if lit:
         rl, rda = oracle.lit_loss_and_grads(a, b, 0.07)
-        pairs = [(da_dma, rda), (da_reg, rda)]
+        pairs = [(da_al, rda), (da_un, rda)]
     else:
         rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
-        pairs = [(da_dma, rda), (db_dma, rdb), (da_reg, rda), (db_reg, rdb)]
+        pairs = [(da_al, rda), (db_al, rdb), (da_un, rda), (db_un, rdb)]
     errs = [max_rel(g, r) for g, r in pairs]
-    say(f"  loss rel {rel_err(l_dma, rl):.2e} / {rel_err(l_reg, rl):.2e}; grads {['%.2e' % e for e in errs]}")
-    assert rel_err(l_dma, rl) <= TOL_LOSS and rel_err(l_reg, rl) <= TOL_LOSS
+    say(f"  loss rel {rel_err(l_al, rl):.2e} / {rel_err(l_un, rl):.2e}; grads {['%.2e' % e for e in errs]}")
+    assert rel_err(l_al, rl) <= TOL_LOSS and rel_err(l_un, rl) <= TOL_LOSS
     assert all(e <= TOL_GRAD for e in errs)
     # the two cores sum the same products in different orders
-    assert max_rel(da_dma, da_reg) < 1e-5
+    assert max_rel(da_al, da_un) < 1e-5
 
 
 def test_f32_row_stride_beyond_the_direct_core_range():

@@ -280,7 +280,7 @@ def test_abi_stages(mode, normalize):
         assert max_rel(w[7], -((r - ed) / r + (c - ed) / c)) < 1e-5
     else:
         assert max_rel(w[7], -((r - ed) / r)) < 1e-5
-    # contractions (off-diagonal, unscaled): acc_x_i = sum_{j != i} G'_ij y^_j
+    # contractions (off-diagonal, unscaled): acc_x_i = rx_i sum_{j != i} G'_ij y^_j
     acc_x = torch.empty(n, d, device=DEV)
     acc_y = torch.empty(n, d, device=DEV) if mode == _lib.MODE_CLIP else None
     nbytes = lib.mec_grad_scratch_bytes(n, d, 0)
@@ -289,10 +289,15 @@ def test_abi_stages(mode, normalize):
               _ptr(acc_x), None if acc_y is None else _ptr(acc_y), _stream())
     off = 1.0 - torch.eye(n, dtype=torch.float64)
     gp = e * (1 / r)[:, None] * off
+    # fp32 contracts H = diag(rx) G' diag(ry) with the raw inputs: each
+    # accumulator row carries its own inverse norm (1 when normalize = 0)
+    ones = torch.ones(n, dtype=torch.float64)
+    rx = 1 / a.double().norm(dim=1) if normalize else ones
+    ry = 1 / b.double().norm(dim=1) if normalize else ones
     if mode == _lib.MODE_CLIP:
         gp = gp + e * (1 / c)[None, :] * off
-        assert max_rel(acc_y.cpu(), gp.T @ xh) < 1e-5
-    assert max_rel(acc_x.cpu(), gp @ yh) < 1e-5
+        assert max_rel(acc_y.cpu(), ry[:, None] * (gp.T @ xh)) < 1e-5
+    assert max_rel(acc_x.cpu(), rx[:, None] * (gp @ yh)) < 1e-5
 
 
 def test_abi_rejects_bad_arguments_on_gpu_box():

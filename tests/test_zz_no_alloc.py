@@ -83,12 +83,14 @@ def test_noalloc_matches_backward_twice(dt, mode, normalize, gen):
 
 
 def test_noalloc_shorter_blocks_when_the_array_is_small():
-    """fp32, n = 8192, d = 2048: mec_backward's scratch (2048-row blocks,
-    402 MB) exceeds the 256 MiB array, so the no-allocation path runs
-    1024-row blocks; the gradients agree to fp32 rounding (bar: 1e-3)."""
-    n, d, t = 8192, 2048, 0.07
+    """fp32, n = 16384, d = 2048: mec_backward's scratch (two 8192-row
+    blocks, double-buffered: 1.07 GB) exceeds the 256 MiB array, so the
+    no-allocation path runs 2048-row blocks; the gradients agree to fp32
+    rounding (bar: 1e-3)."""
+    n, d, t = 16384, 2048, 0.07
     bs, nb = _lib.grad_blocking(n, d, _lib.DTYPE_F32)
-    assert _lib.load().mec_grad_scratch_bytes(n, d, _lib.DTYPE_F32) > _lib.NOALLOC_SCRATCH_BYTES and bs == 2048
+    assert _lib.load().mec_grad_scratch_bytes(n, d, _lib.DTYPE_F32) > _lib.NOALLOC_SCRATCH_BYTES and bs == 8192
+    assert _lib.backward_plan(n, d, _lib.DTYPE_F32).noalloc_block_rows == 2048
     a, b = randn_pair(n, d, seed=3)
     say(f"noalloc f32 CLIP n={n} d={d}: default blocks {nb} x {bs}")
     (rx, ry), (gx, gy) = backward_pair(a, b, _lib.DTYPE_F32, _lib.MODE_CLIP, 1, t)
