@@ -133,3 +133,33 @@ def test_graph_capture_is_refused(monkeypatch):
         _function.backward(None, torch.ones(()), True, True)
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
     _function.refuse_graph_capture()  # no capture: no error
+
+
+def test_reference_import_path_works_unchanged():
+    """With the drop-in directory on PYTHONPATH, the reference's own imports
+    (`from clip_loss import ...`, `from lit_loss import ...`, its README lines
+    29 and 50) load this package's classes, with no edit in the caller."""
+    import os
+    import subprocess
+    import sys
+
+    from memoryefficientclip_amd import dropin
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([dropin.PATH, root]))
+    code = ("from clip_loss import MemoryEfficientCLIPLoss, MemoryEfficientCLIPLossNormed, "
+            "StableMemoryEfficientCLIPLoss, StableMemoryEfficientCLIPLossNormed\n"
+            "from lit_loss import MemoryEfficientLiTLoss, MemoryEfficientLiTLossNormed, "
+            "StableMemoryEfficientLiTLoss, StableMemoryEfficientLiTLossNormed\n"
+            "import memoryefficientclip_amd as m\n"
+            "assert MemoryEfficientCLIPLoss is m.MemoryEfficientCLIPLoss\n"
+            "assert StableMemoryEfficientLiTLossNormed is m.StableMemoryEfficientLiTLossNormed\n"
+            "loss_fn = MemoryEfficientCLIPLoss(temperature=0.07, normalized_inputs=False)\n"
+            "print('ok', type(loss_fn).__module__)\n")
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() == "ok memoryefficientclip_amd.clip_loss"
+    # python -m memoryefficientclip_amd.dropin prints the directory
+    out = subprocess.run([sys.executable, "-m", "memoryefficientclip_amd.dropin"], env=dict(os.environ, PYTHONPATH=root),
+                         capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0 and out.stdout.strip() == dropin.PATH

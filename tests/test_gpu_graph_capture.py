@@ -17,8 +17,10 @@ pytestmark = [
     pytest.mark.gpu,
     pytest.mark.skip(reason="the first case ended in a host segmentation fault inside torch.cuda.graph's "
                             "capture_end (stream-capture end / graph instantiation) on the MI355X box; the cause "
-                            "is not identified, so the test stays off the GPU and the module refuses capture "
-                            "with a RuntimeError (tests/test_api_cpu.py::test_graph_capture_is_refused)"),
+                            "is not identified, so the test stays off the GPU; the module refuses capture "
+                            "with a RuntimeError (tests/test_api_cpu.py::test_graph_capture_is_refused) and every "
+                            "C-ABI entry point with MEC_ERR_UNSUPPORTED "
+                            "(tests/test_abi_cpu.py::test_graph_capture_is_refused_before_any_launch)"),
 ]
 DEV = "cuda:0"
 
