@@ -115,6 +115,25 @@ extern "C" {
  * MEC_DTYPE_F32_BF16 (on normalized copies), always run this way (chained
  * tiles; faster than the atomic forward there), with or without the flag. */
 #define MEC_FLAG_DETERMINISTIC 0x100
+/* OR into `mode` of mec_forward and of the matching mec_grad / mec_backward
+ * (mec_backward_noalloc) for a small problem that mec_keep_exp_supported
+ * accepts: the forward keeps E_ij = exp((S_ij - 1)/T) (zero on the diagonal)
+ * in the workspace, np x np floats (np = n rounded up to 64), and turns it
+ * into H = diag(rx) G' diag(ry) once the sums are known; the backward
+ * contracts H instead of recomputing the similarity tiles.  The forward is
+ * then two launches (similarity tiles, which also form the norms and the
+ * diagonal; finalize), the backward two (contractions; post-pass), and the
+ * backward needs no gradient scratch.  Both passes are deterministic
+ * (fixed-order sums) with or without MEC_FLAG_DETERMINISTIC.  The workspace
+ * must hold mec_workspace_floats_mode(n, d, dtype, mode) floats and be 16-byte
+ * aligned; the flag must be passed to both calls or to neither.  No
+ * counterpart in the reference, whose backward always recomputes
+ * (clip_loss.py:96-124): this trades np^2 floats of workspace, held from the
+ * forward to the backward, for one similarity GEMM, and is limited to
+ * n <= MEC_KEEP_EXP_MAX_N.  The functions that run one stage (mec_sumexp,
+ * mec_finalize, mec_grad_step) reject the flag. */
+#define MEC_FLAG_KEEP_EXP 0x200
+#define MEC_KEEP_EXP_MAX_N 2048
 
 /* Sides of the backward, for the size queries: the x side (acc_x, dx) and
  * the y side (acc_y, dy; CLIP only).  mec_grad and friends compute the sides
@@ -148,6 +167,22 @@ int64_t mec_workspace_floats(int64_t n);
  * 3 * round8(d) (round8(d)) bf16.  Returns < 0 on bad args.  No counterpart
  * in the reference. */
 int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype);
+
+/* Number of floats of the workspace for (n, d, dtype, mode):
+ * mec_workspace_floats_for(n, d, dtype), plus, with MEC_FLAG_KEEP_EXP in
+ * mode, the kept matrix (np x np floats), 2 np^2 / 64 floats of per-tile row
+ * and column sums, np / 64 doubles of loss partials and one counter (np = n
+ * rounded up to 64), each part 256-byte aligned.  Returns < 0 on bad
+ * args, or for MEC_FLAG_KEEP_EXP with a dtype other than MEC_DTYPE_F32 or
+ * n > MEC_KEEP_EXP_MAX_N.  No counterpart in the reference. */
+int64_t mec_workspace_floats_mode(int64_t n, int64_t d, int dtype, int mode);
+
+/* 1 if mec_forward / mec_backward accept MEC_FLAG_KEEP_EXP for these inputs
+ * (MEC_DTYPE_F32, n <= MEC_KEEP_EXP_MAX_N, 16-byte aligned rows: x and y
+ * 16-byte aligned, d, ldx and ldy multiples of 4), else 0 (also for invalid
+ * arguments).  Host-only.  No counterpart in the reference. */
+int mec_keep_exp_supported(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
+                           int dtype);
 
 /* Bytes of gradient scratch that mec_grad / mec_grad_step / mec_backward
  * need for (n, d, dtype, mode, sides), sides a mask of MEC_SIDE_X and

@@ -104,8 +104,15 @@ def forward(ctx, x: torch.Tensor, y: torch.Tensor, temperature: float, mode: int
     n, d = x.shape
     dev = x.device
     dt = compute_dtype(x.dtype)
+    lib = _lib.load()
+    # small fp32 problems keep the exponentials for the backward (four
+    # launches per step instead of six, no gradient scratch), when a gradient
+    # will be asked for
+    if (ctx.needs_input_grad[0] or ctx.needs_input_grad[1]) and \
+            lib.mec_keep_exp_supported(x.data_ptr(), ldx, y.data_ptr(), ldy, n, d, dt):
+        mode |= _lib.FLAG_KEEP_EXP
     with torch.cuda.device(dev):
-        ws = torch.empty(_lib.load().mec_workspace_floats_for(n, d, dt), dtype=torch.float32, device=dev)
+        ws = torch.empty(lib.mec_workspace_floats_mode(n, d, dt, mode), dtype=torch.float32, device=dev)
         loss = torch.empty((), dtype=torch.float32, device=dev)
         # under torch.use_deterministic_algorithms(True) the forward sums are
         # formed without atomics (the backward is deterministic either way)
@@ -123,7 +130,7 @@ def backward(ctx, grad_output: torch.Tensor, need_x: bool, need_y: bool):
     refuse_graph_capture()
     x, y, ws = ctx.saved_tensors
     ldx, ldy, n, d, dt, mode, normalize, temperature, grad_scale = ctx.mec
-    if mode == _lib.MODE_LIT:
+    if mode & 0xFF == _lib.MODE_LIT:
         need_y = False
     if not (need_x or need_y):
         return None, None
@@ -144,9 +151,9 @@ def backward(ctx, grad_output: torch.Tensor, need_x: bool, need_y: bool):
         # torch.use_deterministic_algorithms(True) (gigabytes at large N) would
         # be wasted work.
         sides = (_lib.SIDE_X if need_x else 0) | (_lib.SIDE_Y if need_y else 0)
-        nbytes = lib.mec_grad_scratch_bytes_for(n, d, dt, mode, sides)
+        nbytes = lib.mec_grad_scratch_bytes_for(n, d, dt, mode, sides)  # 0 with the kept exponentials
         stream = torch.cuda.current_stream(dev)
-        scratch = torch.cuda.caching_allocator_alloc(nbytes, dev, stream)
+        scratch = torch.cuda.caching_allocator_alloc(nbytes, dev, stream) if nbytes > 0 else None
 
         def ptr(t):
             return None if t is None else t.data_ptr()
@@ -156,7 +163,8 @@ def backward(ctx, grad_output: torch.Tensor, need_x: bool, need_y: bool):
                       temperature, grad_scale, ws.data_ptr(), go.data_ptr(), scratch, nbytes,
                       ptr(acc_x), ptr(acc_y), ptr(dx), ptr(dy), stream.cuda_stream)
         finally:
-            torch.cuda.caching_allocator_delete(scratch)
+            if scratch is not None:
+                torch.cuda.caching_allocator_delete(scratch)
     return dx, dy
 
 

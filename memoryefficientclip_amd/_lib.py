@@ -26,6 +26,8 @@ DTYPE_F32_BF16 = 4  # fp32 data, bf16 products
 MODE_CLIP = 0
 MODE_LIT = 1
 FLAG_DETERMINISTIC = 0x100  # OR into the mode of mec_sumexp / mec_forward
+FLAG_KEEP_EXP = 0x200  # OR into the mode of mec_forward and the matching backward
+KEEP_EXP_MAX_N = 2048  # MEC_KEEP_EXP_MAX_N
 SIDE_X = 1  # MEC_SIDE_X: the x side of the backward (acc_x, dx)
 SIDE_Y = 2  # MEC_SIDE_Y: the y side (CLIP only)
 
@@ -40,6 +42,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mec_version": (ctypes.c_char_p, []),
     "mec_workspace_floats": (_i64, [_i64]),
     "mec_workspace_floats_for": (_i64, [_i64, _i64, _int]),
+    "mec_workspace_floats_mode": (_i64, [_i64, _i64, _int, _int]),
+    "mec_keep_exp_supported": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int]),
     "mec_grad_scratch_bytes": (_i64, [_i64, _i64, _int]),
     "mec_grad_scratch_bytes_for": (_i64, [_i64, _i64, _int, _int, _int]),
     "mec_backward_plan": (_int, [_i64, _i64, _int, _int, _int, _int, _vp]),

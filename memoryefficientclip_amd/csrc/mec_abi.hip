@@ -10,6 +10,7 @@
 #include <string>
 
 #include "mec.h"
+#include "mec_keep.h"
 #include "mec_kernels.h"
 #include "mec_rowops.h"
 
@@ -148,10 +149,19 @@ int check_common(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
 }
 
 // mode = MEC_MODE_CLIP or MEC_MODE_LIT, optionally OR MEC_FLAG_DETERMINISTIC
+// and MEC_FLAG_KEEP_EXP
 int check_mode(int mode) {
   const int base = mode & MEC_MODE_MASK, flags = mode & ~MEC_MODE_MASK;
-  if ((base != MEC_MODE_CLIP && base != MEC_MODE_LIT) || (flags & ~MEC_FLAG_DETERMINISTIC))
+  if ((base != MEC_MODE_CLIP && base != MEC_MODE_LIT) || (flags & ~(MEC_FLAG_DETERMINISTIC | MEC_FLAG_KEEP_EXP)))
     return fail(MEC_ERR_INVALID, "unknown mode %d", mode);
+  return MEC_OK;
+}
+
+bool keep_flag(int mode) { return (mode & MEC_FLAG_KEEP_EXP) != 0; }
+// the functions that run one stage have no kept-matrix variant
+int check_no_keep(int mode, const char* fn) {
+  if (keep_flag(mode))
+    return fail(MEC_ERR_INVALID, "%s: MEC_FLAG_KEEP_EXP applies to mec_forward, mec_grad and mec_backward only", fn);
   return MEC_OK;
 }
 
@@ -217,6 +227,60 @@ bool vec_ok(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t d, i
   if (!(aligned16(x) && aligned16(y) && d % per == 0 && ldx % per == 0 && ldy % per == 0)) return false;
   const int64_t ld = ldx > ldy ? ldx : ldy;
   return (dma_rows(dtype) - 1) * ld + d <= dma_max_elems(dtype);
+}
+
+// Kept exponentials (MEC_FLAG_KEEP_EXP): E and the forward's bookkeeping
+// follow the dtype's workspace, each part 256-byte aligned (offsets in floats
+// from the workspace start).
+static_assert(KEEP_MAX_N == MEC_KEEP_EXP_MAX_N, "one limit");
+bool keep_shape_ok(int64_t n, int dtype) { return dtype == MEC_DTYPE_F32 && n <= MEC_KEEP_EXP_MAX_N; }
+int64_t align256b(int64_t floats) { return (floats + 63) & ~int64_t(63); }
+struct KeepLayout {
+  int np, kt;                                     // n rounded up to 64, np / 64
+  int64_t e, rowpart, colpart, lossp, cnt, total;
+};
+KeepLayout keep_layout(int64_t n, int64_t d, int dtype) {
+  KeepLayout L;
+  L.kt = (int)((n + KEEP_T - 1) / KEEP_T);
+  L.np = L.kt * KEEP_T;
+  const int64_t np = L.np;
+  int64_t o = align256b(workspace_floats_for(n, d, dtype));
+  L.e = o;
+  o = align256b(o + np * np);
+  L.rowpart = o;
+  o = align256b(o + L.kt * np);
+  L.colpart = o;
+  o = align256b(o + L.kt * np);
+  L.lossp = o;
+  o = align256b(o + 2 * (int64_t)L.kt);
+  L.cnt = o;
+  L.total = o + 1;
+  return L;
+}
+int64_t workspace_floats_mode(int64_t n, int64_t d, int dtype, int mode) {
+  return keep_flag(mode) ? keep_layout(n, d, dtype).total : workspace_floats_for(n, d, dtype);
+}
+KeepBufs keep_bufs(const float* workspace, const KeepLayout& L) {
+  float* ws = const_cast<float*>(workspace);
+  return KeepBufs{ws + L.e, ws + L.rowpart, ws + L.colpart, (double*)(ws + L.lossp), (unsigned*)(ws + L.cnt),
+                  L.np, L.kt};
+}
+// MEC_KEEP_EXP=0 reports no support (the glue asks before it sets the flag;
+// tests of the other path)
+bool keep_supported(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype) {
+  if (const char* env = std::getenv("MEC_KEEP_EXP"))
+    if (env[0] == '0') return false;
+  return n >= 1 && d >= 1 && x && y && ldx >= d && ldy >= d && keep_shape_ok(n, dtype) &&
+         vec_ok(x, ldx, y, ldy, d, dtype);
+}
+int check_keep(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d, int dtype,
+               const float* workspace) {
+  if (!keep_supported(x, ldx, y, ldy, n, d, dtype))
+    return fail(MEC_ERR_INVALID,
+                "MEC_FLAG_KEEP_EXP needs MEC_DTYPE_F32, n <= %d and 16-byte aligned rows (mec_keep_exp_supported)",
+                MEC_KEEP_EXP_MAX_N);
+  if (!aligned16(workspace)) return fail(MEC_ERR_INVALID, "MEC_FLAG_KEEP_EXP needs a 16-byte aligned workspace");
+  return MEC_OK;
 }
 
 // Block decomposition of the N x N gradient matrix for the backward: nb
@@ -524,6 +588,18 @@ int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype) {
   return workspace_floats_for(n, d, dtype);
 }
 
+int64_t mec_workspace_floats_mode(int64_t n, int64_t d, int dtype, int mode) {
+  if (n < 1 || n > kMaxN || d < 1 || d > kMaxD || !known_dtype(dtype)) return -1;
+  if (check_mode(mode) != MEC_OK) return -1;
+  if (keep_flag(mode) && !keep_shape_ok(n, dtype)) return -1;
+  return workspace_floats_mode(n, d, dtype, mode);
+}
+
+int mec_keep_exp_supported(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
+                           int dtype) {
+  return keep_supported(x, ldx, y, ldy, n, d, dtype) ? 1 : 0;
+}
+
 int64_t mec_grad_scratch_bytes(int64_t n, int64_t d, int dtype) {
   if (n < 1 || n > kMaxN || d < 1 || d > kMaxD) return -1;
   if (!known_dtype(dtype)) return -1;
@@ -535,6 +611,7 @@ int64_t mec_grad_scratch_bytes_for(int64_t n, int64_t d, int dtype, int mode, in
   if (check_mode(mode) != MEC_OK) return -1;
   if (is_lit(mode)) sides &= kSideX;
   if (sides < 1 || sides > (kSideX | kSideY)) return -1;
+  if (keep_flag(mode)) return keep_shape_ok(n, dtype) ? 0 : -1;  // contracts the kept matrix
   return scratch_layout(n, d, dtype, sides).total;
 }
 
@@ -548,6 +625,18 @@ int mec_backward_plan(int64_t n, int64_t d, int dtype, int mode, int sides, int 
   if (is_lit(mode)) sides &= kSideX;
   if (sides < 1 || sides > (kSideX | kSideY)) return fail(MEC_ERR_INVALID, "sides must name the x or y side");
   if (!plan) return fail(MEC_ERR_INVALID, "plan must be non-null");
+  if (keep_flag(mode)) {
+    // one block, no scratch, 64 x 64 contraction tiles
+    if (!keep_shape_ok(n, dtype))
+      return fail(MEC_ERR_INVALID, "MEC_FLAG_KEEP_EXP needs MEC_DTYPE_F32 and n <= %d", MEC_KEEP_EXP_MAX_N);
+    const KeepLayout K = keep_layout(n, d, dtype);
+    plan->block_rows = plan->noalloc_block_rows = K.np;
+    plan->num_blocks = 1;
+    plan->scratch_bytes = plan->noalloc_scratch_bytes = 0;
+    plan->contract_tile_rows = plan->contract_tile_features = KEEP_T;
+    plan->narrow_tiles = 0;
+    return MEC_OK;
+  }
   if (cus <= 0) {
     rc = compute_units(&cus);
     if (rc) return rc;
@@ -618,6 +707,7 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
   g_err.clear();
   int rc = check_common(x, ldx, y, ldy, n, d, dtype);
   if (!rc) rc = check_mode(mode);
+  if (!rc) rc = check_no_keep(mode, "mec_sumexp");
   if (!rc) rc = check_temperature(temperature);
   if (rc) return rc;
   if (!workspace) return fail(MEC_ERR_INVALID, "workspace must be non-null");
@@ -688,6 +778,7 @@ int mec_finalize(int64_t n, int mode, float temperature, float* workspace, float
   if (n < 1) return fail(MEC_ERR_INVALID, "n=%lld must be >= 1", (long long)n);
   if (n > kMaxN) return fail(MEC_ERR_UNSUPPORTED, "n=%lld exceeds the supported maximum 2^22", (long long)n);
   int rc = check_mode(mode);
+  if (!rc) rc = check_no_keep(mode, "mec_finalize");
   if (!rc) rc = check_temperature(temperature);
   if (rc) return rc;
   if (!workspace || !loss) return fail(MEC_ERR_INVALID, "workspace and loss must be non-null");
@@ -718,6 +809,26 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
   if (!rc) rc = check_temperature(temperature);
   if (rc) return rc;
   if (!workspace || !loss) return fail(MEC_ERR_INVALID, "workspace and loss must be non-null");
+  if (keep_flag(mode)) {
+    rc = check_keep(x, ldx, y, ldy, n, d, dtype, workspace);
+    if (!rc) rc = check_not_capturing(stream);
+    if (rc) return rc;
+    // the similarity tiles (norms, diagonal, E, per-tile sums), then the
+    // finalize (sums, loss, E -> H)
+    const KeepLayout L = keep_layout(n, d, dtype);
+    const KeepBufs kb = keep_bufs(workspace, L);
+    hipStream_t s = (hipStream_t)stream;
+    const int N = (int)n, D = (int)d;
+    const float c = (float)(1.4426950408889634 / (double)temperature);
+    const double inv_t = 1.0 / (double)temperature;
+    const unsigned grid = (unsigned)(kb.kt * kb.kt);
+    DISPATCH_BOOL(is_lit(mode), LIT, DISPATCH_BOOL(normalize, NORM, {
+      k_keep_forward<LIT, NORM><<<grid, 256, 0, s>>>((const float*)x, ldx, (const float*)y, ldy, N, D, c, workspace,
+                                                     kb);
+      k_keep_finalize<LIT, NORM><<<grid, 256, 0, s>>>(N, inv_t, workspace, kb, loss);
+    }));
+    return check_launch("forward (kept exponentials)");
+  }
   rc = mec_prepass(x, ldx, y, ldy, n, d, dtype, normalize, workspace, stream);
   if (!rc) rc = mec_sumexp(x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, stream);
   if (!rc) rc = mec_finalize(n, mode, temperature, workspace, loss, stream);
@@ -933,6 +1044,21 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   return check_launch("grad_step");
 }
 
+// The backward's contractions from the kept matrix (MEC_FLAG_KEEP_EXP; a
+// checked problem; H since the forward's finalize): one launch, into acc_x /
+// acc_y as mec_grad leaves them.
+static int keep_grad_run(const StepArgs& a, void* stream) {
+  const KeepLayout L = keep_layout(a.n, a.d, a.dtype);
+  const KeepBufs kb = keep_bufs(a.workspace, L);
+  const int ctd = (int)((a.d + KEEP_T - 1) / KEEP_T);
+  const int nx_pad = a.acc_x ? round8(kb.kt * ctd) : 0, ny_pad = a.acc_y ? round8(kb.kt * ctd) : 0;
+  hipStream_t s = (hipStream_t)stream;
+  k_keep_contract<<<(unsigned)(nx_pad + ny_pad), 256, 0, s>>>((const float*)a.x, a.ldx, (const float*)a.y, a.ldy,
+                                                              (int)a.n, (int)a.d, kb, a.acc_x, a.acc_y, ctd, nx_pad,
+                                                              ny_pad);
+  return check_launch("grad (kept exponentials)");
+}
+
 // the caller's scratch against the default layout for the problem's sides
 static int check_scratch(const StepArgs& a, void* scratch, int64_t scratch_bytes, ScratchLayout* L) {
   if (!scratch) return fail(MEC_ERR_INVALID, "scratch must be non-null");
@@ -950,6 +1076,7 @@ int mec_grad_step(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_
   g_err.clear();
   StepArgs a{x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, acc_x, acc_y};
   int rc = check_step_args(a);
+  if (!rc) rc = check_no_keep(mode, "mec_grad_step");
   ScratchLayout L;
   if (!rc) rc = check_scratch(a, scratch, scratch_bytes, &L);
   if (!rc && (step < 0 || step > L.nb))
@@ -965,6 +1092,13 @@ int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, 
   g_err.clear();
   StepArgs a{x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, acc_x, acc_y};
   int rc = check_step_args(a);
+  if (!rc && keep_flag(mode)) {
+    // (no scratch: it may be NULL)
+    rc = check_keep(x, ldx, y, ldy, n, d, dtype, workspace);
+    if (!rc) rc = check_not_capturing(stream);
+    if (rc) return rc;
+    return keep_grad_run(a, stream);
+  }
   ScratchLayout L;
   if (!rc) rc = check_scratch(a, scratch, scratch_bytes, &L);
   if (!rc) rc = check_not_capturing(stream);
@@ -987,6 +1121,15 @@ int mec_backward_noalloc(const void* x, int64_t ldx, const void* y, int64_t ldy,
   if (is_lit(mode)) dy = nullptr;
   if ((a.acc_x == nullptr) != (dx == nullptr) || (a.acc_y == nullptr) != (dy == nullptr))
     return fail(MEC_ERR_INVALID, "each side needs both its accumulator and its output (or neither)");
+  if (keep_flag(mode)) {
+    // the kept matrix needs no scratch, so the array is not touched
+    rc = check_keep(x, ldx, y, ldy, n, d, dtype, workspace);
+    if (!rc) rc = check_not_capturing(stream);
+    if (!rc) rc = keep_grad_run(a, stream);
+    if (rc) return rc;
+    return mec_postpass(x, ldx, y, ldy, n, d, dtype, mode, normalize, grad_scale, workspace, grad_output, a.acc_x,
+                        a.acc_y, dx, dy, stream);
+  }
   bool ok = false;
   const ScratchLayout L = noalloc_layout(n, d, dtype, a.sides(), &ok);
   if (!ok)

@@ -88,7 +88,7 @@ __host__ __device__ constexpr int64_t gb_offset(int j, int i, int bs) {
 }
 
 template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16, int SA_ = 2,
-          bool GB_ = false, int TB_ = 0>
+          bool GB_ = false, int TB_ = 0, int S_ = 2>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_;
   static constexpr int KIND = KIND_;
@@ -97,7 +97,11 @@ struct Geo {
   static constexpr int EPV = 16 / ESZ;                 // elements per 16-byte vector
   // ring: chunks of 128 bytes per operand row (whole cache lines) in 2 stages
   static constexpr int ROWB = 128;                     // bytes per staged row of a chunk
-  static constexpr int S = 2;                          // LDS stages
+  // LDS stages of the ring (A and B together, SA = 2): chunk kt + S - 1 is
+  // loaded while chunk kt is consumed.  2, or more for tiles whose k-loop is
+  // too short per chunk to cover an L2 or HBM round trip (64 x 64 fp32).
+  static constexpr int S = S_;
+  static_assert(S >= 2 && S <= 4 && (S == 2 || SA_ == 2), "2-4 stages of A and B together");
   static constexpr int RPB = 1024 / ROWB;              // rows per 1 KB load block
   static constexpr int SLOTS = ROWB / 16;              // 16-byte vectors per row
   static constexpr int NS = ROWB / 32;                 // k-steps per chunk (one vector per lane half each)
@@ -571,6 +575,43 @@ __device__ __forceinline__ void wait_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
+// Hook on the fp32 operand values as the MFMAs take them (the default of
+// mainloop_core: none).  a(v, i, j, t) / b(v, i, j, t) return the value fed to
+// MFMA t of block (i, j) from A fragment register v (fragment i) / B fragment
+// register v (fragment j).
+struct NoFragHook {
+  __device__ __forceinline__ float a(const i16x8& v, int, int, int t) const { return __builtin_bit_cast(f32x4, v)[t]; }
+  __device__ __forceinline__ float b(const i16x8& v, int, int, int t) const { return __builtin_bit_cast(f32x4, v)[t]; }
+};
+
+// Squared norms of the operand rows, accumulated from the fragments: each
+// lane sees every k of its fragments' rows (m = 32 i + lane % 32 of the
+// wave's A rows, n = 32 j + lane % 32 of its B rows) within its lane half
+// (k = 16 h + 4 s + t of each chunk), so after the k-loop sa[i] + (the same
+// of lane ^ 32) is the row's sum of squares over the whole K.  Each value is
+// counted once: A values at j = 0, B values at i = 0.
+template <class G>
+struct NormHook {
+  static_assert(G::KIND == K_F32, "fp32 operands");
+  mutable float sa[G::FM], sb[G::FN];
+  __device__ __forceinline__ NormHook() {
+#pragma unroll
+    for (int i = 0; i < G::FM; ++i) sa[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < G::FN; ++j) sb[j] = 0.f;
+  }
+  __device__ __forceinline__ float a(const i16x8& v, int i, int j, int t) const {
+    const float x = __builtin_bit_cast(f32x4, v)[t];
+    if (j == 0) sa[i] = fmaf(x, x, sa[i]);
+    return x;
+  }
+  __device__ __forceinline__ float b(const i16x8& v, int i, int j, int t) const {
+    const float x = __builtin_bit_cast(f32x4, v)[t];
+    if (i == 0) sb[j] = fmaf(x, x, sb[j]);
+    return x;
+  }
+};
+
 // MFMAs of one k-step with loads [L0, L1) interleaved, in program order.
 // Loads [L0, L1) spread over the NMF MFMAs of a k-step: LPS loads after
 // every EVERY-th MFMA (one load per slot while there are at most NMF loads)
@@ -601,16 +642,15 @@ struct LoadSlots {
   }
 };
 
-template <class G, int L0, int L1>
+template <class G, int L0, int L1, class FH = NoFragHook>
 __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const LoadPlan<G>& lp,
-                                          int k0, char* ad, char* bd) {
+                                          int k0, char* ad, char* bd, const FH& fh = FH()) {
   static_for<G::NMF>([&](auto mc) {
     constexpr int m = mc;
     if constexpr (G::KIND == K_F32) {
       // block (i, j), sub-step t: lane half h supplies k = 16-byte vector's element t
       constexpr int blk = m / 4, t = m % 4, i = blk / G::FN, j = blk % G::FN;
-      acc[i][j] = mfma_f32_32x32x2(__builtin_bit_cast(f32x4, f.a[i])[t], __builtin_bit_cast(f32x4, f.b[j])[t],
-                                   acc[i][j]);
+      acc[i][j] = mfma_f32_32x32x2(fh.a(f.a[i], i, j, t), fh.b(f.b[j], i, j, t), acc[i][j]);
     } else {
       acc[m / G::FN][m % G::FN] =
           mfma16_32x32x16<G::F16>(f.a[m / G::FN], f.b[m % G::FN], acc[m / G::FN][m % G::FN]);
@@ -621,9 +661,10 @@ __device__ __forceinline__ void mfma_step(const Frags<G>& f, f32x16 (&acc)[G::FM
 
 // mfma_step with the LDS reads of the next fragment set `nf` interleaved: two reads after each of the first MFMAs, so that the reads
 // land during the step and the next step's MFMAs need not wait for them.
-template <class G, int L0, int L1>
+template <class G, int L0, int L1, class FH = NoFragHook>
 __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G::FM][G::FN], const LoadPlan<G>& lp,
-                                             int k0, char* ad, char* bd, const FragReader<G>& rd, Frags<G>& nf) {
+                                             int k0, char* ad, char* bd, const FragReader<G>& rd, Frags<G>& nf,
+                                             const FH& fh = FH()) {
   constexpr int NR = frag_reads<G>();
   static_assert((NR + 1) / 2 <= G::NMF, "read slots");
   static_for<G::NMF>([&](auto mc) {
@@ -631,8 +672,7 @@ __device__ __forceinline__ void mfma_step_rd(const Frags<G>& f, f32x16 (&acc)[G:
     if constexpr (G::KIND == K_F32) {
       // consecutive MFMAs on different blocks (the fences below keep program order)
       constexpr int NB = G::FM * G::FN, blk = m % NB, t = m / NB, i = blk / G::FN, j = blk % G::FN;
-      acc[i][j] = mfma_f32_32x32x2(__builtin_bit_cast(f32x4, f.a[i])[t], __builtin_bit_cast(f32x4, f.b[j])[t],
-                                   acc[i][j]);
+      acc[i][j] = mfma_f32_32x32x2(fh.a(f.a[i], i, j, t), fh.b(f.b[j], i, j, t), acc[i][j]);
     } else {
       acc[m / G::FN][m % G::FN] =
           mfma16_32x32x16<G::F16>(f.a[m / G::FN], f.b[m % G::FN], acc[m / G::FN][m % G::FN]);
@@ -676,6 +716,9 @@ __device__ __forceinline__ void prologue(const Operand& A, const Operand& B, cha
     return;
   }
   static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, G::a_stage(lds, 0), G::b_stage(lds, 0)); });
+  // deeper rings: chunks 1 .. S - 2 as well
+  for (int c = 1; c < G::S - 1; ++c)
+    static_for<G::IPW>([&](auto i) { lp.template issue<i>(c * G::BK, G::a_stage(lds, c), G::b_stage(lds, c)); });
   // three A stages: A's chunk 1 as well, issued last (the first barrier waits for all but it)
   if constexpr (G::SA == 3)
     static_for<LoadPlan<G>::A_LOADS>([&](auto i) { lp.template issue<i>(G::BK, G::a_stage(lds, 1), nullptr); });
@@ -699,13 +742,18 @@ __device__ __forceinline__ void prologue(const Operand& A, const Operand& B, cha
 struct NoHook {
   __device__ __forceinline__ void operator()() const {}
 };
-template <class G, bool ZERO, bool CHAIN, class Hook = NoHook, int VMF = 0>
+template <class G, bool ZERO, bool CHAIN, class Hook = NoHook, int VMF = 0, class FH = NoFragHook>
 __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_rsrc_t ra_next,
                                               __amdgpu_buffer_rsrc_t rb_next, bool has_next, int K, char* lds,
                                               int& p0, f32x16 (&acc)[G::FM][G::FN], const Hook& hook = Hook(),
-                                              bool vmf_first = false) {
-  static_assert(G::S == 2 && G::NS == 4, "two stages, four k-steps per chunk");
+                                              bool vmf_first = false, const FH& fh = FH()) {
+  static_assert(G::NS == 4, "four k-steps per chunk");
   static_assert(G::SA == 2 || !CHAIN, "three A stages: one tile per call");
+  static_assert(G::S == 2 || (!CHAIN && VMF == 0), "deeper rings: one tile per call");
+  // S stages: at chunk kt's barrier the loads of chunks kt + 1 .. kt + S - 2
+  // (issued later, all of them by now) may still be in flight
+  constexpr int VMS = (G::S - 2) * G::IPW;
+  static_assert(VMS < 64, "vmcnt range");
   static_assert(G::SA != 4, "four A half-stages: the rolling schedule only");
   if constexpr (ZERO) {
 #pragma unroll
@@ -734,11 +782,18 @@ __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_r
     else if (VMF > 0 && kt == 0 && vmf_first)
       wait_barrier<VMF>();
     else
-      wait_barrier<0>();
+      wait_barrier<VMS>();
     lgkm_wait<0>(f1);   // f1 (the last step of chunk kt-1) landed before its MFMAs
     sched_fence();
     char *ca, *cb, *na, *nb;
-    if constexpr (G::SA == 2) {
+    if constexpr (G::SA == 2 && G::S > 2) {
+      // chunk kt in stage kt % S; this chunk loads chunk kt + S - 1 into
+      // stage (kt - 1) % S, whose chunk every wave finished before the barrier
+      ca = G::a_stage(lds, kt % G::S);
+      cb = G::b_stage(lds, kt % G::S);
+      na = G::a_stage(lds, (kt + G::S - 1) % G::S);
+      nb = G::b_stage(lds, (kt + G::S - 1) % G::S);
+    } else if constexpr (G::SA == 2) {
       ca = G::a_stage(lds, (kt + p0) & 1);
       cb = G::b_stage(lds, (kt + p0) & 1);
       na = G::a_stage(lds, (kt + p0 + 1) & 1);
@@ -749,7 +804,7 @@ __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_r
       na = G::a_stage(lds, (kt + 2) % 3);
       nb = G::b_stage(lds, (kt + 1) & 1);
     }
-    int k1 = (kt + 1) * BK;
+    int k1 = (kt + G::S - 1) * BK;
     if constexpr (CHAIN) {
       if (kt + 1 == nk && has_next) {
         lp.ra = ra_next;
@@ -760,7 +815,7 @@ __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_r
     const int k2 = G::SA == 2 ? k1 : (kt + 2) * BK;  // the chunk k-step 1 loads
     const FragReader<G> r0(ca, cb, 0), r1(ca, cb, 1), r2(ca, cb, 2), r3(ca, cb, 3);
     if (kt > 0) {
-      mfma_step_rd<G, S0A, S0B>(f1, acc, lp, k1, na, nb, r0, f0);
+      mfma_step_rd<G, S0A, S0B, FH>(f1, acc, lp, k1, na, nb, r0, f0, fh);
     } else {
       read_frags<G>(ca, cb, 0, f0);
       static_for<S0B - S0A>([&](auto i) { lp.template issue<S0A + i>(k1, na, nb); });
@@ -768,18 +823,18 @@ __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_r
     }
     lgkm_wait<0>(f0);
     sched_fence();
-    mfma_step_rd<G, S1A, S1B>(f0, acc, lp, k2, na, nb, r1, f1);
+    mfma_step_rd<G, S1A, S1B, FH>(f0, acc, lp, k2, na, nb, r1, f1, fh);
     lgkm_wait<0>(f1);
     sched_fence();
-    mfma_step_rd<G, 0, 0>(f1, acc, lp, 0, lds, lds, r2, f0);
+    mfma_step_rd<G, 0, 0, FH>(f1, acc, lp, 0, lds, lds, r2, f0, fh);
     lgkm_wait<0>(f0);
     sched_fence();
-    mfma_step_rd<G, 0, 0>(f0, acc, lp, 0, lds, lds, r3, f1);
+    mfma_step_rd<G, 0, 0, FH>(f0, acc, lp, 0, lds, lds, r3, f1, fh);
     sched_fence();
   }
   lgkm_wait<0>(f1);
   sched_fence();
-  mfma_step<G, 0, 0>(f1, acc, lp, 0, lds, lds);
+  mfma_step<G, 0, 0, FH>(f1, acc, lp, 0, lds, lds, fh);
   if constexpr (CHAIN) p0 = (p0 + nk) & 1;
 }
 

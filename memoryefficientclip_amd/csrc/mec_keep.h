@@ -1,0 +1,262 @@
+// Small fp32 problems with the exponentials kept from the forward to the
+// backward (MEC_FLAG_KEEP_EXP, n <= MEC_KEEP_EXP_MAX_N, 16-byte rows).
+//
+// At n ~ 1000 every launch is short and the similarity GEMM is a large part
+// of the step.  The forward keeps E_ij = exp((S_ij - 1)/T) (0 on the diagonal
+// and outside [0, n)), np x np floats (np = n rounded up to 64), and turns it
+// into the scaled gradient matrix H = diag(rx) G' diag(ry) once the sums are
+// known; the backward contracts H instead of recomputing S tile by tile
+// (clip_loss.py:96-124 recomputes it in every backward program).  Launches:
+//   forward   k_keep_forward: 64 x 64 similarity tiles; the inverse norms
+//             from the tiles' own operand fragments (no pre-pass), the raw
+//             diagonal from the diagonal tiles' accumulators, E stored, and
+//             each tile's row and column sums written to per-tile slots;
+//             k_keep_finalize: per 64 x 64 block of E, the sums of its rows
+//             and columns in tile order, 1/R and 1/C, and E -> H in place;
+//             the diagonal blocks also write the loss terms, kappa and the
+//             workspace vectors, and the last of them sums the loss partials
+//             in block order.  Fixed-order sums only: the loss and the
+//             gradients are bitwise reproducible.
+//   backward  k_keep_contract: 64 x 64 output tiles of acc_x = H Y and
+//             acc_y = H^T X, then the usual post-pass (k_postpass with the
+//             accumulators as mec_grad leaves them for fp32).
+#pragma once
+#include "mec_kernels.h"
+#include "mec_rowops.h"
+
+namespace mec {
+
+// Agent-scope fences without the other half: a full __threadfence() also
+// invalidates this XCD's L2 (its acquire half), which throws out the operands
+// of the workgroups still running.  The arrivals only release (write back),
+// and only the workgroup that then reads the others' results acquires.
+__device__ __forceinline__ void release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
+constexpr int KEEP_T = 64;                       // tile (and index block) size
+constexpr int KEEP_MAX_N = 2048;                 // MEC_KEEP_EXP_MAX_N
+constexpr int KEEP_MAX_KT = KEEP_MAX_N / KEEP_T;  // blocks per side
+
+// The kept matrix and the forward's bookkeeping, carved from the workspace by
+// the host (256-byte aligned parts).
+struct KeepBufs {
+  float* E;         // np x np, row-major (pitch np): E, then H after k_keep_finalize
+  float* rowpart;   // [kt][np]: row sums of tile (p, q) at rowpart[q * np + i]
+  float* colpart;   // [kt][np]: column sums of tile (p, q) at colpart[p * np + j] (CLIP)
+  double* lossp;    // [kt]: loss terms of index block x, summed over its rows
+  unsigned* cnt;    // the finalize's count of finished diagonal blocks
+  int np, kt;
+};
+
+// Forward tiles: one 64 x 64 tile (p, q) of S per workgroup (kt x kt grid,
+// XCD-grouped order).  NORM: rx and ry from the squared norms the tile's own
+// fragments accumulate (gdma::NormHook: every wave sees all of K for its 32
+// rows and 32 columns), written to the workspace by the tiles of the first
+// block column (rx) and row (ry); rx = ry = 1 otherwise.
+template <bool LIT, bool NORM>
+__global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict__ X, int64_t ldx,
+                                                         const float* __restrict__ Y, int64_t ldy, int N, int D,
+                                                         float c, float* __restrict__ ws, KeepBufs kb) {
+  using TL = GemmTile<float, true, true>;
+  static_assert(TL::BM == KEEP_T && TL::BN == KEEP_T && TL::NT == 256 && TL::FM == 1 && TL::FN == 1,
+                "64 x 64 tiles of 2 x 2 waves");
+  __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
+  __shared__ float s_rx[KEEP_T], s_ry[KEEP_T], s_row[KEEP_T], s_col[KEEP_T], s_nx[KEEP_T], s_ny[KEEP_T];
+  const int64_t n64 = N;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / 2, wn = w % 2, T = kb.kt;
+  if (blockIdx.x == 0 && t == 0) *kb.cnt = 0u;  // (k_keep_finalize runs after this launch)
+  int tm, tn;
+  tile_swizzle(blockIdx.x, T * T, T, T, 8, tm, tn);
+  const int m0 = tm * KEEP_T, n0 = tn * KEEP_T;
+  const auto A = tile_op<TL>(X + (int64_t)m0 * ldx, ldx, min(N - m0, KEEP_T), D);
+  const auto B = tile_op<TL>(Y + (int64_t)n0 * ldy, ldy, min(N - n0, KEEP_T), D);
+  f32x16 acc[1][1];
+  float rxv = 1.f, ryv = 1.f;
+  if constexpr (NORM) {
+    const gdma::NormHook<typename TL::G> nh;
+    TL::run_fh(A, B, D, lds, acc, nh);
+    const float sa = nh.sa[0] + __shfl_xor(nh.sa[0], 32, 64);
+    const float sb = nh.sb[0] + __shfl_xor(nh.sb[0], 32, 64);
+    if (lane < 32) {
+      // 1/max(||v||, 1e-12), as F.normalize (clip_loss.py:266-268)
+      if (wn == 0) s_nx[wm * 32 + lane] = 1.f / fmaxf(sqrtf(sa), 1e-12f);
+      if (wm == 0) s_ny[wn * 32 + lane] = 1.f / fmaxf(sqrtf(sb), 1e-12f);
+    }
+    __syncthreads();
+    if (t < KEEP_T) {
+      rxv = s_nx[t];
+      ryv = s_ny[t];
+    }
+  } else {
+    TL::template run<true, true>(A, B, D, lds, acc);
+  }
+  if (t < KEEP_T) {
+    if (tn == 0 && m0 + t < N) ws[WS_RX * n64 + m0 + t] = rxv;
+    if (tm == 0 && n0 + t < N) ws[WS_RY * n64 + n0 + t] = ryv;
+  }
+  // the raw diagonal x_i . y_i (clip_loss.py:206): in a diagonal wave of a
+  // diagonal tile, lane l holds entry (c, c), c = l % 32, when l / 32 is bit
+  // 2 of c, in accumulator register 4 (c / 8) + c % 4
+  if (tm == tn && wm == wn) {
+    const int cc = lane & 31;
+    if ((lane >> 5) == ((cc >> 2) & 1)) {
+      const int rr = 4 * (cc >> 3) + (cc & 3);
+      float v = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v = r == rr ? acc[0][0][r] : v;
+      const int i = m0 + wm * 32 + cc;
+      if (i < N) ws[WS_DIAG * n64 + i] = v;
+    }
+  }
+  float rs, cs;
+  sumexp_tile<TL, LIT, NORM>(acc, c, m0, n0, N, rxv, ryv, s_rx, s_ry, s_row, s_col, rs, cs,
+                             kb.E + (int64_t)m0 * kb.np + n0, kb.np);
+  if (t < KEEP_T) {
+    kb.rowpart[(int64_t)tn * kb.np + m0 + t] = rs;
+    if (!LIT) kb.colpart[(int64_t)tm * kb.np + n0 + t] = cs;
+  }
+}
+
+// Forward finalize, one 64 x 64 block (p, q) of E per workgroup: thread r <
+// 64 takes row i = 64 p + r (R_i = its off-diagonal sum, the tile sums in
+// tile order, + e^{t_i}), thread 64 + r column j = 64 q + r (C_j, CLIP), in
+// fp64 as finalize_row; then the block becomes H_ij = rx_i ry_j E_ij
+// (1/R_i + 1/C_j) (LiT: rx_i ry_j E_ij / R_i) in place.  The diagonal blocks
+// (p = q: their rows and columns are the same indices) also write the loss
+// terms and the workspace vectors of their indices (clip_loss.py:206-211,
+// lit_loss.py:199-203), and the last of them to finish writes the loss (the
+// block partials in block order).
+template <bool LIT, bool NORM>
+__global__ __launch_bounds__(256) void k_keep_finalize(int N, double inv_t, float* __restrict__ ws, KeepBufs kb,
+                                                       float* __restrict__ loss) {
+  __shared__ float s_ir[KEEP_T], s_ic[KEEP_T], s_rx[KEEP_T], s_ry[KEEP_T];
+  __shared__ double s_term[2 * KEEP_T], s_kap[2 * KEEP_T];
+  const int64_t n64 = N;
+  const int t = threadIdx.x, T = kb.kt;
+  const int p = blockIdx.x / T, q = blockIdx.x - p * T;
+  const bool dg = p == q;
+  // thread t's part of the block, row t / 4, 16 consecutive columns: loaded
+  // first, so that it lands while the factors are formed
+  const int rr = t >> 2, c0 = (t & 3) * 16;
+  float* e = kb.E + (int64_t)(p * KEEP_T + rr) * kb.np + q * KEEP_T + c0;
+  f32x4 ev[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) ev[v] = *(const f32x4*)(e + 4 * v);
+  if (t < 2 * KEEP_T) {
+    const int role = t >> 6, r = t & 63;  // role 0: row i of block p; 1: column j of block q
+    const int idx = (role ? q : p) * KEEP_T + r;
+    double term = 0.0, kap = 0.0;
+    float inv = 0.f, nrm = 1.f;
+    if (idx < N) {
+      nrm = NORM ? ws[(role ? WS_RY : WS_RX) * n64 + idx] : 1.f;
+      if (!(LIT && role)) {
+        const float* part = role ? kb.colpart : kb.rowpart;
+        float pv[KEEP_MAX_KT];
+#pragma unroll
+        for (int k = 0; k < KEEP_MAX_KT; ++k) pv[k] = k < T ? part[(int64_t)k * kb.np + idx] : 0.f;
+        float off = 0.f;
+#pragma unroll
+        for (int k = 0; k < KEEP_MAX_KT; ++k)
+          if (k < T) off += pv[k];
+        const double s =
+            (double)ws[WS_DIAG * n64 + idx] * (double)ws[WS_RX * n64 + idx] * (double)ws[WS_RY * n64 + idx];
+        const double tt = (s - 1.0) * inv_t;
+        const double R = (double)off + exp(tt);
+        inv = (float)(1.0 / R);
+        if (dg) {
+          term = softplus_log_ratio(off, tt);
+          kap = -((double)off / R);
+          ws[(role ? WS_COL_OFF : WS_ROW_OFF) * n64 + idx] = off;
+          ws[(role ? WS_INV_COL : WS_INV_ROW) * n64 + idx] = inv;
+        }
+      }
+    }
+    (role ? s_ic : s_ir)[r] = inv;
+    (role ? s_ry : s_rx)[r] = nrm;
+    s_term[t] = term;
+    s_kap[t] = kap;
+  }
+  __syncthreads();
+  // E -> H
+  {
+    const float ai = s_rx[rr], ir = s_ir[rr];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      f32x4 h = ev[v];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = c0 + 4 * v + u;
+        h[u] *= ai * s_ry[j] * (LIT ? ir : ir + s_ic[j]);
+      }
+      *(f32x4*)(e + 4 * v) = h;
+    }
+  }
+  if (!dg) return;
+  if (t < KEEP_T) {
+    const int i = p * KEEP_T + t;
+    const double kap = LIT ? s_kap[t] : s_kap[t] + s_kap[KEEP_T + t];
+    const double v = LIT ? s_term[t] : s_term[t] + s_term[KEEP_T + t];
+    if (i < N) ws[WS_KAPPA * n64 + i] = (float)kap;
+    const double tot = wave_sum_f64(v);
+    if (t == 0) {
+      kb.lossp[p] = tot;
+      release_agent();
+      const unsigned old = __hip_atomic_fetch_add(kb.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == (unsigned)T - 1) {
+        acquire_agent();
+        double L = 0.0;
+        for (int x = 0; x < T; ++x) L += kb.lossp[x];
+        *loss = (float)(L / (LIT ? (double)N : 2.0 * (double)N));
+      }
+    }
+  }
+}
+
+// Backward contractions from H (one 64 x 64 output tile per workgroup;
+// x-side tiles first, each side's grid padded to a multiple of 8 and
+// XCD-grouped): the x side reads H by rows, the y side reads it transposed,
+// and both take the raw input rows of the other side as the feature operand
+// (16-byte lanes):
+//   acc_x[i, d] = sum_j H_ij y_j[d] = rx_i (G' Y^)[i, d]
+//   acc_y[j, d] = sum_i H_ij x_i[d] = ry_j (G'^T X^)[j, d]
+// i.e. the accumulators as mec_grad leaves them for fp32.
+__global__ __launch_bounds__(256, 2) void k_keep_contract(const float* __restrict__ X, int64_t ldx,
+                                                          const float* __restrict__ Y, int64_t ldy, int N, int D,
+                                                          KeepBufs kb, float* __restrict__ acc_x,
+                                                          float* __restrict__ acc_y, int ctd, int nx_pad,
+                                                          int ny_pad) {
+  using TCX = typename ConTileSmall<float, true, true>::x;
+  using TCY = typename ConTileSmall<float, true, true>::y;
+  static_assert(TCX::BM == KEEP_T && TCX::BN == KEEP_T && TCY::BM == KEEP_T && TCY::BN == KEEP_T &&
+                    TCX::FM == 1 && TCX::FN == 1 && TCY::FM == 1 && TCY::FN == 1 && TCX::NT == 256 &&
+                    TCY::NT == 256,
+                "64 x 64 tiles of 2 x 2 waves");
+  __shared__ __attribute__((aligned(1024))) char lds[CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int sub = blockIdx.x;
+  const bool is_x = sub < nx_pad;
+  if (!is_x) sub -= nx_pad;
+  const int pid = xcd_remap(sub, is_x ? nx_pad : ny_pad);
+  if (pid >= kb.kt * ctd) return;
+  int tm, td;
+  group_tile(pid, kb.kt, ctd, 8, tm, td);
+  const int r0 = tm * KEEP_T, d0 = td * KEEP_T;
+  const int ncols = min(D - d0, KEEP_T);
+  f32x16 acc[1][1];
+  if (is_x)
+    TCX::template run<true, true>(tile_op<TCX>(kb.E + (int64_t)r0 * kb.np, kb.np, KEEP_T, kb.np),
+                                  tile_op<TCX>(Y + d0, ldy, ncols, N), kb.np, lds, acc);
+  else
+    TCY::template run<true, true>(tile_op<TCY>(kb.E + r0, kb.np, KEEP_T, kb.np), tile_op<TCY>(X + d0, ldx, ncols, N),
+                                  kb.np, lds, acc);
+  float* out = is_x ? acc_x : acc_y;
+  const int wm = w / 2, wn = w % 2;
+  const int d = d0 + wn * 32 + (lane & 31);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = r0 + wm * 32 + acc_row(r, lane);
+    if (row < N && d < D) out[(int64_t)row * D + d] = acc[0][0][r];
+  }
+}
+
+}  // namespace mec

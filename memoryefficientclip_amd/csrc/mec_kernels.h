@@ -100,13 +100,14 @@ template <> struct PackOf<gdma::K_F32> { using type = PackF32; };
 // fp16 or fp32); TA_: A stored k-row-major (a transposed gradient-matrix
 // block); GB_: A a 16-bit gradient-matrix block in the blocked layout
 // (gdma::gb_offset; TA_ then selects the x side's reading); TB_: B stored
-// k-row-major (fp32 raw input rows; 1: 16-byte lanes, 2: 4-byte lanes)
+// k-row-major (fp32 raw input rows; 1: 16-byte lanes, 2: 4-byte lanes); S_:
+// stages of the LDS ring (gdma::Geo::S)
 template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND, int SA_ = 2, bool GB_ = false, bool ROLL_ = false,
-          int TB_ = 0>
+          int TB_ = 0, int S_ = 2>
 struct TileD : PackOf<KIND>::type {
   using Elem = typename std::conditional<KIND == gdma::K_F32, float, uint16_t>::type;
   using Op = gdma::Operand;
-  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, SA_, GB_, TB_>;
+  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, SA_, GB_, TB_, S_>;
   static constexpr bool TA = TA_, GB = GB_, ROLL = ROLL_;
   static constexpr int TB = TB_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
@@ -120,6 +121,18 @@ struct TileD : PackOf<KIND>::type {
     } else {
       gdma::mainloop<G, ZERO>(a, b, K, (char*)lds, acc);
     }
+  }
+  // run() with a hook on the operand values (gdma::NormHook; fp32 tiles)
+  template <class FH>
+  static __device__ __forceinline__ void run_fh(const Op& a, const Op& b, int K, void* lds, f32x16 (&acc)[FM][FN],
+                                                const FH& fh) {
+    static_assert(!ROLL, "the two-fragment-set schedule");
+    gdma::LoadPlan<G> lp;
+    gdma::prologue<G>(a, b, (char*)lds, lp);
+    int p0 = 0;
+    gdma::mainloop_core<G, true, false, gdma::NoHook, 0, FH>(lp, lp.ra, lp.rb, false, K, (char*)lds, p0, acc,
+                                                             gdma::NoHook(), false, fh);
+    gdma::drain_loads();
   }
   // Tiles in a chain (a persistent workgroup): start() issues the first
   // tile's chunk 0; chain() runs one tile and, with has_next, leaves chunk 0
@@ -154,9 +167,17 @@ template <typename T> struct FwdTileSel<T, false, true> { using type = Tile16V<I
 template <typename T, bool VEC> using FwdTile = typename FwdTileSel<T, VEC>::type;
 // fp32 at a small N (few 128 x 128 tiles for the CUs): 64 x 64 direct-to-LDS
 // tiles of 2 x 2 waves (32 x 32 each) for the forward, the gradient-matrix
-// tiles and the contractions
+// tiles and the contractions, on a ring of SMALL_STAGES stages (16 KB each):
+// one wave per SIMD and 16 MFMAs per chunk leave two stages too short a lead
+// for the operand loads
+#ifndef MEC_SMALL_STAGES
+#define MEC_SMALL_STAGES 4
+#endif
+constexpr int SMALL_STAGES = MEC_SMALL_STAGES;
 template <typename T, bool VEC, bool SMALL> struct GemmTileSel { using type = FwdTile<T, VEC>; };
-template <> struct GemmTileSel<float, true, true> { using type = TileD<64, 64, false, 2, 2, gdma::K_F32>; };
+template <> struct GemmTileSel<float, true, true> {
+  using type = TileD<64, 64, false, 2, 2, gdma::K_F32, 2, false, false, 0, SMALL_STAGES>;
+};
 template <typename T, bool VEC, bool SMALL> using GemmTile = typename GemmTileSel<T, VEC, SMALL>::type;
 // Contractions.  fp32 stores each gradient-matrix block once, row-major and
 // scaled by both norms (H = diag(rx) G' diag(ry)), and runs the contractions
@@ -202,8 +223,8 @@ template <typename T, bool VEC, bool SMALL> struct ConTileSmall {
   using y = ConTileY<T, VEC>;
 };
 template <bool VEC> struct ConTileSmall<float, VEC, true> {
-  using x = TileD<64, 64, false, 2, 2, gdma::K_F32, 2, false, false, VEC ? 1 : 2>;
-  using y = TileD<64, 64, true, 2, 2, gdma::K_F32, 2, false, false, VEC ? 1 : 2>;
+  using x = TileD<64, 64, false, 2, 2, gdma::K_F32, 2, false, false, VEC ? 1 : 2, SMALL_STAGES>;
+  using y = TileD<64, 64, true, 2, 2, gdma::K_F32, 2, false, false, VEC ? 1 : 2, SMALL_STAGES>;
 };
 // the 16-bit types keep one layout of the gradient-matrix blocks (G'^T)
 template <typename T> struct GtOnly { static constexpr bool value = Is16<T>::value; };
@@ -232,10 +253,14 @@ template <int A, int B> struct CMax { static constexpr int value = A > B ? A : B
 // E = exp2(S c - c) of this wave's TM x TN accumulators (S scaled by rx_i ry_j
 // when NORM); rowv[bm * 16 + r] and colv[bn] collect this lane's partial row
 // and column sums.  MASK zeroes the diagonal and entries outside [0, N).
+// Eb (not null): every entry of the tile, masked ones as 0, is also stored at
+// Eb[row * ldE + column] (tile-relative; each 32-lane half writes 128 bytes
+// of one row).
 template <class TL, bool NORM, bool MASK>
 __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::FN], float c, int m0, int n0, int N,
                                                 const float* s_rx, const float* s_ry, float (&rowv)[TL::FM * 16],
-                                                float (&colv)[TL::FN]) {
+                                                float (&colv)[TL::FN], float* __restrict__ Eb = nullptr,
+                                                int ldE = 0) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
 #pragma unroll
   for (int k = 0; k < TL::FM * 16; ++k) rowv[k] = 0.f;
@@ -254,6 +279,7 @@ __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::
         const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
         float e = fast_exp2(fmaf(sc, cy, -c));
         if (MASK) e = (i < N && j < N && i != j) ? e : 0.f;
+        if (Eb) Eb[(int64_t)ml * ldE + nl] = e;
         rowv[bm * 16 + r] += e;
         cs += e;
       }
@@ -276,7 +302,8 @@ __device__ __forceinline__ void lds_barrier() {
 template <class TL, bool LIT, bool NORM>
 __device__ __forceinline__ void sumexp_tile(const f32x16 (&acc)[TL::FM][TL::FN], float c, int m0, int n0, int N,
                                             float rxv, float ryv, float* s_rx, float* s_ry, float* s_row,
-                                            float* s_col, float& rs_out, float& cs_out) {
+                                            float* s_col, float& rs_out, float& cs_out, float* __restrict__ Eb = nullptr,
+                                            int ldE = 0) {
   static_assert(TL::NT >= TL::BM && TL::NT >= TL::BN, "one row and one column per thread");
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / TL::WN, wn = w % TL::WN;
   if (t < TL::BM) {
@@ -294,9 +321,9 @@ __device__ __forceinline__ void sumexp_tile(const f32x16 (&acc)[TL::FM][TL::FN],
   // interior tiles (no diagonal entry, no row or column beyond N) need no mask
   const bool diag = m0 < n0 + TL::BN && n0 < m0 + TL::BM;
   if (!diag && m0 + TL::BM <= N && n0 + TL::BN <= N)
-    sumexp_epilogue<TL, NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
+    sumexp_epilogue<TL, NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv, Eb, ldE);
   else
-    sumexp_epilogue<TL, NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv);
+    sumexp_epilogue<TL, NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv, Eb, ldE);
   if constexpr (TL::FM == 1) {
     // one 32-row block: its 16 row sums padded to the 32 of the reduction
     float v[32];

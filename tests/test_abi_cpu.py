@@ -158,7 +158,7 @@ def test_sumexp_rejects_invalid_arguments(field, value, needle):
 
 
 @pytest.mark.parametrize("mode,ok", [(0, True), (1, True), (0x100, True), (0x101, True), (2, False),
-                                     (0x102, False), (0x200, False), (0x300, False), (-1, False)])
+                                     (0x102, False), (0x400, False), (0x500, False), (-1, False)])
 def test_mode_and_deterministic_flag(mode, ok):
     # validation only: a null workspace stops every valid call before any launch
     lib = _lib.load()
@@ -226,6 +226,96 @@ def test_config1_extra_memory():
     ws = lib.mec_workspace_floats_for(n, d, 0) * 4
     assert scratch == dense
     assert scratch + ws <= 2 * dense
+
+
+def test_keep_exp_sizes_and_support(monkeypatch):
+    # MEC_FLAG_KEEP_EXP (small fp32 problems): the kept matrix and the
+    # forward's bookkeeping in the workspace, no gradient scratch
+    lib = _lib.load()
+    K = _lib.FLAG_KEEP_EXP
+    n, d = 1024, 512
+    dense = n * n * 4
+    base = lib.mec_workspace_floats_for(n, d, 0)
+    assert lib.mec_workspace_floats_mode(n, d, 0, 0) == base
+    assert lib.mec_workspace_floats_mode(n, d, 0, 0x100) == base
+
+    def up(f):  # 256-byte aligned parts
+        return (f + 63) // 64 * 64
+
+    def keep_floats(base, np_):
+        kt = np_ // 64
+        o = up(up(up(up(base) + np_ * np_) + kt * np_) + kt * np_)
+        return up(o + 2 * kt) + 1
+
+    expect = keep_floats(base, 1024)
+    assert lib.mec_workspace_floats_mode(n, d, 0, K) == expect
+    assert lib.mec_workspace_floats_mode(n, d, 0, K | 0x100 | 1) == expect
+    # ragged n: np = n rounded up to 64
+    assert lib.mec_workspace_floats_mode(1000, d, 0, K) == keep_floats(lib.mec_workspace_floats_for(1000, d, 0), 1024)
+    assert lib.mec_workspace_floats_mode(65, 8, 0, K) == keep_floats(lib.mec_workspace_floats_for(65, 8, 0), 128)
+    assert lib.mec_grad_scratch_bytes_for(n, d, 0, K, 3) == 0
+    assert lib.mec_grad_scratch_bytes_for(n, d, 0, K | 1, 1) == 0
+    # configuration 1 with the kept matrix: the workspace is all the extra memory
+    assert lib.mec_workspace_floats_mode(n, d, 0, K) * 4 <= 2 * dense
+    # limits: fp32 only, n <= 2048
+    assert _lib.KEEP_EXP_MAX_N == 2048
+    assert lib.mec_workspace_floats_mode(2048, d, 0, K) > 0
+    assert lib.mec_workspace_floats_mode(2049, d, 0, K) < 0
+    for dt in (1, 2, 3, 4):
+        assert lib.mec_workspace_floats_mode(n, d, dt, K) < 0
+        assert lib.mec_grad_scratch_bytes_for(n, d, dt, K, 3) < 0
+    assert lib.mec_grad_scratch_bytes_for(2049, d, 0, K, 3) < 0
+    # which inputs qualify (host-only checks of the pointers and strides)
+    A = 1 << 20
+    assert lib.mec_keep_exp_supported(A, d, A, d, n, d, 0) == 1
+    assert lib.mec_keep_exp_supported(A, d, A, d, 1, 4, 0) == 1
+    assert lib.mec_keep_exp_supported(A + 4, d, A, d, n, d, 0) == 0
+    assert lib.mec_keep_exp_supported(A, d, A + 8, d, n, d, 0) == 0
+    assert lib.mec_keep_exp_supported(A, d + 2, A, d, n, d, 0) == 0
+    assert lib.mec_keep_exp_supported(A, 6, A, 6, n, 6, 0) == 0
+    assert lib.mec_keep_exp_supported(A, d, A, d, 2049, d, 0) == 0
+    assert lib.mec_keep_exp_supported(A, d, A, d, n, d - 1, 0) == 0
+    assert lib.mec_keep_exp_supported(None, d, A, d, n, d, 0) == 0
+    for dt in (1, 2, 3, 4):
+        assert lib.mec_keep_exp_supported(A, d, A, d, n, d, dt) == 0
+    monkeypatch.setenv("MEC_KEEP_EXP", "0")
+    assert lib.mec_keep_exp_supported(A, d, A, d, n, d, 0) == 0
+
+
+def test_keep_exp_flag_validation():
+    # rejected before any launch: the one-stage functions take no
+    # MEC_FLAG_KEEP_EXP, and mec_forward / mec_grad / mec_backward take it only
+    # for inputs that qualify and a 16-byte aligned workspace
+    lib = _lib.load()
+    K = _lib.FLAG_KEEP_EXP
+    A = 1 << 20
+    rc = lib.mec_sumexp(A, 64, A, 64, 100, 64, 0, K, 1, 0.07, A, None)
+    assert rc == _lib.MEC_ERR_INVALID and "MEC_FLAG_KEEP_EXP" in _lib.last_error()
+    rc = lib.mec_finalize(100, K, 0.07, A, A, None)
+    assert rc == _lib.MEC_ERR_INVALID and "MEC_FLAG_KEEP_EXP" in _lib.last_error()
+    rc = lib.mec_grad_step(A, 64, A, 64, 100, 64, 0, K, 1, 0.07, A, 0, A, 1 << 30, A, A, None)
+    assert rc == _lib.MEC_ERR_INVALID and "MEC_FLAG_KEEP_EXP" in _lib.last_error()
+    for dt in (1, 3):
+        rc = lib.mec_forward(A, 64, A, 64, 100, 64, dt, K, 1, 0.07, A, A, None)
+        assert rc == _lib.MEC_ERR_INVALID and "needs" in _lib.last_error()
+    rc = lib.mec_forward(A, 64, A, 64, 3000, 64, 0, K, 1, 0.07, A, A, None)
+    assert rc == _lib.MEC_ERR_INVALID and "n <= 2048" in _lib.last_error()
+    rc = lib.mec_forward(A + 4, 64, A, 64, 100, 64, 0, K, 1, 0.07, A, A, None)
+    assert rc == _lib.MEC_ERR_INVALID and "aligned rows" in _lib.last_error()
+    rc = lib.mec_forward(A, 64, A, 64, 100, 64, 0, K, 1, 0.07, A + 8, A, None)
+    assert rc == _lib.MEC_ERR_INVALID and "aligned workspace" in _lib.last_error()
+    rc = lib.mec_grad(A, 64, A, 64, 100, 64, 0, K, 1, 0.07, A + 8, None, 0, A, A, None)
+    assert rc == _lib.MEC_ERR_INVALID and "aligned workspace" in _lib.last_error()
+    rc = lib.mec_backward(A, 62, A, 62, 100, 62, 0, K, 1, 0.07, 1.0, A, None, None, 0, A, A, A, A, None)
+    assert rc == _lib.MEC_ERR_INVALID and "MEC_FLAG_KEEP_EXP" in _lib.last_error()
+    rc = lib.mec_backward_noalloc(A, 62, A, 62, 100, 62, 0, K, 1, 0.07, 1.0, A, None, A, A, A, A, None)
+    assert rc == _lib.MEC_ERR_INVALID and "MEC_FLAG_KEEP_EXP" in _lib.last_error()
+    # the plan of a kept-matrix backward
+    p = _lib.backward_plan(1000, 512, 0, K, compute_units=256)
+    assert (p.block_rows, p.num_blocks, p.scratch_bytes, p.noalloc_scratch_bytes) == (1024, 1, 0, 0)
+    assert (p.contract_tile_rows, p.contract_tile_features) == (64, 64)
+    with pytest.raises(_lib.MecError, match="MEC_FLAG_KEEP_EXP"):
+        _lib.backward_plan(4096, 512, 0, K, compute_units=256)
 
 
 def test_backward_plan():
