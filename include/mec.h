@@ -42,8 +42,9 @@
  *     16-bit types, 4 for fp32) use the direct-to-LDS tiles; other layouts
  *     are supported at lower speed.
  *   - mode: MEC_MODE_CLIP or MEC_MODE_LIT, optionally OR
- *     MEC_FLAG_DETERMINISTIC.  Every function accepts the flag; only the
- *     forward sums (mec_sumexp, mec_forward) depend on it.
+ *     MEC_FLAG_DETERMINISTIC (every function accepts it; only the forward
+ *     sums, mec_sumexp and mec_forward, depend on it) and MEC_FLAG_KEEP_EXP
+ *     (small fp32 problems; see there).
  *   - All work is enqueued on `stream` (a hipStream_t; NULL = default
  *     stream), which must belong to the current HIP device (the device of
  *     the data; the forward sizes its persistent launches by that device's
@@ -202,6 +203,8 @@ int mec_keep_exp_supported(const void* x, int64_t ldx, const void* y, int64_t ld
  * (fp32) or 256 rows, until the gradient-matrix buffers fit
  * min(16 GiB, max(64 n d elem, 256 MiB)): O(n*d).  Examples: n = 32768,
  * d = 1152 fp32 CLIP 1.07 GB; LiT the same; n = 1024, d = 512 fp32 4.2 MB.
+ * With MEC_FLAG_KEEP_EXP in mode: 0 (the backward contracts the kept
+ * matrix); < 0 where the flag does not apply (dtype, n).
  * Returns < 0 on bad args or n outside [1, 2^22]. */
 int64_t mec_grad_scratch_bytes_for(int64_t n, int64_t d, int dtype, int mode, int sides);
 
@@ -253,7 +256,10 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
 int mec_finalize(int64_t n, int mode, float temperature, float* workspace, float* loss,
                  void* stream);
 
-/* prepass + sumexp + finalize. */
+/* prepass + sumexp + finalize.  With MEC_FLAG_KEEP_EXP: the similarity
+ * tiles (with the norms and the diagonal) and the finalize of the kept
+ * matrix, two launches; the workspace then holds the scaled gradient matrix
+ * for the backward. */
 int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                 int dtype, int mode, int normalize, float temperature, float* workspace,
                 float* loss, void* stream);
@@ -270,7 +276,9 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
  * acc_x is rx_i sum_j G'_ij y^_j (and acc_y's row j ry_j sum_i G'_ij x^_i;
  * rx = ry = 1 when normalize = 0), which mec_postpass expects for that dtype;
  * row strides up to 2^24 elements (MEC_ERR_UNSUPPORTED beyond).
- * Equivalent to mec_grad_step for step = 0 .. num_blocks in order. */
+ * Equivalent to mec_grad_step for step = 0 .. num_blocks in order.  With
+ * MEC_FLAG_KEEP_EXP (as passed to mec_forward): one launch that contracts the
+ * kept matrix, the same accumulators; scratch is not used and may be NULL. */
 int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
              int dtype, int mode, int normalize, float temperature, const float* workspace,
              void* scratch, int64_t scratch_bytes, float* acc_x, float* acc_y, void* stream);
