@@ -717,8 +717,10 @@ __device__ __forceinline__ void prologue(const Operand& A, const Operand& B, cha
   }
   static_for<G::IPW>([&](auto i) { lp.template issue<i>(0, G::a_stage(lds, 0), G::b_stage(lds, 0)); });
   // deeper rings: chunks 1 .. S - 2 as well
-  for (int c = 1; c < G::S - 1; ++c)
-    static_for<G::IPW>([&](auto i) { lp.template issue<i>(c * G::BK, G::a_stage(lds, c), G::b_stage(lds, c)); });
+  if constexpr (G::S > 2) {
+    for (int c = 1; c < G::S - 1; ++c)
+      static_for<G::IPW>([&](auto i) { lp.template issue<i>(c * G::BK, G::a_stage(lds, c), G::b_stage(lds, c)); });
+  }
   // three A stages: A's chunk 1 as well, issued last (the first barrier waits for all but it)
   if constexpr (G::SA == 3)
     static_for<LoadPlan<G>::A_LOADS>([&](auto i) { lp.template issue<i>(G::BK, G::a_stage(lds, 1), nullptr); });
@@ -804,7 +806,7 @@ __device__ __forceinline__ void mainloop_core(LoadPlan<G>& lp, __amdgpu_buffer_r
       na = G::a_stage(lds, (kt + 2) % 3);
       nb = G::b_stage(lds, (kt + 1) & 1);
     }
-    int k1 = (kt + G::S - 1) * BK;
+    int k1 = (kt + (G::S - 1)) * BK;  // (so grouped, S = 2 compiles as the two-stage loop did)
     if constexpr (CHAIN) {
       if (kt + 1 == nk && has_next) {
         lp.ra = ra_next;
