@@ -1179,11 +1179,19 @@ int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   // fp32 (not the split modes): the accumulators carry the row's inverse norm
   // (the contractions of H = diag(rx) G' diag(ry) with the raw inputs)
   const bool accr = dtype == MEC_DTYPE_F32;
+  // fp32 data with every row 16-byte aligned: 16-byte vectors
+  const bool pvec = data_dtype(dtype) == MEC_DTYPE_F32 && d % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 &&
+                    aligned16(x) && aligned16(y) && aligned16(acc_x) && aligned16(acc_y) && aligned16(dx) &&
+                    aligned16(dy);
   DISPATCH_DTYPE(data_dtype(dtype), T, DISPATCH_BOOL(normalize, NORM, DISPATCH_BOOL(accr, ACCR, {
     const PostSide<T> px{(const T*)x, ldx, (const T*)y, ldy, rx, ry, acc_x, (T*)dx};
     const PostSide<T> py{(const T*)y, ldy, (const T*)x, ldx, ry, rx, acc_y, (T*)dy};
-    if constexpr (!ACCR || std::is_same<T, float>::value)
+    if constexpr (std::is_same<T, float>::value) {
+      DISPATCH_BOOL(pvec, VEC,
+          k_postpass<T, NORM, ACCR, VEC><<<grid, 256, 0, s>>>(acc_x ? px : py, py, N, D, kap, a, grad_output));
+    } else if constexpr (!ACCR) {
       k_postpass<T, NORM, ACCR><<<grid, 256, 0, s>>>(acc_x ? px : py, py, N, D, kap, a, grad_output);
+    }
   })));
   return check_launch("postpass");
 }

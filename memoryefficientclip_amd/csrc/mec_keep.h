@@ -177,6 +177,21 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, double inv_t, floa
     s_kap[t] = kap;
   }
   __syncthreads();
+  // the diagonal blocks' loss partial first (its count's round trip then
+  // overlaps the block's E -> H)
+  bool last = false;
+  if (dg && t < KEEP_T) {
+    const int i = p * KEEP_T + t;
+    const double kap = LIT ? s_kap[t] : s_kap[t] + s_kap[KEEP_T + t];
+    const double v = LIT ? s_term[t] : s_term[t] + s_term[KEEP_T + t];
+    if (i < N) ws[WS_KAPPA * n64 + i] = (float)kap;
+    const double tot = wave_sum_f64(v);
+    if (t == 0) {
+      kb.lossp[p] = tot;
+      release_agent();
+      last = __hip_atomic_fetch_add(kb.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)T - 1;
+    }
+  }
   // E -> H
   {
     const float ai = s_rx[rr], ir = s_ir[rr];
@@ -191,24 +206,12 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, double inv_t, floa
       *(f32x4*)(e + 4 * v) = h;
     }
   }
-  if (!dg) return;
-  if (t < KEEP_T) {
-    const int i = p * KEEP_T + t;
-    const double kap = LIT ? s_kap[t] : s_kap[t] + s_kap[KEEP_T + t];
-    const double v = LIT ? s_term[t] : s_term[t] + s_term[KEEP_T + t];
-    if (i < N) ws[WS_KAPPA * n64 + i] = (float)kap;
-    const double tot = wave_sum_f64(v);
-    if (t == 0) {
-      kb.lossp[p] = tot;
-      release_agent();
-      const unsigned old = __hip_atomic_fetch_add(kb.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (old == (unsigned)T - 1) {
-        acquire_agent();
-        double L = 0.0;
-        for (int x = 0; x < T; ++x) L += kb.lossp[x];
-        *loss = (float)(L / (LIT ? (double)N : 2.0 * (double)N));
-      }
-    }
+  if (last) {
+    // every diagonal block's partial is in (they released before counting)
+    acquire_agent();
+    double L = 0.0;
+    for (int x = 0; x < T; ++x) L += kb.lossp[x];
+    *loss = (float)(L / (LIT ? (double)N : 2.0 * (double)N));
   }
 }
 

@@ -175,10 +175,14 @@ struct PostSide {
 // contractions multiply H = diag(rx) G' diag(ry) with the raw inputs.  Then
 // h = a (kappa_i r_i y^_i + acc) = r_i dx^_i, and the normalisation backward
 // r_i (dx^ - x^ <x^, dx^>) is h - x^ <x^, h>: no division by the norm.
-template <typename T, bool NORM, bool ACCR = false>
+// VEC (fp32; every row of own, oth, acc and out 16-byte aligned, D a multiple
+// of 4): the register path reads and writes 16-byte vectors, four
+// consecutive features per lane.
+template <typename T, bool NORM, bool ACCR = false, bool VEC = false>
 __global__ __launch_bounds__(256) void k_postpass(PostSide<T> s0, PostSide<T> s1, int N, int D,
                                                   const float* __restrict__ kappa, float a,
                                                   const float* __restrict__ grad_output) {
+  static_assert(!VEC || std::is_same<T, float>::value, "16-byte vectors of fp32");
   const PostSide<T>& sd = blockIdx.y ? s1 : s0;
   const T* __restrict__ own = sd.own;
   const int64_t ld_own = sd.ld_own;
@@ -201,6 +205,39 @@ __global__ __launch_bounds__(256) void k_postpass(PostSide<T> s0, PostSide<T> s1
   if (NORM) {
     float dot = 0.f;
     const bool clamped = ro >= 1e12f;
+    if (VEC && D <= 64 * POST_REG) {
+      constexpr int NV = POST_REG / 4;
+      f32x4 g[NV], xr[NV];
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int d = 4 * lane + 256 * k;
+        g[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        xr[k] = g[k];
+        if (d < D) {
+          const f32x4 yv = *(const f32x4*)(yo + d), av = *(const f32x4*)(ac + d), xv = *(const f32x4*)(xo + d);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            g[k][u] = a * fmaf(kq, yv[u], av[u]);
+            xr[k][u] = xv[u] * ro;
+            dot = fmaf(xr[k][u], g[k][u], dot);
+          }
+        }
+      }
+      dot = wave_sum(dot);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int d = 4 * lane + 256 * k;
+        if (d < D) {
+          f32x4 v;
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            v[u] = go * (ACCR ? (clamped ? g[k][u] : g[k][u] - xr[k][u] * dot)
+                              : (clamped ? ro * g[k][u] : ro * (g[k][u] - xr[k][u] * dot)));
+          *(f32x4*)((float*)o + d) = v;
+        }
+      }
+      return;
+    }
     if (D <= 64 * POST_REG) {
       // the row stays in registers between the reduction and the stores
       float g[POST_REG], xr[POST_REG];
