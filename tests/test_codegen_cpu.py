@@ -10,6 +10,11 @@ drop without any change in results, so no parity test would notice:
   its hint in the one-plane case, which cost 3% of a config-4 step.)
 * the contractions (`k_grad_contract`) load their gradient-matrix operand
   with direct-to-LDS loads carrying `nt`, and their other operand without.
+* the kept-exponential forward's tile kernel has no cache maintenance at all,
+  and its finalize invalidates the L2 (the acquire half of an agent-scope
+  fence) only in the one workgroup that reads the others' loss partials: a
+  full fence in every workgroup of the tile kernel invalidated the XCD's L2
+  under the workgroups still running and cost 14 us of a 31 us launch.
 """
 import os
 import re
@@ -80,3 +85,12 @@ def test_contraction_streams_its_gradient_matrix_operand(funcs):
         loads = [l for l in body if re.match(r"buffer_load_dwordx4 .* lds", l)]
         nt = [l for l in loads if re.search(r"\bnt\b", l)]
         assert nt and len(nt) < len(loads), (name, len(nt), len(loads))
+
+
+def test_kept_exponential_kernels_fence_once(funcs):
+    for name, body in _select(funcs, "_ZN3mec14k_keep_forward").items():
+        assert not any(re.match(r"buffer_(inv|wbl2)", l) for l in body), name
+    for name, body in _select(funcs, "_ZN3mec15k_keep_finalize").items():
+        inv = [l for l in body if re.match(r"buffer_inv", l)]
+        wbl2 = [l for l in body if re.match(r"buffer_wbl2", l)]
+        assert len(inv) == 1 and len(wbl2) == 1, (name, len(inv), len(wbl2))
