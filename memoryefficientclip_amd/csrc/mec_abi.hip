@@ -237,7 +237,7 @@ bool keep_shape_ok(int64_t n, int dtype) { return dtype == MEC_DTYPE_F32 && n <=
 int64_t align256b(int64_t floats) { return (floats + 63) & ~int64_t(63); }
 struct KeepLayout {
   int np, kt;                                     // n rounded up to 64, np / 64
-  int64_t e, rowpart, colpart, lossp, cnt, total;
+  int64_t s, rowpart, colpart, rowdot, coldot, lossp, cnt, total;
 };
 KeepLayout keep_layout(int64_t n, int64_t d, int dtype) {
   KeepLayout L;
@@ -245,11 +245,15 @@ KeepLayout keep_layout(int64_t n, int64_t d, int dtype) {
   L.np = L.kt * KEEP_T;
   const int64_t np = L.np;
   int64_t o = align256b(workspace_floats_for(n, d, dtype));
-  L.e = o;
+  L.s = o;
   o = align256b(o + np * np);
   L.rowpart = o;
   o = align256b(o + L.kt * np);
   L.colpart = o;
+  o = align256b(o + L.kt * np);
+  L.rowdot = o;
+  o = align256b(o + L.kt * np);
+  L.coldot = o;
   o = align256b(o + L.kt * np);
   L.lossp = o;
   o = align256b(o + 2 * (int64_t)L.kt);
@@ -262,8 +266,9 @@ int64_t workspace_floats_mode(int64_t n, int64_t d, int dtype, int mode) {
 }
 KeepBufs keep_bufs(const float* workspace, const KeepLayout& L) {
   float* ws = const_cast<float*>(workspace);
-  return KeepBufs{ws + L.e, ws + L.rowpart, ws + L.colpart, (double*)(ws + L.lossp), (unsigned*)(ws + L.cnt),
-                  L.np, L.kt};
+  return KeepBufs{ws + L.s,      ws + L.rowpart,          ws + L.colpart,          ws + L.rowdot,
+                  ws + L.coldot, (double*)(ws + L.lossp), (unsigned*)(ws + L.cnt), L.np,
+                  L.kt};
 }
 // MEC_KEEP_EXP=0 reports no support (the glue asks before it sets the flag;
 // tests of the other path)
@@ -813,8 +818,8 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
     rc = check_keep(x, ldx, y, ldy, n, d, dtype, workspace);
     if (!rc) rc = check_not_capturing(stream);
     if (rc) return rc;
-    // the similarity tiles (norms, diagonal, E, per-tile sums), then the
-    // finalize (sums, loss, E -> H)
+    // the similarity tiles (norms, diagonal, similarities, per-tile sums),
+    // then the finalize (sums, loss, similarities -> H, sums of G' cos)
     const KeepLayout L = keep_layout(n, d, dtype);
     const KeepBufs kb = keep_bufs(workspace, L);
     hipStream_t s = (hipStream_t)stream;
@@ -825,7 +830,7 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
     DISPATCH_BOOL(is_lit(mode), LIT, DISPATCH_BOOL(normalize, NORM, {
       k_keep_forward<LIT, NORM><<<grid, 256, 0, s>>>((const float*)x, ldx, (const float*)y, ldy, N, D, c, workspace,
                                                      kb);
-      k_keep_finalize<LIT, NORM><<<grid, 256, 0, s>>>(N, inv_t, workspace, kb, loss);
+      k_keep_finalize<LIT, NORM><<<grid, 256, 0, s>>>(N, c, inv_t, workspace, kb, loss);
     }));
     return check_launch("forward (kept exponentials)");
   }
@@ -1047,16 +1052,35 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
 // The backward's contractions from the kept matrix (MEC_FLAG_KEEP_EXP; a
 // checked problem; H since the forward's finalize): one launch, into acc_x /
 // acc_y as mec_grad leaves them.
-static int keep_grad_run(const StepArgs& a, void* stream) {
+// The kept-exponential backward: the contractions into acc_x / acc_y
+// (mec_grad; post == NULL), or with the post-pass in their epilogue into the
+// outputs of *post (mec_backward, mec_backward_noalloc; one launch).
+static int keep_grad_run(const StepArgs& a, const KeepPost* post, void* stream) {
   const KeepLayout L = keep_layout(a.n, a.d, a.dtype);
   const KeepBufs kb = keep_bufs(a.workspace, L);
   const int ctd = (int)((a.d + KEEP_T - 1) / KEEP_T);
-  const int nx_pad = a.acc_x ? round8(kb.kt * ctd) : 0, ny_pad = a.acc_y ? round8(kb.kt * ctd) : 0;
+  const bool sx = post ? post->dx != nullptr : a.acc_x != nullptr;
+  const bool sy = post ? post->dy != nullptr : a.acc_y != nullptr;
+  const int nx_pad = sx ? round8(kb.kt * ctd) : 0, ny_pad = sy ? round8(kb.kt * ctd) : 0;
+  const unsigned grid = (unsigned)(nx_pad + ny_pad);
   hipStream_t s = (hipStream_t)stream;
-  k_keep_contract<<<(unsigned)(nx_pad + ny_pad), 256, 0, s>>>((const float*)a.x, a.ldx, (const float*)a.y, a.ldy,
-                                                              (int)a.n, (int)a.d, kb, a.acc_x, a.acc_y, ctd, nx_pad,
-                                                              ny_pad);
-  return check_launch("grad (kept exponentials)");
+  const float* x = (const float*)a.x;
+  const float* y = (const float*)a.y;
+  if (!post) {
+    k_keep_contract<false, false><<<grid, 256, 0, s>>>(x, a.ldx, y, a.ldy, (int)a.n, (int)a.d, kb, a.acc_x, a.acc_y,
+                                                      KeepPost{}, ctd, nx_pad, ny_pad);
+    return check_launch("grad (kept exponentials)");
+  }
+  DISPATCH_BOOL(a.normalize, NORM, {
+    k_keep_contract<true, NORM><<<grid, 256, 0, s>>>(x, a.ldx, y, a.ldy, (int)a.n, (int)a.d, kb, nullptr, nullptr,
+                                                     *post, ctd, nx_pad, ny_pad);
+  });
+  return check_launch("backward (kept exponentials)");
+}
+// the fused post-pass operands of a kept-exponential backward
+static KeepPost keep_post(const StepArgs& a, float grad_scale, const float* grad_output, void* dx, void* dy) {
+  const float sc = (float)((double)grad_scale / (is_lit(a.mode) ? (double)a.n : 2.0 * (double)a.n));
+  return KeepPost{a.workspace, grad_output, (float*)dx, is_lit(a.mode) ? nullptr : (float*)dy, sc};
 }
 
 // the caller's scratch against the default layout for the problem's sides
@@ -1097,7 +1121,7 @@ int mec_grad(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, 
     rc = check_keep(x, ldx, y, ldy, n, d, dtype, workspace);
     if (!rc) rc = check_not_capturing(stream);
     if (rc) return rc;
-    return keep_grad_run(a, stream);
+    return keep_grad_run(a, nullptr, stream);
   }
   ScratchLayout L;
   if (!rc) rc = check_scratch(a, scratch, scratch_bytes, &L);
@@ -1125,10 +1149,9 @@ int mec_backward_noalloc(const void* x, int64_t ldx, const void* y, int64_t ldy,
     // the kept matrix needs no scratch, so the array is not touched
     rc = check_keep(x, ldx, y, ldy, n, d, dtype, workspace);
     if (!rc) rc = check_not_capturing(stream);
-    if (!rc) rc = keep_grad_run(a, stream);
     if (rc) return rc;
-    return mec_postpass(x, ldx, y, ldy, n, d, dtype, mode, normalize, grad_scale, workspace, grad_output, a.acc_x,
-                        a.acc_y, dx, dy, stream);
+    const KeepPost post = keep_post(a, grad_scale, grad_output, dx, dy);
+    return keep_grad_run(a, &post, stream);
   }
   bool ok = false;
   const ScratchLayout L = noalloc_layout(n, d, dtype, a.sides(), &ok);
@@ -1201,6 +1224,21 @@ int mec_backward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
                  const float* grad_output, void* scratch, int64_t scratch_bytes, float* acc_x, float* acc_y,
                  void* dx, void* dy, void* stream) {
   g_err.clear();
+  if (keep_flag(mode)) {
+    // the kept matrix: one launch, the post-pass in the contractions' epilogue
+    StepArgs a{x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, acc_x, acc_y};
+    int rc = check_step_args(a);
+    if (rc) return rc;
+    if (!std::isfinite(grad_scale)) return fail(MEC_ERR_INVALID, "grad_scale must be finite");
+    if (is_lit(mode)) dy = nullptr;
+    if ((a.acc_x == nullptr) != (dx == nullptr) || (a.acc_y == nullptr) != (dy == nullptr))
+      return fail(MEC_ERR_INVALID, "each side needs both its accumulator and its output (or neither)");
+    rc = check_keep(x, ldx, y, ldy, n, d, dtype, workspace);
+    if (!rc) rc = check_not_capturing(stream);
+    if (rc) return rc;
+    const KeepPost post = keep_post(a, grad_scale, grad_output, dx, dy);
+    return keep_grad_run(a, &post, stream);
+  }
   int rc = mec_grad(x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, scratch,
                     scratch_bytes, acc_x, acc_y, stream);
   if (rc) return rc;

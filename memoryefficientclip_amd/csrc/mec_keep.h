@@ -2,24 +2,28 @@
 // backward (MEC_FLAG_KEEP_EXP, n <= MEC_KEEP_EXP_MAX_N, 16-byte rows).
 //
 // At n ~ 1000 every launch is short and the similarity GEMM is a large part
-// of the step.  The forward keeps E_ij = exp((S_ij - 1)/T) (0 on the diagonal
-// and outside [0, n)), np x np floats (np = n rounded up to 64), and turns it
-// into the scaled gradient matrix H = diag(rx) G' diag(ry) once the sums are
-// known; the backward contracts H instead of recomputing S tile by tile
-// (clip_loss.py:96-124 recomputes it in every backward program).  Launches:
+// of the step.  The forward keeps the similarities (np x np floats, np = n
+// rounded up to 64) and turns them into the scaled gradient matrix H =
+// diag(rx) G' diag(ry) once the sums are known; the backward contracts H
+// instead of recomputing S tile by tile (clip_loss.py:96-124 recomputes it in
+// every backward program).  Launches:
 //   forward   k_keep_forward: 64 x 64 similarity tiles; the inverse norms
 //             from the tiles' own operand fragments (no pre-pass), the raw
-//             diagonal from the diagonal tiles' accumulators, E stored, and
-//             each tile's row and column sums written to per-tile slots;
-//             k_keep_finalize: per 64 x 64 block of E, the sums of its rows
-//             and columns in tile order, 1/R and 1/C, and E -> H in place;
-//             the diagonal blocks also write the loss terms, kappa and the
+//             diagonal from the diagonal tiles' accumulators, the exponent's
+//             row-scaled similarity S_ij rx_i stored, and each tile's row and
+//             column sums of E = exp((S-1)/T) written to per-tile slots;
+//             k_keep_finalize: per 64 x 64 block, the sums of its rows and
+//             columns in tile order, 1/R and 1/C, the block turned into H in
+//             place, and the block's row and column sums of G'_ij cos_ij
+//             (cos = x^ . y^), which the normalisation backward needs; the
+//             diagonal blocks also write the loss terms, kappa and the
 //             workspace vectors, and the last of them sums the loss partials
 //             in block order.  Fixed-order sums only: the loss and the
 //             gradients are bitwise reproducible.
-//   backward  k_keep_contract: 64 x 64 output tiles of acc_x = H Y and
-//             acc_y = H^T X, then the usual post-pass (k_postpass with the
-//             accumulators as mec_grad leaves them for fp32).
+//   backward  k_keep_contract: 64 x 64 output tiles of H Y and H^T X.
+//             mec_backward: with the post-pass in the tiles' epilogue (one
+//             launch); mec_grad: the accumulators as mec_grad leaves them for
+//             fp32, for the separate post-pass.
 #pragma once
 #include "mec_kernels.h"
 #include "mec_rowops.h"
@@ -40,9 +44,11 @@ constexpr int KEEP_MAX_KT = KEEP_MAX_N / KEEP_T;  // blocks per side
 // The kept matrix and the forward's bookkeeping, carved from the workspace by
 // the host (256-byte aligned parts).
 struct KeepBufs {
-  float* E;         // np x np, row-major (pitch np): E, then H after k_keep_finalize
-  float* rowpart;   // [kt][np]: row sums of tile (p, q) at rowpart[q * np + i]
-  float* colpart;   // [kt][np]: column sums of tile (p, q) at colpart[p * np + j] (CLIP)
+  float* S;         // np x np, row-major (pitch np): S_ij rx_i, then H after k_keep_finalize
+  float* rowpart;   // [kt][np]: row sums of E over tile (p, q) at rowpart[q * np + i]
+  float* colpart;   // [kt][np]: column sums of E over tile (p, q) at colpart[p * np + j] (CLIP)
+  float* rowdot;    // [kt][np]: sum over the columns j of block q of G'_ij cos_ij at rowdot[q * np + i]
+  float* coldot;    // [kt][np]: sum over the rows i of block p of G'_ij cos_ij at coldot[p * np + j] (CLIP)
   double* lossp;    // [kt]: loss terms of index block x, summed over its rows
   unsigned* cnt;    // the finalize's count of finished diagonal blocks
   int np, kt;
@@ -52,7 +58,10 @@ struct KeepBufs {
 // XCD-grouped order).  NORM: rx and ry from the squared norms the tile's own
 // fragments accumulate (gdma::NormHook: every wave sees all of K for its 32
 // rows and 32 columns), written to the workspace by the tiles of the first
-// block column (rx) and row (ry); rx = ry = 1 otherwise.
+// block column (rx) and row (ry); rx = ry = 1 otherwise.  Every tile computes
+// the same rx_i and ry_j (the same fragments in the same order), so the
+// finalize's E_ij = exp2(s_ij c ry_j - c) from the stored s_ij = S_ij rx_i
+// and the workspace's ry_j is bitwise the E these sums add.
 template <bool LIT, bool NORM>
 __global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict__ X, int64_t ldx,
                                                          const float* __restrict__ Y, int64_t ldy, int N, int D,
@@ -109,28 +118,34 @@ __global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict
     }
   }
   float rs, cs;
-  sumexp_tile<TL, LIT, NORM>(acc, c, m0, n0, N, rxv, ryv, s_rx, s_ry, s_row, s_col, rs, cs,
-                             kb.E + (int64_t)m0 * kb.np + n0, kb.np);
+  sumexp_tile<TL, LIT, NORM, true>(acc, c, m0, n0, N, rxv, ryv, s_rx, s_ry, s_row, s_col, rs, cs,
+                                   kb.S + (int64_t)m0 * kb.np + n0, kb.np);
   if (t < KEEP_T) {
     kb.rowpart[(int64_t)tn * kb.np + m0 + t] = rs;
     if (!LIT) kb.colpart[(int64_t)tm * kb.np + n0 + t] = cs;
   }
 }
 
-// Forward finalize, one 64 x 64 block (p, q) of E per workgroup: thread r <
-// 64 takes row i = 64 p + r (R_i = its off-diagonal sum, the tile sums in
-// tile order, + e^{t_i}), thread 64 + r column j = 64 q + r (C_j, CLIP), in
-// fp64 as finalize_row; then the block becomes H_ij = rx_i ry_j E_ij
-// (1/R_i + 1/C_j) (LiT: rx_i ry_j E_ij / R_i) in place.  The diagonal blocks
-// (p = q: their rows and columns are the same indices) also write the loss
-// terms and the workspace vectors of their indices (clip_loss.py:206-211,
-// lit_loss.py:199-203), and the last of them to finish writes the loss (the
-// block partials in block order).
+// Forward finalize, one 64 x 64 block (p, q) per workgroup: thread r < 64
+// takes row i = 64 p + r (R_i = its off-diagonal sum, the tile sums in tile
+// order, + e^{t_i}), thread 64 + r column j = 64 q + r (C_j, CLIP), in fp64
+// as finalize_row; then, per entry, E_ij = exp2(s_ij c ry_j - c) from the
+// stored s_ij = S_ij rx_i (0 on the diagonal and outside [0, N)), G'_ij =
+// E_ij (1/R_i + 1/C_j) (LiT: E_ij / R_i), and the block becomes H_ij = rx_i
+// ry_j G'_ij in place.  The block's row and column sums of G'_ij cos_ij
+// (cos_ij = s_ij ry_j) go to rowdot and coldot: the normalisation backward's
+// <x^_i, dx^_i> is a (kappa_i cos_ii + sum_j G'_ij cos_ij), which the fused
+// backward takes from these instead of a reduction over the features.  The
+// diagonal blocks (p = q: their rows and columns are the same indices) also
+// write the loss terms and the workspace vectors of their indices
+// (clip_loss.py:206-211, lit_loss.py:199-203), and the last of them to
+// finish writes the loss (the block partials in block order).
 template <bool LIT, bool NORM>
-__global__ __launch_bounds__(256) void k_keep_finalize(int N, double inv_t, float* __restrict__ ws, KeepBufs kb,
-                                                       float* __restrict__ loss) {
+__global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double inv_t, float* __restrict__ ws,
+                                                       KeepBufs kb, float* __restrict__ loss) {
   __shared__ float s_ir[KEEP_T], s_ic[KEEP_T], s_rx[KEEP_T], s_ry[KEEP_T];
   __shared__ double s_term[2 * KEEP_T], s_kap[2 * KEEP_T];
+  __shared__ float s_gc[KEEP_T][KEEP_T + 1];  // G'_ij cos_ij of the block
   const int64_t n64 = N;
   const int t = threadIdx.x, T = kb.kt;
   const int p = blockIdx.x / T, q = blockIdx.x - p * T;
@@ -138,28 +153,32 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, double inv_t, floa
   // thread t's part of the block, row t / 4, 16 consecutive columns: loaded
   // first, so that it lands while the factors are formed
   const int rr = t >> 2, c0 = (t & 3) * 16;
-  float* e = kb.E + (int64_t)(p * KEEP_T + rr) * kb.np + q * KEEP_T + c0;
-  f32x4 ev[4];
+  float* e = kb.S + (int64_t)(p * KEEP_T + rr) * kb.np + q * KEEP_T + c0;
+  f32x4 sv[4];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) ev[v] = *(const f32x4*)(e + 4 * v);
+  for (int v = 0; v < 4; ++v) sv[v] = *(const f32x4*)(e + 4 * v);
   if (t < 2 * KEEP_T) {
     const int role = t >> 6, r = t & 63;  // role 0: row i of block p; 1: column j of block q
     const int idx = (role ? q : p) * KEEP_T + r;
+    // every load unconditional, at a valid address (index clamped to N - 1,
+    // tile k to T - 1; what those read is not used), so that they issue
+    // back to back and share one memory round trip
+    const int ic = min(idx, N - 1);
+    const float* part = role ? kb.colpart : kb.rowpart;
+    float pv[KEEP_MAX_KT];
+#pragma unroll
+    for (int k = 0; k < KEEP_MAX_KT; ++k) pv[k] = part[(int64_t)min(k, T - 1) * kb.np + ic];
+    const float nv = ws[(role ? WS_RY : WS_RX) * n64 + ic];
+    const float dgv = ws[WS_DIAG * n64 + ic], rxv = ws[WS_RX * n64 + ic], ryv = ws[WS_RY * n64 + ic];
     double term = 0.0, kap = 0.0;
     float inv = 0.f, nrm = 1.f;
     if (idx < N) {
-      nrm = NORM ? ws[(role ? WS_RY : WS_RX) * n64 + idx] : 1.f;
+      nrm = NORM ? nv : 1.f;
       if (!(LIT && role)) {
-        const float* part = role ? kb.colpart : kb.rowpart;
-        float pv[KEEP_MAX_KT];
-#pragma unroll
-        for (int k = 0; k < KEEP_MAX_KT; ++k) pv[k] = k < T ? part[(int64_t)k * kb.np + idx] : 0.f;
         float off = 0.f;
 #pragma unroll
-        for (int k = 0; k < KEEP_MAX_KT; ++k)
-          if (k < T) off += pv[k];
-        const double s =
-            (double)ws[WS_DIAG * n64 + idx] * (double)ws[WS_RX * n64 + idx] * (double)ws[WS_RY * n64 + idx];
+        for (int k = 0; k < KEEP_MAX_KT; ++k) off += k < T ? pv[k] : 0.f;
+        const double s = (double)dgv * (double)rxv * (double)ryv;
         const double tt = (s - 1.0) * inv_t;
         const double R = (double)off + exp(tt);
         inv = (float)(1.0 / R);
@@ -178,7 +197,7 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, double inv_t, floa
   }
   __syncthreads();
   // the diagonal blocks' loss partial first (its count's round trip then
-  // overlaps the block's E -> H)
+  // overlaps the block's S -> H)
   bool last = false;
   if (dg && t < KEEP_T) {
     const int i = p * KEEP_T + t;
@@ -192,19 +211,40 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, double inv_t, floa
       last = __hip_atomic_fetch_add(kb.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)T - 1;
     }
   }
-  // E -> H
+  // S -> H (the forward's E: the same expression on the same values)
   {
+    const int i = p * KEEP_T + rr;
     const float ai = s_rx[rr], ir = s_ir[rr];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      f32x4 h = ev[v];
+      f32x4 h;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int j = c0 + 4 * v + u;
-        h[u] *= ai * s_ry[j] * (LIT ? ir : ir + s_ic[j]);
+        const int jl = c0 + 4 * v + u, j = q * KEEP_T + jl;
+        const float ry = s_ry[jl], sc = sv[v][u];
+        float ex = fast_exp2(fmaf(sc, NORM ? c * ry : c, -c));
+        ex = (i < N && j < N && i != j) ? ex : 0.f;
+        const float g = ex * (LIT ? ir : ir + s_ic[jl]);
+        s_gc[rr][jl] = g * (sc * ry);
+        h[u] = g * (ai * ry);
       }
       *(f32x4*)(e + 4 * v) = h;
     }
+  }
+  __syncthreads();
+  // the block's sums of G' cos: thread r < 64 row 64 p + r, thread 64 + r
+  // column 64 q + r (CLIP); four interleaved partial sums, then combined, in
+  // a fixed order
+  if (t < (LIT ? 1 : 2) * KEEP_T) {
+    const int role = t >> 6, r = t & 63;
+    float v4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < KEEP_T; ++k) v4[k & 3] += role ? s_gc[k][r] : s_gc[r][k];
+    const float v = (v4[0] + v4[1]) + (v4[2] + v4[3]);
+    if (role)
+      kb.coldot[(int64_t)p * kb.np + q * KEEP_T + r] = v;
+    else
+      kb.rowdot[(int64_t)q * kb.np + p * KEEP_T + r] = v;
   }
   if (last) {
     // every diagonal block's partial is in (they released before counting)
@@ -215,6 +255,18 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, double inv_t, floa
   }
 }
 
+// The post-pass operands of the fused backward (mec_backward): the
+// workspace vectors, grad_output (device scalar, NULL = 1), the outputs
+// (row-major, pitch D; NULL: the side is not computed) and a = grad_scale /
+// (2N) (LiT: / N).
+struct KeepPost {
+  const float* ws;
+  const float* grad_output;
+  float* dx;
+  float* dy;
+  float a;
+};
+
 // Backward contractions from H (one 64 x 64 output tile per workgroup;
 // x-side tiles first, each side's grid padded to a multiple of 8 and
 // XCD-grouped): the x side reads H by rows, the y side reads it transposed,
@@ -222,12 +274,23 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, double inv_t, floa
 // (16-byte lanes):
 //   acc_x[i, d] = sum_j H_ij y_j[d] = rx_i (G' Y^)[i, d]
 //   acc_y[j, d] = sum_i H_ij x_i[d] = ry_j (G'^T X^)[j, d]
-// i.e. the accumulators as mec_grad leaves them for fp32.
+// i.e. the accumulators as mec_grad leaves them for fp32 (!FUSED: stored to
+// acc_x / acc_y for k_postpass).  FUSED: k_postpass's arithmetic on the
+// tile, row i of the own side (x: own = x, oth = y; y side the other way
+// round), r = own's inverse norm:
+//   h   = a (kappa_i r_oth,i r oth_i[d] + acc[i, d])          (= r dx^_i[d])
+//   out = grad_output (h - own_i[d] r dot_i)   (NORM and r < 1e12; else h)
+// with dot_i = <x^_i, h> = a r (kappa_i cos_ii + sum_j G'_ij cos_ij) from the
+// finalize's per-block sums (rowdot, coldot; wave w adds blocks w, w + 4, ...
+// in order, then the four in wave order), instead of a reduction over the
+// features.  The tile's own and other-side values and the rows' vectors are
+// loaded before the k-loop and land during it.
+template <bool FUSED, bool NORM>
 __global__ __launch_bounds__(256, 2) void k_keep_contract(const float* __restrict__ X, int64_t ldx,
                                                           const float* __restrict__ Y, int64_t ldy, int N, int D,
                                                           KeepBufs kb, float* __restrict__ acc_x,
-                                                          float* __restrict__ acc_y, int ctd, int nx_pad,
-                                                          int ny_pad) {
+                                                          float* __restrict__ acc_y, KeepPost pp, int ctd,
+                                                          int nx_pad, int ny_pad) {
   using TCX = typename ConTileSmall<float, true, true>::x;
   using TCY = typename ConTileSmall<float, true, true>::y;
   static_assert(TCX::BM == KEEP_T && TCX::BN == KEEP_T && TCY::BM == KEEP_T && TCY::BN == KEEP_T &&
@@ -235,7 +298,8 @@ __global__ __launch_bounds__(256, 2) void k_keep_contract(const float* __restric
                     TCY::NT == 256,
                 "64 x 64 tiles of 2 x 2 waves");
   __shared__ __attribute__((aligned(1024))) char lds[CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ float s_kq[KEEP_T], s_ro[KEEP_T], s_dot[KEEP_T], s_part[4][KEEP_T];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   int sub = blockIdx.x;
   const bool is_x = sub < nx_pad;
   if (!is_x) sub -= nx_pad;
@@ -245,20 +309,92 @@ __global__ __launch_bounds__(256, 2) void k_keep_contract(const float* __restric
   group_tile(pid, kb.kt, ctd, 8, tm, td);
   const int r0 = tm * KEEP_T, d0 = td * KEEP_T;
   const int ncols = min(D - d0, KEEP_T);
-  f32x16 acc[1][1];
-  if (is_x)
-    TCX::template run<true, true>(tile_op<TCX>(kb.E + (int64_t)r0 * kb.np, kb.np, KEEP_T, kb.np),
-                                  tile_op<TCX>(Y + d0, ldy, ncols, N), kb.np, lds, acc);
-  else
-    TCY::template run<true, true>(tile_op<TCY>(kb.E + r0, kb.np, KEEP_T, kb.np), tile_op<TCY>(X + d0, ldx, ncols, N),
-                                  kb.np, lds, acc);
-  float* out = is_x ? acc_x : acc_y;
   const int wm = w / 2, wn = w % 2;
   const int d = d0 + wn * 32 + (lane & 31);
+  const int64_t n64 = N;
+  // FUSED: this lane's own and other-side values (its accumulator entries),
+  // and thread r < 64's row vectors and block sums, issued before the k-loop
+  const float* own = is_x ? X : Y;
+  const float* oth = is_x ? Y : X;
+  const int64_t ldo = is_x ? ldx : ldy, ldt = is_x ? ldy : ldx;
+  constexpr int PW = KEEP_MAX_KT / 4;  // block sums per wave: blocks w, w + 4, ...
+  float ov[16], tv[16];
+  float pv[PW];
+  float rv_own = 1.f, rv_oth = 1.f, kap = 0.f, dgv = 0.f, go = 1.f;
+  if constexpr (FUSED) {
+    if (pp.grad_output) go = *pp.grad_output;
+    // unconditional loads at valid addresses (row, feature and tile indices
+    // clamped; what the clamped ones read is not used), issued back to back
+    const int dc = min(d, D - 1);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = r0 + wm * 32 + acc_row(r, lane);
-    if (row < N && d < D) out[(int64_t)row * D + d] = acc[0][0][r];
+    for (int r = 0; r < 16; ++r) {
+      const int row = min(r0 + wm * 32 + acc_row(r, lane), N - 1);
+      ov[r] = own[(int64_t)row * ldo + dc];
+      tv[r] = oth[(int64_t)row * ldt + dc];
+    }
+    // row r0 + lane's block sums of G' cos, blocks w, w + 4, ... in wave w
+    // (at most 63 loads in flight per wave, the ring's included)
+    const int i = min(r0 + lane, N - 1);
+    const float* part = is_x ? kb.rowdot : kb.coldot;
+#pragma unroll
+    for (int k = 0; k < PW; ++k) pv[k] = part[(int64_t)min(4 * k + w, kb.kt - 1) * kb.np + i];
+    if (w == 0) {
+      rv_own = pp.ws[(is_x ? WS_RX : WS_RY) * n64 + i];
+      rv_oth = pp.ws[(is_x ? WS_RY : WS_RX) * n64 + i];
+      kap = pp.ws[WS_KAPPA * n64 + i];
+      dgv = pp.ws[WS_DIAG * n64 + i];
+    }
+  }
+  f32x16 acc[1][1];
+  if (is_x)
+    TCX::template run<true, true>(tile_op<TCX>(kb.S + (int64_t)r0 * kb.np, kb.np, KEEP_T, kb.np),
+                                  tile_op<TCX>(Y + d0, ldy, ncols, N), kb.np, lds, acc);
+  else
+    TCY::template run<true, true>(tile_op<TCY>(kb.S + r0, kb.np, KEEP_T, kb.np), tile_op<TCY>(X + d0, ldx, ncols, N),
+                                  kb.np, lds, acc);
+  if constexpr (!FUSED) {
+    float* out = is_x ? acc_x : acc_y;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = r0 + wm * 32 + acc_row(r, lane);
+      if (row < N && d < D) out[(int64_t)row * D + d] = acc[0][0][r];
+    }
+  } else {
+    // the values loaded before the k-loop are used from here on: the empty
+    // asm keeps the arithmetic on them (and so the wait for them) below the
+    // k-loop, whose own waits have covered those loads by now
+#pragma unroll
+    for (int k = 0; k < PW; ++k) asm volatile("" : "+v"(pv[k]));
+    asm volatile("" : "+v"(rv_own), "+v"(rv_oth), "+v"(kap), "+v"(dgv), "+v"(go));
+    const float a = pp.a;
+    {
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < PW; ++k) sum += 4 * k + w < kb.kt ? pv[k] : 0.f;
+      s_part[w][lane] = sum;
+    }
+    __syncthreads();
+    if (t < KEEP_T) {
+      const float sum = (s_part[0][t] + s_part[1][t]) + (s_part[2][t] + s_part[3][t]);
+      // cos_ii = x_i . y_i rx_i ry_i
+      const float cii = dgv * rv_own * rv_oth;
+      s_kq[t] = kap * rv_oth * rv_own;
+      s_ro[t] = rv_own;
+      s_dot[t] = a * rv_own * fmaf(kap, cii, sum);
+    }
+    __syncthreads();
+    float* out = is_x ? pp.dx : pp.dy;
+    // tiles inside [0, N) x [0, D) store without a predicate
+    const bool full = r0 + KEEP_T <= N && d0 + KEEP_T <= D;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int rl = wm * 32 + acc_row(r, lane), row = r0 + rl;
+      const float ro = s_ro[rl], dot = s_dot[rl];
+      const float h = a * fmaf(s_kq[rl], tv[r], acc[0][0][r]);
+      const float hp = h - (ov[r] * ro) * dot;
+      const float v = (NORM && ro < 1e12f) ? hp : h;
+      if (full || (row < N && d < D)) out[(int64_t)row * D + d] = go * v;
+    }
   }
 }
 

@@ -253,8 +253,9 @@ template <int A, int B> struct CMax { static constexpr int value = A > B ? A : B
 // and column sums.  MASK zeroes the diagonal and entries outside [0, N).
 // Eb (not null): every entry of the tile, masked ones as 0, is also stored at
 // Eb[row * ldE + column] (tile-relative; each 32-lane half writes 128 bytes
-// of one row).
-template <class TL, bool NORM, bool MASK>
+// of one row); STORE_S stores the exponent's row-scaled similarity S_ij rx_i
+// there instead (unmasked), from which E is exp2(s c ry_j - c) as here.
+template <class TL, bool NORM, bool MASK, bool STORE_S = false>
 __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::FN], float c, int m0, int n0, int N,
                                                 const float* s_rx, const float* s_ry, float (&rowv)[TL::FM * 16],
                                                 float (&colv)[TL::FN], float* __restrict__ Eb = nullptr,
@@ -277,7 +278,7 @@ __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::
         const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
         float e = fast_exp2(fmaf(sc, cy, -c));
         if (MASK) e = (i < N && j < N && i != j) ? e : 0.f;
-        if (Eb) Eb[(int64_t)ml * ldE + nl] = e;
+        if (Eb) Eb[(int64_t)ml * ldE + nl] = STORE_S ? sc : e;
         rowv[bm * 16 + r] += e;
         cs += e;
       }
@@ -297,7 +298,7 @@ __device__ __forceinline__ void lds_barrier() {
 // Row and column sums of E over one tile: thread t gets the sums of row m0 + t
 // (rs) and column n0 + t (cs), which sums_flush adds into ws.  rxv / ryv:
 // 1/|x| of row m0 + t and 1/|y| of column n0 + t (NORM).
-template <class TL, bool LIT, bool NORM>
+template <class TL, bool LIT, bool NORM, bool STORE_S = false>
 __device__ __forceinline__ void sumexp_tile(const f32x16 (&acc)[TL::FM][TL::FN], float c, int m0, int n0, int N,
                                             float rxv, float ryv, float* s_rx, float* s_ry, float* s_row,
                                             float* s_col, float& rs_out, float& cs_out, float* __restrict__ Eb = nullptr,
@@ -319,9 +320,9 @@ __device__ __forceinline__ void sumexp_tile(const f32x16 (&acc)[TL::FM][TL::FN],
   // interior tiles (no diagonal entry, no row or column beyond N) need no mask
   const bool diag = m0 < n0 + TL::BN && n0 < m0 + TL::BM;
   if (!diag && m0 + TL::BM <= N && n0 + TL::BN <= N)
-    sumexp_epilogue<TL, NORM, false>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv, Eb, ldE);
+    sumexp_epilogue<TL, NORM, false, STORE_S>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv, Eb, ldE);
   else
-    sumexp_epilogue<TL, NORM, true>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv, Eb, ldE);
+    sumexp_epilogue<TL, NORM, true, STORE_S>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv, Eb, ldE);
   if constexpr (TL::FM == 1) {
     // one 32-row block: its 16 row sums padded to the 32 of the reduction
     float v[32];

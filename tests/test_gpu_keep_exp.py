@@ -100,6 +100,24 @@ def test_keep_normed_stable_grad_output_frozen():
     check("clip frozen text", loss, rl, [("da", da, rda)])
 
 
+def test_keep_zero_rows_and_frozen_image():
+    """A zero row on each side (F.normalize clamps its norm: the gradient is
+    dx^ / eps, no projection) and the y side alone (frozen image tower)."""
+    n, d = 300, 64
+    a, b = randn_pair(n, d, seed=13)
+    a[5] = 0.0
+    b[17] = 0.0
+    loss, da, db, kept = fwd_bwd(MemoryEfficientCLIPLoss(0.07), a, b)
+    assert kept
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    rest = [i for i in range(n) if i not in (5, 17)]
+    check("clip zero rows (other rows)", loss, rl, [("da", da[rest], rda[rest]), ("db", db[rest], rdb[rest])])
+    check("clip zero rows (those rows)", loss, rl, [("da", da[5], rda[5]), ("db", db[17], rdb[17])])
+    loss, _, db, kept = fwd_bwd(MemoryEfficientCLIPLoss(0.07), a, b, grad_a=False)
+    assert kept
+    check("clip frozen image (other rows)", loss, rl, [("db", db[rest], rdb[rest])])
+
+
 @pytest.mark.parametrize("lit", [False, True])
 def test_keep_matches_recomputing_path(monkeypatch, lit):
     n, d = 1000, 512
@@ -136,8 +154,11 @@ def test_keep_is_bitwise_reproducible_and_second_backward():
 
 def test_keep_c_abi_entry_points():
     """mec_forward with the flag, then mec_backward (no scratch), mec_grad +
-    mec_postpass and mec_backward_noalloc on the same kept workspace: the
-    same kernels, so identical gradients, and the oracle's."""
+    mec_postpass and mec_backward_noalloc on the same kept workspace.
+    mec_backward and mec_backward_noalloc run the same fused launch
+    (identical gradients); mec_grad + mec_postpass forms the normalisation
+    backward's dot products over the features instead of from the finalize's
+    block sums (agreement to fp32 rounding); all three match the oracle."""
     lib = _lib.load()
     n, d, t = 513, 200, 0.07
     a, b = randn_pair(n, d, seed=21)
@@ -167,10 +188,13 @@ def test_keep_c_abi_entry_points():
                       ws.data_ptr(), None, ax.data_ptr(), ay.data_ptr(), ax.data_ptr(), ay.data_ptr(), stream)
         torch.cuda.synchronize()
         res.append((ax.cpu(), ay.cpu()))
-    for ax, ay in res[1:]:
-        assert torch.equal(ax, res[0][0]) and torch.equal(ay, res[0][1])
+    assert torch.equal(res[2][0], res[0][0]) and torch.equal(res[2][1], res[0][1])
+    fe = max(max_rel(res[1][0], res[0][0]), max_rel(res[1][1], res[0][1]))
+    say(f"fused vs grad + postpass: max-rel {fe:.2e}")
+    assert fe <= 1e-5
     rl, rda, rdb = oracle.clip_loss_and_grads(a, b, t)
     check("c abi keep", loss.cpu(), rl, [("dx", res[0][0], rda), ("dy", res[0][1], rdb)])
+    check("c abi keep, grad + postpass", loss.cpu(), rl, [("dx", res[1][0], rda), ("dy", res[1][1], rdb)])
     # the one-stage entry points refuse the flag
     plan = _lib.backward_plan(n, d, _lib.DTYPE_F32, mode)
     assert (plan.num_blocks, plan.scratch_bytes, plan.contract_tile_rows) == (1, 0, 64)
