@@ -118,13 +118,15 @@ extern "C" {
 #define MEC_FLAG_DETERMINISTIC 0x100
 /* OR into `mode` of mec_forward and of the matching mec_grad / mec_backward
  * (mec_backward_noalloc) for a small problem that mec_keep_exp_supported
- * accepts: the forward keeps E_ij = exp((S_ij - 1)/T) (zero on the diagonal)
- * in the workspace, np x np floats (np = n rounded up to 64), and turns it
- * into H = diag(rx) G' diag(ry) once the sums are known; the backward
- * contracts H instead of recomputing the similarity tiles.  The forward is
- * then two launches (similarity tiles, which also form the norms and the
- * diagonal; finalize), the backward two (contractions; post-pass), and the
- * backward needs no gradient scratch.  Both passes are deterministic
+ * accepts: the forward keeps the similarity matrix in the workspace, np x np
+ * floats (np = n rounded up to 64), and turns it into H = diag(rx) G'
+ * diag(ry) once the sums are known, together with per-block sums of
+ * G'_ij cos_ij for the normalisation backward; the backward contracts H
+ * instead of recomputing the similarity tiles.  The forward is then two
+ * launches (similarity tiles, which also form the norms and the diagonal;
+ * finalize), mec_backward one (the contractions with the post-pass in their
+ * epilogue; mec_grad + mec_postpass: two), and the backward needs no
+ * gradient scratch.  Both passes are deterministic
  * (fixed-order sums) with or without MEC_FLAG_DETERMINISTIC.  The workspace
  * must hold mec_workspace_floats_mode(n, d, dtype, mode) floats and be 16-byte
  * aligned; the flag must be passed to both calls or to neither.  No
@@ -171,9 +173,10 @@ int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype);
 
 /* Number of floats of the workspace for (n, d, dtype, mode):
  * mec_workspace_floats_for(n, d, dtype), plus, with MEC_FLAG_KEEP_EXP in
- * mode, the kept matrix (np x np floats), 2 np^2 / 64 floats of per-tile row
- * and column sums, np / 64 doubles of loss partials and one counter (np = n
- * rounded up to 64), each part 256-byte aligned.  Returns < 0 on bad
+ * mode, the kept matrix (np x np floats), 4 np^2 / 64 floats of per-tile
+ * row and column sums (of E, and of G'_ij cos_ij), np / 64 doubles of loss
+ * partials and one counter (np = n rounded up to 64), each part 256-byte
+ * aligned.  Returns < 0 on bad
  * args, or for MEC_FLAG_KEEP_EXP with a dtype other than MEC_DTYPE_F32 or
  * n > MEC_KEEP_EXP_MAX_N.  No counterpart in the reference. */
 int64_t mec_workspace_floats_mode(int64_t n, int64_t d, int dtype, int mode);
@@ -311,7 +314,13 @@ int mec_postpass(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
                  const float* grad_output, const float* acc_x, const float* acc_y, void* dx,
                  void* dy, void* stream);
 
-/* mec_grad + mec_postpass. */
+/* mec_grad + mec_postpass.  With MEC_FLAG_KEEP_EXP (as passed to
+ * mec_forward): one launch, the contraction tiles applying the post-pass in
+ * their epilogue; acc_x and acc_y are then not written (they may alias dx
+ * and dy as above), and the normalisation backward's <x^_i, dx^_i> comes from
+ * the finalize's block sums of G'_ij cos_ij rather than from a sum over the
+ * features, so dx and dy equal mec_grad + mec_postpass's to fp32 rounding
+ * (not bitwise). */
 int mec_backward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n, int64_t d,
                  int dtype, int mode, int normalize, float temperature, float grad_scale,
                  const float* workspace, const float* grad_output, void* scratch,
