@@ -15,6 +15,12 @@ drop without any change in results, so no parity test would notice:
   fence) only in the one workgroup that reads the others' loss partials: a
   full fence in every workgroup of the tile kernel invalidated the XCD's L2
   under the workgroups still running and cost 14 us of a 31 us launch.
+* the kept-exponential finalize issues its loads back to back and waits for
+  them once, and the fused backward's loads before the k-loop are not waited
+  for before the k-loop's first barrier: written with predicates, the same
+  loads compiled to a branch per load with waits in between (a memory round
+  trip each), and the block sums' addition was hoisted above the k-loop with
+  a wait for them (2-4 us per launch).
 """
 import os
 import re
@@ -94,3 +100,15 @@ def test_kept_exponential_kernels_fence_once(funcs):
         inv = [l for l in body if re.match(r"buffer_inv", l)]
         wbl2 = [l for l in body if re.match(r"buffer_wbl2", l)]
         assert len(inv) == 1 and len(wbl2) == 1, (name, len(inv), len(wbl2))
+
+
+def test_kept_exponential_loads_wait_once(funcs):
+    for name, body in _select(funcs, "_ZN3mec15k_keep_finalize").items():
+        first_wait = next(i for i, l in enumerate(body) if re.match(r"s_waitcnt .*vmcnt", l))
+        loads = [l for l in body[:first_wait] if l.startswith("global_load")]
+        assert len(loads) >= 36, (name, len(loads))  # the block, 32 tile sums, 4 workspace values
+    fused = _select(funcs, "_ZN3mec15k_keep_contractILb1E")
+    for name, body in fused.items():
+        first_wait = next(i for i, l in enumerate(body) if re.match(r"s_waitcnt .*vmcnt", l))
+        assert body[first_wait + 1].startswith("s_barrier"), (name, body[first_wait:first_wait + 2])
+        assert sum(l.startswith("global_load") for l in body[:first_wait]) >= 24, name  # 16 tile values, 8 block sums
