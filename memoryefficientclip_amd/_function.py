@@ -105,7 +105,7 @@ def forward(ctx, x: torch.Tensor, y: torch.Tensor, temperature: float, mode: int
     dev = x.device
     dt = compute_dtype(x.dtype)
     lib = _lib.load()
-    # small fp32 problems keep the exponentials for the backward (four
+    # small fp32 problems keep the similarity matrix for the backward (three
     # launches per step instead of six, no gradient scratch), when a gradient
     # will be asked for
     if (ctx.needs_input_grad[0] or ctx.needs_input_grad[1]) and \

@@ -119,6 +119,30 @@ def test_keep_zero_rows_and_frozen_image():
 
 
 @pytest.mark.parametrize("lit", [False, True])
+def test_keep_row_strided_views(lit):
+    """Column slices of wider tensors (row stride 300 > d = 288, 16-byte
+    rows): the kept path reads the inputs, and the fused backward its
+    epilogue's own and other-side values, at the row stride."""
+    n, d, ld = 500, 288, 300
+    wa, wb = randn_pair(n, ld, seed=17)
+    a, b = wa[:, :d], wb[:, :d]
+    ga = wa.to(DEV)[:, :d].requires_grad_(True)
+    gb = wb.to(DEV)[:, :d].requires_grad_(not lit)
+    assert ga.stride(0) == ld and gb.stride(0) == ld
+    mod = MemoryEfficientLiTLoss(0.07) if lit else MemoryEfficientCLIPLoss(0.07)
+    loss = mod(ga, gb)
+    assert loss.grad_fn.mec[0] == ld and loss.grad_fn.mec[5] & _lib.FLAG_KEEP_EXP
+    loss.backward()
+    torch.cuda.synchronize()
+    if lit:
+        rl, rda = oracle.lit_loss_and_grads(a, b, 0.07)
+        check("lit keep strided", loss.detach().cpu(), rl, [("dtext", ga.grad.cpu(), rda)])
+    else:
+        rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+        check("clip keep strided", loss.detach().cpu(), rl, [("da", ga.grad.cpu(), rda), ("db", gb.grad.cpu(), rdb)])
+
+
+@pytest.mark.parametrize("lit", [False, True])
 def test_keep_matches_recomputing_path(monkeypatch, lit):
     n, d = 1000, 512
     a, b = randn_pair(n, d, seed=5)
