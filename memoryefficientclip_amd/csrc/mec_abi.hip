@@ -1050,11 +1050,10 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
 }
 
 // The backward's contractions from the kept matrix (MEC_FLAG_KEEP_EXP; a
-// checked problem; H since the forward's finalize): one launch, into acc_x /
-// acc_y as mec_grad leaves them.
-// The kept-exponential backward: the contractions into acc_x / acc_y
-// (mec_grad; post == NULL), or with the post-pass in their epilogue into the
-// outputs of *post (mec_backward, mec_backward_noalloc; one launch).
+// checked problem; H since the forward's finalize), one launch: into acc_x /
+// acc_y as mec_grad leaves them (post == NULL), or with the post-pass in
+// their epilogue into the outputs of *post (mec_backward,
+// mec_backward_noalloc).
 static int keep_grad_run(const StepArgs& a, const KeepPost* post, void* stream) {
   const KeepLayout L = keep_layout(a.n, a.d, a.dtype);
   const KeepBufs kb = keep_bufs(a.workspace, L);
@@ -1077,10 +1076,21 @@ static int keep_grad_run(const StepArgs& a, const KeepPost* post, void* stream) 
   });
   return check_launch("backward (kept exponentials)");
 }
-// the fused post-pass operands of a kept-exponential backward
-static KeepPost keep_post(const StepArgs& a, float grad_scale, const float* grad_output, void* dx, void* dy) {
-  const float sc = (float)((double)grad_scale / (is_lit(a.mode) ? (double)a.n : 2.0 * (double)a.n));
-  return KeepPost{a.workspace, grad_output, (float*)dx, is_lit(a.mode) ? nullptr : (float*)dy, sc};
+// mec_backward and mec_backward_noalloc on the kept matrix (after
+// check_step_args): mec_postpass's checks, then the one fused launch (no
+// scratch, so the no-allocation array is not touched either)
+static int keep_backward(const StepArgs& a, float grad_scale, const float* grad_output, void* dx, void* dy,
+                         void* stream) {
+  if (!std::isfinite(grad_scale)) return fail(MEC_ERR_INVALID, "grad_scale must be finite");
+  if (is_lit(a.mode)) dy = nullptr;
+  if ((a.acc_x == nullptr) != (dx == nullptr) || (a.acc_y == nullptr) != (dy == nullptr))
+    return fail(MEC_ERR_INVALID, "each side needs both its accumulator and its output (or neither)");
+  int rc = check_keep(a.x, a.ldx, a.y, a.ldy, a.n, a.d, a.dtype, a.workspace);
+  if (!rc) rc = check_not_capturing(stream);
+  if (rc) return rc;
+  const float scale = (float)((double)grad_scale / (is_lit(a.mode) ? (double)a.n : 2.0 * (double)a.n));
+  const KeepPost post{a.workspace, grad_output, (float*)dx, (float*)dy, scale};
+  return keep_grad_run(a, &post, stream);
 }
 
 // the caller's scratch against the default layout for the problem's sides
@@ -1141,18 +1151,11 @@ int mec_backward_noalloc(const void* x, int64_t ldx, const void* y, int64_t ldy,
   StepArgs a{x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, acc_x, acc_y};
   int rc = check_step_args(a);
   if (rc) return rc;
+  if (keep_flag(mode)) return keep_backward(a, grad_scale, grad_output, dx, dy, stream);
   if (!std::isfinite(grad_scale)) return fail(MEC_ERR_INVALID, "grad_scale must be finite");
   if (is_lit(mode)) dy = nullptr;
   if ((a.acc_x == nullptr) != (dx == nullptr) || (a.acc_y == nullptr) != (dy == nullptr))
     return fail(MEC_ERR_INVALID, "each side needs both its accumulator and its output (or neither)");
-  if (keep_flag(mode)) {
-    // the kept matrix needs no scratch, so the array is not touched
-    rc = check_keep(x, ldx, y, ldy, n, d, dtype, workspace);
-    if (!rc) rc = check_not_capturing(stream);
-    if (rc) return rc;
-    const KeepPost post = keep_post(a, grad_scale, grad_output, dx, dy);
-    return keep_grad_run(a, &post, stream);
-  }
   bool ok = false;
   const ScratchLayout L = noalloc_layout(n, d, dtype, a.sides(), &ok);
   if (!ok)
@@ -1227,17 +1230,8 @@ int mec_backward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t
   if (keep_flag(mode)) {
     // the kept matrix: one launch, the post-pass in the contractions' epilogue
     StepArgs a{x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, acc_x, acc_y};
-    int rc = check_step_args(a);
-    if (rc) return rc;
-    if (!std::isfinite(grad_scale)) return fail(MEC_ERR_INVALID, "grad_scale must be finite");
-    if (is_lit(mode)) dy = nullptr;
-    if ((a.acc_x == nullptr) != (dx == nullptr) || (a.acc_y == nullptr) != (dy == nullptr))
-      return fail(MEC_ERR_INVALID, "each side needs both its accumulator and its output (or neither)");
-    rc = check_keep(x, ldx, y, ldy, n, d, dtype, workspace);
-    if (!rc) rc = check_not_capturing(stream);
-    if (rc) return rc;
-    const KeepPost post = keep_post(a, grad_scale, grad_output, dx, dy);
-    return keep_grad_run(a, &post, stream);
+    const int rc = check_step_args(a);
+    return rc ? rc : keep_backward(a, grad_scale, grad_output, dx, dy, stream);
   }
   int rc = mec_grad(x, ldx, y, ldy, n, d, dtype, mode, normalize, temperature, workspace, scratch,
                     scratch_bytes, acc_x, acc_y, stream);
