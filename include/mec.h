@@ -174,9 +174,9 @@ int64_t mec_workspace_floats_for(int64_t n, int64_t d, int dtype);
 /* Number of floats of the workspace for (n, d, dtype, mode):
  * mec_workspace_floats_for(n, d, dtype), plus, with MEC_FLAG_KEEP_EXP in
  * mode, the kept matrix (np x np floats), 4 np^2 / 64 floats of per-tile
- * row and column sums (of E, and of G'_ij cos_ij), np / 64 doubles of loss
- * partials and one counter (np = n rounded up to 64), each part 256-byte
- * aligned.  Returns < 0 on bad
+ * row and column sums (of E, and of G'_ij cos_ij) and one 64-bit loss
+ * accumulator (np = n rounded up to 64), each part 256-byte aligned.
+ * Returns < 0 on bad
  * args, or for MEC_FLAG_KEEP_EXP with a dtype other than MEC_DTYPE_F32 or
  * n > MEC_KEEP_EXP_MAX_N.  No counterpart in the reference. */
 int64_t mec_workspace_floats_mode(int64_t n, int64_t d, int dtype, int mode);

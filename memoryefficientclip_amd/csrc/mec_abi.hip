@@ -237,7 +237,7 @@ bool keep_shape_ok(int64_t n, int dtype) { return dtype == MEC_DTYPE_F32 && n <=
 int64_t align256b(int64_t floats) { return (floats + 63) & ~int64_t(63); }
 struct KeepLayout {
   int np, kt;                                     // n rounded up to 64, np / 64
-  int64_t s, rowpart, colpart, rowdot, coldot, lossp, cnt, total;
+  int64_t s, rowpart, colpart, rowdot, coldot, lacc, total;
 };
 KeepLayout keep_layout(int64_t n, int64_t d, int dtype) {
   KeepLayout L;
@@ -255,10 +255,8 @@ KeepLayout keep_layout(int64_t n, int64_t d, int dtype) {
   o = align256b(o + L.kt * np);
   L.coldot = o;
   o = align256b(o + L.kt * np);
-  L.lossp = o;
-  o = align256b(o + 2 * (int64_t)L.kt);
-  L.cnt = o;
-  L.total = o + 1;
+  L.lacc = o;  // one 64-bit word
+  L.total = o + 2;
   return L;
 }
 int64_t workspace_floats_mode(int64_t n, int64_t d, int dtype, int mode) {
@@ -266,9 +264,8 @@ int64_t workspace_floats_mode(int64_t n, int64_t d, int dtype, int mode) {
 }
 KeepBufs keep_bufs(const float* workspace, const KeepLayout& L) {
   float* ws = const_cast<float*>(workspace);
-  return KeepBufs{ws + L.s,      ws + L.rowpart,          ws + L.colpart,          ws + L.rowdot,
-                  ws + L.coldot, (double*)(ws + L.lossp), (unsigned*)(ws + L.cnt), L.np,
-                  L.kt};
+  return KeepBufs{ws + L.s,      ws + L.rowpart, ws + L.colpart, ws + L.rowdot,
+                  ws + L.coldot, (unsigned long long*)(ws + L.lacc), L.np, L.kt};
 }
 // MEC_KEEP_EXP=0 reports no support (the glue asks before it sets the flag;
 // tests of the other path)
@@ -826,11 +823,17 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
     const int N = (int)n, D = (int)d;
     const float c = (float)(1.4426950408889634 / (double)temperature);
     const double inv_t = 1.0 / (double)temperature;
+    // fixed-point units of the loss partials: every loss term is at most
+    // ln n + 2/T for |cos| <= 1, so the total is at most B = (2n or n)(ln n +
+    // 2/T); lscale = 2^floor(log2(2^51 / B)) leaves a factor 64 below the 58
+    // bits of the accumulator's sum field
+    const double bound = (is_lit(mode) ? 1.0 : 2.0) * (double)n * (std::log((double)n) + 2.0 * inv_t) + 1.0;
+    const double lscale = std::ldexp(1.0, (int)std::floor(std::log2(std::ldexp(1.0, 51) / bound)));
     const unsigned grid = (unsigned)(kb.kt * kb.kt);
     DISPATCH_BOOL(is_lit(mode), LIT, DISPATCH_BOOL(normalize, NORM, {
       k_keep_forward<LIT, NORM><<<grid, 256, 0, s>>>((const float*)x, ldx, (const float*)y, ldy, N, D, c, workspace,
                                                      kb);
-      k_keep_finalize<LIT, NORM><<<grid, 256, 0, s>>>(N, c, inv_t, workspace, kb, loss);
+      k_keep_finalize<LIT, NORM><<<grid, 256, 0, s>>>(N, c, inv_t, lscale, workspace, kb, loss);
     }));
     return check_launch("forward (kept exponentials)");
   }

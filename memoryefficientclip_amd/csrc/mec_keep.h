@@ -30,13 +30,6 @@
 
 namespace mec {
 
-// Agent-scope fences without the other half: a full __threadfence() also
-// invalidates this XCD's L2 (its acquire half), which throws out the operands
-// of the workgroups still running.  The arrivals only release (write back),
-// and only the workgroup that then reads the others' results acquires.
-__device__ __forceinline__ void release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
-
 constexpr int KEEP_T = 64;                       // tile (and index block) size
 constexpr int KEEP_MAX_N = 2048;                 // MEC_KEEP_EXP_MAX_N
 constexpr int KEEP_MAX_KT = KEEP_MAX_N / KEEP_T;  // blocks per side
@@ -49,8 +42,7 @@ struct KeepBufs {
   float* colpart;   // [kt][np]: column sums of E over tile (p, q) at colpart[p * np + j] (CLIP)
   float* rowdot;    // [kt][np]: sum over the columns j of block q of G'_ij cos_ij at rowdot[q * np + i]
   float* coldot;    // [kt][np]: sum over the rows i of block p of G'_ij cos_ij at coldot[p * np + j] (CLIP)
-  double* lossp;    // [kt]: loss terms of index block x, summed over its rows
-  unsigned* cnt;    // the finalize's count of finished diagonal blocks
+  unsigned long long* lacc;  // the finalize's loss accumulator (k_keep_finalize)
   int np, kt;
 };
 
@@ -73,7 +65,7 @@ __global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict
   __shared__ float s_rx[KEEP_T], s_ry[KEEP_T], s_row[KEEP_T], s_col[KEEP_T], s_nx[KEEP_T], s_ny[KEEP_T];
   const int64_t n64 = N;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / 2, wn = w % 2, T = kb.kt;
-  if (blockIdx.x == 0 && t == 0) *kb.cnt = 0u;  // (k_keep_finalize runs after this launch)
+  if (blockIdx.x == 0 && t == 0) *kb.lacc = 0ull;  // (k_keep_finalize runs after this launch)
   int tm, tn;
   tile_swizzle(blockIdx.x, T * T, T, T, 8, tm, tn);
   const int m0 = tm * KEEP_T, n0 = tn * KEEP_T;
@@ -138,11 +130,18 @@ __global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict
 // backward takes from these instead of a reduction over the features.  The
 // diagonal blocks (p = q: their rows and columns are the same indices) also
 // write the loss terms and the workspace vectors of their indices
-// (clip_loss.py:206-211, lit_loss.py:199-203), and the last of them to
-// finish writes the loss (the block partials in block order).
+// (clip_loss.py:206-211, lit_loss.py:199-203).  Their loss partials (fp64
+// sums over the block's rows in row order) meet in one 64-bit word, added by
+// one atomic each: the partial rounded to a fixed-point integer (lscale, a
+// power of two, units per 1), shifted up 6 bits, plus 1 in the low bits
+// that count the blocks.  Integer addition is exact and does not depend on
+// the order of arrival, so the total is reproducible bit for bit; the word
+// carries both the data and the count, so no fence is needed; and the block
+// whose addition completes the count writes the loss.  The host sizes lscale
+// so that the total stays 64 times below the 58-bit field for |cos| <= 1.
 template <bool LIT, bool NORM>
-__global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double inv_t, float* __restrict__ ws,
-                                                       KeepBufs kb, float* __restrict__ loss) {
+__global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double inv_t, double lscale,
+                                                       float* __restrict__ ws, KeepBufs kb, float* __restrict__ loss) {
   __shared__ float s_ir[KEEP_T], s_ic[KEEP_T], s_rx[KEEP_T], s_ry[KEEP_T];
   __shared__ double s_term[2 * KEEP_T], s_kap[2 * KEEP_T];
   __shared__ float s_gc[KEEP_T][KEEP_T + 1];  // G'_ij cos_ij of the block
@@ -196,19 +195,21 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double in
     s_kap[t] = kap;
   }
   __syncthreads();
-  // the diagonal blocks' loss partial first (its count's round trip then
+  // the diagonal blocks' loss partial first (its atomic's round trip then
   // overlaps the block's S -> H)
+  unsigned long long lsum = 0ull;
   bool last = false;
   if (dg && t < KEEP_T) {
     const int i = p * KEEP_T + t;
     const double kap = LIT ? s_kap[t] : s_kap[t] + s_kap[KEEP_T + t];
     const double v = LIT ? s_term[t] : s_term[t] + s_term[KEEP_T + t];
     if (i < N) ws[WS_KAPPA * n64 + i] = (float)kap;
-    const double tot = wave_sum_f64(v);
+    const double tot = wave_sum_f64(v);  // >= 0: every term is
     if (t == 0) {
-      kb.lossp[p] = tot;
-      release_agent();
-      last = __hip_atomic_fetch_add(kb.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)T - 1;
+      const unsigned long long add = ((unsigned long long)llrint(tot * lscale) << 6) + 1ull;
+      const unsigned long long old = __hip_atomic_fetch_add(kb.lacc, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = (old & 63ull) == (unsigned long long)(T - 1);
+      lsum = (old + add) >> 6;
     }
   }
   // S -> H (the forward's E: the same expression on the same values)
@@ -246,13 +247,7 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double in
     else
       kb.rowdot[(int64_t)q * kb.np + p * KEEP_T + r] = v;
   }
-  if (last) {
-    // every diagonal block's partial is in (they released before counting)
-    acquire_agent();
-    double L = 0.0;
-    for (int x = 0; x < T; ++x) L += kb.lossp[x];
-    *loss = (float)(L / (LIT ? (double)N : 2.0 * (double)N));
-  }
+  if (last) *loss = (float)((double)lsum / lscale / (LIT ? (double)N : 2.0 * (double)N));
 }
 
 // The post-pass operands of the fused backward (mec_backward): the

@@ -230,8 +230,8 @@ def test_config1_extra_memory():
 
 def test_keep_exp_sizes_and_support(monkeypatch):
     # MEC_FLAG_KEEP_EXP (small fp32 problems): the kept matrix and the
-    # forward's bookkeeping (tile sums of E, block sums of G' cos, loss
-    # partials, a counter) in the workspace, no gradient scratch
+    # forward's bookkeeping (tile sums of E, block sums of G' cos, a 64-bit
+    # loss accumulator) in the workspace, no gradient scratch
     lib = _lib.load()
     K = _lib.FLAG_KEEP_EXP
     n, d = 1024, 512
@@ -248,7 +248,7 @@ def test_keep_exp_sizes_and_support(monkeypatch):
         o = up(up(base) + np_ * np_)  # the kept matrix
         for _ in range(4):  # rowpart, colpart, rowdot, coldot
             o = up(o + kt * np_)
-        return up(o + 2 * kt) + 1  # kt doubles of loss partials, then the counter
+        return o + 2  # the loss accumulator
 
     expect = keep_floats(base, 1024)
     assert lib.mec_workspace_floats_mode(n, d, 0, K) == expect
