@@ -588,9 +588,13 @@ struct NoFragHook {
 // lane sees every k of its fragments' rows (m = 32 i + lane % 32 of the
 // wave's A rows, n = 32 j + lane % 32 of its B rows) within its lane half
 // (k = 16 h + 4 s + t of each chunk), so after the k-loop sa[i] + (the same
-// of lane ^ 32) is the row's sum of squares over the whole K.  Each value is
-// counted once: A values at j = 0, B values at i = 0.
-template <class G>
+// of lane ^ 32) is the row's sum of squares over the k it took.  Each value
+// is counted once per wave: A values at j = 0, B values at i = 0; and only
+// at the k-values t % 2 == PA (A) and t % 2 == PB (B), so that two waves that
+// share rows (the same wm, wn = 0 and 1, with PA = wn) split the work: one
+// FMA per MFMA per wave on 2 x 2 waves, where every wave taking every k
+// needed two.  The row's norm is the sum of the two waves' partials.
+template <class G, int PA = -1, int PB = -1>
 struct NormHook {
   static_assert(G::KIND == K_F32, "fp32 operands");
   mutable float sa[G::FM], sb[G::FN];
@@ -602,12 +606,12 @@ struct NormHook {
   }
   __device__ __forceinline__ float a(const i16x8& v, int i, int j, int t) const {
     const float x = __builtin_bit_cast(f32x4, v)[t];
-    if (j == 0) sa[i] = fmaf(x, x, sa[i]);
+    if (j == 0 && (PA < 0 || t % 2 == PA)) sa[i] = fmaf(x, x, sa[i]);
     return x;
   }
   __device__ __forceinline__ float b(const i16x8& v, int i, int j, int t) const {
     const float x = __builtin_bit_cast(f32x4, v)[t];
-    if (i == 0) sb[j] = fmaf(x, x, sb[j]);
+    if (i == 0 && (PB < 0 || t % 2 == PB)) sb[j] = fmaf(x, x, sb[j]);
     return x;
   }
 };

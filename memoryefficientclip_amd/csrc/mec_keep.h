@@ -49,9 +49,10 @@ struct KeepBufs {
 // Forward tiles: one 64 x 64 tile (p, q) of S per workgroup (kt x kt grid,
 // XCD-grouped order).  NORM: rx and ry from the squared norms the tile's own
 // fragments accumulate (gdma::NormHook: every wave sees all of K for its 32
-// rows and 32 columns), written to the workspace by the tiles of the first
-// block column (rx) and row (ry); rx = ry = 1 otherwise.  Every tile computes
-// the same rx_i and ry_j (the same fragments in the same order), so the
+// rows and 32 columns, and the two waves that share them split the k),
+// written to the workspace by the tiles of the first block column (rx) and
+// row (ry); rx = ry = 1 otherwise.  Every tile computes the same rx_i and
+// ry_j (the same fragments in the same order), so the
 // finalize's E_ij = exp2(s_ij c ry_j - c) from the stored s_ij = S_ij rx_i
 // and the workspace's ry_j is bitwise the E these sums add.
 template <bool LIT, bool NORM>
@@ -62,7 +63,7 @@ __global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict
   static_assert(TL::BM == KEEP_T && TL::BN == KEEP_T && TL::NT == 256 && TL::FM == 1 && TL::FN == 1,
                 "64 x 64 tiles of 2 x 2 waves");
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
-  __shared__ float s_rx[KEEP_T], s_ry[KEEP_T], s_row[KEEP_T], s_col[KEEP_T], s_nx[KEEP_T], s_ny[KEEP_T];
+  __shared__ float s_rx[KEEP_T], s_ry[KEEP_T], s_row[KEEP_T], s_col[KEEP_T], s_pa[2][KEEP_T], s_pb[2][KEEP_T];
   const int64_t n64 = N;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / 2, wn = w % 2, T = kb.kt;
   if (blockIdx.x == 0 && t == 0) *kb.lacc = 0ull;  // (k_keep_finalize runs after this launch)
@@ -74,19 +75,36 @@ __global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict
   f32x16 acc[1][1];
   float rxv = 1.f, ryv = 1.f;
   if constexpr (NORM) {
-    const gdma::NormHook<typename TL::G> nh;
-    TL::run_fh(A, B, D, lds, acc, nh);
-    const float sa = nh.sa[0] + __shfl_xor(nh.sa[0], 32, 64);
-    const float sb = nh.sb[0] + __shfl_xor(nh.sb[0], 32, 64);
+    // wave (wm, wn) takes the A squares at the k-values t % 2 == wn and the B
+    // squares at t % 2 == wm: the two waves that share a row (column) split
+    // its k between them (a compile-time split: one loop per wave position)
+    using G = typename TL::G;
+    float pa = 0.f, pb = 0.f;
+    auto run = [&](auto hook) {
+      TL::run_fh(A, B, D, lds, acc, hook);
+      pa = hook.sa[0] + __shfl_xor(hook.sa[0], 32, 64);
+      pb = hook.sb[0] + __shfl_xor(hook.sb[0], 32, 64);
+    };
+    if (wm == 0) {
+      if (wn == 0)
+        run(gdma::NormHook<G, 0, 0>());
+      else
+        run(gdma::NormHook<G, 1, 0>());
+    } else {
+      if (wn == 0)
+        run(gdma::NormHook<G, 0, 1>());
+      else
+        run(gdma::NormHook<G, 1, 1>());
+    }
     if (lane < 32) {
-      // 1/max(||v||, 1e-12), as F.normalize (clip_loss.py:266-268)
-      if (wn == 0) s_nx[wm * 32 + lane] = 1.f / fmaxf(sqrtf(sa), 1e-12f);
-      if (wm == 0) s_ny[wn * 32 + lane] = 1.f / fmaxf(sqrtf(sb), 1e-12f);
+      s_pa[wn][wm * 32 + lane] = pa;
+      s_pb[wm][wn * 32 + lane] = pb;
     }
     __syncthreads();
     if (t < KEEP_T) {
-      rxv = s_nx[t];
-      ryv = s_ny[t];
+      // 1/max(||v||, 1e-12), as F.normalize (clip_loss.py:266-268)
+      rxv = 1.f / fmaxf(sqrtf(s_pa[0][t] + s_pa[1][t]), 1e-12f);
+      ryv = 1.f / fmaxf(sqrtf(s_pb[0][t] + s_pb[1][t]), 1e-12f);
     }
   } else {
     TL::template run<true, true>(A, B, D, lds, acc);
