@@ -831,8 +831,8 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
     const double lscale = std::ldexp(1.0, (int)std::floor(std::log2(std::ldexp(1.0, 51) / bound)));
     const unsigned grid = (unsigned)(kb.kt * kb.kt);
     DISPATCH_BOOL(is_lit(mode), LIT, DISPATCH_BOOL(normalize, NORM, {
-      k_keep_forward<LIT, NORM><<<grid, 256, 0, s>>>((const float*)x, ldx, (const float*)y, ldy, N, D, c, workspace,
-                                                     kb);
+      k_keep_forward<LIT, NORM><<<grid, KEEP_NT, 0, s>>>((const float*)x, ldx, (const float*)y, ldy, N, D, c,
+                                                         workspace, kb);
       k_keep_finalize<LIT, NORM><<<grid, 256, 0, s>>>(N, c, inv_t, lscale, workspace, kb, loss);
     }));
     return check_launch("forward (kept exponentials)");
@@ -1069,13 +1069,13 @@ static int keep_grad_run(const StepArgs& a, const KeepPost* post, void* stream) 
   const float* x = (const float*)a.x;
   const float* y = (const float*)a.y;
   if (!post) {
-    k_keep_contract<false, false><<<grid, 256, 0, s>>>(x, a.ldx, y, a.ldy, (int)a.n, (int)a.d, kb, a.acc_x, a.acc_y,
-                                                      KeepPost{}, ctd, nx_pad, ny_pad);
+    k_keep_contract<false, false><<<grid, KEEP_NT, 0, s>>>(x, a.ldx, y, a.ldy, (int)a.n, (int)a.d, kb, a.acc_x,
+                                                          a.acc_y, KeepPost{}, ctd, nx_pad, ny_pad);
     return check_launch("grad (kept exponentials)");
   }
   DISPATCH_BOOL(a.normalize, NORM, {
-    k_keep_contract<true, NORM><<<grid, 256, 0, s>>>(x, a.ldx, y, a.ldy, (int)a.n, (int)a.d, kb, nullptr, nullptr,
-                                                     *post, ctd, nx_pad, ny_pad);
+    k_keep_contract<true, NORM><<<grid, KEEP_NT, 0, s>>>(x, a.ldx, y, a.ldy, (int)a.n, (int)a.d, kb, nullptr,
+                                                         nullptr, *post, ctd, nx_pad, ny_pad);
   });
   return check_launch("backward (kept exponentials)");
 }

@@ -88,7 +88,7 @@ __host__ __device__ constexpr int64_t gb_offset(int j, int i, int bs) {
 }
 
 template <int BM_, int BN_, bool TA_ = false, int WM_ = 2, int WN_ = 2, int KIND_ = K_BF16, int SA_ = 2,
-          bool GB_ = false, int TB_ = 0, int S_ = 2>
+          bool GB_ = false, int TB_ = 0, int S_ = 2, int KS_ = 1>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_;
   static constexpr int KIND = KIND_;
@@ -147,7 +147,20 @@ struct Geo {
       ib = b & 3;
     }
   }
-  static constexpr int WM = WM_, WN = WN_, NW = WM * WN, NT = 64 * NW;
+  // KS = 2 splits k: waves w and w + WM WN compute the same sub-tile from
+  // alternate halves of every chunk's k-steps (mainloop_ks2), so that two
+  // waves share each SIMD; the loads are split over all KS WM WN waves
+  static constexpr int KS = KS_;
+  static_assert(KS == 1 || KS == 2, "k split by 1 or 2");
+  static constexpr int WM = WM_, WN = WN_, NW = WM * WN * KS, NT = 64 * NW;
+  // this wave's sub-tile (wave_m, wave_n) and k-group
+  static __device__ __forceinline__ unsigned wave_mnu() {
+    return KS == 1 ? (threadIdx.x >> 6) : (threadIdx.x >> 6) % (WM * WN);
+  }
+  static __device__ __forceinline__ int wave_mn() { return (int)wave_mnu(); }
+  static __device__ __forceinline__ int wave_m() { return (int)(wave_mnu() / WN); }
+  static __device__ __forceinline__ int wave_n() { return (int)(wave_mnu() % WN); }
+  static __device__ __forceinline__ int wave_k() { return KS == 1 ? 0 : (int)((threadIdx.x >> 6) / (WM * WN)); }
   static constexpr int TM = BM / WM, TN = BN / WN;     // wave sub-tile
   static constexpr int FM = TM / 32, FN = TN / 32;     // 32x32 MFMA blocks per wave
   static constexpr int ROWS = BM + BN;
@@ -413,7 +426,7 @@ __device__ __forceinline__ i16x4_t read_tr4(const char* p) {
 // fragment 0.
 template <class G>
 __device__ __forceinline__ const char* a_ptr(const char* stage, int s) {
-  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) / G::WN;
+  const int lane = threadIdx.x & 63, wm = G::KS == 1 ? (int)((threadIdx.x >> 6) / G::WN) : G::wave_m();
   const int q = lane & 31, h = lane >> 5;
   if constexpr (G::GB && G::SA == 4) {
     // four A half-stages: block (wm * TM / 32, s) of the half-slot of k-step s
@@ -428,7 +441,7 @@ __device__ __forceinline__ const char* a_ptr(const char* stage, int s) {
 }
 template <class G>
 __device__ __forceinline__ const char* ta_ptr(const char* stage, int s, int i, int half) {
-  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) / G::WN;
+  const int lane = threadIdx.x & 63, wm = G::KS == 1 ? (int)((threadIdx.x >> 6) / G::WN) : G::wave_m();
   const int g = lane >> 4, j = lane & 15;
   const int kb = G::kvec(s, g >> 1) * 8;
   const int m = wm * G::TM + i * 32 + 16 * (g & 1) + 4 * (j & 3);
@@ -446,7 +459,7 @@ __device__ __forceinline__ const char* ta_ptr(const char* stage, int s, int i, i
 }
 template <class G>
 __device__ __forceinline__ const char* b_ptr(const char* bstage, int s) {
-  const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) % G::WN;
+  const int lane = threadIdx.x & 63, wn = G::KS == 1 ? (int)((threadIdx.x >> 6) % G::WN) : G::wave_n();
   const int q = lane & 31, h = lane >> 5;
   return bstage + (wn * G::TN + q) * G::ROWB + ((G::kvec(s, h) ^ G::swz(q)) << 4);
 }
@@ -488,7 +501,15 @@ struct FragReader {
   uint32_t a32[TA32 ? G::FM : 1];     // fp32 transposed A: per fragment
   uint32_t b32[G::TB ? G::FN : 1];    // fp32 transposed B: per fragment
   __device__ __forceinline__ FragReader(const char* stage, const char* bstage, int s) {
-    const int w = threadIdx.x >> 6, wm = w / G::WN, wn = w % G::WN;
+    int wm, wn;
+    if constexpr (G::KS == 1) {
+      const int w = threadIdx.x >> 6;
+      wm = w / G::WN;
+      wn = w % G::WN;
+    } else {
+      wm = G::wave_m();
+      wn = G::wave_n();
+    }
     if constexpr (G::TB) {
       bbase = 0;
 #pragma unroll
@@ -850,16 +871,102 @@ __device__ __forceinline__ void drain_loads() {
   __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));
 }
 
+// The k-loop with a split k (G::KS = 2): the waves of k-group g take k-steps
+// 2g and 2g + 1 of every chunk, so that each SIMD runs two waves of one
+// sub-tile.  One wave per SIMD serialises its MFMAs with its own operand
+// reads, loads and address arithmetic (measured on the 64 x 64 fp32 tiles:
+// the k-loop took the sum of the MFMA time and the time of the same loop with
+// the MFMAs removed); with two, one wave's other work issues while the
+// other's MFMAs run.  Otherwise mainloop_core's schedule for an S-stage ring:
+// chunk kt in stage kt % S, chunk kt + S - 1 loaded during chunk kt (this
+// wave's load 0 in its first k-step, load 1 in its second), fragment sets f0
+// and f1 alternating, loads also past the last chunk (they read zeros).
+template <class G, class FH = NoFragHook>
+__device__ __forceinline__ void mainloop_ks2(LoadPlan<G>& lp, int K, char* lds, f32x16 (&acc)[G::FM][G::FN],
+                                             const FH& fh = FH()) {
+  static_assert(G::KS == 2 && G::NS == 4 && G::SA == 2 && G::IPW == 2, "split k: 2 x 2 k-steps, 2 loads a wave");
+  constexpr int VMS = (G::S - 2) * G::IPW;
+#pragma unroll
+  for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < G::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  constexpr int BK = G::BK;
+  const int s0 = 2 * G::wave_k();
+  const int nk = (K + BK - 1) / BK;
+  Frags<G> f0, f1;
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_barrier<VMS>();
+    lgkm_wait<0>(f1);
+    sched_fence();
+    char* ca = G::a_stage(lds, kt % G::S);
+    char* cb = G::b_stage(lds, kt % G::S);
+    char* na = G::a_stage(lds, (kt + G::S - 1) % G::S);
+    char* nb = G::b_stage(lds, (kt + G::S - 1) % G::S);
+    const int k1 = (kt + (G::S - 1)) * BK;
+    const FragReader<G> r0(ca, cb, s0), r1(ca, cb, s0 + 1);
+    if (kt > 0) {
+      mfma_step_rd<G, 0, 1, FH>(f1, acc, lp, k1, na, nb, r0, f0, fh);
+    } else {
+      read_frags<G>(ca, cb, s0, f0);
+      lp.template issue<0>(k1, na, nb);
+    }
+    lgkm_wait<0>(f0);
+    sched_fence();
+    mfma_step_rd<G, 1, 2, FH>(f0, acc, lp, k1, na, nb, r1, f1, fh);
+    sched_fence();
+  }
+  lgkm_wait<0>(f1);
+  sched_fence();
+  mfma_step<G, 0, 0, FH>(f1, acc, lp, 0, lds, lds, fh);
+}
+
+// Split k: k-group 1's accumulators added to k-group 0's through LDS (over
+// the ring, after every wave's last ring read and load), acc(0) + acc(1) in
+// that order; the waves of group 0 then hold the tile's sums.  The ring is
+// scratch afterwards (callers reuse it only after a barrier of their own).
+template <class G>
+__device__ __forceinline__ void ks_reduce(char* lds, f32x16 (&acc)[G::FM][G::FN]) {
+  static_assert(G::KS == 2, "split k");
+  constexpr int NB = G::FM * G::FN;
+  static_assert(G::WM * G::WN * NB * 16 * 64 * 4 <= G::LDS_BYTES, "one k-group's accumulators fit the ring");
+  float* buf = (float*)lds;
+  const int lane = threadIdx.x & 63, wmn = G::wave_mn(), g = G::wave_k();
+  __syncthreads();
+  if (g == 1) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) buf[((wmn * NB + b) * 16 + r) * 64 + lane] = acc[b / G::FN][b % G::FN][r];
+  }
+  __syncthreads();
+  if (g == 0) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[b / G::FN][b % G::FN][r] += buf[((wmn * NB + b) * 16 + r) * 64 + lane];
+  }
+}
+
 // One tile: chunk 0 into stage 0, the k-loop, and the zero loads past the
-// last chunk awaited before the caller reuses the ring.
+// last chunk awaited before the caller reuses the ring.  Split k: the k-loop
+// of mainloop_ks2 and ks_reduce (the sums in k-group 0).
 template <class G, bool ZERO = true>
 __device__ __forceinline__ void mainloop(const Operand& A, const Operand& B, int K, char* lds,
                                          f32x16 (&acc)[G::FM][G::FN]) {
   LoadPlan<G> lp;
   prologue<G>(A, B, lds, lp);
-  int p0 = 0;
-  mainloop_core<G, ZERO, false>(lp, lp.ra, lp.rb, false, K, lds, p0, acc);
-  drain_loads();
+  if constexpr (G::KS == 2) {
+    static_assert(ZERO, "split k: fresh accumulators");
+    mainloop_ks2<G>(lp, K, lds, acc);
+    drain_loads();
+    ks_reduce<G>(lds, acc);
+  } else {
+    int p0 = 0;
+    mainloop_core<G, ZERO, false>(lp, lp.ra, lp.rb, false, K, lds, p0, acc);
+    drain_loads();
+  }
 }
 
 // ------------------------------------------------- rolling operand schedule

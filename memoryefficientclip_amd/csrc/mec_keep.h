@@ -46,26 +46,44 @@ struct KeepBufs {
   int np, kt;
 };
 
+// The 64 x 64 fp32 tiles of the forward and the contractions: 2 x 2
+// sub-tiles of 32 x 32, each computed by two waves from alternate halves of
+// every chunk's k-steps (KS = 2: eight waves, two per SIMD; one wave per SIMD
+// left the MFMA pipe idle while it issued its own operand reads and loads),
+// on a ring of SMALL_STAGES stages.  After the k-loop the sums are in k-group
+// 0 (threads 0-255, the waves of a 2 x 2 tile); k-group 1 only takes part in
+// the barriers.  The y side's contraction reads H transposed; both take the
+// raw input rows as a k-major feature operand (16-byte lanes).
+constexpr int KEEP_NT = 512;
+using KeepTile = TileD<64, 64, false, 2, 2, gdma::K_F32, 2, false, false, 0, SMALL_STAGES, 2>;
+using KeepConX = TileD<64, 64, false, 2, 2, gdma::K_F32, 2, false, false, 1, SMALL_STAGES, 2>;
+using KeepConY = TileD<64, 64, true, 2, 2, gdma::K_F32, 2, false, false, 1, SMALL_STAGES, 2>;
+
 // Forward tiles: one 64 x 64 tile (p, q) of S per workgroup (kt x kt grid,
 // XCD-grouped order).  NORM: rx and ry from the squared norms the tile's own
-// fragments accumulate (gdma::NormHook: every wave sees all of K for its 32
-// rows and 32 columns, and the two waves that share them split the k),
-// written to the workspace by the tiles of the first block column (rx) and
+// fragments accumulate (gdma::NormHook: a wave sees its k-group's half of
+// every chunk for its 32 rows and 32 columns, and the two waves of a k-group
+// that share those rows (columns) split that half by k parity; the four
+// partials are added in a fixed order), written to the workspace by the tiles
+// of the first block column (rx) and
 // row (ry); rx = ry = 1 otherwise.  Every tile computes the same rx_i and
 // ry_j (the same fragments in the same order), so the
 // finalize's E_ij = exp2(s_ij c ry_j - c) from the stored s_ij = S_ij rx_i
 // and the workspace's ry_j is bitwise the E these sums add.
 template <bool LIT, bool NORM>
-__global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict__ X, int64_t ldx,
-                                                         const float* __restrict__ Y, int64_t ldy, int N, int D,
-                                                         float c, float* __restrict__ ws, KeepBufs kb) {
-  using TL = GemmTile<float, true, true>;
-  static_assert(TL::BM == KEEP_T && TL::BN == KEEP_T && TL::NT == 256 && TL::FM == 1 && TL::FN == 1,
-                "64 x 64 tiles of 2 x 2 waves");
+__global__ __launch_bounds__(KEEP_NT, 2) void k_keep_forward(const float* __restrict__ X, int64_t ldx,
+                                                             const float* __restrict__ Y, int64_t ldy, int N, int D,
+                                                             float c, float* __restrict__ ws, KeepBufs kb) {
+  using TL = KeepTile;
+  static_assert(TL::BM == KEEP_T && TL::BN == KEEP_T && TL::NT == KEEP_NT && TL::FM == 1 && TL::FN == 1 &&
+                    TL::G::KS == 2,
+                "64 x 64 tiles of 2 x 2 x 2 waves");
   __shared__ __attribute__((aligned(1024))) char lds[TL::LDS_BYTES];
-  __shared__ float s_rx[KEEP_T], s_ry[KEEP_T], s_row[KEEP_T], s_col[KEEP_T], s_pa[2][KEEP_T], s_pb[2][KEEP_T];
+  __shared__ float s_rx[KEEP_T], s_ry[KEEP_T], s_row[KEEP_T], s_col[KEEP_T];
+  __shared__ float s_pa[2][2][KEEP_T], s_pb[2][2][KEEP_T];  // [k-group][wave column / row][index]
   const int64_t n64 = N;
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / 2, wn = w % 2, T = kb.kt;
+  const int t = threadIdx.x, lane = t & 63, T = kb.kt;
+  const int wm = TL::G::wave_m(), wn = TL::G::wave_n(), g = TL::G::wave_k();
   if (blockIdx.x == 0 && t == 0) *kb.lacc = 0ull;  // (k_keep_finalize runs after this launch)
   int tm, tn;
   tile_swizzle(blockIdx.x, T * T, T, T, 8, tm, tn);
@@ -97,14 +115,14 @@ __global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict
         run(gdma::NormHook<G, 1, 1>());
     }
     if (lane < 32) {
-      s_pa[wn][wm * 32 + lane] = pa;
-      s_pb[wm][wn * 32 + lane] = pb;
+      s_pa[g][wn][wm * 32 + lane] = pa;
+      s_pb[g][wm][wn * 32 + lane] = pb;
     }
     __syncthreads();
     if (t < KEEP_T) {
       // 1/max(||v||, 1e-12), as F.normalize (clip_loss.py:266-268)
-      rxv = 1.f / fmaxf(sqrtf(s_pa[0][t] + s_pa[1][t]), 1e-12f);
-      ryv = 1.f / fmaxf(sqrtf(s_pb[0][t] + s_pb[1][t]), 1e-12f);
+      rxv = 1.f / fmaxf(sqrtf((s_pa[0][0][t] + s_pa[0][1][t]) + (s_pa[1][0][t] + s_pa[1][1][t])), 1e-12f);
+      ryv = 1.f / fmaxf(sqrtf((s_pb[0][0][t] + s_pb[0][1][t]) + (s_pb[1][0][t] + s_pb[1][1][t])), 1e-12f);
     }
   } else {
     TL::template run<true, true>(A, B, D, lds, acc);
@@ -116,7 +134,7 @@ __global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict
   // the raw diagonal x_i . y_i (clip_loss.py:206): in a diagonal wave of a
   // diagonal tile, lane l holds entry (c, c), c = l % 32, when l / 32 is bit
   // 2 of c, in accumulator register 4 (c / 8) + c % 4
-  if (tm == tn && wm == wn) {
+  if (tm == tn && wm == wn && g == 0) {
     const int cc = lane & 31;
     if ((lane >> 5) == ((cc >> 2) & 1)) {
       const int rr = 4 * (cc >> 3) + (cc & 3);
@@ -129,7 +147,7 @@ __global__ __launch_bounds__(256, 2) void k_keep_forward(const float* __restrict
   }
   float rs, cs;
   sumexp_tile<TL, LIT, NORM, true>(acc, c, m0, n0, N, rxv, ryv, s_rx, s_ry, s_row, s_col, rs, cs,
-                                   kb.S + (int64_t)m0 * kb.np + n0, kb.np);
+                                   kb.S + (int64_t)m0 * kb.np + n0, kb.np, g == 0);
   if (t < KEEP_T) {
     kb.rowpart[(int64_t)tn * kb.np + m0 + t] = rs;
     if (!LIT) kb.colpart[(int64_t)tm * kb.np + n0 + t] = cs;
@@ -299,20 +317,22 @@ struct KeepPost {
 // features.  The tile's own and other-side values and the rows' vectors are
 // loaded before the k-loop and land during it.
 template <bool FUSED, bool NORM>
-__global__ __launch_bounds__(256, 2) void k_keep_contract(const float* __restrict__ X, int64_t ldx,
-                                                          const float* __restrict__ Y, int64_t ldy, int N, int D,
-                                                          KeepBufs kb, float* __restrict__ acc_x,
-                                                          float* __restrict__ acc_y, KeepPost pp, int ctd,
-                                                          int nx_pad, int ny_pad) {
-  using TCX = typename ConTileSmall<float, true, true>::x;
-  using TCY = typename ConTileSmall<float, true, true>::y;
+__global__ __launch_bounds__(KEEP_NT, 2) void k_keep_contract(const float* __restrict__ X, int64_t ldx,
+                                                              const float* __restrict__ Y, int64_t ldy, int N, int D,
+                                                              KeepBufs kb, float* __restrict__ acc_x,
+                                                              float* __restrict__ acc_y, KeepPost pp, int ctd,
+                                                              int nx_pad, int ny_pad) {
+  using TCX = KeepConX;
+  using TCY = KeepConY;
   static_assert(TCX::BM == KEEP_T && TCX::BN == KEEP_T && TCY::BM == KEEP_T && TCY::BN == KEEP_T &&
-                    TCX::FM == 1 && TCX::FN == 1 && TCY::FM == 1 && TCY::FN == 1 && TCX::NT == 256 &&
-                    TCY::NT == 256,
-                "64 x 64 tiles of 2 x 2 waves");
+                    TCX::FM == 1 && TCX::FN == 1 && TCY::FM == 1 && TCY::FN == 1 && TCX::NT == KEEP_NT &&
+                    TCY::NT == KEEP_NT && TCX::G::KS == 2 && TCY::G::KS == 2,
+                "64 x 64 tiles of 2 x 2 x 2 waves");
   __shared__ __attribute__((aligned(1024))) char lds[CMax<TCX::LDS_BYTES, TCY::LDS_BYTES>::value];
   __shared__ float s_kq[KEEP_T], s_ro[KEEP_T], s_dot[KEEP_T], s_part[4][KEEP_T];
+  // waves 0-3 (k-group 0) hold the sums after the k-loop: w is their sub-tile
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const bool g0 = w < 4;
   int sub = blockIdx.x;
   const bool is_x = sub < nx_pad;
   if (!is_x) sub -= nx_pad;
@@ -322,7 +342,7 @@ __global__ __launch_bounds__(256, 2) void k_keep_contract(const float* __restric
   group_tile(pid, kb.kt, ctd, 8, tm, td);
   const int r0 = tm * KEEP_T, d0 = td * KEEP_T;
   const int ncols = min(D - d0, KEEP_T);
-  const int wm = w / 2, wn = w % 2;
+  const int wm = (w & 3) / 2, wn = w & 1;
   const int d = d0 + wn * 32 + (lane & 31);
   const int64_t n64 = N;
   // FUSED: this lane's own and other-side values (its accumulator entries),
@@ -334,7 +354,7 @@ __global__ __launch_bounds__(256, 2) void k_keep_contract(const float* __restric
   float ov[16], tv[16];
   float pv[PW];
   float rv_own = 1.f, rv_oth = 1.f, kap = 0.f, dgv = 0.f, go = 1.f;
-  if constexpr (FUSED) {
+  if (FUSED && g0) {
     if (pp.grad_output) go = *pp.grad_output;
     // unconditional loads at valid addresses (row, feature and tile indices
     // clamped; what the clamped ones read is not used), issued back to back
@@ -367,20 +387,24 @@ __global__ __launch_bounds__(256, 2) void k_keep_contract(const float* __restric
                                   kb.np, lds, acc);
   if constexpr (!FUSED) {
     float* out = is_x ? acc_x : acc_y;
+    if (g0) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = r0 + wm * 32 + acc_row(r, lane);
-      if (row < N && d < D) out[(int64_t)row * D + d] = acc[0][0][r];
+      for (int r = 0; r < 16; ++r) {
+        const int row = r0 + wm * 32 + acc_row(r, lane);
+        if (row < N && d < D) out[(int64_t)row * D + d] = acc[0][0][r];
+      }
     }
   } else {
     // the values loaded before the k-loop are used from here on: the empty
     // asm keeps the arithmetic on them (and so the wait for them) below the
     // k-loop, whose own waits have covered those loads by now
+    if (g0) {
 #pragma unroll
-    for (int k = 0; k < PW; ++k) asm volatile("" : "+v"(pv[k]));
-    asm volatile("" : "+v"(rv_own), "+v"(rv_oth), "+v"(kap), "+v"(dgv), "+v"(go));
+      for (int k = 0; k < PW; ++k) asm volatile("" : "+v"(pv[k]));
+      asm volatile("" : "+v"(rv_own), "+v"(rv_oth), "+v"(kap), "+v"(dgv), "+v"(go));
+    }
     const float a = pp.a;
-    {
+    if (g0) {
       float sum = 0.f;
 #pragma unroll
       for (int k = 0; k < PW; ++k) sum += 4 * k + w < kb.kt ? pv[k] : 0.f;
@@ -399,6 +423,7 @@ __global__ __launch_bounds__(256, 2) void k_keep_contract(const float* __restric
     float* out = is_x ? pp.dx : pp.dy;
     // tiles inside [0, N) x [0, D) store without a predicate
     const bool full = r0 + KEEP_T <= N && d0 + KEEP_T <= D;
+    if (!g0) return;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int rl = wm * 32 + acc_row(r, lane), row = r0 + rl;

@@ -103,11 +103,11 @@ template <> struct PackOf<gdma::K_F32> { using type = PackF32; };
 // k-row-major (fp32 raw input rows; 1: 16-byte lanes, 2: 4-byte lanes); S_:
 // stages of the LDS ring (gdma::Geo::S)
 template <int BM_, int BN_, bool TA_, int WM_, int WN_, int KIND, int SA_ = 2, bool GB_ = false, bool ROLL_ = false,
-          int TB_ = 0, int S_ = 2>
+          int TB_ = 0, int S_ = 2, int KS_ = 1>
 struct TileD : PackOf<KIND>::type {
   using Elem = typename std::conditional<KIND == gdma::K_F32, float, uint16_t>::type;
   using Op = gdma::Operand;
-  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, SA_, GB_, TB_, S_>;
+  using G = gdma::Geo<BM_, BN_, TA_, WM_, WN_, KIND, SA_, GB_, TB_, S_, KS_>;
   static constexpr bool TA = TA_, GB = GB_, ROLL = ROLL_;
   static constexpr int TB = TB_;
   static constexpr int BM = G::BM, BN = G::BN, TM = G::TM, TN = G::TN, FM = G::FM, FN = G::FN;
@@ -129,10 +129,16 @@ struct TileD : PackOf<KIND>::type {
     static_assert(!ROLL, "the two-fragment-set schedule");
     gdma::LoadPlan<G> lp;
     gdma::prologue<G>(a, b, (char*)lds, lp);
-    int p0 = 0;
-    gdma::mainloop_core<G, true, false, gdma::NoHook, 0, FH>(lp, lp.ra, lp.rb, false, K, (char*)lds, p0, acc,
-                                                             gdma::NoHook(), false, fh);
-    gdma::drain_loads();
+    if constexpr (G::KS == 2) {
+      gdma::mainloop_ks2<G, FH>(lp, K, (char*)lds, acc, fh);
+      gdma::drain_loads();
+      gdma::ks_reduce<G>((char*)lds, acc);
+    } else {
+      int p0 = 0;
+      gdma::mainloop_core<G, true, false, gdma::NoHook, 0, FH>(lp, lp.ra, lp.rb, false, K, (char*)lds, p0, acc,
+                                                               gdma::NoHook(), false, fh);
+      gdma::drain_loads();
+    }
   }
   // Tiles in a chain (a persistent workgroup): start() issues the first
   // tile's chunk 0; chain() runs one tile and, with has_next, leaves chunk 0
@@ -302,7 +308,7 @@ template <class TL, bool LIT, bool NORM, bool STORE_S = false>
 __device__ __forceinline__ void sumexp_tile(const f32x16 (&acc)[TL::FM][TL::FN], float c, int m0, int n0, int N,
                                             float rxv, float ryv, float* s_rx, float* s_ry, float* s_row,
                                             float* s_col, float& rs_out, float& cs_out, float* __restrict__ Eb = nullptr,
-                                            int ldE = 0) {
+                                            int ldE = 0, bool active = true) {
   static_assert(TL::NT >= TL::BM && TL::NT >= TL::BN, "one row and one column per thread");
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, wm = w / TL::WN, wn = w % TL::WN;
   if (t < TL::BM) {
@@ -314,41 +320,44 @@ __device__ __forceinline__ void sumexp_tile(const f32x16 (&acc)[TL::FM][TL::FN],
     s_col[t] = 0.f;
   }
   lds_barrier();
-
-  float rowv[TL::FM * 16];
-  float colv[TL::FN];
-  // interior tiles (no diagonal entry, no row or column beyond N) need no mask
-  const bool diag = m0 < n0 + TL::BN && n0 < m0 + TL::BM;
-  if (!diag && m0 + TL::BM <= N && n0 + TL::BN <= N)
-    sumexp_epilogue<TL, NORM, false, STORE_S>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv, Eb, ldE);
-  else
-    sumexp_epilogue<TL, NORM, true, STORE_S>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv, Eb, ldE);
-  if constexpr (TL::FM == 1) {
-    // one 32-row block: its 16 row sums padded to the 32 of the reduction
-    float v[32];
+  // (active: waves that hold accumulators; the others, k-group 1 of a split-k
+  // tile, only take part in the barriers)
+  if (active) {
+    float rowv[TL::FM * 16];
+    float colv[TL::FN];
+    // interior tiles (no diagonal entry, no row or column beyond N) need no mask
+    const bool diag = m0 < n0 + TL::BN && n0 < m0 + TL::BM;
+    if (!diag && m0 + TL::BM <= N && n0 + TL::BN <= N)
+      sumexp_epilogue<TL, NORM, false, STORE_S>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv, Eb, ldE);
+    else
+      sumexp_epilogue<TL, NORM, true, STORE_S>(acc, c, m0, n0, N, s_rx, s_ry, rowv, colv, Eb, ldE);
+    if constexpr (TL::FM == 1) {
+      // one 32-row block: its 16 row sums padded to the 32 of the reduction
+      float v[32];
 #pragma unroll
-    for (int k = 0; k < 32; ++k) v[k] = k < 16 ? rowv[k] : 0.f;
-    const float rs = transpose_reduce32(v, lane);
-    const int q = lane & 31;
-    if (q < 16)
-      __hip_atomic_fetch_add(&s_row[wm * TL::TM + acc_row(q, lane)], rs, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_WORKGROUP);
-  } else {
-#pragma unroll
-    for (int h = 0; h < TL::FM / 2; ++h) {
-      const float rs = transpose_reduce32(*reinterpret_cast<float(*)[32]>(&rowv[32 * h]), lane);
+      for (int k = 0; k < 32; ++k) v[k] = k < 16 ? rowv[k] : 0.f;
+      const float rs = transpose_reduce32(v, lane);
       const int q = lane & 31;
-      const int ml = wm * TL::TM + h * 64 + (q >> 4) * 32 + acc_row(q & 15, lane);
-      __hip_atomic_fetch_add(&s_row[ml], rs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-  }
-  if (!LIT) {
-#pragma unroll
-    for (int bn = 0; bn < TL::FN; ++bn) {
-      colv[bn] += __shfl_xor(colv[bn], 32, 64);
-      if (lane < 32)
-        __hip_atomic_fetch_add(&s_col[wn * TL::TN + bn * 32 + lane], colv[bn], __ATOMIC_RELAXED,
+      if (q < 16)
+        __hip_atomic_fetch_add(&s_row[wm * TL::TM + acc_row(q, lane)], rs, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+#pragma unroll
+      for (int h = 0; h < TL::FM / 2; ++h) {
+        const float rs = transpose_reduce32(*reinterpret_cast<float(*)[32]>(&rowv[32 * h]), lane);
+        const int q = lane & 31;
+        const int ml = wm * TL::TM + h * 64 + (q >> 4) * 32 + acc_row(q & 15, lane);
+        __hip_atomic_fetch_add(&s_row[ml], rs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+    if (!LIT) {
+#pragma unroll
+      for (int bn = 0; bn < TL::FN; ++bn) {
+        colv[bn] += __shfl_xor(colv[bn], 32, 64);
+        if (lane < 32)
+          __hip_atomic_fetch_add(&s_col[wn * TL::TN + bn * 32 + lane], colv[bn], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
     }
   }
   lds_barrier();
