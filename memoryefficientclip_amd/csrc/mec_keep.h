@@ -1,5 +1,5 @@
-// Small fp32 problems with the exponentials kept from the forward to the
-// backward (MEC_FLAG_KEEP_EXP, n <= MEC_KEEP_EXP_MAX_N, 16-byte rows).
+// Small fp32 problems with the similarity matrix kept from the forward to
+// the backward (MEC_FLAG_KEEP_EXP, n <= MEC_KEEP_EXP_MAX_N, 16-byte rows).
 //
 // At n ~ 1000 every launch is short and the similarity GEMM is a large part
 // of the step.  The forward keeps the similarities (np x np floats, np = n
@@ -7,7 +7,8 @@
 // diag(rx) G' diag(ry) once the sums are known; the backward contracts H
 // instead of recomputing S tile by tile (clip_loss.py:96-124 recomputes it in
 // every backward program).  Launches:
-//   forward   k_keep_forward: 64 x 64 similarity tiles; the inverse norms
+//   forward   k_keep_forward: 64 x 64 similarity tiles (eight waves, a
+//             split k); the inverse norms
 //             from the tiles' own operand fragments (no pre-pass), the raw
 //             diagonal from the diagonal tiles' accumulators, the exponent's
 //             row-scaled similarity S_ij rx_i stored, and each tile's row and
@@ -17,8 +18,9 @@
 //             place, and the block's row and column sums of G'_ij cos_ij
 //             (cos = x^ . y^), which the normalisation backward needs; the
 //             diagonal blocks also write the loss terms, kappa and the
-//             workspace vectors, and the last of them sums the loss partials
-//             in block order.  Fixed-order sums only: the loss and the
+//             workspace vectors, and add their loss partials as fixed-point
+//             integers into one atomic word, the last of them writing the
+//             loss.  Fixed-order or exact sums only: the loss and the
 //             gradients are bitwise reproducible.
 //   backward  k_keep_contract: 64 x 64 output tiles of H Y and H^T X.
 //             mec_backward: with the post-pass in the tiles' epilogue (one
