@@ -182,7 +182,11 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double in
                                                        float* __restrict__ ws, KeepBufs kb, float* __restrict__ loss) {
   __shared__ float s_ir[KEEP_T], s_ic[KEEP_T], s_rx[KEEP_T], s_ry[KEEP_T];
   __shared__ double s_term[2 * KEEP_T], s_kap[2 * KEEP_T];
-  __shared__ float s_gc[KEEP_T][KEEP_T + 1];  // G'_ij cos_ij of the block
+  // G'_ij cos_ij of the block; column j at j ^ 8 in the upper half of the
+  // row: with the odd pitch this keeps the 16-column groups of a half-wave's
+  // stores (rows r .. r + 7, columns 0, 16, 32, 48 + k) on distinct banks
+  __shared__ float s_gc[KEEP_T][KEEP_T + 1];
+  auto gcol = [](int j) { return j ^ (((j >> 5) & 1) << 3); };
   const int64_t n64 = N;
   const int t = threadIdx.x, T = kb.kt;
   const int p = blockIdx.x / T, q = blockIdx.x - p * T;
@@ -264,7 +268,7 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double in
         float ex = fast_exp2(fmaf(sc, NORM ? c * ry : c, -c));
         ex = (i < N && j < N && i != j) ? ex : 0.f;
         const float g = ex * (LIT ? ir : ir + s_ic[jl]);
-        s_gc[rr][jl] = g * (sc * ry);
+        s_gc[rr][gcol(jl)] = g * (sc * ry);
         h[u] = g * (ai * ry);
       }
       *(f32x4*)(e + 4 * v) = h;
@@ -278,7 +282,7 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double in
     const int role = t >> 6, r = t & 63;
     float v4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < KEEP_T; ++k) v4[k & 3] += role ? s_gc[k][r] : s_gc[r][k];
+    for (int k = 0; k < KEEP_T; ++k) v4[k & 3] += role ? s_gc[k][gcol(r)] : s_gc[r][gcol(k)];
     const float v = (v4[0] + v4[1]) + (v4[2] + v4[3]);
     if (role)
       kb.coldot[(int64_t)p * kb.np + q * KEEP_T + r] = v;
