@@ -54,7 +54,7 @@ def check(name, loss, ref_loss, grads):
         assert e <= F32["grad"], (name, g, e)
 
 
-SHAPES = [(1024, 512), (1000, 384), (65, 36), (1, 8), (2048, 64), (130, 1028), (777, 4)]
+SHAPES = [(1024, 512), (1000, 384), (65, 36), (1, 8), (2048, 64), (2048, 512), (130, 1028), (777, 4)]
 
 
 @pytest.mark.parametrize("n,d", SHAPES)
