@@ -74,6 +74,16 @@ __device__ __forceinline__ uint32_t pack2_f16(float a, float b) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Store at device scope: a relaxed atomic store, which gfx950 issues as a
+// global store with sc1 (written through this XCD's L2).  For a launch's last
+// stores, read by the next launch.  Measured against plain stores on the
+// kept-matrix path (1024 x 1024 similarities, 1024 x 512 outputs): the forward
+// 1.2 us and the fused backward 1.3 us shorter; the finalize's in-place
+// stores, which sit mid-launch, 0.7 us longer, so they stay plain.
+__device__ __forceinline__ void store_device(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ f32x16 mfma_f32_32x32x2(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }

@@ -397,7 +397,7 @@ __global__ __launch_bounds__(KEEP_NT, 2) void k_keep_contract(const float* __res
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = r0 + wm * 32 + acc_row(r, lane);
-        if (row < N && d < D) out[(int64_t)row * D + d] = acc[0][0][r];
+        if (row < N && d < D) store_device(&out[(int64_t)row * D + d], acc[0][0][r]);
       }
     }
   } else {
@@ -430,14 +430,21 @@ __global__ __launch_bounds__(KEEP_NT, 2) void k_keep_contract(const float* __res
     // tiles inside [0, N) x [0, D) store without a predicate
     const bool full = r0 + KEEP_T <= N && d0 + KEEP_T <= D;
     if (!g0) return;
+    // every value first, then the stores (a store through a generic pointer
+    // may alias LDS, so stores between the reads made each read wait), at
+    // device scope
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int rl = wm * 32 + acc_row(r, lane), row = r0 + rl;
+      const int rl = wm * 32 + acc_row(r, lane);
       const float ro = s_ro[rl], dot = s_dot[rl];
       const float h = a * fmaf(s_kq[rl], tv[r], acc[0][0][r]);
       const float hp = h - (ov[r] * ro) * dot;
-      const float v = (NORM && ro < 1e12f) ? hp : h;
-      if (full || (row < N && d < D)) out[(int64_t)row * D + d] = go * v;
+      acc[0][0][r] = go * ((NORM && ro < 1e12f) ? hp : h);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = r0 + wm * 32 + acc_row(r, lane);
+      if (full || (row < N && d < D)) store_device(&out[(int64_t)row * D + d], acc[0][0][r]);
     }
   }
 }

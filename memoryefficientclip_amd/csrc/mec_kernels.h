@@ -267,6 +267,7 @@ __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::
                                                 float (&colv)[TL::FN], float* __restrict__ Eb = nullptr,
                                                 int ldE = 0) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w / TL::WN, wn = w % TL::WN;
+  float sv[STORE_S ? TL::FN : 1][STORE_S ? TL::FM * 16 : 1];  // STORE_S: the similarities to store
 #pragma unroll
   for (int k = 0; k < TL::FM * 16; ++k) rowv[k] = 0.f;
 #pragma unroll
@@ -284,12 +285,30 @@ __device__ __forceinline__ void sumexp_epilogue(const f32x16 (&acc)[TL::FM][TL::
         const float sc = NORM ? acc[bm][bn][r] * s_rx[ml] : acc[bm][bn][r];
         float e = fast_exp2(fmaf(sc, cy, -c));
         if (MASK) e = (i < N && j < N && i != j) ? e : 0.f;
-        if (Eb) Eb[(int64_t)ml * ldE + nl] = STORE_S ? sc : e;
+        if constexpr (STORE_S)
+          sv[bn][bm * 16 + r] = sc;
+        else if (Eb)
+          Eb[(int64_t)ml * ldE + nl] = e;
         rowv[bm * 16 + r] += e;
         cs += e;
       }
     }
     colv[bn] = cs;
+  }
+  // STORE_S: the stores after every LDS read of the scales (a store through a
+  // generic pointer may alias LDS, so each store interleaved with the reads
+  // made the next read wait for it), at device scope (the next launch reads
+  // them)
+  if constexpr (STORE_S) {
+#pragma unroll
+    for (int bn = 0; bn < TL::FN; ++bn)
+#pragma unroll
+      for (int bm = 0; bm < TL::FM; ++bm)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          store_device(&Eb[(int64_t)(wm * TL::TM + bm * 32 + acc_row(r, lane)) * ldE + wn * TL::TN + bn * 32 +
+                           (lane & 31)],
+                       sv[bn][bm * 16 + r]);
   }
 }
 
