@@ -7,8 +7,8 @@ recomputing path use.  Checked here: the loss and both gradients against the
 fp64 CPU oracle (fp32 tolerances: loss rel 1e-4, gradient max-rel 1e-3) on
 ragged n and d, CLIP and LiT, fused normalisation on and off, the Stable
 variants, grad_output scaling and a frozen tower; agreement with the
-recomputing path; bitwise reproducibility without the deterministic flag; a
-second backward of the same graph; and the C ABI's three backward entry
+recomputing path; bitwise reproducibility without the deterministic flag, and
+the same bits with it; a second backward of the same graph; and the C ABI's three backward entry
 points on one kept workspace.
 """
 import ctypes
@@ -174,6 +174,27 @@ def test_keep_is_bitwise_reproducible_and_second_backward():
         outs.append((loss.detach().cpu(), g1[0].cpu(), g1[1].cpu()))
     assert torch.equal(outs[0][0], outs[1][0])
     assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
+
+
+def test_keep_under_deterministic_algorithms():
+    """With torch.use_deterministic_algorithms(True) the module still keeps
+    the matrix (the flag and MEC_FLAG_DETERMINISTIC together), and the result
+    is bitwise the one without: every sum of the kept path is in a fixed
+    order either way."""
+    n, d = 700, 128
+    a, b = randn_pair(n, d, seed=17)
+    plain = fwd_bwd(MemoryEfficientCLIPLoss(0.07), a, b)
+    prev = torch.are_deterministic_algorithms_enabled()
+    torch.use_deterministic_algorithms(True)
+    try:
+        det = fwd_bwd(MemoryEfficientCLIPLoss(0.07), a, b)
+    finally:
+        torch.use_deterministic_algorithms(prev)
+    assert plain[3] and det[3]
+    for u, v in zip(plain[:3], det[:3]):
+        assert torch.equal(u, v)
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    check("keep, deterministic", det[0], rl, [("dx", det[1], rda), ("dy", det[2], rdb)])
 
 
 def test_keep_c_abi_entry_points():
