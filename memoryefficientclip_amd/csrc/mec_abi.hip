@@ -833,7 +833,10 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
     DISPATCH_BOOL(is_lit(mode), LIT, DISPATCH_BOOL(normalize, NORM, {
       k_keep_forward<LIT, NORM><<<grid, KEEP_NT, 0, s>>>((const float*)x, ldx, (const float*)y, ldy, N, D, c,
                                                          workspace, kb);
-      k_keep_finalize<LIT, NORM><<<grid, 256, 0, s>>>(N, c, inv_t, lscale, workspace, kb, loss);
+      DISPATCH_BOOL(kb.kt <= 16, SMALLT, {
+        k_keep_finalize<LIT, NORM, SMALLT ? 16 : KEEP_MAX_KT><<<grid, 256, 0, s>>>(N, c, inv_t, lscale, workspace,
+                                                                                 kb, loss);
+      });
     }));
     return check_launch("forward (kept exponentials)");
   }
@@ -1073,10 +1076,10 @@ static int keep_grad_run(const StepArgs& a, const KeepPost* post, void* stream) 
                                                           a.acc_y, KeepPost{}, ctd, nx_pad, ny_pad);
     return check_launch("grad (kept exponentials)");
   }
-  DISPATCH_BOOL(a.normalize, NORM, {
-    k_keep_contract<true, NORM><<<grid, KEEP_NT, 0, s>>>(x, a.ldx, y, a.ldy, (int)a.n, (int)a.d, kb, nullptr,
-                                                         nullptr, *post, ctd, nx_pad, ny_pad);
-  });
+  DISPATCH_BOOL(a.normalize, NORM, DISPATCH_BOOL(kb.kt <= 16, SMALLT, {
+    k_keep_contract<true, NORM, SMALLT ? 16 : KEEP_MAX_KT><<<grid, KEEP_NT, 0, s>>>(
+        x, a.ldx, y, a.ldy, (int)a.n, (int)a.d, kb, nullptr, nullptr, *post, ctd, nx_pad, ny_pad);
+  }));
   return check_launch("backward (kept exponentials)");
 }
 // mec_backward and mec_backward_noalloc on the kept matrix (after

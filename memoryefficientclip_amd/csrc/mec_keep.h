@@ -177,9 +177,12 @@ __global__ __launch_bounds__(KEEP_NT, 2) void k_keep_forward(const float* __rest
 // carries both the data and the count, so no fence is needed; and the block
 // whose addition completes the count writes the loss.  The host sizes lscale
 // so that the total stays 64 times below the 58-bit field for |cos| <= 1.
-template <bool LIT, bool NORM>
+// MKT >= kt: the tile partials each row's thread loads (16 when kt <= 16,
+// which halves the finalize's loads at n <= 1024).
+template <bool LIT, bool NORM, int MKT = KEEP_MAX_KT>
 __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double inv_t, double lscale,
                                                        float* __restrict__ ws, KeepBufs kb, float* __restrict__ loss) {
+  static_assert(MKT % 4 == 0 && MKT <= KEEP_MAX_KT, "tile partials per row");
   __shared__ float s_ir[KEEP_T], s_ic[KEEP_T], s_rx[KEEP_T], s_ry[KEEP_T];
   __shared__ double s_term[2 * KEEP_T], s_kap[2 * KEEP_T];
   // G'_ij cos_ij of the block; column j at j ^ 8 in the upper half of the
@@ -206,9 +209,9 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double in
     // back to back and share one memory round trip
     const int ic = min(idx, N - 1);
     const float* part = role ? kb.colpart : kb.rowpart;
-    float pv[KEEP_MAX_KT];
+    float pv[MKT];
 #pragma unroll
-    for (int k = 0; k < KEEP_MAX_KT; ++k) pv[k] = part[(int64_t)min(k, T - 1) * kb.np + ic];
+    for (int k = 0; k < MKT; ++k) pv[k] = part[(int64_t)min(k, T - 1) * kb.np + ic];
     const float nv = ws[(role ? WS_RY : WS_RX) * n64 + ic];
     const float dgv = ws[WS_DIAG * n64 + ic], rxv = ws[WS_RX * n64 + ic], ryv = ws[WS_RY * n64 + ic];
     double term = 0.0, kap = 0.0;
@@ -218,7 +221,7 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double in
       if (!(LIT && role)) {
         float off = 0.f;
 #pragma unroll
-        for (int k = 0; k < KEEP_MAX_KT; ++k) off += k < T ? pv[k] : 0.f;
+        for (int k = 0; k < MKT; ++k) off += k < T ? pv[k] : 0.f;
         const double s = (double)dgv * (double)rxv * (double)ryv;
         const double tt = (s - 1.0) * inv_t;
         const double R = (double)off + exp(tt);
@@ -321,8 +324,9 @@ struct KeepPost {
 // finalize's per-block sums (rowdot, coldot; wave w adds blocks w, w + 4, ...
 // in order, then the four in wave order), instead of a reduction over the
 // features.  The tile's own and other-side values and the rows' vectors are
-// loaded before the k-loop and land during it.
-template <bool FUSED, bool NORM>
+// loaded before the k-loop and land during it.  MKT >= kt, as in
+// k_keep_finalize.
+template <bool FUSED, bool NORM, int MKT = KEEP_MAX_KT>
 __global__ __launch_bounds__(KEEP_NT, 2) void k_keep_contract(const float* __restrict__ X, int64_t ldx,
                                                               const float* __restrict__ Y, int64_t ldy, int N, int D,
                                                               KeepBufs kb, float* __restrict__ acc_x,
@@ -356,7 +360,8 @@ __global__ __launch_bounds__(KEEP_NT, 2) void k_keep_contract(const float* __res
   const float* own = is_x ? X : Y;
   const float* oth = is_x ? Y : X;
   const int64_t ldo = is_x ? ldx : ldy, ldt = is_x ? ldy : ldx;
-  constexpr int PW = KEEP_MAX_KT / 4;  // block sums per wave: blocks w, w + 4, ...
+  static_assert(MKT % 4 == 0 && MKT <= KEEP_MAX_KT, "block sums per row");
+  constexpr int PW = MKT / 4;  // block sums per wave: blocks w, w + 4, ...
   float ov[16], tv[16];
   float pv[PW];
   float rv_own = 1.f, rv_oth = 1.f, kap = 0.f, dgv = 0.f, go = 1.f;
