@@ -462,13 +462,22 @@ ScratchLayout noalloc_layout(int64_t n, int64_t d, int dtype, int sides, bool* o
 
 int round8(int v) { return (v + 7) & ~7; }
 
-// 64 x 64 fp32 tiles (f32_small_n; MEC_F32_SMALL_TILES=0 or 1 overrides, for tests)
-bool f32_small_tiles(int64_t n) {
+// 64 x 64 fp32 tiles of the forward (f32_small_fwd) and of the backward's
+// steps (f32_small_bwd); MEC_F32_SMALL_TILES=0 or 1 overrides both, for tests
+int small_tiles_env() {
   if (const char* env = std::getenv("MEC_F32_SMALL_TILES")) {
-    if (env[0] == '0') return false;
-    if (env[0] == '1') return true;
+    if (env[0] == '0') return 0;
+    if (env[0] == '1') return 1;
   }
-  return f32_small_n(n);
+  return -1;
+}
+bool f32_small_fwd_tiles(int64_t n, int64_t d, int cus) {
+  const int e = small_tiles_env();
+  return e >= 0 ? e == 1 : f32_small_fwd(n, d, cus);
+}
+bool f32_small_bwd_tiles(int64_t n, int64_t d, int64_t bs, int cus) {
+  const int e = small_tiles_env();
+  return e >= 0 ? e == 1 : f32_small_bwd(n, d, bs, cus);
 }
 
 // 16-bit narrow contraction tiles (narrow_contract_shape) for blocks of bs
@@ -649,7 +658,7 @@ int mec_backward_plan(int64_t n, int64_t d, int dtype, int mode, int sides, int 
   plan->scratch_bytes = L.total;
   // the tiles of a launch with contractions (16-byte rows assumed)
   const int gdt = is_split(dtype) ? MEC_DTYPE_BF16 : dtype;
-  const bool small = gdt == MEC_DTYPE_F32 && f32_small_tiles(n);
+  const bool small = gdt == MEC_DTYPE_F32 && f32_small_bwd_tiles(n, d, L.bs, cus);
   bool w384 = false;
   const BlockGrid bg = block_grid(d, gdt, sides, L.bs, L.nb, L.ldt, cus, fwd_tile_dims(gdt, true, small),
                                   con_tile_dims(gdt, small), &w384);
@@ -737,7 +746,12 @@ int mec_sumexp(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t n
     chain = FwdChain<T, VEC, NORM>::value;
   })));
   const bool det = (mode & MEC_FLAG_DETERMINISTIC) || chain;
-  const bool small = dtype == MEC_DTYPE_F32 && vec && !det && f32_small_tiles(n);
+  int cus = 0;
+  if (dtype == MEC_DTYPE_F32 && vec && !det) {
+    rc = compute_units(&cus);
+    if (rc) return rc;
+  }
+  const bool small = dtype == MEC_DTYPE_F32 && vec && !det && f32_small_fwd_tiles(n, d, cus);
   const TileDims td = fwd_tile_dims(dtype, vec, small);
   const int tiles_m = (int)((n + td.bm - 1) / td.bm), tiles_n = (int)((n + td.bn - 1) / td.bn);
   const int64_t nwg = (int64_t)tiles_m * tiles_n;
@@ -922,7 +936,7 @@ static int grad_step_run(const StepArgs& a, int64_t step, const ScratchLayout& L
   const GemmOperands go = split ? split_operands(workspace, n, d, dtype) : GemmOperands{x, ldx, y, ldy, d, dtype};
   const bool vec = vec_ok(go.x, go.ldx, go.y, go.ldy, go.d, go.dtype);
   if (split && !vec) return fail(MEC_ERR_UNSUPPORTED, "split operands beyond the direct-load range");
-  const bool small = dtype == MEC_DTYPE_F32 && vec && f32_small_tiles(n);
+  const bool small = dtype == MEC_DTYPE_F32 && vec && f32_small_bwd_tiles(n, d, bs, cus);
   bool w384 = false;  // 16-bit contractions in 256 x 384 tiles
   const BlockGrid bg = block_grid(d, dtype, a.sides(), bs, nb, L.ldt, cus, fwd_tile_dims(dtype, vec, small),
                                   con_tile_dims(dtype, small), &w384);

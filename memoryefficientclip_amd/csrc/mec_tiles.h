@@ -42,6 +42,33 @@ inline bool f32_small_n(int64_t n) {
   const int64_t t = (n + 127) / 128;
   return t * t < 512;
 }
+// Share of the CU slots of a launch of `tiles` workgroups, one per CU per
+// round, that its rounds keep busy: tiles / (cus * rounds).
+inline double round_fill(int64_t tiles, int cus) {
+  const int64_t rounds = (tiles + cus - 1) / cus;
+  return (double)tiles / ((double)rounds * cus);
+}
+// fp32 forward tiles: 64 x 64 for f32_small_n, and for D >= 512 where the
+// 128 x 128 grid fills its rounds below 90% (measured on one MI355X: the
+// forward 7-23% faster at N = 3072 and 5120, D = 512-1024; at D = 128-256 and
+// elsewhere the 128 x 128 tiles were as fast or up to 26% faster).
+inline bool f32_small_fwd(int64_t n, int64_t d, int cus) {
+  if (f32_small_n(n)) return true;
+  const int64_t t = (n + 127) / 128;
+  return d >= 512 && round_fill(t * t, cus) < 0.9;
+}
+// fp32 backward tiles for blocks of bs rows: 64 x 64 for f32_small_n, and
+// where a step's 128 x 128 gradient-matrix tiles (ceil(n/128) ceil(bs/128))
+// are few for their K (tiles x D <= 2^17) or fill their rounds below 90%.
+// Measured on one MI355X: at D = 128-256 (1024-row blocks) the 64 x 64
+// backward was 1.2-2.6x faster up to N = 8192 and even at 2^17; with a poor
+// last round (N = 3072 and 5120 at D = 512-1024) 9-20% faster; elsewhere the
+// 128 x 128 tiles were as fast or up to 10% faster.
+inline bool f32_small_bwd(int64_t n, int64_t d, int64_t bs, int cus) {
+  if (f32_small_n(n)) return true;
+  const int64_t g = ((n + 127) / 128) * ((bs + 127) / 128);
+  return g * d <= ((int64_t)1 << 17) || round_fill(g, cus) < 0.9;
+}
 // forward sums and gradient-matrix tiles (x rows x y rows)
 inline TileDims fwd_tile_dims(int dtype, bool vec, bool small = false) {
   if (dtype == kDtypeX3 || dtype == kDtypeF32B) return {256, 256};

@@ -338,6 +338,35 @@ def test_backward_plan():
         _lib.backward_plan((1 << 22) + 1, 512, 0, compute_units=256)
 
 
+def test_fp32_backward_tile_rule(monkeypatch):
+    # 64 x 64 backward tiles where a step's 128 x 128 gradient-matrix tiles
+    # (ceil(n/128) ceil(bs/128)) are few for their K (tiles x D <= 2^17) or
+    # leave the last round of 256 CUs under 90% full; the configurations of
+    # the measurements behind the rule, on both sides of it
+    monkeypatch.delenv("MEC_F32_SMALL_TILES", raising=False)
+    cases = {
+        (4096, 128): 64,    # 1024-row blocks: 256 tiles per step, tiles x D = 2^15
+        (8192, 256): 64,    # 512 tiles, tiles x D = 2^17
+        (12288, 256): 128,  # 768 tiles, 3 full rounds
+        (3072, 512): 64,    # 288 tiles: a second round 12% full
+        (4096, 512): 128,   # 512 tiles, 2 full rounds
+        (5120, 512): 64,    # 800 tiles: 78%
+        (6144, 512): 128,   # 768 tiles
+        (5120, 1024): 64,   # 1600 tiles: 89%
+        (6144, 1024): 128,  # 1152 tiles: 90%
+        (2816, 1024): 64,   # below the 512 forward tiles of 128 x 128 (f32_small_n)
+        (32768, 1152): 128,  # the headline
+    }
+    for (n, d), rows in cases.items():
+        p = _lib.backward_plan(n, d, 0, compute_units=256)
+        assert p.contract_tile_rows == rows, (n, d, p.block_rows, p.contract_tile_rows)
+    # the environment override, as the tests use it
+    monkeypatch.setenv("MEC_F32_SMALL_TILES", "0")
+    assert _lib.backward_plan(4096, 128, 0, compute_units=256).contract_tile_rows == 128
+    monkeypatch.setenv("MEC_F32_SMALL_TILES", "1")
+    assert _lib.backward_plan(32768, 1152, 0, compute_units=256).contract_tile_rows == 64
+
+
 def test_wide_contraction_tiles_stay_within_32bit_offsets(monkeypatch):
     # a 384-wide tile reads a 384-row panel of a transposed input ([d][ldt])
     # with 32-bit byte offsets: (383 ldt + bs) x 2 < 2^31, ldt up to ~2.8M;

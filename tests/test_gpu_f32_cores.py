@@ -9,8 +9,11 @@ checked against the oracle and against each other, and a row stride past the
 direct core's 32-bit panel range takes the second path too.
 
 Up to N = 2816 the direct-to-LDS kernels run 64 x 64 tiles (a 128 x 128
-grid would leave CUs idle); MEC_F32_SMALL_TILES=0 / 1 forces either tile
-size, so both are checked on both sides of that bound.
+grid would leave CUs idle), above it where a launch's 128 x 128 grid would be
+small for its K or fill its rounds of CUs poorly (the forward and each
+backward step choose on their own); MEC_F32_SMALL_TILES=0 / 1 forces either
+tile size, so both are checked on both sides of those bounds, with the kept
+similarity matrix (which takes over at N <= 2048) turned off.
 """
 import os
 
@@ -122,17 +125,19 @@ def run_env(env, module, a, b, grad_b=True):
 
 
 @pytest.mark.parametrize("lit", [False, True], ids=["clip", "lit"])
-@pytest.mark.parametrize("n,d", [(1024, 512), (1000, 130), (2900, 72), (63, 8)])
+@pytest.mark.parametrize("n,d", [(1024, 512), (1000, 130), (2900, 72), (63, 8), (4096, 128), (5120, 516)])
 def test_f32_small_and_large_tiles(lit, n, d):
     """64 x 64 and 128 x 128 direct-to-LDS tiles (forward sums,
-    gradient-matrix tiles, contractions) agree with the oracle and with each
-    other, below the 2816-row bound (where 64 x 64 is the default: config 1's
-    shape, a ragged N, a tiny N) and above it (n = 2900)."""
+    gradient-matrix tiles, contractions) of the recomputing path agree with
+    the oracle and with each other, below the 2816-row bound (where 64 x 64 is
+    the default: config 1's shape, a ragged N, a tiny N) and above it (n =
+    2900; 4096 with 1024-row backward blocks and 5120 with a poorly filled
+    last round, where the backward's default is 64 x 64 again)."""
     a, b = randn_pair(n, d, seed=41 + n)
     mod = MemoryEfficientLiTLoss(0.07) if lit else MemoryEfficientCLIPLoss(0.07)
     say(f"fp32 {'LiT' if lit else 'CLIP'} n={n} d={d}: 64 x 64 vs 128 x 128 tiles")
-    l_s, da_s, db_s = run_env({"MEC_F32_SMALL_TILES": "1"}, mod, a, b, grad_b=not lit)
-    l_l, da_l, db_l = run_env({"MEC_F32_SMALL_TILES": "0"}, mod, a, b, grad_b=not lit)
+    l_s, da_s, db_s = run_env({"MEC_F32_SMALL_TILES": "1", "MEC_KEEP_EXP": "0"}, mod, a, b, grad_b=not lit)
+    l_l, da_l, db_l = run_env({"MEC_F32_SMALL_TILES": "0", "MEC_KEEP_EXP": "0"}, mod, a, b, grad_b=not lit)
     if lit:
         rl, rda = oracle.lit_loss_and_grads(a, b, 0.07)
         pairs = [(da_s, rda), (da_l, rda)]
@@ -145,3 +150,17 @@ def test_f32_small_and_large_tiles(lit, n, d):
     assert all(e <= TOL_GRAD for e in errs)
     # the same products summed in a different order
     assert rel_err(l_s, l_l) < 1e-5 and max_rel(da_s, da_l) < 1e-5
+
+
+@pytest.mark.parametrize("n,d", [(4096, 128), (3072, 512), (6144, 64)])
+def test_f32_default_tile_choice(n, d):
+    """The default choice, where forward and backward differ: 128 x 128
+    forward tiles with 64 x 64 backward tiles (n = 4096, 6144 at small D),
+    64 x 64 for both (n = 3072, D = 512); against the oracle."""
+    a, b = randn_pair(n, d, seed=43 + n)
+    say(f"fp32 CLIP n={n} d={d}: default tiles")
+    l, da, db = run_env({}, MemoryEfficientCLIPLoss(0.07), a, b)
+    rl, rda, rdb = oracle.clip_loss_and_grads(a, b, 0.07)
+    errs = [max_rel(da, rda), max_rel(db, rdb)]
+    say(f"  loss rel {rel_err(l, rl):.2e}; grads {['%.2e' % e for e in errs]}")
+    assert rel_err(l, rl) <= TOL_LOSS and all(e <= TOL_GRAD for e in errs)
