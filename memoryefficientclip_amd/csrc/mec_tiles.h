@@ -4,7 +4,10 @@
 //                             loads (mec_gemm_dma.h) for 16-byte vectors,
 //                             else staged through registers (mec_gemm_f32.h);
 //                             64 x 64 direct-to-LDS tiles at a small n
-//                             (f32_small_n), so that the grid covers the CUs
+//                             (f32_small_n), so that the grid covers the CUs,
+//                             and per launch where a 128 x 128 grid is small
+//                             for its K or fills its rounds of CUs poorly
+//                             (f32_small_fwd, f32_small_bwd)
 //   bf16 / fp16, 16-byte      forward sums and gradient-matrix tiles 256 x 256
 //   vectors                   (x rows x y rows, 8 waves), direct global->LDS
 //                             loads (mec_gemm_dma.h); contractions 256 x 256
