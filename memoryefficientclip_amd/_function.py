@@ -62,8 +62,39 @@ def _rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
     return t, t.stride(0)
 
 
-def _stream(dev: torch.device) -> int:
-    return torch.cuda.current_stream(dev).cuda_stream
+# the current stream's handle without building a torch.cuda.Stream object
+# (about 2 us of host time per call at N = 1024, where the step is host-bound)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(index: int) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+class _on_device:
+    """Make device `index` current for the C-ABI calls (which launch on the
+    current device), restoring the previous one; nothing to do, and no
+    device switch, in the common case where it already is."""
+
+    __slots__ = ("index", "prev")
+
+    def __init__(self, index: int):
+        self.index = index
+        self.prev = -1
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.index:
+            self.prev = cur
+            torch.cuda.set_device(self.index)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev >= 0:
+            torch.cuda.set_device(self.prev)
+        return False
 
 
 def refuse_graph_capture() -> None:
@@ -103,6 +134,7 @@ def forward(ctx, x: torch.Tensor, y: torch.Tensor, temperature: float, mode: int
     y, ldy = _rows(y)
     n, d = x.shape
     dev = x.device
+    di = x.get_device()
     dt = compute_dtype(x.dtype)
     lib = _lib.load()
     # small fp32 problems keep the similarity matrix for the backward (three
@@ -111,14 +143,14 @@ def forward(ctx, x: torch.Tensor, y: torch.Tensor, temperature: float, mode: int
     if (ctx.needs_input_grad[0] or ctx.needs_input_grad[1]) and \
             lib.mec_keep_exp_supported(x.data_ptr(), ldx, y.data_ptr(), ldy, n, d, dt):
         mode |= _lib.FLAG_KEEP_EXP
-    with torch.cuda.device(dev):
-        ws = torch.empty(lib.mec_workspace_floats_mode(n, d, dt, mode), dtype=torch.float32, device=dev)
-        loss = torch.empty((), dtype=torch.float32, device=dev)
-        # under torch.use_deterministic_algorithms(True) the forward sums are
-        # formed without atomics (the backward is deterministic either way)
-        fmode = mode | (_lib.FLAG_DETERMINISTIC if torch.are_deterministic_algorithms_enabled() else 0)
+    ws = torch.empty(lib.mec_workspace_floats_mode(n, d, dt, mode), dtype=torch.float32, device=dev)
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    # under torch.use_deterministic_algorithms(True) the forward sums are
+    # formed without atomics (the backward is deterministic either way)
+    fmode = mode | (_lib.FLAG_DETERMINISTIC if torch.are_deterministic_algorithms_enabled() else 0)
+    with _on_device(di):
         _lib.call("mec_forward", x.data_ptr(), ldx, y.data_ptr(), ldy, n, d, dt, fmode, int(normalize),
-                  temperature, ws.data_ptr(), loss.data_ptr(), _stream(dev))
+                  temperature, ws.data_ptr(), loss.data_ptr(), _stream(di))
     ctx.save_for_backward(x, y, ws)
     ctx.mec = (ldx, ldy, n, d, dt, mode, bool(normalize), temperature,
                math.sqrt(n / temperature) if stable else 1.0 / temperature)
@@ -135,33 +167,36 @@ def backward(ctx, grad_output: torch.Tensor, need_x: bool, need_y: bool):
     if not (need_x or need_y):
         return None, None
     dev = x.device
+    di = x.get_device()
     lib = _lib.load()
-    with torch.cuda.device(dev):
-        go = grad_output.detach().to(device=dev, dtype=torch.float32).reshape(()).contiguous()
-        acc_x = torch.empty((n, d), dtype=torch.float32, device=dev) if need_x else None
-        acc_y = torch.empty((n, d), dtype=torch.float32, device=dev) if need_y else None
-        if dt in (_lib.DTYPE_F32, _lib.DTYPE_F32_BF16X3, _lib.DTYPE_F32_BF16):
-            dx, dy = acc_x, acc_y  # the post-pass runs in place
-        else:
-            dx = torch.empty((n, d), dtype=x.dtype, device=dev) if need_x else None
-            dy = torch.empty((n, d), dtype=y.dtype, device=dev) if need_y else None
-        # The gradient scratch comes straight from PyTorch's caching allocator
-        # (stream-ordered, like a tensor): the kernels write every byte of it
-        # before reading it, so the NaN fill that torch.empty performs under
-        # torch.use_deterministic_algorithms(True) (gigabytes at large N) would
-        # be wasted work.
-        sides = (_lib.SIDE_X if need_x else 0) | (_lib.SIDE_Y if need_y else 0)
-        nbytes = lib.mec_grad_scratch_bytes_for(n, d, dt, mode, sides)  # 0 with the kept exponentials
-        stream = torch.cuda.current_stream(dev)
-        scratch = torch.cuda.caching_allocator_alloc(nbytes, dev, stream) if nbytes > 0 else None
+    go = grad_output
+    if go.dtype != torch.float32 or go.device != dev or go.dim() != 0:
+        go = go.detach().to(device=dev, dtype=torch.float32).reshape(())
+    acc_x = torch.empty((n, d), dtype=torch.float32, device=dev) if need_x else None
+    acc_y = torch.empty((n, d), dtype=torch.float32, device=dev) if need_y else None
+    if dt in (_lib.DTYPE_F32, _lib.DTYPE_F32_BF16X3, _lib.DTYPE_F32_BF16):
+        dx, dy = acc_x, acc_y  # the post-pass runs in place
+    else:
+        dx = torch.empty((n, d), dtype=x.dtype, device=dev) if need_x else None
+        dy = torch.empty((n, d), dtype=y.dtype, device=dev) if need_y else None
+    # The gradient scratch comes straight from PyTorch's caching allocator
+    # (stream-ordered, like a tensor): the kernels write every byte of it
+    # before reading it, so the NaN fill that torch.empty performs under
+    # torch.use_deterministic_algorithms(True) (gigabytes at large N) would
+    # be wasted work.
+    sides = (_lib.SIDE_X if need_x else 0) | (_lib.SIDE_Y if need_y else 0)
+    nbytes = lib.mec_grad_scratch_bytes_for(n, d, dt, mode, sides)  # 0 with the kept exponentials
 
-        def ptr(t):
-            return None if t is None else t.data_ptr()
+    def ptr(t):
+        return None if t is None else t.data_ptr()
 
+    with _on_device(di):
+        scratch = torch.cuda.caching_allocator_alloc(nbytes, di, torch.cuda.current_stream(di)) if nbytes > 0 \
+            else None
         try:
             _lib.call("mec_backward", x.data_ptr(), ldx, y.data_ptr(), ldy, n, d, dt, mode, int(normalize),
                       temperature, grad_scale, ws.data_ptr(), go.data_ptr(), scratch, nbytes,
-                      ptr(acc_x), ptr(acc_y), ptr(dx), ptr(dy), stream.cuda_stream)
+                      ptr(acc_x), ptr(acc_y), ptr(dx), ptr(dy), _stream(di))
         finally:
             if scratch is not None:
                 torch.cuda.caching_allocator_delete(scratch)
