@@ -153,7 +153,7 @@ const char* mec_version(void);
 /* Number of floats of the per-call workspace: 8 vectors of length n
  * (inverse norms rx, ry; raw diagonal x_i.y_i; off-diagonal row/column sums
  * of E = exp((S-1)/T); 1/R; 1/C; diagonal gradient coefficient), then
- * ceil(n/1024) doubles of loss partials (mec_finalize), then 48 x n floats
+ * ceil(n/256) doubles of loss partials (mec_finalize), then 48 x n floats
  * of partial sums (the deterministic forward, MEC_FLAG_DETERMINISTIC).  The
  * workspace must be 8-byte aligned.  The same workspace must be passed to
  * mec_forward and the matching mec_backward (it replaces

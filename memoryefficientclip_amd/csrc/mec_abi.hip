@@ -807,8 +807,8 @@ int mec_finalize(int64_t n, int mode, float temperature, float* workspace, float
   // partials after the 8 slots (8 n floats: 8-byte aligned when the workspace is)
   double* partial = (double*)(workspace + (int64_t)WS_NSLOTS * n);
   DISPATCH_BOOL(is_lit(mode), LIT, {
-    if (nparts <= FIN_SINGLE) {
-      k_finalize_rows<LIT, true><<<1, FIN_ROWS, 0, s>>>((int)n, inv_t, workspace, partial, loss);
+    if (n <= FIN_SINGLE_ROWS) {
+      k_finalize_rows<LIT, true><<<1, FIN_SINGLE_ROWS, 0, s>>>((int)n, inv_t, workspace, partial, loss);
     } else {
       k_finalize_rows<LIT, false><<<nparts, FIN_ROWS, 0, s>>>((int)n, inv_t, workspace, partial, loss);
       k_finalize_sum<LIT><<<1, 1024, 0, s>>>((int)n, nparts, partial, loss);
@@ -839,8 +839,7 @@ int mec_forward(const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t 
     const double inv_t = 1.0 / (double)temperature;
     // fixed-point units of the loss partials: every loss term is at most
     // ln n + 2/T for |cos| <= 1, so the total is at most B = (2n or n)(ln n +
-    // 2/T); lscale = 2^floor(log2(2^51 / B)) leaves a factor 64 below the 58
-    // bits of the accumulator's sum field
+    // 2/T); lscale = 2^floor(log2(2^51 / B)) keeps it within KEEP_LOSS_CAP
     const double bound = (is_lit(mode) ? 1.0 : 2.0) * (double)n * (std::log((double)n) + 2.0 * inv_t) + 1.0;
     const double lscale = std::ldexp(1.0, (int)std::floor(std::log2(std::ldexp(1.0, 51) / bound)));
     const unsigned grid = (unsigned)(kb.kt * kb.kt);

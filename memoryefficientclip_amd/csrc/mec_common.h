@@ -45,7 +45,7 @@ enum WsSlot {
   WS_RX = 0, WS_RY = 1, WS_DIAG = 2, WS_ROW_OFF = 3, WS_COL_OFF = 4,
   WS_INV_ROW = 5, WS_INV_COL = 6, WS_KAPPA = 7, WS_NSLOTS = 8
 };
-constexpr int FIN_ROWS = 1024;  // rows per workgroup of the loss finalize
+constexpr int FIN_ROWS = 256;  // rows per workgroup of the loss finalize (one per thread)
 // deterministic forward: at most DET_P row blocks x DET_Q column blocks of
 // tiles, whose (DET_Q + DET_P) x n partial sums follow the loss partials in
 // the workspace (DET_Q row partials per row, then DET_P column partials per

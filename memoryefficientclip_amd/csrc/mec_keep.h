@@ -35,6 +35,12 @@ namespace mec {
 constexpr int KEEP_T = 64;                       // tile (and index block) size
 constexpr int KEEP_MAX_N = 2048;                 // MEC_KEEP_EXP_MAX_N
 constexpr int KEEP_MAX_KT = KEEP_MAX_N / KEEP_T;  // blocks per side
+// the finalize's loss word: bits 0-5 count the diagonal blocks, bits 6-61
+// hold the fixed-point sum, bit 62 flags a partial past KEEP_LOSS_CAP, bit 63
+// a NaN partial
+constexpr unsigned long long KEEP_LOSS_OVF = 1ull << 62, KEEP_LOSS_NAN = 1ull << 63;
+constexpr double KEEP_LOSS_CAP = 2251799813685248.0;  // 2^51: 32 of them fill bits 6-61
+static_assert(KEEP_MAX_KT <= 63 && KEEP_LOSS_CAP * KEEP_MAX_KT * 64 <= (double)KEEP_LOSS_OVF, "loss word fields");
 
 // The kept matrix and the forward's bookkeeping, carved from the workspace by
 // the host (256-byte aligned parts).
@@ -176,7 +182,10 @@ __global__ __launch_bounds__(KEEP_NT, 2) void k_keep_forward(const float* __rest
 // the order of arrival, so the total is reproducible bit for bit; the word
 // carries both the data and the count, so no fence is needed; and the block
 // whose addition completes the count writes the loss.  The host sizes lscale
-// so that the total stays 64 times below the 58-bit field for |cos| <= 1.
+// so that the total stays within KEEP_LOSS_CAP for |cos| <= 1; the 32
+// blocks' sums of at most KEEP_LOSS_CAP each fill the 56-bit field below two
+// flag bits, which a NaN partial (KEEP_LOSS_NAN: the loss is NaN) or one past
+// the cap (KEEP_LOSS_OVF: +inf) set instead of adding.
 // MKT >= kt: the tile partials each row's thread loads (16 when kt <= 16,
 // which halves the finalize's loads at n <= 1024).
 template <bool LIT, bool NORM, int MKT = KEEP_MAX_KT>
@@ -242,7 +251,7 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double in
   __syncthreads();
   // the diagonal blocks' loss partial first (its atomic's round trip then
   // overlaps the block's S -> H)
-  unsigned long long lsum = 0ull;
+  unsigned long long lword = 0ull;
   bool last = false;
   if (dg && t < KEEP_T) {
     const int i = p * KEEP_T + t;
@@ -251,10 +260,22 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double in
     if (i < N) ws[WS_KAPPA * n64 + i] = (float)kap;
     const double tot = wave_sum_f64(v);  // >= 0: every term is
     if (t == 0) {
-      const unsigned long long add = ((unsigned long long)llrint(tot * lscale) << 6) + 1ull;
+      // a NaN partial, or one past the bound (an infinite term, |cos| > 1
+      // with normalized_inputs=True), sets a flag bit instead of adding: an
+      // OR to the same word, which the last block's addition then returns
+      // (one location: this block's OR precedes its own addition, which
+      // precedes the last block's)
+      const double u = tot * lscale;
+      unsigned long long add = 1ull;
+      if (u != u)
+        __hip_atomic_fetch_or(kb.lacc, KEEP_LOSS_NAN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else if (!(u <= KEEP_LOSS_CAP))
+        __hip_atomic_fetch_or(kb.lacc, KEEP_LOSS_OVF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        add += (unsigned long long)llrint(u) << 6;
       const unsigned long long old = __hip_atomic_fetch_add(kb.lacc, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = (old & 63ull) == (unsigned long long)(T - 1);
-      lsum = (old + add) >> 6;
+      lword = old + add;
     }
   }
   // S -> H (the forward's E: the same expression on the same values)
@@ -292,7 +313,12 @@ __global__ __launch_bounds__(256) void k_keep_finalize(int N, float c, double in
     else
       kb.rowdot[(int64_t)q * kb.np + p * KEEP_T + r] = v;
   }
-  if (last) *loss = (float)((double)lsum / lscale / (LIT ? (double)N : 2.0 * (double)N));
+  if (last) {
+    const double sum = (double)((lword & (KEEP_LOSS_OVF - 1)) >> 6);
+    *loss = (lword & KEEP_LOSS_NAN) ? __builtin_nanf("")
+            : (lword & KEEP_LOSS_OVF) ? __builtin_inff()
+                                      : (float)(sum / lscale / (LIT ? (double)N : 2.0 * (double)N));
+  }
 }
 
 // The post-pass operands of the fused backward (mec_backward): the

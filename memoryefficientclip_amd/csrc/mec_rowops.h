@@ -96,31 +96,32 @@ __device__ __forceinline__ double finalize_row(int i, int64_t n, double inv_t, f
   return acc;
 }
 
-// Pass 1: one thread per row (rows beyond N contribute nothing); each
-// workgroup writes the fp64 sum of its rows' loss terms to partial[blockIdx.x].
-// SINGLE (N <= FIN_SINGLE * FIN_ROWS, one workgroup): thread t takes rows
-// t, t + FIN_ROWS, ... in that order, and the workgroup writes the loss
-// itself (no second pass, one launch fewer for a small N).
-constexpr int FIN_SINGLE = 4;
+// Pass 1: one thread per row (rows beyond N contribute nothing), FIN_ROWS
+// rows per workgroup; each workgroup writes the fp64 sum of its rows' loss
+// terms to partial[blockIdx.x].  SINGLE (N <= FIN_SINGLE_ROWS): one
+// workgroup of FIN_SINGLE_ROWS threads, one row each, writes the loss itself
+// (no second pass).  One row per thread spreads the rows' fp64 work over N /
+// 256 CUs: with one 1024-thread workgroup taking up to four rows per thread
+// up to N = 4096, the finalize took 11 us at N = 2048 and 21 us at N = 4096
+// (each row's loads, fp64 exp / log and stores one after the other on one
+// CU), against 8.8 and 9.4 us for both passes now; up to 1024 rows the one
+// workgroup stays faster than two launches (6 against 9 us).
+constexpr int FIN_SINGLE_ROWS = 1024;
 template <bool LIT, bool SINGLE>
-__global__ __launch_bounds__(FIN_ROWS) void k_finalize_rows(int N, double inv_t, float* __restrict__ ws,
-                                                            double* __restrict__ partial, float* __restrict__ loss) {
-  __shared__ double red[FIN_ROWS / 64];
+__global__ __launch_bounds__(SINGLE ? FIN_SINGLE_ROWS : FIN_ROWS) void k_finalize_rows(
+    int N, double inv_t, float* __restrict__ ws, double* __restrict__ partial, float* __restrict__ loss) {
+  constexpr int NT = SINGLE ? FIN_SINGLE_ROWS : FIN_ROWS;
+  __shared__ double red[NT / 64];
   const int64_t n = N;
-  double acc = 0.0;
-  if (SINGLE) {
-    for (int i = threadIdx.x; i < N; i += FIN_ROWS) acc += finalize_row<LIT>(i, n, inv_t, ws);
-  } else {
-    const int i = blockIdx.x * FIN_ROWS + threadIdx.x;
-    if (i < N) acc = finalize_row<LIT>(i, n, inv_t, ws);
-  }
+  const int i = blockIdx.x * NT + threadIdx.x;
+  double acc = i < N ? finalize_row<LIT>(i, n, inv_t, ws) : 0.0;
   acc = wave_sum_f64(acc);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (lane == 0) red[w] = acc;
   __syncthreads();
   if (threadIdx.x == 0) {
     double tot = 0.0;
-    for (int k = 0; k < FIN_ROWS / 64; ++k) tot += red[k];
+    for (int k = 0; k < NT / 64; ++k) tot += red[k];
     if (SINGLE)
       *loss = (float)(tot / (LIT ? (double)N : 2.0 * (double)N));
     else

@@ -59,8 +59,10 @@ def budget(n, d, dt):
 def test_sizes():
     lib = _lib.load()
     # 8 vectors, the fp64 loss partials (2 floats per 1024 rows), 48 x n deterministic partials
-    assert lib.mec_workspace_floats(1000) == 8000 + 2 + 48000
-    assert lib.mec_workspace_floats(1025) == 8 * 1025 + 4 + 48 * 1025
+    # 8 vectors, one fp64 loss partial per 256 rows, the deterministic forward's 48 partials per index
+    assert lib.mec_workspace_floats(1000) == 8000 + 2 * 4 + 48000
+    assert lib.mec_workspace_floats(1025) == 8 * 1025 + 2 * 5 + 48 * 1025
+    assert lib.mec_workspace_floats(256) == 56 * 256 + 2
     assert lib.mec_workspace_floats(0) < 0
     for n, d in [(1024, 512), (32768, 1152), (65536, 768), (262144, 1152), (1000, 3), (777, 1152)]:
         for dt in (0, 1, 2, 3, 4):

@@ -197,6 +197,35 @@ def test_keep_under_deterministic_algorithms():
     check("keep, deterministic", det[0], rl, [("dx", det[1], rda), ("dy", det[2], rdb)])
 
 
+@pytest.mark.parametrize("case", ["nan", "overflow"])
+def test_keep_non_finite_loss(monkeypatch, case):
+    """A NaN input gives a NaN loss, and rows far outside the unit sphere
+    under normalized_inputs=True (cos >> 1: exp overflows in fp32) an
+    infinite one, on the kept path as on the recomputing path (the kept
+    finalize's fixed-point loss word carries both as flag bits)."""
+    n, d = 300, 64
+    a, b = randn_pair(n, d, seed=31)
+    if case == "nan":
+        a[7, 5] = float("nan")
+        mod = MemoryEfficientCLIPLoss(0.07)
+    else:
+        # every row near one direction at norm 3: the off-diagonal cos are
+        # about 9, and exp((cos - 1) / T) overflows in the tiles' fp32 sums
+        u = torch.nn.functional.normalize(a[:1], dim=1)
+        a = 3.0 * torch.nn.functional.normalize(u + 0.01 * a, dim=1)
+        b = 3.0 * torch.nn.functional.normalize(u + 0.01 * b, dim=1)
+        mod = MemoryEfficientCLIPLoss(0.07, normalized_inputs=True)
+    kept = fwd_bwd(mod, a, b)
+    monkeypatch.setenv("MEC_KEEP_EXP", "0")
+    rec = fwd_bwd(mod, a, b)
+    assert kept[3] and not rec[3]
+    say(f"{case}: kept loss {float(kept[0])}, recomputing {float(rec[0])}")
+    if case == "nan":
+        assert torch.isnan(kept[0]) and torch.isnan(rec[0])
+    else:
+        assert torch.isinf(kept[0]) and kept[0] > 0 and not torch.isfinite(rec[0])
+
+
 def test_keep_c_abi_entry_points():
     """mec_forward with the flag, then mec_backward (no scratch), mec_grad +
     mec_postpass and mec_backward_noalloc on the same kept workspace.
